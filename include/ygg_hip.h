@@ -1,0 +1,96 @@
+/*
+ * ygg_hip: the int8 streaming step of Yggdrasil on AMD Instinct MI355X (gfx950), as a C-ABI shared library
+ * (yggdrasil_amd/libygg_hip.so).
+ *
+ * The reference runs this step in cpu/ygg.cpp (one stream per process, one core, AVX-512 VNNI) and exposes it only as
+ * a CLI with files in and out (cpu/ygg.cpp:25-29, 500-574). This library keeps the same model file (YGG1, written by
+ * cpu/export.py:444-468) and the same arithmetic bit for bit, and runs B independent streams per launch on the GPU.
+ *
+ * Conventions:
+ *   - Every pointer named d_* is device memory on the model's device. Every call is ordered on the caller's HIP
+ *     stream (`stream`, a hipStream_t passed as void*; NULL is the default stream) and returns without waiting.
+ *   - Errors are returned as YGG_* status codes; the message of the last error on the calling thread is
+ *     ygg_last_error(). Nothing exits the process (the reference's die(), cpu/ygg.cpp:41-43, exits).
+ *   - State is int8 (B, L, n) row-major: the L layer states of one stream are contiguous, as State.q in
+ *     cpu/ygg.cpp:439, 474-481. A zero state is the reference's reset() (cpu/ygg.cpp:481).
+ *   - Tokens must lie in [0, vocab). The kernels never read out of bounds for a bad token: the stream stops at that
+ *     token (its state keeps the value before it, its later outputs are left unwritten) and the model's error word
+ *     records it; ygg_take_errors() reports it (the reference checks the whole token file first, cpu/ygg.cpp:493-495).
+ */
+#ifndef YGG_HIP_H
+#define YGG_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    YGG_OK = 0,
+    YGG_ERR_IO = 1,        /* file cannot be opened or read */
+    YGG_ERR_FORMAT = 2,    /* not a YGG1 file, short file, missing array (cpu/ygg.cpp:139-140, 153, 163, 176) */
+    YGG_ERR_LIMITS = 3,    /* outside the supported LIMITS (cpu/ygg.cpp:141-146, 183-184) */
+    YGG_ERR_NOMEM = 4,     /* host or device allocation failed (cpu/ygg.cpp:120, 476-477) */
+    YGG_ERR_ARG = 5,       /* bad argument (null pointer, negative size) */
+    YGG_ERR_TOKEN = 6,     /* a token outside [0, vocab) reached a kernel (cpu/ygg.cpp:493-495) */
+    YGG_ERR_DEVICE = 7     /* a HIP runtime call failed */
+};
+
+typedef struct ygg_model ygg_model;
+
+typedef struct {
+    int32_t n_layers, d_state, block_size, vocab, vocab_pad, router_depth, n_experts;
+    int32_t readout_rank, layer_input_rank, input_rank, shift;
+    int32_t factored;          /* routed layers use factored input storage */
+    int32_t group;             /* group scales present */
+    int32_t device;            /* HIP device holding the weights */
+    int64_t file_array_bytes;  /* bytes of the file's arrays (the reference's Model::bytes, cpu/ygg.cpp:158, 167) */
+    int64_t device_bytes;      /* device memory held by the model */
+    int64_t gather_bytes[8];   /* per layer: bytes of one expert's transition, layer-input and readout weights */
+} ygg_info;
+
+/* Load a YGG1 model file onto `device`, relaying the weights out for the kernels.
+   Replaces load() and read_header() of cpu/ygg.cpp:137-220. d_state may be 64, 96, 128 or 256. */
+int ygg_load(const char *path, int device, ygg_model **out);
+
+/* The same from a model file already in host memory (`bytes` bytes at `data`). */
+int ygg_load_blob(const void *data, size_t bytes, int device, ygg_model **out);
+
+/* Shape of a loaded model (the Model fields of cpu/ygg.cpp:112-116). */
+int ygg_model_info(const ygg_model *m, ygg_info *info);
+
+/* Release a model's device and host memory. Safe on NULL. */
+void ygg_free(ygg_model *m);
+
+/* One token for each of B streams: step<>() of cpu/ygg.cpp:441-459 applied to B independent streams.
+   d_tokens (B) int32; d_state_in, d_state_out (B, L, n) int8, which may be the same buffer; d_logits (B, vocab) f32;
+   d_leaves (B, L) int32 or NULL: the expert of every layer (layer 0: the token), as the Triton step's expert_out
+   (yggdrasil/inference_triton.py:45, 86). */
+int ygg_step(const ygg_model *m, const int32_t *d_tokens, const int8_t *d_state_in, int8_t *d_state_out,
+             float *d_logits, int32_t *d_leaves, int B, void *stream);
+
+/* T tokens for each of B streams in one launch, the state carried from token to token and left in d_state: the hot
+   loop of cmd_logits_score (cpu/ygg.cpp:507-517) for B streams at once.
+   d_tokens (B, T) int32; d_state (B, L, n) int8 in and out; optional outputs (NULL: not written):
+   d_logits (B, T, vocab) f32, d_leaves (B, T, L) int32, d_states (B, T, L, n) int8 (the state after every token),
+   d_digest (B) uint64 in and out: d = d * 0x100000001B3 + (leaf * 0xD6E8FEB86659FD93
+   + sum_i (u8(q_i) + 1) * ((2 i + 1) * 0x9E3779B97F4A7C15) + l) for every token and layer in order (mod 2^64). */
+int ygg_run(const ygg_model *m, const int32_t *d_tokens, int B, int T, int8_t *d_state, float *d_logits,
+            int32_t *d_leaves, int8_t *d_states, uint64_t *d_digest, void *stream);
+
+/* Wait for `stream`, then return and clear the model's error word: bit 0 set when a kernel met a token outside
+   [0, vocab) since the last call. */
+int ygg_take_errors(const ygg_model *m, void *stream, uint32_t *errors);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char *ygg_last_error(void);
+
+/* Library ABI version (bumped when a signature above changes). */
+int ygg_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* YGG_HIP_H */

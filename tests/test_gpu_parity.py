@@ -1,0 +1,194 @@
+"""GPU parity: the gfx950 step through the C-ABI against the CPU oracle, bit-exact.
+
+Leaves, int8 states (after every token and layer) and f32 logits must equal the oracle's exactly; the oracle is
+pinned to the reference kernel (cpu/ygg.cpp) in tests/test_oracle.py. Shapes: the 17 shapes of the reference's
+kernel test (cpu/tests/test_kernel.py:22-33, seed 7, 8 streams x 64 tokens, zero state per stream), the benchmark
+configurations at reduced stream counts, and edge cases (empty batch, zero tokens, aliased state, bad tokens,
+carried state, graph replay).
+"""
+import ctypes
+import os
+
+import numpy as np
+import pytest
+
+from oracle.oracle import Oracle
+from yggdrasil_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+@pytest.fixture(scope="module")
+def hip():
+    import torch  # noqa: F401
+    from yggdrasil_amd.inference import Yggdrasil
+    return Yggdrasil
+
+
+def _compare(got, ref, keys=("leaves", "states", "logits")):
+    for k in keys:
+        a, b = got[k], ref[k]
+        assert a.shape == b.shape, (k, a.shape, b.shape)
+        if not np.array_equal(a, b):
+            bad = np.argwhere(a != b)
+            raise AssertionError(f"{k}: {len(bad)} mismatches, first at {bad[:4].tolist()}: "
+                                 f"gpu {a[tuple(bad[0])]} oracle {b[tuple(bad[0])]}")
+
+
+def _gpu_run(model, x, state=None, states=True):
+    import torch
+    r = model.run(x, state=state, leaves=True, states=states)
+    torch.cuda.synchronize()
+    return {k: v.cpu().numpy() for k, v in r.items()}
+
+
+@pytest.mark.parametrize("ci", range(len(synth.KERNEL_CASES)))
+def test_kernel_case(hip, model_dir, ci):
+    spec = synth.KERNEL_CASES[ci]
+    _say(f"case {ci}: {spec}")
+    path = model_dir / f"kernel{ci}.bin"
+    synth.write_model(spec, synth.KERNEL_SEED, path)
+    x = synth.kernel_tokens(spec.vocab)
+    ref = Oracle(path).run(x, states=True)
+    model = hip.load(path)
+    got = _gpu_run(model, x)
+    _compare(got, ref)
+    np.testing.assert_array_equal(got["state"], ref["state"])
+    model.close()
+
+
+@pytest.fixture(scope="module")
+def c12(model_dir):
+    w = synth.CONFIGS[2]
+    path = model_dir / "c12.bin"
+    synth.write_model(w.spec, w.model_seed, path)
+    return path
+
+
+def test_config1_full_stream(hip, c12):
+    """Config 1: one stream of 4096 uniform bytes (the reference's CPU plumbing case), every token checked."""
+    w = synth.CONFIGS[1]
+    x = w.make_tokens()
+    _say(f"config 1: {x.shape}")
+    ref = Oracle(c12).run(x, states=True)
+    model = hip.load(c12)
+    _compare(_gpu_run(model, x), ref)
+
+
+def test_config2_subset(hip, c12):
+    """Config 2 at 64 streams x 512 Zipf(1.1) tokens."""
+    w = synth.CONFIGS[2]
+    x = w.make_tokens(64, 512)
+    _say(f"config 2: {x.shape}")
+    ref = Oracle(c12).run(x, states=True)
+    model = hip.load(c12)
+    _compare(_gpu_run(model, x), ref)
+
+
+def test_config3_subset(hip, model_dir):
+    """Config 3 (V = 5, d = 96, D = 13, 3 layers) at 32 streams x 256 tokens."""
+    w = synth.CONFIGS[3]
+    path = model_dir / "c3.bin"
+    synth.write_model(w.spec, w.model_seed, path)
+    x = w.make_tokens(32, 256)
+    _say(f"config 3: {x.shape}")
+    ref = Oracle(path).run(x, states=True)
+    model = hip.load(path)
+    _compare(_gpu_run(model, x), ref)
+
+
+def test_carried_state_and_step(hip, c12):
+    """A launch continuing from a nonzero state; step() token by token equals one run()."""
+    import torch
+    w = synth.CONFIGS[2]
+    x = w.make_tokens(16, 48)
+    model = hip.load(c12)
+    o = Oracle(c12)
+    first = o.run(x[:, :16])
+    ref = o.run(x[:, 16:], state=first["state"], states=True)
+    st0 = torch.as_tensor(first["state"], device=model.device)
+    _compare(_gpu_run(model, x[:, 16:], state=st0), ref)
+    st = st0.clone()
+    for t in range(16, 24):
+        lg, st = model.step(x[:, t], st)
+        np.testing.assert_array_equal(lg.cpu().numpy(), ref["logits"][:, t - 16])
+        np.testing.assert_array_equal(st.cpu().numpy(), ref["states"][:, t - 16])
+
+
+def test_step_in_place_and_edges(hip, c12):
+    """ygg_step with state_in == state_out; B = 0 and T = 0 are no-ops."""
+    import torch
+    from yggdrasil_amd import _lib
+    model = hip.load(c12)
+    L = _lib.lib()
+    x = synth.CONFIGS[2].make_tokens(8, 1)
+    ref = Oracle(c12).run(x)
+    xt = torch.as_tensor(x[:, 0], device=model.device).contiguous()
+    st = model.init_state(8)
+    lg = torch.empty(8, model.vocab, device=model.device)
+    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    _lib.check(L.ygg_step(model._h, p(xt), p(st), p(st), p(lg), None, 8, s))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(lg.cpu().numpy(), ref["logits"][:, 0])
+    np.testing.assert_array_equal(st.cpu().numpy(), ref["state"])
+    _lib.check(L.ygg_step(model._h, None, None, None, None, None, 0, s))
+    before = st.clone()
+    _lib.check(L.ygg_run(model._h, p(xt), 8, 0, p(st), None, None, None, None, s))
+    torch.cuda.synchronize()
+    assert torch.equal(before, st)
+    assert L.ygg_run(model._h, p(xt), -1, 1, p(st), None, None, None, None, s) == 5
+
+
+def test_bad_token_stops_stream(hip, c12):
+    """A token outside [0, V) stops its stream at that token and sets the error word; other streams go on."""
+    import torch
+    from yggdrasil_amd import _lib
+    model = hip.load(c12)
+    x = synth.CONFIGS[2].make_tokens(4, 8)
+    bad = x.copy()
+    bad[1, 5] = 999
+    ref = Oracle(c12).run(x)
+    ref_bad_prefix = Oracle(c12).run(x[1:2, :5])
+    xt = torch.as_tensor(bad, device=model.device).contiguous()
+    st = model.init_state(4)
+    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    _lib.check(_lib.lib().ygg_run(model._h, ctypes.c_void_p(xt.data_ptr()), 4, 8, ctypes.c_void_p(st.data_ptr()),
+                                  None, None, None, None, s))
+    assert model.take_errors() == 1
+    assert model.take_errors() == 0
+    got = st.cpu().numpy()
+    np.testing.assert_array_equal(got[[0, 2, 3]], ref["state"][[0, 2, 3]])
+    np.testing.assert_array_equal(got[1], ref_bad_prefix["state"][0])
+    with pytest.raises(ValueError):
+        model.run(bad)
+
+
+def test_digest_matches_oracle(hip, c12):
+    import torch
+    x = synth.CONFIGS[2].make_tokens(32, 64)
+    model = hip.load(c12)
+    r = model.run(x, logits=False, digest=True)
+    torch.cuda.synchronize()
+    ref = Oracle(c12).run(x, logits=False, leaves=False, digest=True)
+    np.testing.assert_array_equal(r["digest"].cpu().numpy().view(np.uint64), ref["digest"])
+
+
+def test_graph_replay(hip, c12):
+    """graph=True: one captured step per batch size, replayed with eager work between replays, every replay
+    equal to the eager step."""
+    import torch
+    x = synth.CONFIGS[2].make_tokens(8, 6)
+    eager = hip.load(c12)
+    g = hip.load(c12, graph=True)
+    se, sg = eager.init_state(8), g.init_state(8)
+    for t in range(6):
+        le, se = eager.step(x[:, t], se)
+        lgr, sg = g.step(x[:, t], sg)
+        _ = torch.randn(1000, device=eager.device).sum()   # eager work between replays
+        torch.cuda.synchronize()
+        assert torch.equal(le, lgr) and torch.equal(se, sg), t

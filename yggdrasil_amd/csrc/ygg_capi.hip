@@ -1,0 +1,562 @@
+// C-ABI of the MI355X int8 streaming step: model loading (YGG1 parse, validation, relayout into the device layout of
+// ygg_layout.h, upload) and the stream-ordered step/run entry points declared in include/ygg_hip.h.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "../../include/ygg_hip.h"
+#include "ygg_layout.h"
+
+namespace ygg {
+// kernel launchers, one per (d_state, block, readout rank); defined in ygg_kernels_*.hip
+typedef hipError_t (*Launcher)(const YggDevModel &, const int32_t *, int, int, int8_t *, float *, int32_t *, int8_t *,
+                               unsigned long long *, hipStream_t);
+Launcher find_launcher(int n, int blk, int R);
+}  // namespace ygg
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+#define HIP_TRY(expr)                                                                                  \
+    do {                                                                                               \
+        hipError_t e_ = (expr);                                                                        \
+        if (e_ != hipSuccess) return fail(YGG_ERR_DEVICE, "%s: %s", #expr, hipGetErrorString(e_));     \
+    } while (0)
+
+struct FileArrays {
+    int32_t n_layers, n, blk, V, D, R, R2, reserved, router_token_dim, K, shift, n_arrays;
+    std::map<std::string, std::pair<const uint8_t *, int64_t>> arr;
+    int64_t bytes;
+    const uint8_t *get(const std::string &name, int64_t *nb = nullptr) const {
+        auto it = arr.find(name);
+        if (it == arr.end()) return nullptr;
+        if (nb) *nb = it->second.second;
+        return it->second.first;
+    }
+};
+
+// Header + array table (cpu/ygg.cpp:137-171); LIMITS of the reference plus d_state 96.
+int parse(const uint8_t *data, size_t size, FileArrays &fa) {
+    if (size < 52 || memcmp(data, "YGG1", 4)) return fail(YGG_ERR_FORMAT, "not a model file");
+    int32_t h[12];
+    memcpy(h, data + 4, sizeof h);
+    fa.n_layers = h[0]; fa.n = h[1]; fa.blk = h[2]; fa.V = h[3]; fa.D = h[4]; fa.R = h[5]; fa.R2 = h[6];
+    fa.reserved = h[7]; fa.router_token_dim = h[8]; fa.K = h[9]; fa.shift = h[10]; fa.n_arrays = h[11];
+    const bool ok = (fa.n == 64 || fa.n == 96 || fa.n == 128 || fa.n == 256) && (fa.blk == 8 || fa.blk == 16) &&
+                    (fa.R == 8 || fa.R == 16 || fa.R == 32) && fa.R2 >= 0 && fa.R2 <= YGG_MAX_RANK &&
+                    fa.R2 % 4 == 0 && fa.n_layers >= 1 && fa.n_layers <= YGG_MAX_LAYERS && fa.V >= 1 &&
+                    fa.V <= 256 && fa.D >= 0 && fa.D <= 16 && (fa.n_layers == 1 || fa.D >= 1) && fa.reserved == 0 &&
+                    fa.shift >= 1 && fa.shift <= 30 && fa.n_arrays > 0;
+    if (!ok) return fail(YGG_ERR_LIMITS, "unsupported model (LIMITS)");
+    const size_t tab_end = 52 + (size_t)fa.n_arrays * 48;
+    if (size < tab_end) return fail(YGG_ERR_FORMAT, "short array table");
+    const size_t base = (tab_end + 63) / 64 * 64;
+    if (size < base) return fail(YGG_ERR_FORMAT, "short model file");
+    fa.bytes = (int64_t)(size - base);
+    for (int i = 0; i < fa.n_arrays; i++) {
+        char name[33] = {0};
+        int64_t off, nb;
+        memcpy(name, data + 52 + (size_t)i * 48, 32);
+        memcpy(&off, data + 52 + (size_t)i * 48 + 32, 8);
+        memcpy(&nb, data + 52 + (size_t)i * 48 + 40, 8);
+        if (off < 0 || nb < 0 || off + nb > fa.bytes)
+            return fail(YGG_ERR_FORMAT, "short model file (array %s)", name);
+        fa.arr[name] = {data + base + off, nb};
+    }
+    return YGG_OK;
+}
+
+// Layout sizes of one layer's gather record (see ygg_layout.h).
+struct GatherLayout {
+    int64_t bytes;
+    int off_P, off_U, off_F, off_FB, off_FS;
+};
+GatherLayout gather_layout(int n, int blk, int R, int R2, int K, bool routed, bool factored) {
+    GatherLayout g;
+    int64_t o = (int64_t)n * blk * 2;  // A
+    g.off_P = (int)o;
+    o += (int64_t)R * n;
+    g.off_U = -1;
+    if (routed && R2) { g.off_U = (int)o; o += (int64_t)R2 * n; }
+    g.off_F = g.off_FB = g.off_FS = -1;
+    if (factored) {
+        g.off_F = (int)o; o += (int64_t)K * n;
+        g.off_FB = (int)o; o += 2 * (int64_t)n;
+        g.off_FS = (int)o; o += 4;
+    }
+    g.bytes = (o + 127) / 128 * 128;
+    return g;
+}
+
+// One file layer's views.
+struct FileLayer {
+    const uint8_t *rec = nullptr; int64_t rec_nb = 0;
+    int record_bytes = 0, off_A = -1, off_U2 = -1, off_P = -1, off_T = -1, off_F = -1, off_C = -1, off_S = -1;
+    const uint8_t *Q = nullptr; int64_t Q_nb = 0;
+    const float *scal = nullptr;
+    const uint8_t *w = nullptr; int64_t w_nb = 0;
+    const float *thr = nullptr; int64_t thr_nb = 0;
+    const uint8_t *vl = nullptr; int64_t vl_nb = 0;
+    const float *mv = nullptr; int64_t mv_nb = 0;
+    const float *mulv = nullptr, *r2b = nullptr, *mzl = nullptr, *sqv = nullptr, *mT = nullptr;
+    int64_t mulv_nb = 0, r2b_nb = 0, mzl_nb = 0, sqv_nb = 0, mT_nb = 0;
+    const int8_t *vt = nullptr; int64_t vt_nb = 0;
+};
+
+// Binds and size-checks the arrays of layer l (cpu/ygg.cpp:173-202); every array the kernels read is checked to hold
+// the bytes the kernels will read, so a malformed file fails here instead of faulting on the GPU.
+int bind_layer(const FileArrays &fa, int l, FileLayer &y) {
+    const std::string P = "l" + std::to_string(l) + "_";
+    const int n = fa.n, V = fa.V, E = l == 0 ? fa.V : (1 << fa.D), R = fa.R, R2 = fa.R2;
+    const int VP = (V + 31) / 32 * 32;
+    int64_t nb = 0;
+    auto need = [&](const char *tag, int64_t want, int64_t *got) -> const uint8_t * {
+        const uint8_t *p = fa.get(P + tag, got);
+        if (!p) { fail(YGG_ERR_FORMAT, "model file: missing %s%s", P.c_str(), tag); return nullptr; }
+        if (want >= 0 && *got < want) {
+            fail(YGG_ERR_FORMAT, "model file: %s%s holds %lld bytes, needs %lld", P.c_str(), tag, (long long)*got,
+                 (long long)want);
+            return nullptr;
+        }
+        return p;
+    };
+    const int32_t *meta = (const int32_t *)need("meta", 20, &nb);
+    if (!meta) return YGG_ERR_FORMAT;
+    const int nmeta = (int)(nb / 4);
+    y.record_bytes = meta[0]; y.off_A = meta[1]; y.off_U2 = meta[2]; y.off_P = meta[3]; y.off_T = meta[4];
+    y.vt = (const int8_t *)fa.get(P + "vt", &y.vt_nb);
+    const bool routed = l > 0;
+    if (y.vt) {
+        if (!routed) return fail(YGG_ERR_FORMAT, "model file: factored token layer");
+        if (fa.K % 4 || fa.K > YGG_MAX_RANK || fa.K < 4)
+            return fail(YGG_ERR_LIMITS, "model file: factored input_rank %d", fa.K);
+        if (nmeta < 8) return fail(YGG_ERR_FORMAT, "model file: %smeta lacks the factored offsets", P.c_str());
+        y.off_F = meta[5]; y.off_C = meta[6]; y.off_S = meta[7];
+        if (y.vt_nb < (int64_t)V * fa.K) return fail(YGG_ERR_FORMAT, "model file: %svt too short", P.c_str());
+        if (!(y.mT = (const float *)need("mT", 4LL * n, &y.mT_nb))) return YGG_ERR_FORMAT;
+    }
+    if (y.record_bytes <= 0) return fail(YGG_ERR_FORMAT, "model file: %smeta record size", P.c_str());
+    // the record parts must lie inside a record
+    auto part_ok = [&](int off, int64_t len) { return off >= 0 && off + len <= y.record_bytes; };
+    if (!part_ok(y.off_A, 2LL * n * fa.blk) || !part_ok(y.off_P, (int64_t)R * n))
+        return fail(YGG_ERR_FORMAT, "model file: %smeta offsets", P.c_str());
+    if (routed && R2 && !part_ok(y.off_U2, (int64_t)R2 * n))
+        return fail(YGG_ERR_FORMAT, "model file: %smeta layer-input offset", P.c_str());
+    if (y.vt) {
+        if (!part_ok(y.off_F, (int64_t)fa.K * n) || !part_ok(y.off_C, 2LL * n) || !part_ok(y.off_S, 4))
+            return fail(YGG_ERR_FORMAT, "model file: %smeta factored offsets", P.c_str());
+    } else if (!part_ok(y.off_T, 2LL * n * (routed ? V : 1))) {
+        return fail(YGG_ERR_FORMAT, "model file: %smeta table offset", P.c_str());
+    }
+    if (!(y.rec = need("rec", (int64_t)E * y.record_bytes, &y.rec_nb))) return YGG_ERR_FORMAT;
+    if (!(y.Q = need("Q", (int64_t)R * VP, &y.Q_nb))) return YGG_ERR_FORMAT;
+    if (!(y.scal = (const float *)need("scal", 16, &nb))) return YGG_ERR_FORMAT;
+    y.mzl = (const float *)fa.get(P + "mzl", &y.mzl_nb);
+    if (y.mzl && y.mzl_nb < 4LL * E * (R == 8 ? 16 : R)) return fail(YGG_ERR_FORMAT, "model file: %smzl", P.c_str());
+    y.sqv = (const float *)fa.get(P + "sqv", &y.sqv_nb);
+    if (y.sqv && y.sqv_nb < 4LL * VP) return fail(YGG_ERR_FORMAT, "model file: %ssqv", P.c_str());
+    if (routed) {
+        if (!(y.w = need("w", (int64_t)E * n, &y.w_nb))) return YGG_ERR_FORMAT;
+        if (!(y.thr = (const float *)need("thr", 4LL * V * E, &y.thr_nb))) return YGG_ERR_FORMAT;
+        if (R2) {
+            const int RG = (R2 + 15) / 16;
+            if (!(y.vl = need("vl", 16LL * RG * n, &y.vl_nb))) return YGG_ERR_FORMAT;
+            if (!(y.mv = (const float *)need("mv", 4LL * 16 * RG, &y.mv_nb))) return YGG_ERR_FORMAT;
+        }
+        y.mulv = (const float *)fa.get(P + "mulv", &y.mulv_nb);
+        if (y.mulv && y.mulv_nb < 4LL * n) return fail(YGG_ERR_FORMAT, "model file: %smulv", P.c_str());
+        y.r2b = (const float *)fa.get(P + "r2b", &y.r2b_nb);
+        if (y.r2b && y.r2b_nb < 4LL * (n / 16)) return fail(YGG_ERR_FORMAT, "model file: %sr2b", P.c_str());
+    }
+    return YGG_OK;
+}
+
+inline int16_t rd16(const uint8_t *p) { int16_t v; memcpy(&v, p, 2); return v; }
+
+// File record of one expert -> its gather record (layout in ygg_layout.h).
+void relayout_expert(const FileArrays &fa, const FileLayer &fy, const GatherLayout &gl, bool routed,
+                     const uint8_t *frec, uint8_t *g) {
+    const int n = fa.n, blk = fa.blk, R = fa.R, R2 = fa.R2, K = fa.K;
+    const int C = lanes_c(n), NL = n / C;
+    // A: lane l's rows C l .. C l + C - 1, each its b block columns; file [n/16][b/2][16][2] int16
+    const uint8_t *A = frec + fy.off_A;
+    for (int l = 0; l < NL; l++)
+        for (int c = 0; c < C; c++) {
+            const int i = C * l + c, g16 = i / 16, rr = i % 16;
+            for (int j = 0; j < blk; j++) {
+                const int16_t v = rd16(A + (((size_t)(g16 * (blk / 2) + j / 2) * 16 + rr) * 2 + (j & 1)) * 2);
+                const int byte = (c * blk + j) * 2, chunk = byte / 16, within = byte % 16;
+                memcpy(g + ((size_t)chunk * NL + l) * 16 + within, &v, 2);
+            }
+        }
+    // P: lane l -> row j = l / RL, coordinates [(l % RL) SP, +SP); file R = 8: [n/8][16][4], R >= 16: [R/16][n/4][16][4]
+    const uint8_t *Pf = frec + fy.off_P;
+    const int RL = 64 / R, SP = n / RL, GP = readout_gp(SP);
+    for (int l = 0; l < 64; l++) {
+        const int j = l / RL, k = l % RL;
+        for (int b = 0; b < SP; b++) {
+            const int i = k * SP + b;
+            size_t o;
+            if (R == 8) o = ((size_t)(i / 8) * 16 + 2 * j + (i % 8) / 4) * 4 + i % 4;
+            else o = (((size_t)(j / 16) * (n / 4) + i / 4) * 16 + j % 16) * 4 + i % 4;
+            g[gl.off_P + ((size_t)(b / GP) * 64 + l) * GP + b % GP] = (uint8_t)((int)Pf[o] - 128);
+        }
+    }
+    // U' and U: file [rank/4][n][4] u8 -> (k4, lane, c) dwords
+    auto proj = [&](const uint8_t *src, int rank, int off) {
+        for (int k4 = 0; k4 < rank / 4; k4++)
+            for (int l = 0; l < NL; l++)
+                for (int c = 0; c < C; c++) {
+                    const int i = C * l + c;
+                    for (int e = 0; e < 4; e++)
+                        g[off + (((size_t)k4 * NL + l) * C + c) * 4 + e] =
+                            (uint8_t)((int)src[((size_t)k4 * n + i) * 4 + e] - 128);
+                }
+    };
+    if (routed && R2) proj(frec + fy.off_U2, R2, gl.off_U);
+    if (gl.off_F >= 0) {
+        proj(frec + fy.off_F, K, gl.off_F);
+        memcpy(g + gl.off_FB, frec + fy.off_C, 2 * (size_t)n);
+        memcpy(g + gl.off_FS, frec + fy.off_S, 4);
+    }
+}
+
+template <class F> void parallel_for(int64_t count, F f) {
+    int nt = (int)std::min<int64_t>(std::max(1u, std::thread::hardware_concurrency()), 16);
+    if (count < 256) nt = 1;
+    std::vector<std::thread> th;
+    for (int k = 0; k < nt; k++)
+        th.emplace_back([=]() {
+            for (int64_t i = count * k / nt; i < count * (k + 1) / nt; i++) f(i);
+        });
+    for (auto &t : th) t.join();
+}
+
+}  // namespace
+
+struct ygg_model {
+    YggDevModel dev;
+    ygg_info info;
+    int device = 0;
+    void *arena = nullptr;
+    size_t arena_bytes = 0;
+    ygg::Launcher launch = nullptr;
+};
+
+namespace {
+
+int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
+    FileArrays fa;
+    if (int rc = parse(data, size, fa)) return rc;
+    const int L = fa.n_layers, n = fa.n, V = fa.V, VP = (V + 31) / 32 * 32, E = 1 << fa.D, R = fa.R, R2 = fa.R2;
+    ygg::Launcher launch = ygg::find_launcher(n, fa.blk, R);
+    if (!launch) return fail(YGG_ERR_LIMITS, "no kernel for d_state %d, block %d, readout rank %d", n, fa.blk, R);
+    int64_t hb_nb = 0;
+    const float *head_b = (const float *)fa.get("head_b", &hb_nb);
+    if (!head_b) return fail(YGG_ERR_FORMAT, "missing head_b");
+    if (hb_nb < 4LL * VP) return fail(YGG_ERR_FORMAT, "head_b too short");
+    std::vector<FileLayer> fl(L);
+    bool factored = false, group = false;
+    for (int l = 0; l < L; l++) {
+        if (int rc = bind_layer(fa, l, fl[l])) return rc;
+        factored = factored || fl[l].vt;
+        group = group || fl[l].mzl || fl[l].sqv || fl[l].r2b || fl[l].mulv;
+    }
+    for (int l = 1; l < L; l++)
+        if ((fl[l].vt != nullptr) != (fl[1].vt != nullptr))
+            return fail(YGG_ERR_FORMAT, "model file: mixed table and factored routed layers");
+
+    // device arena plan: every array 256-byte aligned
+    struct Piece { size_t off, bytes; };
+    size_t total = 0;
+    auto plan = [&](size_t bytes) { Piece p{total, bytes}; total += (bytes + 255) / 256 * 256; return p; };
+    const Piece p_err = plan(256);
+    const Piece p_bias = plan(4 * (size_t)VP);
+    struct LayerPlan {
+        GatherLayout gl;
+        Piece gath, table, w, thr, vl, mv, mulv, r2b, mz, sqv, Q, vt, mT;
+    };
+    std::vector<LayerPlan> lp(L);
+    for (int l = 0; l < L; l++) {
+        const FileLayer &y = fl[l];
+        const bool routed = l > 0;
+        const int El = routed ? E : V;
+        LayerPlan &p = lp[l];
+        p.gl = gather_layout(n, fa.blk, R, R2, fa.K, routed, y.vt != nullptr);
+        p.gath = plan((size_t)El * p.gl.bytes);
+        p.table = y.vt ? Piece{0, 0} : plan(2 * (size_t)n * (routed ? (size_t)E * V : (size_t)V));
+        p.Q = plan((size_t)VP * R);
+        p.mz = y.mzl ? plan(4 * (size_t)El * R) : Piece{0, 0};
+        p.sqv = y.sqv ? plan(4 * (size_t)VP) : Piece{0, 0};
+        if (routed) {
+            p.w = plan((size_t)E * n);
+            p.thr = plan(4 * (size_t)V * E);
+            const int RG = (R2 + 15) / 16;
+            p.vl = R2 ? plan(16 * (size_t)RG * n) : Piece{0, 0};
+            p.mv = R2 ? plan(4 * 16 * (size_t)RG) : Piece{0, 0};
+            p.mulv = y.mulv ? plan(4 * (size_t)n) : Piece{0, 0};
+            p.r2b = y.r2b ? plan(4 * (size_t)(n / 16)) : Piece{0, 0};
+            p.vt = y.vt ? plan((size_t)V * fa.K) : Piece{0, 0};
+            p.mT = y.vt ? plan(4 * (size_t)n) : Piece{0, 0};
+        }
+    }
+    // host image of the arena
+    std::vector<uint8_t> host;
+    try {
+        host.assign(total, 0);
+    } catch (const std::bad_alloc &) {
+        return fail(YGG_ERR_NOMEM, "out of host memory (%zu bytes)", total);
+    }
+    uint8_t *H = host.data();
+    memcpy(H + p_bias.off, head_b, 4 * (size_t)VP);
+    for (int l = 0; l < L; l++) {
+        const FileLayer &y = fl[l];
+        const LayerPlan &p = lp[l];
+        const bool routed = l > 0;
+        const int El = routed ? E : V;
+        uint8_t *gath = H + p.gath.off;
+        const GatherLayout gl = p.gl;
+        parallel_for(El, [&, gath, gl, routed](int64_t e) {
+            relayout_expert(fa, y, gl, routed, y.rec + e * y.record_bytes, gath + e * gl.bytes);
+        });
+        if (!y.vt) {
+            int16_t *tb = (int16_t *)(H + p.table.off);
+            if (routed) {
+                parallel_for(E, [&, tb](int64_t e) {
+                    memcpy(tb + (size_t)e * V * n, y.rec + e * y.record_bytes + y.off_T, 2 * (size_t)V * n);
+                });
+            } else {
+                for (int x = 0; x < V; x++) memcpy(tb + (size_t)x * n, y.rec + (size_t)x * y.record_bytes + y.off_T, 2 * (size_t)n);
+            }
+        }
+        int8_t *Qd = (int8_t *)(H + p.Q.off);
+        for (int c = 0; c < VP; c++)
+            for (int j = 0; j < R; j++) Qd[(size_t)c * R + j] = (int8_t)((int)y.Q[((size_t)(j / 4) * VP + c) * 4 + j % 4] - 128);
+        if (y.mzl) {
+            float *mz = (float *)(H + p.mz.off);
+            const int W = R == 8 ? 16 : R;
+            for (int e = 0; e < El; e++)
+                for (int j = 0; j < R; j++) mz[(size_t)e * R + j] = y.mzl[(size_t)e * W + (R == 8 ? 2 * j : j)];
+        }
+        if (y.sqv) memcpy(H + p.sqv.off, y.sqv, 4 * (size_t)VP);
+        if (routed) {
+            int8_t *wd = (int8_t *)(H + p.w.off);
+            for (size_t i = 0; i < (size_t)E * n; i++) wd[i] = (int8_t)((int)y.w[i] - 128);
+            memcpy(H + p.thr.off, y.thr, 4 * (size_t)V * E);
+            if (R2) {
+                const int RG = (R2 + 15) / 16;
+                int8_t *vd = (int8_t *)(H + p.vl.off);
+                for (int k = 0; k < 16 * RG; k++)
+                    for (int i = 0; i < n; i++)
+                        vd[(size_t)k * n + i] =
+                            (int8_t)((int)y.vl[(((size_t)(k / 16) * (n / 4) + i / 4) * 16 + k % 16) * 4 + i % 4] - 128);
+                memcpy(H + p.mv.off, y.mv, 4 * 16 * (size_t)RG);
+            }
+            if (y.mulv) memcpy(H + p.mulv.off, y.mulv, 4 * (size_t)n);
+            if (y.r2b) memcpy(H + p.r2b.off, y.r2b, 4 * (size_t)(n / 16));
+            if (y.vt) {
+                memcpy(H + p.vt.off, y.vt, (size_t)V * fa.K);
+                memcpy(H + p.mT.off, y.mT, 4 * (size_t)n);
+            }
+        }
+    }
+
+    // upload
+    int prev = 0;
+    HIP_TRY(hipGetDevice(&prev));
+    HIP_TRY(hipSetDevice(device));
+    void *arena = nullptr;
+    hipError_t e = hipMalloc(&arena, total);
+    if (e != hipSuccess) {
+        (void)hipSetDevice(prev);
+        return fail(YGG_ERR_NOMEM, "device allocation of %zu bytes failed: %s", total, hipGetErrorString(e));
+    }
+    e = hipMemcpy(arena, H, total, hipMemcpyHostToDevice);
+    (void)hipSetDevice(prev);
+    if (e != hipSuccess) {
+        (void)hipFree(arena);
+        return fail(YGG_ERR_DEVICE, "upload failed: %s", hipGetErrorString(e));
+    }
+    ygg_model *m = new ygg_model();
+    m->device = device;
+    m->arena = arena;
+    m->arena_bytes = total;
+    m->launch = launch;
+    uint8_t *A = (uint8_t *)arena;
+    auto at = [&](const Piece &p) -> void * { return p.bytes ? A + p.off : nullptr; };
+    YggDevModel &d = m->dev;
+    d.L = L; d.N = n; d.BLK = fa.blk; d.V = V; d.VP = VP; d.D = fa.D; d.E = E; d.R = R; d.R2 = R2; d.K = fa.K;
+    d.shift = fa.shift;
+    d.output_bias = (const float *)at(p_bias);
+    d.err = (uint32_t *)at(p_err);
+    for (int l = 0; l < L; l++) {
+        const FileLayer &y = fl[l];
+        const LayerPlan &p = lp[l];
+        YggDevLayer &z = d.layers[l];
+        z.gath = (const uint8_t *)at(p.gath);
+        z.table = (const int16_t *)at(p.table);
+        z.w = (const int8_t *)at(p.w);
+        z.thr = (const float *)at(p.thr);
+        z.vl = (const int8_t *)at(p.vl);
+        z.mv = (const float *)at(p.mv);
+        z.mulv = (const float *)at(p.mulv);
+        z.r2b = (const float *)at(p.r2b);
+        z.mz = (const float *)at(p.mz);
+        z.sqv = (const float *)at(p.sqv);
+        z.Q = (const int8_t *)at(p.Q);
+        z.vt = (const int8_t *)at(p.vt);
+        z.mT = (const float *)at(p.mT);
+        z.gath_bytes = p.gl.bytes;
+        z.table_sr = l == 0 ? n : (int64_t)V * n;
+        z.table_sx = l == 0 ? 0 : n;
+        z.off_P = p.gl.off_P; z.off_U = p.gl.off_U; z.off_F = p.gl.off_F; z.off_FB = p.gl.off_FB;
+        z.off_FS = p.gl.off_FS;
+        z.readout_scale = y.scal[0]; z.unembed_scale = y.scal[1]; z.rms_eps = y.scal[2];
+        z.layer_input_scale = y.scal[3];
+    }
+    ygg_info &I = m->info;
+    memset(&I, 0, sizeof I);
+    I.n_layers = L; I.d_state = n; I.block_size = fa.blk; I.vocab = V; I.vocab_pad = VP; I.router_depth = fa.D;
+    I.n_experts = E; I.readout_rank = R; I.layer_input_rank = R2; I.input_rank = fa.K; I.shift = fa.shift;
+    I.factored = factored; I.group = group; I.device = device; I.file_array_bytes = fa.bytes;
+    I.device_bytes = (int64_t)total;
+    for (int l = 0; l < L; l++) I.gather_bytes[l] = lp[l].gl.bytes;
+    *out = m;
+    return YGG_OK;
+}
+
+struct DeviceGuard {
+    int prev = -1;
+    hipError_t set(int dev) {
+        hipError_t e = hipGetDevice(&prev);
+        if (e != hipSuccess) return e;
+        return prev == dev ? hipSuccess : hipSetDevice(dev);
+    }
+    ~DeviceGuard() {
+        int cur = -1;
+        if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+    }
+};
+
+}  // namespace
+
+extern "C" {
+
+int ygg_version(void) { return 1; }
+
+const char *ygg_last_error(void) { return g_err.c_str(); }
+
+int ygg_load_blob(const void *data, size_t bytes, int device, ygg_model **out) {
+    if (!out) return fail(YGG_ERR_ARG, "out is NULL");
+    *out = nullptr;
+    if (!data) return fail(YGG_ERR_ARG, "data is NULL");
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count <= 0) return fail(YGG_ERR_DEVICE, "no HIP device");
+    if (device < 0 || device >= count) return fail(YGG_ERR_ARG, "device %d out of range [0, %d)", device, count);
+    return load_impl((const uint8_t *)data, bytes, device, out);
+}
+
+int ygg_load(const char *path, int device, ygg_model **out) {
+    if (!out) return fail(YGG_ERR_ARG, "out is NULL");
+    *out = nullptr;
+    if (!path) return fail(YGG_ERR_ARG, "path is NULL");
+    FILE *f = fopen(path, "rb");
+    if (!f) return fail(YGG_ERR_IO, "%s: cannot open", path);
+    fseek(f, 0, SEEK_END);
+    const long sz = ftell(f);
+    fseek(f, 0, SEEK_SET);
+    if (sz < 0) { fclose(f); return fail(YGG_ERR_IO, "%s: cannot size", path); }
+    std::vector<uint8_t> buf;
+    try {
+        buf.resize((size_t)sz);
+    } catch (const std::bad_alloc &) {
+        fclose(f);
+        return fail(YGG_ERR_NOMEM, "out of host memory (%ld bytes)", sz);
+    }
+    size_t got = 0;
+    while (got < (size_t)sz) {
+        const size_t c = fread(buf.data() + got, 1, std::min<size_t>((size_t)sz - got, 64u << 20), f);
+        if (!c) break;
+        got += c;
+    }
+    fclose(f);
+    if (got != (size_t)sz) return fail(YGG_ERR_IO, "%s: short read", path);
+    return ygg_load_blob(buf.data(), buf.size(), device, out);
+}
+
+int ygg_model_info(const ygg_model *m, ygg_info *info) {
+    if (!m || !info) return fail(YGG_ERR_ARG, "NULL argument");
+    *info = m->info;
+    return YGG_OK;
+}
+
+void ygg_free(ygg_model *m) {
+    if (!m) return;
+    DeviceGuard g;
+    if (g.set(m->device) == hipSuccess) (void)hipFree(m->arena);
+    delete m;
+}
+
+int ygg_run(const ygg_model *m, const int32_t *d_tokens, int B, int T, int8_t *d_state, float *d_logits,
+            int32_t *d_leaves, int8_t *d_states, uint64_t *d_digest, void *stream) {
+    if (!m) return fail(YGG_ERR_ARG, "model is NULL");
+    if (B < 0 || T < 0) return fail(YGG_ERR_ARG, "negative B (%d) or T (%d)", B, T);
+    if (B == 0) return YGG_OK;
+    if (!d_state || (T > 0 && !d_tokens)) return fail(YGG_ERR_ARG, "tokens or state is NULL");
+    DeviceGuard g;
+    HIP_TRY(g.set(m->device));
+    HIP_TRY(m->launch(m->dev, d_tokens, B, T, d_state, d_logits, d_leaves, d_states,
+                      (unsigned long long *)d_digest, (hipStream_t)stream));
+    return YGG_OK;
+}
+
+int ygg_step(const ygg_model *m, const int32_t *d_tokens, const int8_t *d_state_in, int8_t *d_state_out,
+             float *d_logits, int32_t *d_leaves, int B, void *stream) {
+    if (!m) return fail(YGG_ERR_ARG, "model is NULL");
+    if (B < 0) return fail(YGG_ERR_ARG, "negative B (%d)", B);
+    if (B == 0) return YGG_OK;
+    if (!d_tokens || !d_state_in || !d_state_out || !d_logits) return fail(YGG_ERR_ARG, "NULL buffer");
+    DeviceGuard g;
+    HIP_TRY(g.set(m->device));
+    if (d_state_in != d_state_out)
+        HIP_TRY(hipMemcpyAsync(d_state_out, d_state_in, (size_t)B * m->dev.L * m->dev.N, hipMemcpyDeviceToDevice,
+                               (hipStream_t)stream));
+    HIP_TRY(m->launch(m->dev, d_tokens, B, 1, d_state_out, d_logits, d_leaves, nullptr, nullptr, (hipStream_t)stream));
+    return YGG_OK;
+}
+
+int ygg_take_errors(const ygg_model *m, void *stream, uint32_t *errors) {
+    if (!m || !errors) return fail(YGG_ERR_ARG, "NULL argument");
+    DeviceGuard g;
+    HIP_TRY(g.set(m->device));
+    HIP_TRY(hipStreamSynchronize((hipStream_t)stream));
+    uint32_t v = 0;
+    HIP_TRY(hipMemcpy(&v, m->dev.err, 4, hipMemcpyDeviceToHost));
+    if (v) {
+        const uint32_t zero = 0;
+        HIP_TRY(hipMemcpy(m->dev.err, &zero, 4, hipMemcpyHostToDevice));
+    }
+    *errors = v;
+    return YGG_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,371 @@
+// The fused int8 streaming step for gfx950: one 64-lane wavefront per stream, every layer of every token of a
+// T-token launch in one kernel, the int8 states of all layers resident in LDS for the whole launch.
+//
+// Per token and layer (cpu/ygg.cpp:441-459):
+//   routed layer   rho from the layer below (per-16-coordinate sums in 16 lanes, cpu/ygg.cpp:248-266); the router
+//                  descent in rounds of up to 4 levels: 15 quads take the 15 nodes of the 4-level subtree below the
+//                  current node, each quad forms one node's dot product (quad lanes split the coordinates, a DPP
+//                  quad sum joins them), one ballot of the 15 comparisons gives the whole 4-level path in scalar
+//                  registers (cpu/ygg.cpp:271-280); the layer input zl from V' in the same quad layout
+//                  (cpu/ygg.cpp:285-296)
+//   every layer    the expert's gather record (A16, U', P) and its table row are loaded as soon as the expert is
+//                  known; transition with v_dot2 (int16 x int16), table or factored input, layer input with v_dot4,
+//                  sat8 (cpu/ygg.cpp:311-389); readout P q with v_dot4 and a DPP sum over the lanes of each row,
+//                  zq, then the unembedding of 4 classes per lane into the f32 logits (cpu/ygg.cpp:395-435)
+//
+// f32 arithmetic is one rounded operation per step in the reference's order; the file is compiled with
+// -ffp-contract=off, sqrtf is the correctly rounded square root and '/' the correctly rounded division.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "ygg_layout.h"
+
+namespace ygg {
+
+typedef short s16x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+__device__ __forceinline__ int dot2(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot2(__builtin_bit_cast(s16x2, a), __builtin_bit_cast(s16x2, b), c, false);
+}
+// DPP sums over 2, 4 and 8 consecutive lanes (every lane of the group gets the sum)
+__device__ __forceinline__ int sum2(int v) { return v + __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false); }
+__device__ __forceinline__ int sum4(int v) {
+    v = sum2(v);
+    return v + __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);
+}
+__device__ __forceinline__ int sum8(int v) {
+    v = sum4(v);
+    return v + __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);  // row_half_mirror
+}
+template <int G> __device__ __forceinline__ int group_sum(int v) {
+    if constexpr (G == 1) return v;
+    else if constexpr (G == 2) return sum2(v);
+    else if constexpr (G == 4) return sum4(v);
+    else return sum8(v);
+}
+__device__ __forceinline__ unsigned long long wave_sum_u64(unsigned long long v) {
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+// _mm512_cvtps_epi32 in round-to-nearest-even: NaN and |x| >= 2^31 give INT32_MIN (cpu/ygg.cpp:292 and others)
+__device__ __forceinline__ int cvt_rne(float x) {
+    return (x >= -2147483648.0f && x < 2147483648.0f) ? (int)__builtin_rintf(x) : (int)0x80000000;
+}
+__device__ __forceinline__ int clamp127(int v) { return v > 127 ? 127 : (v < -127 ? -127 : v); }
+__device__ __forceinline__ int sat8(int v) { return v > 127 ? 127 : (v < -128 ? -128 : v); }
+__device__ __forceinline__ int wadd(int a, int b) { return (int)((uint32_t)a + (uint32_t)b); }
+__device__ __forceinline__ int sbyte(uint32_t w, int k) { return (int)(int8_t)(w >> (8 * k)); }
+// two int8 (bytes k, k+1 of w) as an int16 pair
+__device__ __forceinline__ uint32_t pair16(uint32_t w, int k) {
+    return ((uint32_t)sbyte(w, k) & 0xFFFFu) | ((uint32_t)sbyte(w, k + 1) << 16);
+}
+
+// NW dwords from p, which is aligned to ALIGN bytes
+template <int NW, int ALIGN>
+__device__ __forceinline__ void load_words(uint32_t (&d)[NW], const void *p) {
+    if constexpr (ALIGN % 16 == 0 && NW % 4 == 0) {
+#pragma unroll
+        for (int i = 0; i < NW / 4; i++) {
+            const uint4 v = ((const uint4 *)p)[i];
+            d[4 * i] = v.x; d[4 * i + 1] = v.y; d[4 * i + 2] = v.z; d[4 * i + 3] = v.w;
+        }
+    } else if constexpr (ALIGN % 8 == 0 && NW % 2 == 0) {
+#pragma unroll
+        for (int i = 0; i < NW / 2; i++) {
+            const uint2 v = ((const uint2 *)p)[i];
+            d[2 * i] = v.x; d[2 * i + 1] = v.y;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < NW; i++) d[i] = ((const uint32_t *)p)[i];
+    }
+}
+
+constexpr unsigned long long kDigestMul = 0x100000001B3ull;
+constexpr unsigned long long kDigestLeaf = 0xD6E8FEB86659FD93ull;
+constexpr unsigned long long kDigestCoord = 0x9E3779B97F4A7C15ull;
+
+template <int N, int BLK, int R>
+__global__ __launch_bounds__(64) void run_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int T,
+                                                 int8_t *__restrict__ state, float *__restrict__ logits,
+                                                 int32_t *__restrict__ leaves, int8_t *__restrict__ states,
+                                                 unsigned long long *__restrict__ digest) {
+    constexpr int C = Lanes<N>::C, NL = Lanes<N>::NL;
+    constexpr int Q4 = N / 4, QW = Q4 / 4;                       // quad-lane chunk of a row
+    constexpr int QA = (Q4 % 16 == 0) ? 16 : 8;                  // its alignment
+    constexpr int RL = ReadoutLanes<N, R>::RL, SP = ReadoutLanes<N, R>::SP, GP = ReadoutLanes<N, R>::GP;
+    constexpr int SPW = SP / 4;
+    constexpr int AW = C * BLK / 2;                              // A dwords per lane
+    constexpr int NA = AW / 4;                                   // 16-byte A chunks per lane
+    constexpr float kInvN = 1.0f / (float)N;
+
+    __shared__ __attribute__((aligned(16))) int8_t qs[YGG_MAX_LAYERS * N];
+    __shared__ __attribute__((aligned(16))) int8_t zls[YGG_MAX_RANK];
+    __shared__ __attribute__((aligned(16))) int8_t zqs[32];
+
+    const int lane = threadIdx.x;
+    const int s = blockIdx.x;
+    const int L = m.L, V = m.V, VP = m.VP, E = m.E, D = m.D, R2 = m.R2, K = m.K;
+    const int qk = lane & 3, qj = lane >> 2;                     // quad lane, quad
+    const int rj = lane / RL, rk = lane % RL;                    // readout row, readout lane
+
+    int8_t *st = state + (size_t)s * L * N;
+    for (int i = lane; i < L * N; i += 64) qs[i] = st[i];
+    for (int i = lane; i < YGG_MAX_RANK; i += 64) zls[i] = 0;
+    __syncthreads();
+    unsigned long long dg = digest ? digest[s] : 0ull;
+    const int32_t *tok = tokens + (size_t)s * T;
+    int x_next = T > 0 ? tok[0] : 0;
+
+    for (int t = 0; t < T; t++) {
+        const int x = x_next;
+        if (t + 1 < T) x_next = tok[t + 1];
+        if (x < 0 || x >= V) {
+            if (lane == 0) atomicOr(m.err, 1u);
+            break;
+        }
+        float lg[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) lg[u] = 4 * lane + u < VP ? m.output_bias[4 * lane + u] : 0.0f;
+
+        for (int l = 0; l < L; l++) {
+            const YggDevLayer &y = m.layers[l];
+            int r = x;
+            float rho = 0.0f;
+            uint32_t qbw[QW];
+            if (l > 0) {
+                const int8_t *qb = qs + (l - 1) * N;
+                load_words<QW, QA>(qbw, qb + qk * Q4);
+                // rho: lane g < n/16 holds the sum of squares of coordinates [16 g, 16 g + 16)
+                int sg = 0;
+                if (lane < N / 16) {
+                    uint32_t g4[4];
+                    load_words<4, 16>(g4, qb + 16 * lane);
+#pragma unroll
+                    for (int i = 0; i < 4; i++) sg = dot4(g4[i], g4[i], sg);
+                }
+                if (y.r2b) {
+                    float sum = 0.0f;
+#pragma unroll
+                    for (int g = 0; g < N / 16; g++) sum = sum + y.r2b[g] * (float)__builtin_amdgcn_readlane(sg, g);
+                    rho = 1.0f / sqrtf(sum * kInvN + y.rms_eps);
+                } else {
+                    int S = 0;
+#pragma unroll
+                    for (int g = 0; g < N / 16; g++) S += __builtin_amdgcn_readlane(sg, g);
+                    rho = 1.0f / sqrtf((float)S * kInvN + y.rms_eps);
+                }
+                // router descent, up to 4 levels per round
+                const float *thr = y.thr + (size_t)x * E;
+                int ix = 1;
+                for (int d0 = 0; d0 < D; d0 += 4) {
+                    const int h = D - d0 < 4 ? D - d0 : 4;
+                    const int nn = (1 << h) - 1;
+                    int dot = 0;
+                    float th = 0.0f;
+                    if (qj < nn) {
+                        const int dj = 31 - __builtin_clz(qj + 1);
+                        const int node = (ix << dj) + (qj + 1 - (1 << dj));
+                        uint32_t wv[QW];
+                        load_words<QW, QA>(wv, y.w + (size_t)node * N + qk * Q4);
+#pragma unroll
+                        for (int i = 0; i < QW; i++) dot = dot4(wv[i], qbw[i], dot);
+                        th = thr[node];
+                    }
+                    dot = sum4(dot);
+                    const bool right = (float)dot * rho > th;
+                    const unsigned long long mask = __ballot(right && qk == 0 && qj < nn);
+                    int loc = 0;
+                    for (int lev = 0; lev < h; lev++) loc = 2 * loc + 1 + (int)((mask >> (4 * loc)) & 1ull);
+                    ix = (ix << h) + (loc - nn);
+                }
+                r = ix - E;
+            }
+
+            // the expert's gather record and table row
+            const uint8_t *g = y.gath + (size_t)r * y.gath_bytes;
+            uint32_t aw[AW];
+            uint32_t pw[SPW];
+            int trow[C];
+            if (lane < NL) {
+#pragma unroll
+                for (int c = 0; c < NA; c++) {
+                    const uint4 v = *(const uint4 *)(g + (c * NL + lane) * 16);
+                    aw[4 * c] = v.x; aw[4 * c + 1] = v.y; aw[4 * c + 2] = v.z; aw[4 * c + 3] = v.w;
+                }
+                if (y.table) {
+                    const int16_t *tr = y.table + (size_t)r * y.table_sr + (size_t)x * y.table_sx + C * lane;
+#pragma unroll
+                    for (int c = 0; c < C; c++) trow[c] = tr[c];
+                }
+            }
+            {
+                const uint8_t *pp = g + y.off_P;
+#pragma unroll
+                for (int gi = 0; gi < SP / GP; gi++) {
+                    uint32_t tmp[GP / 4];
+                    load_words<GP / 4, GP>(tmp, pp + (gi * 64 + lane) * GP);
+#pragma unroll
+                    for (int i = 0; i < GP / 4; i++) pw[gi * (GP / 4) + i] = tmp[i];
+                }
+            }
+
+            // layer input zl from V' (cpu/ygg.cpp:285-296)
+            if (l > 0 && R2 > 0) {
+                const int RG = (R2 + 15) >> 4;
+                for (int gg = 0; gg < RG; gg++) {
+                    const int k = gg * 16 + qj;
+                    uint32_t vv[QW];
+                    load_words<QW, QA>(vv, y.vl + (size_t)k * N + qk * Q4);
+                    int a = 0;
+#pragma unroll
+                    for (int i = 0; i < QW; i++) a = dot4(vv[i], qbw[i], a);
+                    a = sum4(a);
+                    if (qk == 0) {
+                        float zf = (float)a * y.mv[k];
+                        zf = zf * rho;
+                        zls[k] = (int8_t)clamp127(cvt_rne(zf));
+                    }
+                }
+            }
+            __syncthreads();
+
+            // transition + input + layer input -> sat8 (cpu/ygg.cpp:311-389)
+            int qn[C];
+            if (lane < NL) {
+                const int blk0 = (C * lane / BLK) * BLK;
+                uint32_t qv[BLK / 4];
+                load_words<BLK / 4, BLK>(qv, qs + l * N + blk0);
+                uint32_t qp[BLK / 2];
+#pragma unroll
+                for (int i = 0; i < BLK / 4; i++) { qp[2 * i] = pair16(qv[i], 0); qp[2 * i + 1] = pair16(qv[i], 2); }
+                int acc[C];
+#pragma unroll
+                for (int c = 0; c < C; c++) {
+                    int a = 0;
+#pragma unroll
+                    for (int p = 0; p < BLK / 2; p++) a = dot2(aw[c * (BLK / 2) + p], qp[p], a);
+                    acc[c] = (a + (1 << (m.shift - 1))) >> m.shift;
+                }
+                if (y.table) {
+#pragma unroll
+                    for (int c = 0; c < C; c++) acc[c] = wadd(acc[c], trow[c]);
+                } else {
+                    // factored: rint(f32(U_r v[x]) * f32(su_r * mT_i)) + c_r (cpu/ygg.cpp:339-358)
+                    const uint8_t *fp = g + y.off_F;
+                    const uint32_t *vx = (const uint32_t *)(y.vt + (size_t)x * K);
+                    int d[C];
+#pragma unroll
+                    for (int c = 0; c < C; c++) d[c] = 0;
+                    for (int k4 = 0; k4 < K / 4; k4++) {
+                        const uint32_t vw = vx[k4];
+                        const uint32_t *up = (const uint32_t *)(fp + ((size_t)(k4 * NL + lane) * C) * 4);
+#pragma unroll
+                        for (int c = 0; c < C; c++) d[c] = dot4(up[c], vw, d[c]);
+                    }
+                    const float su = *(const float *)(g + y.off_FS);
+                    const int16_t *cb = (const int16_t *)(g + y.off_FB) + C * lane;
+#pragma unroll
+                    for (int c = 0; c < C; c++) {
+                        const float mul = su * y.mT[C * lane + c];
+                        acc[c] = wadd(acc[c], wadd(cvt_rne((float)d[c] * mul), cb[c]));
+                    }
+                }
+                if (l > 0 && R2 > 0) {
+                    // rint(f32(U'_r zl) * m_ul) (cpu/ygg.cpp:360-377)
+                    const uint8_t *up0 = g + y.off_U;
+                    int d[C];
+#pragma unroll
+                    for (int c = 0; c < C; c++) d[c] = 0;
+                    for (int k4 = 0; k4 < R2 / 4; k4++) {
+                        const uint32_t zw = ((const uint32_t *)zls)[k4];
+                        const uint32_t *up = (const uint32_t *)(up0 + ((size_t)(k4 * NL + lane) * C) * 4);
+#pragma unroll
+                        for (int c = 0; c < C; c++) d[c] = dot4(up[c], zw, d[c]);
+                    }
+#pragma unroll
+                    for (int c = 0; c < C; c++) {
+                        const float mu = y.mulv ? y.mulv[C * lane + c] : y.layer_input_scale;
+                        acc[c] = wadd(acc[c], cvt_rne((float)d[c] * mu));
+                    }
+                }
+#pragma unroll
+                for (int c = 0; c < C; c++) qn[c] = sat8(acc[c]);
+            }
+            __syncthreads();
+            if (lane < NL) {
+#pragma unroll
+                for (int c = 0; c < C; c++) qs[l * N + C * lane + c] = (int8_t)qn[c];
+            }
+            __syncthreads();
+
+            // readout zq = sat(rint(f32(P_r q) m_z)) and the unembedding (cpu/ygg.cpp:395-435)
+            {
+                uint32_t qv[SPW];
+                load_words<SPW, (SP % 16 == 0 ? 16 : (SP % 8 == 0 ? 8 : 4))>(qv, qs + l * N + rk * SP);
+                int z = 0;
+#pragma unroll
+                for (int i = 0; i < SPW; i++) z = dot4(pw[i], qv[i], z);
+                z = group_sum<RL>(z);
+                if (rk == 0) {
+                    const float mz = y.mz ? y.mz[(size_t)r * R + rj] : y.readout_scale;
+                    zqs[rj] = (int8_t)clamp127(cvt_rne((float)z * mz));
+                }
+            }
+            __syncthreads();
+            if (4 * lane < VP) {
+                uint32_t zw[R / 4];
+                load_words<R / 4, 16>(zw, zqs);
+                const int8_t *Qr = y.Q + (size_t)(4 * lane) * R;
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    uint32_t qq[R / 4];
+                    load_words<R / 4, 8>(qq, Qr + u * R);
+                    int d = 0;
+#pragma unroll
+                    for (int i = 0; i < R / 4; i++) d = dot4(qq[i], zw[i], d);
+                    const float sc = y.sqv ? y.sqv[4 * lane + u] : y.unembed_scale;
+                    lg[u] = lg[u] + (float)d * sc;
+                }
+            }
+            if (leaves && lane == 0) leaves[((size_t)s * T + t) * L + l] = r;
+            if (digest) {
+                unsigned long long f = 0;
+                if (lane < NL) {
+#pragma unroll
+                    for (int c = 0; c < C; c++)
+                        f += (unsigned long long)((uint8_t)qn[c] + 1u) *
+                             ((unsigned long long)(2 * (C * lane + c) + 1) * kDigestCoord);
+                }
+                f = wave_sum_u64(f);
+                dg = dg * kDigestMul + ((unsigned long long)(uint32_t)r * kDigestLeaf + f + (unsigned long long)l);
+            }
+            __syncthreads();
+        }
+
+        if (logits) {
+            float *o = logits + ((size_t)s * T + t) * V;
+            if ((V & 3) == 0 && 4 * lane + 3 < V) {
+                *(float4 *)(o + 4 * lane) = make_float4(lg[0], lg[1], lg[2], lg[3]);
+            } else {
+#pragma unroll
+                for (int u = 0; u < 4; u++)
+                    if (4 * lane + u < V) o[4 * lane + u] = lg[u];
+            }
+        }
+        if (states) {
+            int8_t *so = states + ((size_t)s * T + t) * L * N;
+            for (int i = lane; i < L * N; i += 64) so[i] = qs[i];
+        }
+    }
+    __syncthreads();
+    for (int i = lane; i < L * N; i += 64) st[i] = qs[i];
+    if (digest && lane == 0) digest[s] = dg;
+}
+
+}  // namespace ygg

@@ -1,0 +1,31 @@
+// Instantiations of the fused step kernel for every supported (d_state, block, readout rank), and the lookup the
+// C-ABI dispatches through.
+#include "ygg_kernel.h"
+
+namespace ygg {
+
+typedef hipError_t (*Launcher)(const YggDevModel &, const int32_t *, int, int, int8_t *, float *, int32_t *, int8_t *,
+                               unsigned long long *, hipStream_t);
+
+template <int N, int BLK, int R>
+hipError_t launch(const YggDevModel &m, const int32_t *tokens, int B, int T, int8_t *state, float *logits,
+                  int32_t *leaves, int8_t *states, unsigned long long *digest, hipStream_t stream) {
+    hipLaunchKernelGGL((run_kernel<N, BLK, R>), dim3(B), dim3(64), 0, stream, m, tokens, T, state, logits, leaves,
+                       states, digest);
+    return hipGetLastError();
+}
+
+#define YGG_R(N, BLK) \
+    if (R == 8) return launch<N, BLK, 8>; if (R == 16) return launch<N, BLK, 16>; if (R == 32) return launch<N, BLK, 32>;
+#define YGG_B(N) \
+    if (blk == 8) { YGG_R(N, 8) } if (blk == 16) { YGG_R(N, 16) }
+
+Launcher find_launcher(int n, int blk, int R) {
+    if (n == 64) { YGG_B(64) }
+    if (n == 96) { YGG_B(96) }
+    if (n == 128) { YGG_B(128) }
+    if (n == 256) { YGG_B(256) }
+    return nullptr;
+}
+
+}  // namespace ygg

@@ -1,0 +1,75 @@
+// Device layout of a loaded model: what the host relayout writes and the kernels read.
+//
+// The file layout (YGG1) is the interface; the device layout is this library's own. At load every expert's weights
+// that one stream reads at one step (transition A16, layer-input projection U', readout P, factored input U) are
+// rewritten into one contiguous "gather record", with every part signed (the file's u8 = w + 128 storage is undone,
+// so no 128 * sum corrections remain in the kernels) and interleaved by lane, so that each load instruction of a
+// wavefront reads one contiguous span. Shared arrays (router rows, layer-input down-projection, unembedding) become
+// plain signed row-major arrays.
+//
+// Lane mapping (one 64-lane wavefront per stream):
+//   state rows      lane l < NL owns the C consecutive coordinates [C l, C l + C), C = 1 (n <= 64), 2 (n <= 128),
+//                   4 (n <= 256), NL = n / C (n = 96: 48 lanes)
+//   router / V'     quad j = l / 4 takes one row (a tree node, a V' row), quad lane k = l % 4 the n/4 coordinates
+//                   [k n/4, (k + 1) n/4)
+//   readout P       RL = 64 / R lanes per readout row: row j = l / RL, coordinates [(l % RL) SP, (l % RL + 1) SP),
+//                   SP = n / RL bytes
+//   unembedding     lane l owns classes [4 l, 4 l + 4) of the padded class count VP
+//
+// Gather record of one expert (gath_bytes, a multiple of 128):
+//   A   at 0:      16-byte chunks, chunk c of lane l at (c NL + l) 16. A lane's bytes are its C rows in order, each
+//                  row the b int16 of that row inside its diagonal block (columns in block order).
+//   P   at off_P:  granules of GP bytes (16, 8 or 4: the largest dividing SP), granule g of lane l at
+//                  off_P + (g 64 + l) GP. A lane's bytes are P[j][i] (s8) for its row j and coordinates i in order.
+//   U'  at off_U:  for k4 < R2/4: lane l's C dwords at off_U + ((k4 NL + l) C + c) 4; dword c holds
+//                  U'[C l + c][4 k4 .. 4 k4 + 3] (s8).
+//   U   at off_F:  the same for the factored input projection with input_rank in place of R2.
+//   Cb  at off_FB: int16[n] factored bias.  S at off_FS: f32 factored input scale.
+#pragma once
+#include <stdint.h>
+
+#define YGG_MAX_LAYERS 8
+#define YGG_MAX_RANK 64
+
+struct YggDevLayer {
+    const uint8_t *gath;     // E gather records
+    const int16_t *table;    // token layer [V][n] (expert x = its own row); routed table storage [E][V][n]
+    const int8_t *w;         // routed: [E][n] router rows in heap order (row 0 unused)
+    const float *thr;        // routed: [V][E] thresholds (slot 0 unused)
+    const int8_t *vl;        // routed, R2 > 0: [16 RG][n] layer-input down-projection V' (rows >= R2 zero)
+    const float *mv;         // routed, R2 > 0: [16 RG]
+    const float *mulv;       // [n] per-coordinate layer-input scale, or null
+    const float *r2b;        // [n/16] squared group scales of the layer below, or null
+    const float *mz;         // [E][R] per expert and row readout scale, or null
+    const float *sqv;        // [VP] per class unembedding scale, or null
+    const int8_t *Q;         // [VP][R] unembedding, class-major
+    const int8_t *vt;        // factored: [V][k] token codes, or null
+    const float *mT;         // factored: [n] token scale
+    int64_t gath_bytes;
+    int64_t table_sr;        // table elements per expert (token layer: n; routed: V n)
+    int32_t table_sx;        // table elements per token (token layer: 0; routed: n)
+    int32_t off_P, off_U, off_F, off_FB, off_FS;  // byte offsets in the gather record, -1 absent
+    float readout_scale, unembed_scale, rms_eps, layer_input_scale;
+};
+
+struct YggDevModel {
+    int32_t L, N, BLK, V, VP, D, E, R, R2, K, shift;
+    const float *output_bias;   // [VP]
+    uint32_t *err;              // error word (bit 0: token out of range)
+    YggDevLayer layers[YGG_MAX_LAYERS];
+};
+
+// Compile-time lane constants of a d_state N, readout rank R.
+template <int N> struct Lanes {
+    static constexpr int C = N <= 64 ? 1 : (N <= 128 ? 2 : 4);
+    static constexpr int NL = N / C;
+};
+template <int N, int R> struct ReadoutLanes {
+    static constexpr int RL = 64 / R;
+    static constexpr int SP = N / RL;
+    static constexpr int GP = SP % 16 == 0 ? 16 : (SP % 8 == 0 ? 8 : 4);
+};
+
+// Runtime versions for the host relayout.
+static inline int lanes_c(int n) { return n <= 64 ? 1 : (n <= 128 ? 2 : 4); }
+static inline int readout_gp(int sp) { return sp % 16 == 0 ? 16 : (sp % 8 == 0 ? 8 : 4); }

@@ -1,0 +1,227 @@
+"""Yggdrasil int8 inference on the GPU: the reference's step/state API over the int8 model file.
+
+    model = Yggdrasil.load("model.bin")              # backend="hip": the fused gfx950 step (libygg_hip.so)
+    state = model.init_state(batch_size)            # (B, layers, n) int8 on the GPU, zero
+    logits, state = model.step(tokens, state)       # tokens (B,) -> logits (B, classes) f32, new state
+    bits = model.score(windows)                     # (B, L) -> bits of windows[:, 1:] per window (B,) f64
+    text = model.generate(prompt, 200, temperature=0.8, top_k=20)
+
+This mirrors ``Yggdrasil`` in yggdrasil/inference.py:142-202 and ``TritonYggdrasil`` in
+yggdrasil/inference_triton.py:123-248 (same method names, argument meaning, functional state and error behaviour),
+but loads the int8 ``model.bin`` of cpu/export.py instead of a float checkpoint, and its state is the int8 state of
+cpu/ygg.cpp (State.q, cpu/ygg.cpp:439). Steps run through the C-ABI of include/ygg_hip.h on the caller's current
+torch stream; torch only provides device memory and streams.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+from pathlib import Path
+from typing import Optional
+
+import numpy as np
+import torch
+
+from . import _lib
+from ._lib import YggError, YggInfo, check
+
+LN2 = math.log(2.0)
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+class Yggdrasil:
+    """An int8 model on one GPU (the ``hip`` backend)."""
+
+    def __init__(self, path, device=None, graph: bool = False):
+        if not torch.cuda.is_available():
+            raise RuntimeError("backend='hip' needs a ROCm GPU (torch.cuda.is_available() is False)")
+        L = _lib.lib()
+        self.device = torch.device("cuda", torch.cuda.current_device() if device is None else
+                                   torch.device(device).index or 0)
+        h = ctypes.c_void_p()
+        with torch.cuda.device(self.device):
+            check(L.ygg_load(str(path).encode(), self.device.index, ctypes.byref(h)))
+        self._h = h
+        info = YggInfo()
+        check(L.ygg_model_info(h, ctypes.byref(info)))
+        self.info = info
+        self.layers, self.n, self.vocab = info.n_layers, info.d_state, info.vocab
+        self.classes, self.depth = info.vocab, info.router_depth
+        self.graph = graph
+        self._graphs = {}
+
+    @classmethod
+    def load(cls, path, backend: str = "hip", **kw):
+        """From an int8 model file (YGG1, cpu/export.py). backend "hip": the fused gfx950 step; kw device, graph
+        (replay one captured step per batch size, as the Triton backend's cuda_graph)."""
+        if backend != "hip":
+            raise ValueError(f"backend {backend!r}: hip")
+        if not Path(path).exists():
+            raise FileNotFoundError(path)
+        try:
+            _lib.lib()
+        except ImportError as e:
+            raise ImportError(f"backend='hip' needs the built library ({e})") from e
+        return cls(path, **kw)
+
+    def close(self):
+        if getattr(self, "_h", None):
+            self._graphs.clear()
+            _lib.lib().ygg_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # ------------------------------------------------------------------------------------------------ state
+    def init_state(self, batch_size: int) -> torch.Tensor:
+        """Zero state of batch_size streams, (B, layers, n) int8 on the GPU."""
+        return torch.zeros(batch_size, self.layers, self.n, dtype=torch.int8, device=self.device)
+
+    def _tokens(self, tokens, shape=None) -> torch.Tensor:
+        x = torch.as_tensor(tokens, device=self.device)
+        if x.dtype != torch.int32:
+            x = x.to(torch.int32)
+        x = x.contiguous()
+        if shape is not None and tuple(x.shape) != tuple(shape):
+            raise ValueError(f"tokens of shape {tuple(x.shape)}, expected {tuple(shape)}")
+        if x.numel() and (int(x.min()) < 0 or int(x.max()) >= self.vocab):
+            raise ValueError(f"token out of range [0, {self.vocab})")
+        return x
+
+    def _check_state(self, state: torch.Tensor, B: int) -> torch.Tensor:
+        if state.dtype != torch.int8 or tuple(state.shape) != (B, self.layers, self.n):
+            raise ValueError(f"state must be int8 {(B, self.layers, self.n)}, got {state.dtype} {tuple(state.shape)}")
+        if state.device != self.device:
+            raise ValueError(f"state on {state.device}, model on {self.device}")
+        return state.contiguous()
+
+    # ------------------------------------------------------------------------------------------------ step
+    def _step(self, x: torch.Tensor, state: torch.Tensor):
+        B = x.shape[0]
+        logits = torch.empty(B, self.vocab, dtype=torch.float32, device=self.device)
+        out = torch.empty_like(state)
+        check(_lib.lib().ygg_step(self._h, _ptr(x), _ptr(state), _ptr(out), _ptr(logits), None, B, _stream()))
+        return logits, out
+
+    def step(self, tokens, state: torch.Tensor):
+        """One token per stream: tokens (B,) -> logits (B, classes) of the next token, new state (B, layers, n)."""
+        x = self._tokens(tokens)
+        if x.dim() != 1:
+            raise ValueError("tokens must be (B,)")
+        state = self._check_state(state, x.shape[0])
+        if not self.graph:
+            return self._step(x, state)
+        B = x.shape[0]
+        if B not in self._graphs:
+            sx = torch.zeros(B, dtype=torch.int32, device=self.device)
+            sh = self.init_state(B)
+            self._step(sx, sh)
+            torch.cuda.synchronize(self.device)
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                out = self._step(sx, sh)
+            self._graphs[B] = g, sx, sh, out
+        g, sx, sh, (logits, h) = self._graphs[B]
+        sx.copy_(x)
+        sh.copy_(state)
+        g.replay()
+        return logits.clone(), h.clone()
+
+    def run(self, tokens, state: Optional[torch.Tensor] = None, logits: bool = True, leaves: bool = False,
+            states: bool = False, digest=False) -> dict:
+        """T tokens per stream in one launch: tokens (B, T) from state (default zero; not modified) ->
+        dict(state=(B, layers, n) after the last token, logits=(B, T, classes), leaves=(B, T, layers) int32,
+        states=(B, T, layers, n) int8, digest=(B,) int64 bit pattern of the uint64 digest)."""
+        x = self._tokens(tokens)
+        if x.dim() != 2:
+            raise ValueError("tokens must be (B, T)")
+        B, T = x.shape
+        st = self.init_state(B) if state is None else self._check_state(state, B).clone()
+        dev = self.device
+        out = {"state": st}
+        lg = torch.empty(B, T, self.vocab, dtype=torch.float32, device=dev) if logits else None
+        lv = torch.empty(B, T, self.layers, dtype=torch.int32, device=dev) if leaves else None
+        sv = torch.empty(B, T, self.layers, self.n, dtype=torch.int8, device=dev) if states else None
+        if isinstance(digest, torch.Tensor):
+            dg = digest.to(device=dev, dtype=torch.int64).clone()
+        elif digest:
+            dg = torch.full((B,), np.int64(np.uint64(0xCBF29CE484222325).view(np.int64)), dtype=torch.int64,
+                            device=dev)
+        else:
+            dg = None
+        check(_lib.lib().ygg_run(self._h, _ptr(x), B, T, _ptr(st), _ptr(lg), _ptr(lv), _ptr(sv), _ptr(dg),
+                                 _stream()))
+        for k, v in (("logits", lg), ("leaves", lv), ("states", sv), ("digest", dg)):
+            if v is not None:
+                out[k] = v
+        return out
+
+    def take_errors(self) -> int:
+        """Wait for the current stream; the error bits kernels set since the last call (bit 0: bad token)."""
+        e = ctypes.c_uint32()
+        check(_lib.lib().ygg_take_errors(self._h, _stream(), ctypes.byref(e)))
+        return e.value
+
+    # ------------------------------------------------------------------------------------------------ consumers
+    @torch.no_grad()
+    def score(self, tokens, state: Optional[torch.Tensor] = None, batch: int = 1024, chunk: int = 256) -> np.ndarray:
+        """Bits of tokens[:, 1:] given the tokens before them, per row of tokens (B, L), as float64 (B,).
+        Rows start from state, or from zero (yggdrasil/inference.py:179-188); the log-softmax is taken in float64
+        as the reference's score mode (cpu/ygg.cpp:513-516)."""
+        tokens = np.atleast_2d(np.asarray(tokens, np.int64))
+        out = []
+        for i in range(0, len(tokens), batch):
+            x = self._tokens(tokens[i:i + batch])
+            B, Lw = x.shape
+            st = self.init_state(B) if state is None else self._check_state(state[i:i + B], B)
+            nll = torch.zeros(B, dtype=torch.float64, device=self.device)
+            for t0 in range(0, Lw - 1, chunk):
+                t1 = min(Lw - 1, t0 + chunk)
+                r = self.run(x[:, t0:t1], st)
+                st = r["state"]
+                lp = torch.log_softmax(r["logits"].double(), -1)
+                nll -= lp.gather(2, x[:, t0 + 1:t1 + 1, None].long())[..., 0].sum(1)
+            out.append((nll / LN2).cpu().numpy())
+        return np.concatenate(out) if out else np.zeros(0)
+
+    @torch.no_grad()
+    def generate(self, prompt, n: int, temperature: float = 1.0, top_k: int = 0, seed: int = 0):
+        """Prompt (L,) or (B, L), L >= 1, followed by n sampled tokens. temperature 0: greedy
+        (yggdrasil/inference.py:190-202, yggdrasil/inference_triton.py:229-248)."""
+        prompt = np.asarray(prompt, np.int64)
+        x = self._tokens(np.atleast_2d(prompt))
+        r = self.run(x)
+        state, logits = r["state"], r["logits"][:, -1]
+        gen = torch.Generator(self.device).manual_seed(seed)
+        out = [x.long()]
+        for i in range(n):
+            if temperature == 0:
+                tok = logits.argmax(-1)
+            else:
+                lg = logits
+                if top_k:
+                    lg = lg.masked_fill(lg < lg.topk(top_k, -1).values[:, -1:], -float("inf"))
+                tok = torch.multinomial(torch.softmax(lg / temperature, -1), 1, generator=gen)[:, 0]
+            out.append(tok[:, None])
+            if i + 1 < n:
+                logits, state = self.step(tok, state)
+        res = torch.cat(out, 1).cpu().numpy()
+        return res[0] if prompt.ndim == 1 else res
+
+
+def load(path, backend: str = "hip", **kw) -> Yggdrasil:
+    return Yggdrasil.load(path, backend=backend, **kw)
+
+
+__all__ = ["Yggdrasil", "YggError", "load"]
