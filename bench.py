@@ -231,7 +231,8 @@ def main():
                      "compulsory_bytes_per_token": round(alg["per_token_compulsory"], 1),
                      "per_stream_bytes_per_token": round(alg["per_token_per_stream"], 1),
                      "per_stream_GBps": round(alg["per_stream"] / (ms / 1e3) / 1e9, 1),
-                     "kernel": "ygg::run_kernel<128, 16, 8>"},
+                     "kernel": (f"ygg::fast_kernel<{info.d_state}, {info.n_layers}>" if info.kernel == 1 else
+                                f"ygg::run_kernel<{info.d_state}, {info.block_size}, {info.readout_rank}>")},
         "cpu_baseline": cpu,
         "batch1": batch1,
     }

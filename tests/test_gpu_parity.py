@@ -39,6 +39,17 @@ def _compare(got, ref, keys=("leaves", "states", "logits")):
                                  f"gpu {a[tuple(bad[0])]} oracle {b[tuple(bad[0])]}")
 
 
+@pytest.fixture(params=["default", "generic"])
+def kernel_env(request, monkeypatch):
+    """Load models with the kernel the library picks ("default": the specialised one where the shape allows) or with
+    the general kernel forced (YGG_KERNEL=generic)."""
+    if request.param == "generic":
+        monkeypatch.setenv("YGG_KERNEL", "generic")
+    else:
+        monkeypatch.delenv("YGG_KERNEL", raising=False)
+    return request.param
+
+
 def _gpu_run(model, x, state=None, states=True):
     import torch
     r = model.run(x, state=state, leaves=True, states=states)
@@ -69,35 +80,65 @@ def c12(model_dir):
     return path
 
 
-def test_config1_full_stream(hip, c12):
+def _expect_kernel(model, kernel_env):
+    assert model.info.kernel == (0 if kernel_env == "generic" else 1), model.info.kernel
+
+
+def test_config1_full_stream(hip, c12, kernel_env):
     """Config 1: one stream of 4096 uniform bytes (the reference's CPU plumbing case), every token checked."""
     w = synth.CONFIGS[1]
     x = w.make_tokens()
-    _say(f"config 1: {x.shape}")
+    _say(f"config 1: {x.shape} kernel {kernel_env}")
     ref = Oracle(c12).run(x, states=True)
     model = hip.load(c12)
+    _expect_kernel(model, kernel_env)
     _compare(_gpu_run(model, x), ref)
 
 
-def test_config2_subset(hip, c12):
-    """Config 2 at 64 streams x 512 Zipf(1.1) tokens."""
+def test_config2_subset(hip, c12, kernel_env):
+    """Config 2 at 64 streams x 512 Zipf(1.1) tokens; 66 streams for a partly filled last workgroup."""
     w = synth.CONFIGS[2]
-    x = w.make_tokens(64, 512)
-    _say(f"config 2: {x.shape}")
-    ref = Oracle(c12).run(x, states=True)
-    model = hip.load(c12)
-    _compare(_gpu_run(model, x), ref)
+    for B, T in ((64, 512), (66, 40)):
+        x = w.make_tokens(B, T)
+        _say(f"config 2: {x.shape} kernel {kernel_env}")
+        ref = Oracle(c12).run(x, states=True)
+        model = hip.load(c12)
+        _expect_kernel(model, kernel_env)
+        _compare(_gpu_run(model, x), ref)
 
 
-def test_config3_subset(hip, model_dir):
-    """Config 3 (V = 5, d = 96, D = 13, 3 layers) at 32 streams x 256 tokens."""
+@pytest.fixture(scope="module")
+def c3(model_dir):
     w = synth.CONFIGS[3]
     path = model_dir / "c3.bin"
     synth.write_model(w.spec, w.model_seed, path)
+    return path
+
+
+def test_config3_subset(hip, c3, kernel_env):
+    """Config 3 (V = 5, d = 96, D = 13, 3 layers) at 32 streams x 256 tokens."""
+    w = synth.CONFIGS[3]
     x = w.make_tokens(32, 256)
-    _say(f"config 3: {x.shape}")
+    _say(f"config 3: {x.shape} kernel {kernel_env}")
+    ref = Oracle(c3).run(x, states=True)
+    model = hip.load(c3)
+    _expect_kernel(model, kernel_env)
+    _compare(_gpu_run(model, x), ref)
+
+
+@pytest.mark.parametrize("router", ["gauss", "skew"])
+def test_config4_shape_reduced(hip, model_dir, kernel_env, router):
+    """The config-4/5 layer shapes (V = 256, 4 layers, d = 128, b = 16, R = 8, R2 = 16) with a depth-10 router so the
+    model stays small: 64 streams x 96 Zipf tokens."""
+    spec = synth.ModelSpec(128, 16, 10, 256, 4, router=router)
+    path = model_dir / f"c4small_{router}.bin"
+    if not path.exists():
+        synth.write_model(spec, 11, path)
+    x = synth.zipf_bytes(64, 96, 5)
+    _say(f"config-4 shape (D=10, {router}): {x.shape} kernel {kernel_env}")
     ref = Oracle(path).run(x, states=True)
     model = hip.load(path)
+    _expect_kernel(model, kernel_env)
     _compare(_gpu_run(model, x), ref)
 
 
@@ -144,7 +185,7 @@ def test_step_in_place_and_edges(hip, c12):
     assert L.ygg_run(model._h, p(xt), -1, 1, p(st), None, None, None, None, s) == 5
 
 
-def test_bad_token_stops_stream(hip, c12):
+def test_bad_token_stops_stream(hip, c12, kernel_env):
     """A token outside [0, V) stops its stream at that token and sets the error word; other streams go on."""
     import torch
     from yggdrasil_amd import _lib
@@ -168,10 +209,11 @@ def test_bad_token_stops_stream(hip, c12):
         model.run(bad)
 
 
-def test_digest_matches_oracle(hip, c12):
+def test_digest_matches_oracle(hip, c12, kernel_env):
     import torch
     x = synth.CONFIGS[2].make_tokens(32, 64)
     model = hip.load(c12)
+    _expect_kernel(model, kernel_env)
     r = model.run(x, logits=False, digest=True)
     torch.cuda.synchronize()
     ref = Oracle(c12).run(x, logits=False, leaves=False, digest=True)

@@ -20,6 +20,7 @@ namespace ygg {
 typedef hipError_t (*Launcher)(const YggDevModel &, const int32_t *, int, int, int8_t *, float *, int32_t *, int8_t *,
                                unsigned long long *, hipStream_t);
 Launcher find_launcher(int n, int blk, int R);
+Launcher find_fast_launcher(int n, int L);
 }  // namespace ygg
 
 namespace {
@@ -284,6 +285,13 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     for (int l = 1; l < L; l++)
         if ((fl[l].vt != nullptr) != (fl[1].vt != nullptr))
             return fail(YGG_ERR_FORMAT, "model file: mixed table and factored routed layers");
+    // the specialised kernel covers the common shape; YGG_KERNEL=generic forces the general one
+    const char *kenv = getenv("YGG_KERNEL");
+    const bool want_fast = !(kenv && !strcmp(kenv, "generic"));
+    ygg::Launcher fast = nullptr;
+    if (want_fast && R == 8 && fa.blk == 16 && R2 <= 16 && !factored && !group && L <= 4 && VP <= 256)
+        fast = ygg::find_fast_launcher(n, L);
+    if (fast) launch = fast;
 
     // device arena plan: every array 256-byte aligned
     struct Piece { size_t off, bytes; };
@@ -437,7 +445,8 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     memset(&I, 0, sizeof I);
     I.n_layers = L; I.d_state = n; I.block_size = fa.blk; I.vocab = V; I.vocab_pad = VP; I.router_depth = fa.D;
     I.n_experts = E; I.readout_rank = R; I.layer_input_rank = R2; I.input_rank = fa.K; I.shift = fa.shift;
-    I.factored = factored; I.group = group; I.device = device; I.file_array_bytes = fa.bytes;
+    I.factored = factored; I.group = group; I.device = device; I.kernel = fast ? 1 : 0;
+    I.file_array_bytes = fa.bytes;
     I.device_bytes = (int64_t)total;
     for (int l = 0; l < L; l++) I.gather_bytes[l] = lp[l].gl.bytes;
     *out = m;
@@ -461,7 +470,7 @@ struct DeviceGuard {
 
 extern "C" {
 
-int ygg_version(void) { return 1; }
+int ygg_version(void) { return 2; }
 
 const char *ygg_last_error(void) { return g_err.c_str(); }
 

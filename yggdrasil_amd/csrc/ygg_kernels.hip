@@ -1,6 +1,7 @@
 // Instantiations of the fused step kernel for every supported (d_state, block, readout rank), and the lookup the
 // C-ABI dispatches through.
 #include "ygg_kernel.h"
+#include "ygg_kernel_fast.h"
 
 namespace ygg {
 
@@ -19,6 +20,26 @@ hipError_t launch(const YggDevModel &m, const int32_t *tokens, int B, int T, int
     if (R == 8) return launch<N, BLK, 8>; if (R == 16) return launch<N, BLK, 16>; if (R == 32) return launch<N, BLK, 32>;
 #define YGG_B(N) \
     if (blk == 8) { YGG_R(N, 8) } if (blk == 16) { YGG_R(N, 16) }
+
+template <int N, int L>
+hipError_t launch_fast(const YggDevModel &m, const int32_t *tokens, int B, int T, int8_t *state, float *logits,
+                       int32_t *leaves, int8_t *states, unsigned long long *digest, hipStream_t stream) {
+    hipLaunchKernelGGL((fast_kernel<N, L>), dim3((B + kFastWaves - 1) / kFastWaves), dim3(64 * kFastWaves), 0, stream,
+                       m, tokens, B, T, state, logits, leaves, states, digest);
+    return hipGetLastError();
+}
+
+#define YGG_L(N) \
+    if (L == 1) return launch_fast<N, 1>; if (L == 2) return launch_fast<N, 2>; \
+    if (L == 3) return launch_fast<N, 3>; if (L == 4) return launch_fast<N, 4>;
+
+// the specialised kernel: readout rank 8, block 16, layer-input rank <= 16, table storage, tensor scales, L <= 4
+Launcher find_fast_launcher(int n, int L) {
+    if (n == 64) { YGG_L(64) }
+    if (n == 96) { YGG_L(96) }
+    if (n == 128) { YGG_L(128) }
+    return nullptr;
+}
 
 Launcher find_launcher(int n, int blk, int R) {
     if (n == 64) { YGG_B(64) }
