@@ -1,0 +1,264 @@
+"""The CPU oracle (oracle/ygg_oracle.c) pinned to the reference int8 kernel.
+
+1. Golden fixtures (tests/golden/golden.json, written by tests/golden/make_golden.py from the reference itself):
+   the oracle reproduces the reference kernel's logits, leaves, states and digests on the 17 kernel-test shapes
+   (cpu/tests/test_kernel.py:22-33) and on configurations 1, 2, 4, 5; on configuration 3 (d = 96, which
+   cpu/ygg.cpp cannot load) it reproduces the logits of the reference's NumPy model export.int_forward.
+2. Live reference: where oracle/_ref/ holds the reference kernel built from cpu/ygg.cpp, fresh tokens on every
+   kernel-test shape, compared in full.
+3. Closed forms on hand-built models (d = 64 and 96), each chosen so that a plausible slip fails it: identity
+   transitions accumulate the table rows with int8 saturation; one off-diagonal transition entry moves one
+   coordinate to another (a transposed A fails); forced thresholds route token x to leaf x mod E (a transposed
+   thr[x][node] index or heap order fails); readout of unit rows through unit unembedding exposes rint half-even
+   and the +-127 clamp; a zero state below routes by the strict comparison 0 > thr.
+4. Errors: bad magic, truncated file, over-limit header, missing array, out-of-range token.
+"""
+import hashlib
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from yggdrasil_amd import fmt, synth
+from yggdrasil_amd.fmt import QuantLayer, f32
+
+GOLDEN = json.loads((Path(__file__).parent / "golden" / "golden.json").read_text())
+CASES = {c["name"]: c for c in GOLDEN["cases"]}
+BIG = f32(1e30)
+
+
+def sha(a):
+    return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+
+
+def file_sha(p):
+    h = hashlib.sha256()
+    with open(p, "rb") as f:
+        for chunk in iter(lambda: f.read(1 << 24), b""):
+            h.update(chunk)
+    return h.hexdigest()
+
+
+def golden_inputs(name):
+    """(spec, seed, tokens) of a golden case, rebuilt exactly as make_golden.py does."""
+    from tests.golden.make_golden import cases
+    for n, spec, seed, _, x in cases():
+        if n == name:
+            return spec, seed, x
+    raise KeyError(name)
+
+
+def check_golden(path, name, x):
+    c = CASES[name]
+    assert file_sha(path) == c["model_sha256"], f"{name}: the generator no longer writes the golden model"
+    assert sha(x.astype(np.int32)) == c["tokens_sha256"]
+    r = O.Oracle(path).run(x, states=True, digest=True)
+    assert sha(r["logits"]) == c["logits_sha256"], f"{name}: logits differ from the reference"
+    np.testing.assert_array_equal(r["logits"][0, :2, :len(c["logits_sample"][0])], np.float32(c["logits_sample"]))
+    if "leaves_sha256" in c:
+        assert sha(r["leaves"]) == c["leaves_sha256"], f"{name}: leaves differ from the reference"
+        assert sha(r["states"]) == c["states_sha256"], f"{name}: states differ from the reference"
+        assert [f"{d:016x}" for d in r["digest"]] == c["digest"]
+        np.testing.assert_array_equal(r["leaves"][0, :4], c["leaves_sample"])
+
+
+SMALL = [n for n in CASES if not n.startswith(("config4", "config5"))]
+
+
+@pytest.mark.parametrize("name", SMALL)
+def test_golden(tmp_path, name):
+    spec, seed, x = golden_inputs(name)
+    path = tmp_path / "m.bin"
+    synth.write_model(spec, seed, path)
+    check_golden(path, name, x)
+
+
+@pytest.mark.parametrize("name", ["config4", "config5"])
+def test_golden_large(tmp_path, name):
+    """The 3.6 GB configuration-4 model and its routing-skew variant (8 streams x 128 tokens)."""
+    spec, seed, x = golden_inputs(name)
+    path = tmp_path / "m.bin"
+    synth.write_model(spec, seed, path)
+    check_golden(path, name, x)
+    if name == "config5":
+        # the skew construction: most tokens land in 2^(D - hot_levels) = 16 leaves per routed layer
+        r = O.Oracle(path).run(synth.CONFIGS[5].make_tokens(64, 64), logits=False)
+        lv = r["leaves"][:, :, 1:]
+        for l in range(lv.shape[2]):
+            counts = np.bincount(lv[:, :, l].ravel(), minlength=2 ** spec.router_depth)
+            top16 = np.sort(counts)[-16:].sum() / counts.sum()
+            assert 0.85 < top16 < 0.95, top16
+    path.unlink()
+
+
+def test_digest_numpy_equals_c(tmp_path):
+    spec = synth.KERNEL_CASES[2]
+    path = tmp_path / "m.bin"
+    synth.write_model(spec, 3, path)
+    x = synth.uniform_tokens(spec.vocab, 5, 40, 9)
+    r = O.Oracle(path).run(x, states=True, digest=True)
+    np.testing.assert_array_equal(O.digest_of(r["leaves"], r["states"]), r["digest"])
+    # continuing a digest across launches equals one launch
+    a = O.Oracle(path).run(x[:, :17], digest=True)
+    b = O.Oracle(path).run(x[:, 17:], state=a["state"], digest=a["digest"])
+    np.testing.assert_array_equal(b["digest"], r["digest"])
+
+
+@pytest.mark.skipif(not O.have_ref(), reason="reference kernel not built in oracle/_ref")
+@pytest.mark.parametrize("ci", range(len(synth.KERNEL_CASES)))
+def test_live_reference(tmp_path, ci):
+    spec = synth.KERNEL_CASES[ci]
+    path = tmp_path / "m.bin"
+    synth.write_model(spec, 100 + ci, path)
+    x = synth.uniform_tokens(spec.vocab, 6, 48, ci)
+    ref = O.ref_dump(path, x)
+    r = O.Oracle(path).run(x, states=True)
+    for k in ("logits", "leaves", "states"):
+        np.testing.assert_array_equal(r[k], ref[k], err_msg=k)
+
+
+# ----------------------------------------------------------------------------------------------- closed forms
+
+def base_model(n=64, b=16, D=2, V=8, L=2, R=8):
+    """Identity transitions (A16 = 2^14 I), zero tables, zero readout and unembedding, unit scales, routers that
+    always go left, no layer input."""
+    layers = []
+    for l in range(L):
+        E = V if l == 0 else 2 ** D
+        A = np.zeros((E, n // b, b, b), np.int16)
+        A[:] = (2 ** 14 * np.eye(b)).astype(np.int16)
+        q = QuantLayer(token_layer=l == 0, n=n, block=b, depth=0 if l == 0 else D, transition=A,
+                       readout=np.zeros((E, R, n), np.int8), readout_scale=f32(1),
+                       unembed=np.zeros((V, R), np.int8), unembed_scale=f32(1),
+                       table=np.zeros((E, 1 if l == 0 else V, n), np.int16))
+        if l:
+            q.router_weight = np.zeros((E - 1, n), np.int16)
+            q.router_threshold = np.full((V, E - 1), BIG, np.float32)
+            q.rms_eps = f32(1)
+        layers.append(q)
+    return layers
+
+
+def write(tmp_path, layers, V, bias=None):
+    path = tmp_path / "m.bin"
+    fmt.write(layers, np.zeros(V) if bias is None else bias, path)
+    return path
+
+
+@pytest.mark.parametrize("n", [64, 96])
+def test_identity_accumulates_with_saturation(tmp_path, n):
+    V = 8
+    layers = base_model(n=n, V=V)
+    rng = np.random.default_rng(1)
+    T0 = rng.integers(-60, 61, (V, 1, n)).astype(np.int16)
+    layers[0].table = T0
+    path = write(tmp_path, layers, V)
+    x = rng.integers(0, V, (3, 12)).astype(np.int32)
+    r = O.Oracle(path).run(x, states=True)
+    for s in range(3):
+        q = np.zeros(n, np.int64)
+        for t in range(12):
+            q = np.clip(q + T0[x[s, t], 0], -128, 127)
+            np.testing.assert_array_equal(r["states"][s, t, 0], q)
+            np.testing.assert_array_equal(r["states"][s, t, 1], 0)
+
+
+@pytest.mark.parametrize("n", [64, 96])
+def test_one_transition_entry_moves_one_coordinate(tmp_path, n):
+    V = 4
+    layers = base_model(n=n, V=V, L=1)
+    A = np.zeros_like(layers[0].transition)
+    A[:, 1, 3, 9] = 2 ** 14          # block 1: new row 16 + 3 takes old column 16 + 9
+    layers[0].transition = A
+    T0 = np.zeros((V, 1, n), np.int16)
+    T0[:, 0, 16 + 9] = 50
+    layers[0].table = T0
+    path = write(tmp_path, layers, V)
+    r = O.Oracle(path).run(np.zeros((1, 2), np.int32), states=True)
+    q1, q2 = r["states"][0, 0, 0], r["states"][0, 1, 0]
+    assert q1[16 + 9] == 50 and np.count_nonzero(q1) == 1
+    assert q2[16 + 3] == 50 and q2[16 + 9] == 50 and np.count_nonzero(q2) == 2
+
+
+@pytest.mark.parametrize("n", [64, 96])
+def test_forced_routes(tmp_path, n):
+    V, D = 8, 3
+    E = 2 ** D
+    layers = base_model(n=n, V=V, D=D)
+    thr = np.zeros((V, E - 1), np.float32)
+    for x in range(V):
+        leaf = (5 * x + 3) % E
+        node = 1
+        for d in range(D):
+            bit = (leaf >> (D - 1 - d)) & 1
+            thr[x, node - 1] = -BIG if bit else BIG   # right iff value > thr
+            node = 2 * node + bit
+    layers[1].router_threshold = thr
+    path = write(tmp_path, layers, V)
+    x = np.random.default_rng(2).integers(0, V, (4, 10)).astype(np.int32)
+    r = O.Oracle(path).run(x)
+    np.testing.assert_array_equal(r["leaves"][:, :, 0], x)
+    np.testing.assert_array_equal(r["leaves"][:, :, 1], (5 * x + 3) % E)
+
+
+@pytest.mark.parametrize("n", [64, 96])
+def test_readout_rint_half_even_and_clamp(tmp_path, n):
+    V, R = 8, 8
+    layers = base_model(n=n, V=V, L=1, R=R)
+    P = np.zeros((V, R, n), np.int8)
+    for j in range(R):
+        P[:, j, j] = 1
+    layers[0].readout = P
+    layers[0].readout_scale = f32(0.5)
+    layers[0].unembed = np.eye(V, R, dtype=np.int8)
+    vals = np.array([1, 3, 5, -1, -3, -5, 127, -128], np.int16)    # zq = rint(v / 2), clamped to +-127
+    T0 = np.zeros((V, 1, n), np.int16)
+    T0[:, 0, :R] = vals
+    layers[0].table = T0
+    path = write(tmp_path, layers, V)
+    r = O.Oracle(path).run(np.zeros((1, 1), np.int32))
+    np.testing.assert_array_equal(r["logits"][0, 0], np.float32([0, 2, 2, -0.0, -2, -2, 64, -64]))
+    # twice the same row: the state saturates at 127 / -128 and zq clamps at +-127 with scale 1
+    layers[0].readout_scale = f32(1)
+    path = write(tmp_path, layers, V)
+    r = O.Oracle(path).run(np.zeros((1, 2), np.int32))
+    np.testing.assert_array_equal(r["logits"][0, 1], np.float32([2, 6, 10, -2, -6, -10, 127, -127]))
+
+
+def test_zero_state_routes_by_strict_comparison(tmp_path):
+    V, D = 4, 1
+    layers = base_model(V=V, D=D)
+    layers[1].router_threshold = np.float32([[-1e-30], [1e-30], [0.0], [-0.0]])
+    path = write(tmp_path, layers, V)
+    r = O.Oracle(path).run(np.array([[0, 1, 2, 3]], np.int32))
+    np.testing.assert_array_equal(r["leaves"][0, :, 1], [1, 0, 0, 0])
+
+
+# ----------------------------------------------------------------------------------------------- errors
+
+def test_errors(tmp_path):
+    spec = synth.KERNEL_CASES[3]
+    good = tmp_path / "good.bin"
+    synth.write_model(spec, 1, good)
+    data = good.read_bytes()
+    cases = {
+        "magic": b"XGG1" + data[4:],
+        "truncated": data[:len(data) // 2],
+        "limits": data[:8] + np.int32(72).tobytes() + data[12:],     # d_state 72
+    }
+    for name, blob in cases.items():
+        p = tmp_path / f"{name}.bin"
+        p.write_bytes(blob)
+        with pytest.raises(O.OracleError) as e:
+            O.Oracle(p)
+        assert e.value.code in (2, 3), (name, e.value)
+    # missing array: rename l1_w
+    i = data.find(b"l1_w\0")
+    p = tmp_path / "missing.bin"
+    p.write_bytes(data[:i] + b"l1_X" + data[i + 4:])
+    with pytest.raises(O.OracleError, match="missing l1_w"):
+        O.Oracle(p)
+    with pytest.raises(O.OracleError, match="out of range"):
+        O.Oracle(good).run(np.array([[0, spec.vocab]], np.int32))

@@ -388,7 +388,10 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
         }
     }
 
-    // upload
+    // upload: the device is checked only now, so a malformed file is reported as such on any host
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count <= 0) return fail(YGG_ERR_DEVICE, "no HIP device");
+    if (device < 0 || device >= count) return fail(YGG_ERR_ARG, "device %d out of range [0, %d)", device, count);
     int prev = 0;
     HIP_TRY(hipGetDevice(&prev));
     HIP_TRY(hipSetDevice(device));
@@ -478,9 +481,7 @@ int ygg_load_blob(const void *data, size_t bytes, int device, ygg_model **out) {
     if (!out) return fail(YGG_ERR_ARG, "out is NULL");
     *out = nullptr;
     if (!data) return fail(YGG_ERR_ARG, "data is NULL");
-    int count = 0;
-    if (hipGetDeviceCount(&count) != hipSuccess || count <= 0) return fail(YGG_ERR_DEVICE, "no HIP device");
-    if (device < 0 || device >= count) return fail(YGG_ERR_ARG, "device %d out of range [0, %d)", device, count);
+    if (device < 0) return fail(YGG_ERR_ARG, "device %d out of range", device);
     return load_impl((const uint8_t *)data, bytes, device, out);
 }
 

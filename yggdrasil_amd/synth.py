@@ -29,6 +29,7 @@ from .fmt import SHIFT, STATE_GROUP, Factored, QuantLayer, f32, layer_arrays, he
 
 BIG = f32(1e30)   # a threshold no routing value crosses: forces the branch at that node
 CHUNK = 1024      # experts per random stream
+_small_limit = 1 << 24   # write_model builds a layer in memory when E n (V) is at most this, else streams it
 
 
 @dataclasses.dataclass(frozen=True)
@@ -161,7 +162,7 @@ def write_model(spec: ModelSpec, seed: int, path, bias: Optional[np.ndarray] = N
     layers = []
     for l in range(spec.n_layers):
         E = V if l == 0 else E_routed
-        small = E * spec.d_state * (V if l else 1) <= (1 << 24)
+        small = E * spec.d_state * (V if l else 1) <= _small_limit
         layers.append(_layer(spec, seed, l, orth, _experts(spec, seed, l, 0, E, orth) if small else None))
     # the header needs the shapes only: describe the streamed layers by one chunk
     probe = []
