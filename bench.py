@@ -193,11 +193,16 @@ def main():
     log(f"{a.steps} steps: {ms:.3f} ms/step, {tokens_per_s / 1e6:.2f} M tokens/s, compulsory {achieved:.0f} GB/s "
         f"({achieved / PEAK_HBM_GBS:.3f} of 8 TB/s), per-stream {alg['per_stream'] / (ms / 1e3) / 1e9:.0f} GB/s")
 
+    kernel = (f"ygg::fast_kernel<{info.d_state}, {info.n_layers}>" if info.kernel == 1 else
+              f"ygg::run_kernel<{info.d_state}, {info.block_size}, {info.readout_rank}>")
+    # HBM bytes per launch measured by rocprofv3 (FETCH_SIZE, WRITE_SIZE, copy-calibrated) for this workload and kernel
     traffic = None
     tf = ROOT / "profiles" / f"traffic_{w.name}.json"
     if tf.exists() and B == w.streams and T == w.steps:
         try:
-            traffic = json.loads(tf.read_text()).get("hbm_bytes_per_launch")
+            doc = json.loads(tf.read_text())
+            if doc.get("kernel") == kernel:
+                traffic = doc.get("hbm_bytes_per_launch")
         except (OSError, ValueError):
             traffic = None
 
@@ -231,8 +236,7 @@ def main():
                      "compulsory_bytes_per_token": round(alg["per_token_compulsory"], 1),
                      "per_stream_bytes_per_token": round(alg["per_token_per_stream"], 1),
                      "per_stream_GBps": round(alg["per_stream"] / (ms / 1e3) / 1e9, 1),
-                     "kernel": (f"ygg::fast_kernel<{info.d_state}, {info.n_layers}>" if info.kernel == 1 else
-                                f"ygg::run_kernel<{info.d_state}, {info.block_size}, {info.readout_rank}>")},
+                     "kernel": kernel},
         "cpu_baseline": cpu,
         "batch1": batch1,
     }
