@@ -2,7 +2,7 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 4]
 
-Workload (default: configuration 4 of BASELINE.json): the synthetic V=256, 4-layer, d=128, D=14 int8 model
+Workload (default: configuration 4, the batch-4096 headline case): the synthetic V=256, 4-layer, d=128, D=14 int8 model
 (3.63 GB YGG1 file, seed 3), 4096 independent streams x 1024 Zipf(1.1) byte tokens (seed 3), zero initial state.
 One step = one ygg_run launch over the whole batch (every token of every stream, logits written for every token),
 inputs resident in HBM before the timed region. Prints one JSON line (rank 0) with:

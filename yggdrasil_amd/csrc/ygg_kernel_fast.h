@@ -126,7 +126,7 @@ __global__ __launch_bounds__(64 * kFastWaves) __attribute__((amdgpu_waves_per_eu
 #pragma unroll
                 for (int g = 0; g < N / 16; g++) S += __builtin_amdgcn_readlane(sg, g);
                 rho = 1.0f / sqrtf((float)S * kInvN + y.rms_eps);
-                // round 1: nodes 1..15 from LDS, thresholds already loaded
+                // first router round: nodes 1..15 from LDS, thresholds already loaded
                 int ix = 1;
                 {
                     int dot = 0;
