@@ -193,6 +193,36 @@ int bind_layer(const FileArrays &fa, int l, FileLayer &y) {
 
 inline int16_t rd16(const uint8_t *p) { int16_t v; memcpy(&v, p, 2); return v; }
 
+// Floats per token of the round-blocked thresholds (ygg_layout.h): sum over rounds of 2^(d0 + h).
+int64_t thr_stride(int D) {
+    int64_t ts = 0;
+    for (int d0 = 0; d0 < D; d0 += 4) ts += (int64_t)1 << (d0 + std::min(4, D - d0));
+    return ts;
+}
+
+// file thr [V][E] (heap order) -> [V][thr_stride] blocked by round and subtree (ygg_layout.h)
+void block_thresholds(const float *thr, int V, int D, float *out) {
+    const int64_t E = (int64_t)1 << D, ts = thr_stride(D);
+    for (int x = 0; x < V; x++) {
+        const float *src = thr + (size_t)x * E;
+        float *dst = out + (size_t)x * ts;
+        int64_t base = 0;
+        for (int d0 = 0; d0 < D; d0 += 4) {
+            const int h = std::min(4, D - d0), bf = 1 << h;
+            for (int64_t sub = 0; sub < ((int64_t)1 << d0); sub++) {
+                const int64_t ix = ((int64_t)1 << d0) + sub;
+                float *blk = dst + base + sub * bf;
+                for (int j = 0; j < bf - 1; j++) {
+                    const int dj = 31 - __builtin_clz((unsigned)(j + 1));
+                    blk[j] = src[(ix << dj) + (j + 1 - (1 << dj))];
+                }
+                blk[bf - 1] = 0.0f;
+            }
+            base += (int64_t)bf << d0;
+        }
+    }
+}
+
 // File record of one expert -> its gather record (layout in ygg_layout.h).
 void relayout_expert(const FileArrays &fa, const FileLayer &fy, const GatherLayout &gl, bool routed,
                      const uint8_t *frec, uint8_t *g) {
@@ -317,7 +347,7 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
         p.sqv = y.sqv ? plan(4 * (size_t)VP) : Piece{0, 0};
         if (routed) {
             p.w = plan((size_t)E * n);
-            p.thr = plan(4 * (size_t)V * E);
+            p.thr = plan(4 * (size_t)V * thr_stride(fa.D));
             const int RG = (R2 + 15) / 16;
             p.vl = R2 ? plan(16 * (size_t)RG * n) : Piece{0, 0};
             p.mv = R2 ? plan(4 * 16 * (size_t)RG) : Piece{0, 0};
@@ -369,7 +399,7 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
         if (routed) {
             int8_t *wd = (int8_t *)(H + p.w.off);
             for (size_t i = 0; i < (size_t)E * n; i++) wd[i] = (int8_t)((int)y.w[i] - 128);
-            memcpy(H + p.thr.off, y.thr, 4 * (size_t)V * E);
+            block_thresholds(y.thr, V, fa.D, (float *)(H + p.thr.off));
             if (R2) {
                 const int RG = (R2 + 15) / 16;
                 int8_t *vd = (int8_t *)(H + p.vl.off);
@@ -441,6 +471,7 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
         z.table_sx = l == 0 ? 0 : n;
         z.off_P = p.gl.off_P; z.off_U = p.gl.off_U; z.off_F = p.gl.off_F; z.off_FB = p.gl.off_FB;
         z.off_FS = p.gl.off_FS;
+        z.thr_stride = l > 0 ? (int32_t)thr_stride(fa.D) : 0;
         z.readout_scale = y.scal[0]; z.unembed_scale = y.scal[1]; z.rms_eps = y.scal[2];
         z.layer_input_scale = y.scal[3];
     }

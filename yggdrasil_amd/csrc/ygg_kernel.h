@@ -86,6 +86,46 @@ __device__ __forceinline__ void load_words(uint32_t (&d)[NW], const void *p) {
     }
 }
 
+// the same with non-temporal loads, for the per-expert streams that are read once per stream and token
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+template <int NW, int ALIGN>
+__device__ __forceinline__ void load_words_nt(uint32_t (&d)[NW], const void *p) {
+    if constexpr (ALIGN % 16 == 0 && NW % 4 == 0) {
+#pragma unroll
+        for (int i = 0; i < NW / 4; i++) {
+            const u32x4 v = __builtin_nontemporal_load((const u32x4 *)p + i);
+            d[4 * i] = v.x; d[4 * i + 1] = v.y; d[4 * i + 2] = v.z; d[4 * i + 3] = v.w;
+        }
+    } else if constexpr (ALIGN % 8 == 0 && NW % 2 == 0) {
+#pragma unroll
+        for (int i = 0; i < NW / 2; i++) {
+            const u32x2 v = __builtin_nontemporal_load((const u32x2 *)p + i);
+            d[2 * i] = v.x; d[2 * i + 1] = v.y;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < NW; i++) d[i] = __builtin_nontemporal_load((const uint32_t *)p + i);
+    }
+}
+__device__ __forceinline__ uint4 load16_nt(const void *p) {
+    const u32x4 v = __builtin_nontemporal_load((const u32x4 *)p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+// plain or non-temporal, chosen at compile time
+template <bool NT> __device__ __forceinline__ uint4 load16(const void *p) {
+    if constexpr (NT) return load16_nt(p);
+    else return *(const uint4 *)p;
+}
+template <bool NT, int NW, int ALIGN> __device__ __forceinline__ void load_words_sel(uint32_t (&d)[NW], const void *p) {
+    if constexpr (NT) load_words_nt<NW, ALIGN>(d, p);
+    else load_words<NW, ALIGN>(d, p);
+}
+template <bool NT> __device__ __forceinline__ int load_i16(const int16_t *p) {
+    if constexpr (NT) return __builtin_nontemporal_load(p);
+    else return *p;
+}
+
 constexpr unsigned long long kDigestMul = 0x100000001B3ull;
 constexpr unsigned long long kDigestLeaf = 0xD6E8FEB86659FD93ull;
 constexpr unsigned long long kDigestCoord = 0x9E3779B97F4A7C15ull;
@@ -161,8 +201,8 @@ __global__ __launch_bounds__(64) void run_kernel(const YggDevModel m, const int3
                     rho = 1.0f / sqrtf((float)S * kInvN + y.rms_eps);
                 }
                 // router descent, up to 4 levels per round
-                const float *thr = y.thr + (size_t)x * E;
-                int ix = 1;
+                const float *thr = y.thr + (size_t)x * y.thr_stride;
+                int ix = 1, base = 0;
                 for (int d0 = 0; d0 < D; d0 += 4) {
                     const int h = D - d0 < 4 ? D - d0 : 4;
                     const int nn = (1 << h) - 1;
@@ -173,15 +213,16 @@ __global__ __launch_bounds__(64) void run_kernel(const YggDevModel m, const int3
                         const int node = (ix << dj) + (qj + 1 - (1 << dj));
                         uint32_t wv[QW];
                         load_words<QW, QA>(wv, y.w + (size_t)node * N + qk * Q4);
+                        th = thr[base + ((ix - (1 << d0)) << h) + qj];
 #pragma unroll
                         for (int i = 0; i < QW; i++) dot = dot4(wv[i], qbw[i], dot);
-                        th = thr[node];
                     }
                     dot = sum4(dot);
                     const bool right = (float)dot * rho > th;
                     const unsigned long long mask = __ballot(right && qk == 0 && qj < nn);
                     int loc = 0;
                     for (int lev = 0; lev < h; lev++) loc = 2 * loc + 1 + (int)((mask >> (4 * loc)) & 1ull);
+                    base += (1 << d0) << h;
                     ix = (ix << h) + (loc - nn);
                 }
                 r = ix - E;

@@ -7,7 +7,7 @@
 //   - the 15 thresholds of that first round, thr[x][1..15] for every routed layer, depend only on the token, so they
 //     are loaded when the token is read, before the layer loop;
 //   - the whole gather record of an expert (A16, U', P) and its table row are loaded in one burst as soon as the
-//     expert is known;
+//     expert is known (plain loads: non-temporal ones cut the fetched bytes by 6% but made the step 36% slower);
 //   - LDS exchanges inside a stream's wavefront are ordered by wave-level fences instead of workgroup barriers, so the
 //     4 streams of a workgroup never wait for each other.
 #pragma once
@@ -101,7 +101,7 @@ __global__ __launch_bounds__(64 * kFastWaves) __attribute__((amdgpu_waves_per_eu
         // thresholds of the first router round of every routed layer
         float th1[LR];
 #pragma unroll
-        for (int l = 1; l < L; l++) th1[l - 1] = qj < nn1 ? m.layers[l].thr[(size_t)x * E + qj + 1] : 0.0f;
+        for (int l = 1; l < L; l++) th1[l - 1] = qj < nn1 ? m.layers[l].thr[(size_t)x * m.layers[l].thr_stride + qj] : 0.0f;
         float lg[4];
 #pragma unroll
         for (int u = 0; u < 4; u++) lg[u] = 4 * lane + u < VP ? m.output_bias[4 * lane + u] : 0.0f;
@@ -143,7 +143,8 @@ __global__ __launch_bounds__(64 * kFastWaves) __attribute__((amdgpu_waves_per_eu
                     for (int lev = 0; lev < h1; lev++) loc = 2 * loc + 1 + (int)((mask >> (4 * loc)) & 1ull);
                     ix = (1 << h1) + (loc - nn1);
                 }
-                const float *thr = y.thr + (size_t)x * E;
+                const float *thr = y.thr + (size_t)x * y.thr_stride;
+                int base = 1 << h1;
                 for (int d0 = h1; d0 < D; d0 += 4) {
                     const int h = D - d0 < 4 ? D - d0 : 4;
                     const int nn = (1 << h) - 1;
@@ -154,7 +155,7 @@ __global__ __launch_bounds__(64 * kFastWaves) __attribute__((amdgpu_waves_per_eu
                         const int node = (ix << dj) + (qj + 1 - (1 << dj));
                         uint32_t wvv[QW];
                         load_words<QW, QA>(wvv, y.w + (size_t)node * N + qk * Q4);
-                        th = thr[node];
+                        th = thr[base + ((ix - (1 << d0)) << h) + qj];
 #pragma unroll
                         for (int i = 0; i < QW; i++) dot = dot4(wvv[i], qbw[i], dot);
                     }
@@ -163,6 +164,7 @@ __global__ __launch_bounds__(64 * kFastWaves) __attribute__((amdgpu_waves_per_eu
                     const unsigned long long mask = __ballot(right && qk == 0 && qj < nn);
                     int loc = 0;
                     for (int lev = 0; lev < h; lev++) loc = 2 * loc + 1 + (int)((mask >> (4 * loc)) & 1ull);
+                    base += (1 << d0) << h;
                     ix = (ix << h) + (loc - nn);
                 }
                 r = ix - E;
@@ -175,7 +177,7 @@ __global__ __launch_bounds__(64 * kFastWaves) __attribute__((amdgpu_waves_per_eu
             if (lane < NL) {
 #pragma unroll
                 for (int c = 0; c < NA; c++) {
-                    const uint4 v = *(const uint4 *)(g + (c * NL + lane) * 16);
+                    const uint4 v = load16<false>(g + (c * NL + lane) * 16);
                     aw[4 * c] = v.x; aw[4 * c + 1] = v.y; aw[4 * c + 2] = v.z; aw[4 * c + 3] = v.w;
                 }
                 if (l > 0) {
@@ -183,7 +185,7 @@ __global__ __launch_bounds__(64 * kFastWaves) __attribute__((amdgpu_waves_per_eu
                     for (int k4 = 0; k4 < 4; k4++) {
                         if (k4 < R2 / 4) {
                             uint32_t tmp[C];
-                            load_words<C, 4 * C>(tmp, g + y.off_U + ((size_t)(k4 * NL + lane) * C) * 4);
+                            load_words_sel<false, C, 4 * C>(tmp, g + y.off_U + ((size_t)(k4 * NL + lane) * C) * 4);
 #pragma unroll
                             for (int c = 0; c < C; c++) uw[k4][c] = tmp[c];
                         }
@@ -191,14 +193,14 @@ __global__ __launch_bounds__(64 * kFastWaves) __attribute__((amdgpu_waves_per_eu
                 }
                 const int16_t *tr = y.table + (size_t)r * y.table_sr + (size_t)x * y.table_sx + C * lane;
 #pragma unroll
-                for (int c = 0; c < C; c++) trow[c] = tr[c];
+                for (int c = 0; c < C; c++) trow[c] = load_i16<false>(tr + c);
             }
             {
                 const uint8_t *pp = g + y.off_P;
 #pragma unroll
                 for (int gi = 0; gi < SP / GP; gi++) {
                     uint32_t tmp[GP / 4];
-                    load_words<GP / 4, GP>(tmp, pp + (gi * 64 + lane) * GP);
+                    load_words_sel<false, GP / 4, GP>(tmp, pp + (gi * 64 + lane) * GP);
 #pragma unroll
                     for (int i = 0; i < GP / 4; i++) pw[gi * (GP / 4) + i] = tmp[i];
                 }

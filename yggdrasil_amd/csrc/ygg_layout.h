@@ -25,6 +25,13 @@
 //                  U'[C l + c][4 k4 .. 4 k4 + 3] (s8).
 //   U   at off_F:  the same for the factored input projection with input_rank in place of R2.
 //   Cb  at off_FB: int16[n] factored bias.  S at off_FS: f32 factored input scale.
+//
+// Router thresholds (file: thr[x][node], heap order) are regrouped by descent round. Round k covers depths
+// [d0, d0 + h), d0 = 4 k, h = min(4, D - d0); each subtree root ix at depth d0 owns one block of 2^h floats holding
+// the thresholds of its 2^h - 1 nodes in breadth-first order (node j of the block: depth dj = floor(log2(j + 1)),
+// heap index (ix << dj) + j + 1 - 2^dj), the last float unused. Blocks of round k start at base_k = sum over earlier
+// rounds of 2^(d0 + h); the block of root ix is at base_k + (ix - 2^d0) 2^h. One round of one stream then reads one
+// 64-byte block instead of one cache line per level.
 #pragma once
 #include <stdint.h>
 
@@ -35,7 +42,7 @@ struct YggDevLayer {
     const uint8_t *gath;     // E gather records
     const int16_t *table;    // token layer [V][n] (expert x = its own row); routed table storage [E][V][n]
     const int8_t *w;         // routed: [E][n] router rows in heap order (row 0 unused)
-    const float *thr;        // routed: [V][E] thresholds (slot 0 unused)
+    const float *thr;        // routed: [V][thr_stride] thresholds, blocked by router round (see below)
     const int8_t *vl;        // routed, R2 > 0: [16 RG][n] layer-input down-projection V' (rows >= R2 zero)
     const float *mv;         // routed, R2 > 0: [16 RG]
     const float *mulv;       // [n] per-coordinate layer-input scale, or null
@@ -49,6 +56,7 @@ struct YggDevLayer {
     int64_t table_sr;        // table elements per expert (token layer: n; routed: V n)
     int32_t table_sx;        // table elements per token (token layer: 0; routed: n)
     int32_t off_P, off_U, off_F, off_FB, off_FS;  // byte offsets in the gather record, -1 absent
+    int32_t thr_stride;      // floats per token row of thr
     float readout_scale, unembed_scale, rms_eps, layer_input_scale;
 };
 
