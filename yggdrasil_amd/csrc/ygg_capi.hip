@@ -193,34 +193,72 @@ int bind_layer(const FileArrays &fa, int l, FileLayer &y) {
 
 inline int16_t rd16(const uint8_t *p) { int16_t v; memcpy(&v, p, 2); return v; }
 
-// Floats per token of the round-blocked thresholds (ygg_layout.h): sum over rounds of 2^(d0 + h).
-int64_t thr_stride(int D) {
+// Router descent plan (ygg_layout.h): min(4, D) levels, then the rest in ceil(rest / 4) near-equal rounds, larger
+// first; YGG_ROUNDS=greedy takes 4 levels per round instead.
+struct RoundPlan {
+    int n = 0, h[YGG_MAX_ROUNDS] = {0};
+};
+RoundPlan round_plan(int D) {
+    RoundPlan p;
+    if (D <= 0) return p;
+    const char *env = getenv("YGG_ROUNDS");
+    const bool greedy = env && !strcmp(env, "greedy");
+    const int h0 = std::min(4, D);
+    p.h[p.n++] = h0;
+    int rest = D - h0;
+    const int nr = (rest + 3) / 4;
+    for (int r = 0; r < nr; r++) {
+        const int h = greedy ? std::min(4, rest) : (D - h0) / nr + (r < (D - h0) % nr ? 1 : 0);
+        p.h[p.n++] = h;
+        rest -= h;
+    }
+    return p;
+}
+
+// Slots per token of the round-blocked router arrays: sum over rounds of 2^(d0 + h).
+int64_t plan_slots(const RoundPlan &p) {
     int64_t ts = 0;
-    for (int d0 = 0; d0 < D; d0 += 4) ts += (int64_t)1 << (d0 + std::min(4, D - d0));
+    int d0 = 0;
+    for (int r = 0; r < p.n; r++) { ts += (int64_t)1 << (d0 + p.h[r]); d0 += p.h[r]; }
     return ts;
 }
 
-// file thr [V][E] (heap order) -> [V][thr_stride] blocked by round and subtree (ygg_layout.h)
-void block_thresholds(const float *thr, int V, int D, float *out) {
-    const int64_t E = (int64_t)1 << D, ts = thr_stride(D);
+// Visit every (slot, heap node) of the plan; slots with no node (the last of each block) get node -1.
+template <class F> void for_each_slot(const RoundPlan &p, F f) {
+    int64_t base = 0;
+    int d0 = 0;
+    for (int r = 0; r < p.n; r++) {
+        const int h = p.h[r], bf = 1 << h;
+        for (int64_t sub = 0; sub < ((int64_t)1 << d0); sub++) {
+            const int64_t ix = ((int64_t)1 << d0) + sub;
+            for (int j = 0; j < bf; j++) {
+                if (j == bf - 1) { f(base + sub * bf + j, (int64_t)-1); continue; }
+                const int dj = 31 - __builtin_clz((unsigned)(j + 1));
+                f(base + sub * bf + j, (ix << dj) + (j + 1 - (1 << dj)));
+            }
+        }
+        base += (int64_t)bf << d0;
+        d0 += h;
+    }
+}
+
+// file thr [V][E] (heap order) -> [V][slots] blocked by round and subtree
+void block_thresholds(const float *thr, int V, int D, const RoundPlan &p, float *out) {
+    const int64_t E = (int64_t)1 << D, ts = plan_slots(p);
     for (int x = 0; x < V; x++) {
         const float *src = thr + (size_t)x * E;
         float *dst = out + (size_t)x * ts;
-        int64_t base = 0;
-        for (int d0 = 0; d0 < D; d0 += 4) {
-            const int h = std::min(4, D - d0), bf = 1 << h;
-            for (int64_t sub = 0; sub < ((int64_t)1 << d0); sub++) {
-                const int64_t ix = ((int64_t)1 << d0) + sub;
-                float *blk = dst + base + sub * bf;
-                for (int j = 0; j < bf - 1; j++) {
-                    const int dj = 31 - __builtin_clz((unsigned)(j + 1));
-                    blk[j] = src[(ix << dj) + (j + 1 - (1 << dj))];
-                }
-                blk[bf - 1] = 0.0f;
-            }
-            base += (int64_t)bf << d0;
-        }
+        for_each_slot(p, [&](int64_t slot, int64_t node) { dst[slot] = node < 0 ? 0.0f : src[node]; });
     }
+}
+
+// file w [E][n] u8 (w + 128, heap order) -> [slots][n] s8 blocked by round and subtree
+void block_rows(const uint8_t *w, int n, const RoundPlan &p, int8_t *out) {
+    for_each_slot(p, [&](int64_t slot, int64_t node) {
+        int8_t *dst = out + (size_t)slot * n;
+        if (node < 0) { memset(dst, 0, (size_t)n); return; }
+        for (int i = 0; i < n; i++) dst[i] = (int8_t)((int)w[(size_t)node * n + i] - 128);
+    });
 }
 
 // File record of one expert -> its gather record (layout in ygg_layout.h).
@@ -323,6 +361,8 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
         fast = ygg::find_fast_launcher(n, L);
     if (fast) launch = fast;
 
+    const RoundPlan rplan = round_plan(L > 1 ? fa.D : 0);
+    const int64_t slots = plan_slots(rplan);
     // device arena plan: every array 256-byte aligned
     struct Piece { size_t off, bytes; };
     size_t total = 0;
@@ -346,8 +386,8 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
         p.mz = y.mzl ? plan(4 * (size_t)El * R) : Piece{0, 0};
         p.sqv = y.sqv ? plan(4 * (size_t)VP) : Piece{0, 0};
         if (routed) {
-            p.w = plan((size_t)E * n);
-            p.thr = plan(4 * (size_t)V * thr_stride(fa.D));
+            p.w = plan((size_t)slots * n);
+            p.thr = plan(4 * (size_t)V * slots);
             const int RG = (R2 + 15) / 16;
             p.vl = R2 ? plan(16 * (size_t)RG * n) : Piece{0, 0};
             p.mv = R2 ? plan(4 * 16 * (size_t)RG) : Piece{0, 0};
@@ -397,9 +437,8 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
         }
         if (y.sqv) memcpy(H + p.sqv.off, y.sqv, 4 * (size_t)VP);
         if (routed) {
-            int8_t *wd = (int8_t *)(H + p.w.off);
-            for (size_t i = 0; i < (size_t)E * n; i++) wd[i] = (int8_t)((int)y.w[i] - 128);
-            block_thresholds(y.thr, V, fa.D, (float *)(H + p.thr.off));
+            block_rows(y.w, n, rplan, (int8_t *)(H + p.w.off));
+            block_thresholds(y.thr, V, fa.D, rplan, (float *)(H + p.thr.off));
             if (R2) {
                 const int RG = (R2 + 15) / 16;
                 int8_t *vd = (int8_t *)(H + p.vl.off);
@@ -447,6 +486,8 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     YggDevModel &d = m->dev;
     d.L = L; d.N = n; d.BLK = fa.blk; d.V = V; d.VP = VP; d.D = fa.D; d.E = E; d.R = R; d.R2 = R2; d.K = fa.K;
     d.shift = fa.shift;
+    d.n_rounds = rplan.n;
+    for (int r = 0; r < YGG_MAX_ROUNDS; r++) d.round_h[r] = rplan.h[r];
     d.output_bias = (const float *)at(p_bias);
     d.err = (uint32_t *)at(p_err);
     for (int l = 0; l < L; l++) {
@@ -471,7 +512,7 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
         z.table_sx = l == 0 ? 0 : n;
         z.off_P = p.gl.off_P; z.off_U = p.gl.off_U; z.off_F = p.gl.off_F; z.off_FB = p.gl.off_FB;
         z.off_FS = p.gl.off_FS;
-        z.thr_stride = l > 0 ? (int32_t)thr_stride(fa.D) : 0;
+        z.thr_stride = l > 0 ? (int32_t)slots : 0;
         z.readout_scale = y.scal[0]; z.unembed_scale = y.scal[1]; z.rms_eps = y.scal[2];
         z.layer_input_scale = y.scal[3];
     }

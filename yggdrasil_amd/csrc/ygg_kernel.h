@@ -3,10 +3,11 @@
 //
 // Per token and layer (cpu/ygg.cpp:441-459):
 //   routed layer   rho from the layer below (per-16-coordinate sums in 16 lanes, cpu/ygg.cpp:248-266); the router
-//                  descent in rounds of up to 4 levels: 15 quads take the 15 nodes of the 4-level subtree below the
-//                  current node, each quad forms one node's dot product (quad lanes split the coordinates, a DPP
-//                  quad sum joins them), one ballot of the 15 comparisons gives the whole 4-level path in scalar
-//                  registers (cpu/ygg.cpp:271-280); the layer input zl from V' in the same quad layout
+//                  descent in rounds of up to 4 levels (the model's round plan): up to 15 quads take the nodes of
+//                  the subtree below the current node, each quad forms one node's dot product (quad lanes split the
+//                  coordinates, a DPP quad sum joins them), one ballot of the comparisons gives the whole path
+//                  through the subtree in scalar registers (cpu/ygg.cpp:271-280); the layer input zl from V' in the
+//                  same quad layout
 //                  (cpu/ygg.cpp:285-296)
 //   every layer    the expert's gather record (A16, U', P) and its table row are loaded as soon as the expert is
 //                  known; transition with v_dot2 (int16 x int16), table or factored input, layer input with v_dot4,
@@ -202,18 +203,17 @@ __global__ __launch_bounds__(64) void run_kernel(const YggDevModel m, const int3
                 }
                 // router descent, up to 4 levels per round
                 const float *thr = y.thr + (size_t)x * y.thr_stride;
-                int ix = 1, base = 0;
-                for (int d0 = 0; d0 < D; d0 += 4) {
-                    const int h = D - d0 < 4 ? D - d0 : 4;
+                int ix = 1, base = 0, d0 = 0;
+                for (int rd = 0; rd < m.n_rounds; rd++) {
+                    const int h = m.round_h[rd];
                     const int nn = (1 << h) - 1;
+                    const int slot = base + ((ix - (1 << d0)) << h) + qj;
                     int dot = 0;
                     float th = 0.0f;
                     if (qj < nn) {
-                        const int dj = 31 - __builtin_clz(qj + 1);
-                        const int node = (ix << dj) + (qj + 1 - (1 << dj));
                         uint32_t wv[QW];
-                        load_words<QW, QA>(wv, y.w + (size_t)node * N + qk * Q4);
-                        th = thr[base + ((ix - (1 << d0)) << h) + qj];
+                        load_words<QW, QA>(wv, y.w + (size_t)slot * N + qk * Q4);
+                        th = thr[slot];
 #pragma unroll
                         for (int i = 0; i < QW; i++) dot = dot4(wv[i], qbw[i], dot);
                     }
@@ -223,6 +223,7 @@ __global__ __launch_bounds__(64) void run_kernel(const YggDevModel m, const int3
                     int loc = 0;
                     for (int lev = 0; lev < h; lev++) loc = 2 * loc + 1 + (int)((mask >> (4 * loc)) & 1ull);
                     base += (1 << d0) << h;
+                    d0 += h;
                     ix = (ix << h) + (loc - nn);
                 }
                 r = ix - E;

@@ -3,7 +3,7 @@
 // run_kernel (ygg_kernel.h); what changes is where the latency of one token goes:
 //   - 4 streams per workgroup (one wavefront each) share LDS copies of what every stream reads at every token: the
 //     unembedding Q of every layer, the layer-input down-projection V' of every routed layer, and the router rows of
-//     the top 4 tree levels (nodes 1..15). The first router round then reads only LDS plus thresholds.
+//     the first descent round (the top 4 tree levels, nodes 1..15). That round then reads only LDS plus thresholds.
 //   - the 15 thresholds of that first round, thr[x][1..15] for every routed layer, depend only on the token, so they
 //     are loaded when the token is read, before the layer loop;
 //   - the whole gather record of an expert (A16, U', P) and its table row are loaded in one burst as soon as the
@@ -61,8 +61,8 @@ __global__ __launch_bounds__(64 * kFastWaves) __attribute__((amdgpu_waves_per_eu
 #pragma unroll
     for (int l = 1; l < L; l++) {
         const YggDevLayer &y = m.layers[l];
-        const int rows = E - 1 < 15 ? E - 1 : 15;
-        const uint32_t *ws = (const uint32_t *)(y.w + N);
+        const int rows = (1 << m.round_h[0]) - 1;     // the first round's block: slots 0 .. 2^h0 - 2
+        const uint32_t *ws = (const uint32_t *)y.w;
         uint32_t *wd = (uint32_t *)Ws[l - 1];
         for (int i = tid; i < 15 * N / 4; i += 64 * W) wd[i] = i < rows * N / 4 ? ws[i] : 0u;
         uint32_t *vd = (uint32_t *)Vs[l - 1];
@@ -89,7 +89,7 @@ __global__ __launch_bounds__(64 * kFastWaves) __attribute__((amdgpu_waves_per_eu
     unsigned long long dg = digest ? digest[s] : 0ull;
     const int32_t *tok = tokens + (size_t)s * T;
     int x_next = T > 0 ? tok[0] : 0;
-    const int h1 = D < 4 ? D : 4, nn1 = (1 << h1) - 1;
+    const int h1 = m.round_h[0], nn1 = (1 << h1) - 1;
 
     for (int t = 0; t < T; t++) {
         const int x = x_next;
@@ -144,18 +144,17 @@ __global__ __launch_bounds__(64 * kFastWaves) __attribute__((amdgpu_waves_per_eu
                     ix = (1 << h1) + (loc - nn1);
                 }
                 const float *thr = y.thr + (size_t)x * y.thr_stride;
-                int base = 1 << h1;
-                for (int d0 = h1; d0 < D; d0 += 4) {
-                    const int h = D - d0 < 4 ? D - d0 : 4;
+                int base = 1 << h1, d0 = h1;
+                for (int rd = 1; rd < m.n_rounds; rd++) {
+                    const int h = m.round_h[rd];
                     const int nn = (1 << h) - 1;
+                    const int slot = base + ((ix - (1 << d0)) << h) + qj;
                     int dot = 0;
                     float th = 0.0f;
                     if (qj < nn) {
-                        const int dj = 31 - __builtin_clz(qj + 1);
-                        const int node = (ix << dj) + (qj + 1 - (1 << dj));
                         uint32_t wvv[QW];
-                        load_words<QW, QA>(wvv, y.w + (size_t)node * N + qk * Q4);
-                        th = thr[base + ((ix - (1 << d0)) << h) + qj];
+                        load_words<QW, QA>(wvv, y.w + (size_t)slot * N + qk * Q4);
+                        th = thr[slot];
 #pragma unroll
                         for (int i = 0; i < QW; i++) dot = dot4(wvv[i], qbw[i], dot);
                     }
@@ -165,6 +164,7 @@ __global__ __launch_bounds__(64 * kFastWaves) __attribute__((amdgpu_waves_per_eu
                     int loc = 0;
                     for (int lev = 0; lev < h; lev++) loc = 2 * loc + 1 + (int)((mask >> (4 * loc)) & 1ull);
                     base += (1 << d0) << h;
+                    d0 += h;
                     ix = (ix << h) + (loc - nn);
                 }
                 r = ix - E;

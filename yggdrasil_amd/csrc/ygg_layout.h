@@ -26,12 +26,16 @@
 //   U   at off_F:  the same for the factored input projection with input_rank in place of R2.
 //   Cb  at off_FB: int16[n] factored bias.  S at off_FS: f32 factored input scale.
 //
-// Router thresholds (file: thr[x][node], heap order) are regrouped by descent round. Round k covers depths
-// [d0, d0 + h), d0 = 4 k, h = min(4, D - d0); each subtree root ix at depth d0 owns one block of 2^h floats holding
-// the thresholds of its 2^h - 1 nodes in breadth-first order (node j of the block: depth dj = floor(log2(j + 1)),
-// heap index (ix << dj) + j + 1 - 2^dj), the last float unused. Blocks of round k start at base_k = sum over earlier
-// rounds of 2^(d0 + h); the block of root ix is at base_k + (ix - 2^d0) 2^h. One round of one stream then reads one
-// 64-byte block instead of one cache line per level.
+// Router descent plan: the D levels are taken in rounds of h_k levels (round_h), the first of min(4, D) levels, the
+// rest split as evenly as possible into ceil((D - h_0) / 4) rounds, larger first (D = 14: 4, 4, 3, 3). A round of h
+// levels evaluates the 2^h - 1 nodes of one subtree in parallel.
+//
+// Router rows and thresholds (file: w[node][n], thr[x][node], heap order) are regrouped by round. Round k covers
+// depths [d0, d0 + h); each subtree root ix at depth d0 owns one block of 2^h slots holding its 2^h - 1 nodes in
+// breadth-first order (slot j: depth dj = floor(log2(j + 1)), heap index (ix << dj) + j + 1 - 2^dj), the last slot
+// unused. Blocks of round k start at base_k = sum over earlier rounds of 2^(d0 + h); the block of root ix is at
+// base_k + (ix - 2^d0) 2^h. w holds one n-byte row per slot, thr one float per slot and token; one round of one stream
+// reads one contiguous block of rows and one block of thresholds (64 bytes for h = 4).
 #pragma once
 #include <stdint.h>
 
@@ -41,7 +45,7 @@
 struct YggDevLayer {
     const uint8_t *gath;     // E gather records
     const int16_t *table;    // token layer [V][n] (expert x = its own row); routed table storage [E][V][n]
-    const int8_t *w;         // routed: [E][n] router rows in heap order (row 0 unused)
+    const int8_t *w;         // routed: [thr_stride][n] router rows, blocked by round (see below)
     const float *thr;        // routed: [V][thr_stride] thresholds, blocked by router round (see below)
     const int8_t *vl;        // routed, R2 > 0: [16 RG][n] layer-input down-projection V' (rows >= R2 zero)
     const float *mv;         // routed, R2 > 0: [16 RG]
@@ -56,12 +60,15 @@ struct YggDevLayer {
     int64_t table_sr;        // table elements per expert (token layer: n; routed: V n)
     int32_t table_sx;        // table elements per token (token layer: 0; routed: n)
     int32_t off_P, off_U, off_F, off_FB, off_FS;  // byte offsets in the gather record, -1 absent
-    int32_t thr_stride;      // floats per token row of thr
+    int32_t thr_stride;      // slots per token: floats per token row of thr, rows of w
     float readout_scale, unembed_scale, rms_eps, layer_input_scale;
 };
 
+#define YGG_MAX_ROUNDS 16
+
 struct YggDevModel {
     int32_t L, N, BLK, V, VP, D, E, R, R2, K, shift;
+    int32_t n_rounds, round_h[YGG_MAX_ROUNDS];   // router descent plan
     const float *output_bias;   // [VP]
     uint32_t *err;              // error word (bit 0: token out of range)
     YggDevLayer layers[YGG_MAX_LAYERS];
