@@ -39,14 +39,11 @@ def _compare(got, ref, keys=("leaves", "states", "logits")):
                                  f"gpu {a[tuple(bad[0])]} oracle {b[tuple(bad[0])]}")
 
 
-@pytest.fixture(params=["default", "generic"])
+@pytest.fixture(params=["pipe", "fast", "generic"])
 def kernel_env(request, monkeypatch):
-    """Load models with the kernel the library picks ("default": the specialised one where the shape allows) or with
-    the general kernel forced (YGG_KERNEL=generic)."""
-    if request.param == "generic":
-        monkeypatch.setenv("YGG_KERNEL", "generic")
-    else:
-        monkeypatch.delenv("YGG_KERNEL", raising=False)
+    """Load models with one kernel forced (YGG_KERNEL): the layer-pipelined one, the specialised per-stream one, or
+    the general one; the first two apply only to the common shape (readout rank 8, block 16, ...)."""
+    monkeypatch.setenv("YGG_KERNEL", request.param)
     return request.param
 
 
@@ -58,14 +55,20 @@ def _gpu_run(model, x, state=None, states=True):
 
 
 @pytest.mark.parametrize("ci", range(len(synth.KERNEL_CASES)))
-def test_kernel_case(hip, model_dir, ci):
+def test_kernel_case(hip, model_dir, ci, kernel_env):
     spec = synth.KERNEL_CASES[ci]
-    _say(f"case {ci}: {spec}")
+    _say(f"case {ci}: {spec} kernel {kernel_env}")
     path = model_dir / f"kernel{ci}.bin"
     synth.write_model(spec, synth.KERNEL_SEED, path)
     x = synth.kernel_tokens(spec.vocab)
     ref = Oracle(path).run(x, states=True)
     model = hip.load(path)
+    common = spec.readout_rank == 8 and spec.block_size == 16 and spec.layer_input_rank <= 16 and \
+        not spec.input_rank and not spec.group and spec.n_layers <= 4 and spec.d_state <= 128
+    if common:
+        _expect_kernel(model, kernel_env)
+    else:
+        assert model.info.kernel == 0 and model.info.pipe_max_streams == 0
     got = _gpu_run(model, x)
     _compare(got, ref)
     np.testing.assert_array_equal(got["state"], ref["state"])
@@ -81,7 +84,9 @@ def c12(model_dir):
 
 
 def _expect_kernel(model, kernel_env):
+    """The forced kernel is the one in use (the shapes passed here are all common-shape models)."""
     assert model.info.kernel == (0 if kernel_env == "generic" else 1), model.info.kernel
+    assert (model.info.pipe_max_streams > 0) == (kernel_env == "pipe"), model.info.pipe_max_streams
 
 
 def test_config1_full_stream(hip, c12, kernel_env):

@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <climits>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -21,6 +22,7 @@ typedef hipError_t (*Launcher)(const YggDevModel &, const int32_t *, int, int, i
                                unsigned long long *, hipStream_t);
 Launcher find_launcher(int n, int blk, int R);
 Launcher find_fast_launcher(int n, int L);
+Launcher find_pipe_launcher(int n, int L);
 }  // namespace ygg
 
 namespace {
@@ -329,6 +331,8 @@ struct ygg_model {
     void *arena = nullptr;
     size_t arena_bytes = 0;
     ygg::Launcher launch = nullptr;
+    ygg::Launcher launch_pipe = nullptr;   // for calls with B <= pipe_max_streams
+    int pipe_max_streams = 0;
 };
 
 namespace {
@@ -353,12 +357,15 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     for (int l = 1; l < L; l++)
         if ((fl[l].vt != nullptr) != (fl[1].vt != nullptr))
             return fail(YGG_ERR_FORMAT, "model file: mixed table and factored routed layers");
-    // the specialised kernel covers the common shape; YGG_KERNEL=generic forces the general one
+    // the specialised kernels cover the common shape: fast_kernel for many streams, pipe_kernel (one wavefront per
+    // layer) when the call's B L wavefronts fit on the device at once. YGG_KERNEL=generic|fast|pipe forces one.
     const char *kenv = getenv("YGG_KERNEL");
-    const bool want_fast = !(kenv && !strcmp(kenv, "generic"));
-    ygg::Launcher fast = nullptr;
-    if (want_fast && R == 8 && fa.blk == 16 && R2 <= 16 && !factored && !group && L <= 4 && VP <= 256)
+    const std::string kmode = kenv ? kenv : "";
+    ygg::Launcher fast = nullptr, pipe = nullptr;
+    if (kmode != "generic" && R == 8 && fa.blk == 16 && R2 <= 16 && !factored && !group && L <= 4 && VP <= 256) {
         fast = ygg::find_fast_launcher(n, L);
+        if (kmode != "fast") pipe = ygg::find_pipe_launcher(n, L);
+    }
     if (fast) launch = fast;
 
     const RoundPlan rplan = round_plan(L > 1 ? fa.D : 0);
@@ -476,7 +483,12 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
         (void)hipFree(arena);
         return fail(YGG_ERR_DEVICE, "upload failed: %s", hipGetErrorString(e));
     }
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || cus <= 0) cus = 256;
     ygg_model *m = new ygg_model();
+    m->launch_pipe = pipe;
+    // pipe_kernel when all B L wavefronts of a call are resident at once (16 per CU), or always with YGG_KERNEL=pipe
+    m->pipe_max_streams = pipe ? (kmode == "pipe" ? INT32_MAX : 16 * cus / L) : 0;
     m->device = device;
     m->arena = arena;
     m->arena_bytes = total;
@@ -521,6 +533,7 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     I.n_layers = L; I.d_state = n; I.block_size = fa.blk; I.vocab = V; I.vocab_pad = VP; I.router_depth = fa.D;
     I.n_experts = E; I.readout_rank = R; I.layer_input_rank = R2; I.input_rank = fa.K; I.shift = fa.shift;
     I.factored = factored; I.group = group; I.device = device; I.kernel = fast ? 1 : 0;
+    I.pipe_max_streams = m->pipe_max_streams;
     I.file_array_bytes = fa.bytes;
     I.device_bytes = (int64_t)total;
     for (int l = 0; l < L; l++) I.gather_bytes[l] = lp[l].gl.bytes;
@@ -545,7 +558,7 @@ struct DeviceGuard {
 
 extern "C" {
 
-int ygg_version(void) { return 2; }
+int ygg_version(void) { return 3; }
 
 const char *ygg_last_error(void) { return g_err.c_str(); }
 
@@ -606,8 +619,10 @@ int ygg_run(const ygg_model *m, const int32_t *d_tokens, int B, int T, int8_t *d
     if (!d_state || (T > 0 && !d_tokens)) return fail(YGG_ERR_ARG, "tokens or state is NULL");
     DeviceGuard g;
     HIP_TRY(g.set(m->device));
-    HIP_TRY(m->launch(m->dev, d_tokens, B, T, d_state, d_logits, d_leaves, d_states,
-                      (unsigned long long *)d_digest, (hipStream_t)stream));
+    // the pipelined kernel overlaps the layers of consecutive tokens, so it needs more than one token per launch
+    ygg::Launcher k = (m->launch_pipe && B <= m->pipe_max_streams && T > 1) ? m->launch_pipe : m->launch;
+    HIP_TRY(k(m->dev, d_tokens, B, T, d_state, d_logits, d_leaves, d_states, (unsigned long long *)d_digest,
+              (hipStream_t)stream));
     return YGG_OK;
 }
 
@@ -622,7 +637,9 @@ int ygg_step(const ygg_model *m, const int32_t *d_tokens, const int8_t *d_state_
     if (d_state_in != d_state_out)
         HIP_TRY(hipMemcpyAsync(d_state_out, d_state_in, (size_t)B * m->dev.L * m->dev.N, hipMemcpyDeviceToDevice,
                                (hipStream_t)stream));
-    HIP_TRY(m->launch(m->dev, d_tokens, B, 1, d_state_out, d_logits, d_leaves, nullptr, nullptr, (hipStream_t)stream));
+    // one token: the per-stream kernel (a one-token launch cannot overlap layers), or the pipelined one when forced
+    ygg::Launcher k = (m->launch_pipe && m->pipe_max_streams == INT32_MAX) ? m->launch_pipe : m->launch;
+    HIP_TRY(k(m->dev, d_tokens, B, 1, d_state_out, d_logits, d_leaves, nullptr, nullptr, (hipStream_t)stream));
     return YGG_OK;
 }
 

@@ -1,15 +1,23 @@
-// The fused step specialised for the common shape: readout rank 8, block 16, layer-input rank <= 16, table storage,
-// one scale per tensor, at most 4 layers (every benchmark configuration). Same arithmetic and lane mapping as
-// run_kernel (ygg_kernel.h); what changes is where the latency of one token goes:
-//   - 4 streams per workgroup (one wavefront each) share LDS copies of what every stream reads at every token: the
-//     unembedding Q of every layer, the layer-input down-projection V' of every routed layer, and the router rows of
-//     the first descent round (the top 4 tree levels, nodes 1..15). That round then reads only LDS plus thresholds.
-//   - the 15 thresholds of that first round, thr[x][1..15] for every routed layer, depend only on the token, so they
-//     are loaded when the token is read, before the layer loop;
-//   - the whole gather record of an expert (A16, U', P) and its table row are loaded in one burst as soon as the
-//     expert is known (plain loads: non-temporal ones cut the fetched bytes by 6% but made the step 36% slower);
-//   - LDS exchanges inside a stream's wavefront are ordered by wave-level fences instead of workgroup barriers, so the
-//     4 streams of a workgroup never wait for each other.
+// Two kernels for the common shape: readout rank 8, block 16, layer-input rank <= 16, table storage, one scale per
+// tensor, at most 4 layers (every benchmark configuration). Same arithmetic and lane mapping as run_kernel
+// (ygg_kernel.h); the per-layer pieces below are shared by both.
+//
+// fast_kernel (throughput: many streams): one wavefront per stream runs every layer of every token, 4 streams per
+// workgroup. What every stream reads at every token is in LDS once per workgroup: the unembedding Q of every layer,
+// the layer-input down-projection V' of every routed layer and the router rows of the first descent round (nodes
+// 1..15). The thresholds of that round, thr[x][1..15], depend only on the token and are loaded when the token is
+// read. An expert's whole gather record (A16, U', P) and table row are loaded in one burst as soon as the expert is
+// known (plain loads: non-temporal ones cut the fetched bytes by 6% but made the step 36% slower). LDS exchanges
+// inside a wavefront are ordered by wave-level fences, so the streams of a workgroup never wait for each other.
+//
+// pipe_kernel (latency: few streams): one workgroup per stream and one wavefront per layer. In tick k wavefront l
+// processes token k - l, so the L layers of a stream work on L consecutive tokens at once and a token costs about
+// one layer's chain of dependent loads instead of L of them. Layer l at token t needs the state of layer l - 1 at
+// token t (written by wavefront l - 1 in tick k - 1) and its own state at token t - 1 (double-buffered by token
+// parity); one workgroup barrier per tick orders them. Logits of a token are summed layer by layer in a ring of L
+// LDS rows in layer order (as the reference does, cpu/ygg.cpp:457) and stored by the last layer's wavefront. The
+// token layer's gather record and the routed layers' first-round thresholds of the next token are loaded a tick
+// ahead.
 #pragma once
 #include "ygg_kernel.h"
 
@@ -23,64 +31,303 @@ __device__ __forceinline__ void wave_sync() {
 
 constexpr int kFastWaves = 4;
 
+template <int N> struct Fast {
+    static constexpr int R = 8, BLK = 16;
+    static constexpr int C = Lanes<N>::C, NL = Lanes<N>::NL;
+    static constexpr int Q4 = N / 4, QW = Q4 / 4;
+    static constexpr int QA = (Q4 % 16 == 0) ? 16 : 8;
+    static constexpr int RL = ReadoutLanes<N, R>::RL, SP = ReadoutLanes<N, R>::SP, GP = ReadoutLanes<N, R>::GP;
+    static constexpr int SPW = SP / 4;
+    static constexpr int SPA = SP % 16 == 0 ? 16 : (SP % 8 == 0 ? 8 : 4);
+    static constexpr int AW = C * BLK / 2, NA = AW / 4;
+    static constexpr float kInvN = 1.0f / (float)N;
+};
+
+// the per-expert registers of one stream and layer
+template <int N> struct Gather {
+    uint32_t aw[Fast<N>::AW], pw[Fast<N>::SPW], uw[4][Fast<N>::C];
+    int trow[Fast<N>::C];
+};
+
+// the workgroup's LDS copies of Q (all layers), V' and the first-round router rows (routed layers)
+template <int N, int L> struct SharedTables {
+    static constexpr int LR = L > 1 ? L - 1 : 1;
+    int8_t Q[L][256 * 8];
+    int8_t W[LR][15 * N];
+    int8_t V[LR][16 * N];
+};
+
 template <int N, int L>
-__global__ __launch_bounds__(64 * kFastWaves) __attribute__((amdgpu_waves_per_eu(4))) void fast_kernel(const YggDevModel m, const int32_t *__restrict__ tokens,
-                                                               int B, int T, int8_t *__restrict__ state,
-                                                               float *__restrict__ logits,
-                                                               int32_t *__restrict__ leaves,
-                                                               int8_t *__restrict__ states,
-                                                               unsigned long long *__restrict__ digest) {
-    constexpr int R = 8, BLK = 16, W = kFastWaves;
-    constexpr int C = Lanes<N>::C, NL = Lanes<N>::NL;
-    constexpr int Q4 = N / 4, QW = Q4 / 4;
-    constexpr int QA = (Q4 % 16 == 0) ? 16 : 8;
-    constexpr int RL = ReadoutLanes<N, R>::RL, SP = ReadoutLanes<N, R>::SP, GP = ReadoutLanes<N, R>::GP;
-    constexpr int SPW = SP / 4;
-    constexpr int AW = C * BLK / 2, NA = AW / 4;
-    constexpr int LR = L > 1 ? L - 1 : 1;         // routed layers (array extent)
-    constexpr float kInvN = 1.0f / (float)N;
-
-    __shared__ __attribute__((aligned(16))) int8_t Qs[L][256 * R];
-    __shared__ __attribute__((aligned(16))) int8_t Ws[LR][15 * N];
-    __shared__ __attribute__((aligned(16))) int8_t Vs[LR][16 * N];
-    __shared__ __attribute__((aligned(16))) int8_t qsw[W][L * N];
-    __shared__ __attribute__((aligned(16))) int8_t zlw[W][16];
-    __shared__ __attribute__((aligned(16))) int8_t zqw[W][16];
-
-    const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63;
-    const int s = blockIdx.x * W + wv;
-    const int V = m.V, VP = m.VP, E = m.E, D = m.D, R2 = m.R2;
-
-    // the shared tables, once per workgroup
+__device__ __forceinline__ void load_tables(SharedTables<N, L> &S, const YggDevModel &m, int tid, int nthreads) {
 #pragma unroll
     for (int l = 0; l < L; l++) {
         const uint32_t *src = (const uint32_t *)m.layers[l].Q;
-        uint32_t *dst = (uint32_t *)Qs[l];
-        for (int i = tid; i < VP * R / 4; i += 64 * W) dst[i] = src[i];
+        uint32_t *dst = (uint32_t *)S.Q[l];
+        for (int i = tid; i < m.VP * 8 / 4; i += nthreads) dst[i] = src[i];
     }
 #pragma unroll
     for (int l = 1; l < L; l++) {
         const YggDevLayer &y = m.layers[l];
         const int rows = (1 << m.round_h[0]) - 1;     // the first round's block: slots 0 .. 2^h0 - 2
         const uint32_t *ws = (const uint32_t *)y.w;
-        uint32_t *wd = (uint32_t *)Ws[l - 1];
-        for (int i = tid; i < 15 * N / 4; i += 64 * W) wd[i] = i < rows * N / 4 ? ws[i] : 0u;
-        uint32_t *vd = (uint32_t *)Vs[l - 1];
-        if (R2 > 0) {
+        uint32_t *wd = (uint32_t *)S.W[l - 1];
+        for (int i = tid; i < 15 * N / 4; i += nthreads) wd[i] = i < rows * N / 4 ? ws[i] : 0u;
+        uint32_t *vd = (uint32_t *)S.V[l - 1];
+        if (m.R2 > 0) {
             const uint32_t *vs = (const uint32_t *)y.vl;
-            for (int i = tid; i < 16 * N / 4; i += 64 * W) vd[i] = vs[i];
+            for (int i = tid; i < 16 * N / 4; i += nthreads) vd[i] = vs[i];
         } else {
-            for (int i = tid; i < 16 * N / 4; i += 64 * W) vd[i] = 0u;
+            for (int i = tid; i < 16 * N / 4; i += nthreads) vd[i] = 0u;
         }
     }
+}
+
+// the quad-lane chunk of the state below and rho = 1 / sqrt(mean(q^2) + eps) (cpu/ygg.cpp:248-255)
+template <int N>
+__device__ __forceinline__ float below_and_rho(uint32_t (&qbw)[Fast<N>::QW], const int8_t *qb, float eps, int lane) {
+    using F = Fast<N>;
+    load_words<F::QW, F::QA>(qbw, qb + (lane & 3) * F::Q4);
+    int sg = 0;
+    if (lane < N / 16) {
+        uint32_t g4[4];
+        load_words<4, 16>(g4, qb + 16 * lane);
+#pragma unroll
+        for (int i = 0; i < 4; i++) sg = dot4(g4[i], g4[i], sg);
+    }
+    int S = 0;
+#pragma unroll
+    for (int g = 0; g < N / 16; g++) S += __builtin_amdgcn_readlane(sg, g);
+    return 1.0f / sqrtf((float)S * F::kInvN + eps);
+}
+
+// the router descent (cpu/ygg.cpp:271-280) -> leaf index; the first round from the LDS rows W0 and the thresholds
+// th0 (thr[x][slot qj] of that round, loaded by the caller), the others from global memory
+template <int N>
+__device__ __forceinline__ int descend(const YggDevModel &m, const YggDevLayer &y, const int8_t *W0, float th0,
+                                       const uint32_t (&qbw)[Fast<N>::QW], float rho, int x, int lane) {
+    using F = Fast<N>;
+    const int qk = lane & 3, qj = lane >> 2;
+    const int h1 = m.round_h[0], nn1 = (1 << h1) - 1;
+    int ix;
+    {
+        int dot = 0;
+        if (qj < nn1) {
+            uint32_t wv[F::QW];
+            load_words<F::QW, F::QA>(wv, W0 + qj * N + qk * F::Q4);
+#pragma unroll
+            for (int i = 0; i < F::QW; i++) dot = dot4(wv[i], qbw[i], dot);
+        }
+        dot = sum4(dot);
+        const bool right = (float)dot * rho > th0;
+        const unsigned long long mask = __ballot(right && qk == 0 && qj < nn1);
+        int loc = 0;
+        for (int lev = 0; lev < h1; lev++) loc = 2 * loc + 1 + (int)((mask >> (4 * loc)) & 1ull);
+        ix = (1 << h1) + (loc - nn1);
+    }
+    const float *thr = y.thr + (size_t)x * y.thr_stride;
+    int base = 1 << h1, d0 = h1;
+    for (int rd = 1; rd < m.n_rounds; rd++) {
+        const int h = m.round_h[rd];
+        const int nn = (1 << h) - 1;
+        const int slot = base + ((ix - (1 << d0)) << h) + qj;
+        int dot = 0;
+        float th = 0.0f;
+        if (qj < nn) {
+            uint32_t wv[F::QW];
+            load_words<F::QW, F::QA>(wv, y.w + (size_t)slot * N + qk * F::Q4);
+            th = thr[slot];
+#pragma unroll
+            for (int i = 0; i < F::QW; i++) dot = dot4(wv[i], qbw[i], dot);
+        }
+        dot = sum4(dot);
+        const bool right = (float)dot * rho > th;
+        const unsigned long long mask = __ballot(right && qk == 0 && qj < nn);
+        int loc = 0;
+        for (int lev = 0; lev < h; lev++) loc = 2 * loc + 1 + (int)((mask >> (4 * loc)) & 1ull);
+        base += (1 << d0) << h;
+        d0 += h;
+        ix = (ix << h) + (loc - nn);
+    }
+    return ix - m.E;
+}
+
+// the expert's whole gather record and table row, in one burst
+template <int N>
+__device__ __forceinline__ void gather(Gather<N> &G, const YggDevLayer &y, int r, int x, bool routed, int R2,
+                                       int lane) {
+    using F = Fast<N>;
+    const uint8_t *g = y.gath + (size_t)r * y.gath_bytes;
+    if (lane < F::NL) {
+#pragma unroll
+        for (int c = 0; c < F::NA; c++) {
+            const uint4 v = *(const uint4 *)(g + (c * F::NL + lane) * 16);
+            G.aw[4 * c] = v.x; G.aw[4 * c + 1] = v.y; G.aw[4 * c + 2] = v.z; G.aw[4 * c + 3] = v.w;
+        }
+        if (routed) {
+#pragma unroll
+            for (int k4 = 0; k4 < 4; k4++) {
+                if (k4 < R2 / 4) {
+                    uint32_t tmp[F::C];
+                    load_words<F::C, 4 * F::C>(tmp, g + y.off_U + ((size_t)(k4 * F::NL + lane) * F::C) * 4);
+#pragma unroll
+                    for (int c = 0; c < F::C; c++) G.uw[k4][c] = tmp[c];
+                }
+            }
+        }
+        const int16_t *tr = y.table + (size_t)r * y.table_sr + (size_t)x * y.table_sx + F::C * lane;
+#pragma unroll
+        for (int c = 0; c < F::C; c++) G.trow[c] = tr[c];
+    }
+    const uint8_t *pp = g + y.off_P;
+#pragma unroll
+    for (int gi = 0; gi < F::SP / F::GP; gi++) {
+        uint32_t tmp[F::GP / 4];
+        load_words<F::GP / 4, F::GP>(tmp, pp + (gi * 64 + lane) * F::GP);
+#pragma unroll
+        for (int i = 0; i < F::GP / 4; i++) G.pw[gi * (F::GP / 4) + i] = tmp[i];
+    }
+}
+
+// zl[k] = clamp(rint((f32(V'_k . q_below) m_v[k]) rho), +-127) into LDS (cpu/ygg.cpp:285-296)
+template <int N>
+__device__ __forceinline__ void layer_input(int8_t *zls, const int8_t *V0, const YggDevLayer &y,
+                                            const uint32_t (&qbw)[Fast<N>::QW], float rho, int lane) {
+    using F = Fast<N>;
+    const int qk = lane & 3, qj = lane >> 2;
+    uint32_t vv[F::QW];
+    load_words<F::QW, F::QA>(vv, V0 + qj * N + qk * F::Q4);
+    int a = 0;
+#pragma unroll
+    for (int i = 0; i < F::QW; i++) a = dot4(vv[i], qbw[i], a);
+    a = sum4(a);
+    if (qk == 0) {
+        float zf = (float)a * y.mv[qj];
+        zf = zf * rho;
+        zls[qj] = (int8_t)clamp127(cvt_rne(zf));
+    }
+}
+
+// new state rows of this lane: sat8(((A16 q_old + 2^(s-1)) >> s) + T_r[x] + rint(f32(U'_r zl) m_ul))
+// (cpu/ygg.cpp:311-389); qold is the layer's state before the token (LDS)
+template <int N>
+__device__ __forceinline__ void update(int (&qn)[Fast<N>::C], const Gather<N> &G, const int8_t *qold,
+                                       const int8_t *zls, const YggDevLayer &y, bool routed, int R2, int shift,
+                                       int lane) {
+    using F = Fast<N>;
+    constexpr int BLK = F::BLK, C = F::C;
+    const int blk0 = (C * lane / BLK) * BLK;
+    uint32_t qv[BLK / 4];
+    load_words<BLK / 4, BLK>(qv, qold + blk0);
+    uint32_t qp[BLK / 2];
+#pragma unroll
+    for (int i = 0; i < BLK / 4; i++) { qp[2 * i] = pair16(qv[i], 0); qp[2 * i + 1] = pair16(qv[i], 2); }
+    int acc[C];
+#pragma unroll
+    for (int c = 0; c < C; c++) {
+        int a = 0;
+#pragma unroll
+        for (int p = 0; p < BLK / 2; p++) a = dot2(G.aw[c * (BLK / 2) + p], qp[p], a);
+        acc[c] = wadd((a + (1 << (shift - 1))) >> shift, G.trow[c]);
+    }
+    if (routed && R2 > 0) {
+        int d[C];
+#pragma unroll
+        for (int c = 0; c < C; c++) d[c] = 0;
+#pragma unroll
+        for (int k4 = 0; k4 < 4; k4++) {
+            if (k4 < R2 / 4) {
+                const uint32_t zw = ((const uint32_t *)zls)[k4];
+#pragma unroll
+                for (int c = 0; c < C; c++) d[c] = dot4(G.uw[k4][c], zw, d[c]);
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < C; c++) acc[c] = wadd(acc[c], cvt_rne((float)d[c] * y.layer_input_scale));
+    }
+#pragma unroll
+    for (int c = 0; c < C; c++) qn[c] = sat8(acc[c]);
+}
+
+// zq[j] = clamp(rint(f32(P_r q) m_z), +-127) into LDS (cpu/ygg.cpp:395-420); qnew is the new state (LDS)
+template <int N>
+__device__ __forceinline__ void readout(int8_t *zqs, const Gather<N> &G, const int8_t *qnew, const YggDevLayer &y,
+                                        int lane) {
+    using F = Fast<N>;
+    const int rj = lane / F::RL, rk = lane % F::RL;
+    uint32_t qv[F::SPW];
+    load_words<F::SPW, F::SPA>(qv, qnew + rk * F::SP);
+    int z = 0;
+#pragma unroll
+    for (int i = 0; i < F::SPW; i++) z = dot4(G.pw[i], qv[i], z);
+    z = group_sum<F::RL>(z);
+    if (rk == 0) zqs[rj] = (int8_t)clamp127(cvt_rne((float)z * y.readout_scale));
+}
+
+// f32(Q zq) s_q for the 4 classes of this lane (cpu/ygg.cpp:421-434)
+__device__ __forceinline__ void unembed_terms(float (&term)[4], const int8_t *zqs, const int8_t *Qs, float scale,
+                                              int lane) {
+    uint32_t zw[2];
+    load_words<2, 16>(zw, zqs);
+    uint32_t qq[8];
+    load_words<8, 16>(qq, Qs + 4 * lane * 8);
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        int d = dot4(qq[2 * u], zw[0], 0);
+        d = dot4(qq[2 * u + 1], zw[1], d);
+        term[u] = (float)d * scale;
+    }
+}
+
+template <int N>
+__device__ __forceinline__ unsigned long long digest_term(const int (&qn)[Fast<N>::C], int r, int l, int lane) {
+    using F = Fast<N>;
+    unsigned long long f = 0;
+    if (lane < F::NL) {
+#pragma unroll
+        for (int c = 0; c < F::C; c++)
+            f += (unsigned long long)((uint8_t)qn[c] + 1u) * ((unsigned long long)(2 * (F::C * lane + c) + 1) *
+                                                              kDigestCoord);
+    }
+    f = wave_sum_u64(f);
+    return (unsigned long long)(uint32_t)r * kDigestLeaf + f + (unsigned long long)l;
+}
+
+__device__ __forceinline__ void store_logits(float *o, const float (&lg)[4], int V, int lane) {
+    if ((V & 3) == 0 && 4 * lane + 3 < V) {
+        *(float4 *)(o + 4 * lane) = make_float4(lg[0], lg[1], lg[2], lg[3]);
+    } else {
+#pragma unroll
+        for (int u = 0; u < 4; u++)
+            if (4 * lane + u < V) o[4 * lane + u] = lg[u];
+    }
+}
+
+// ----------------------------------------------------------------------------------------------- fast_kernel
+
+template <int N, int L>
+__global__ __launch_bounds__(64 * kFastWaves) __attribute__((amdgpu_waves_per_eu(4)))
+void fast_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B, int T, int8_t *__restrict__ state,
+                 float *__restrict__ logits, int32_t *__restrict__ leaves, int8_t *__restrict__ states,
+                 unsigned long long *__restrict__ digest) {
+    using F = Fast<N>;
+    constexpr int W = kFastWaves, LR = L > 1 ? L - 1 : 1;
+    __shared__ __attribute__((aligned(16))) SharedTables<N, L> S;
+    __shared__ __attribute__((aligned(16))) int8_t qsw[W][L * N];
+    __shared__ __attribute__((aligned(16))) int8_t zlw[W][16];
+    __shared__ __attribute__((aligned(16))) int8_t zqw[W][16];
+
+    const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63;
+    const int s = blockIdx.x * W + wv;
+    const int V = m.V, VP = m.VP, R2 = m.R2;
+    load_tables<N, L>(S, m, tid, 64 * W);
     __syncthreads();
     if (s >= B) return;
 
     int8_t *qs = qsw[wv];
     int8_t *zls = zlw[wv];
     int8_t *zqs = zqw[wv];
-    const int qk = lane & 3, qj = lane >> 2;
-    const int rj = lane / RL, rk = lane % RL;
+    const int qj = lane >> 2;
+    const int nn1 = (1 << m.round_h[0]) - 1;
 
     int8_t *st = state + (size_t)s * L * N;
     for (int i = lane; i < L * N; i += 64) qs[i] = st[i];
@@ -89,7 +336,6 @@ __global__ __launch_bounds__(64 * kFastWaves) __attribute__((amdgpu_waves_per_eu
     unsigned long long dg = digest ? digest[s] : 0ull;
     const int32_t *tok = tokens + (size_t)s * T;
     int x_next = T > 0 ? tok[0] : 0;
-    const int h1 = m.round_h[0], nn1 = (1 << h1) - 1;
 
     for (int t = 0; t < T; t++) {
         const int x = x_next;
@@ -101,215 +347,52 @@ __global__ __launch_bounds__(64 * kFastWaves) __attribute__((amdgpu_waves_per_eu
         // thresholds of the first router round of every routed layer
         float th1[LR];
 #pragma unroll
-        for (int l = 1; l < L; l++) th1[l - 1] = qj < nn1 ? m.layers[l].thr[(size_t)x * m.layers[l].thr_stride + qj] : 0.0f;
+        for (int l = 1; l < L; l++)
+            th1[l - 1] = qj < nn1 ? m.layers[l].thr[(size_t)x * m.layers[l].thr_stride + qj] : 0.0f;
         float lg[4];
 #pragma unroll
         for (int u = 0; u < 4; u++) lg[u] = 4 * lane + u < VP ? m.output_bias[4 * lane + u] : 0.0f;
 
-#pragma unroll
+        // not unrolled: an unrolled loop keeps every layer's pointers in scalar registers at once and spills them
+#pragma unroll 1
         for (int l = 0; l < L; l++) {
             const YggDevLayer &y = m.layers[l];
             int r = x;
             float rho = 0.0f;
-            uint32_t qbw[QW];
+            uint32_t qbw[F::QW];
             if (l > 0) {
-                const int8_t *qb = qs + (l - 1) * N;
-                load_words<QW, QA>(qbw, qb + qk * Q4);
-                int sg = 0;
-                if (lane < N / 16) {
-                    uint32_t g4[4];
-                    load_words<4, 16>(g4, qb + 16 * lane);
+                float th = th1[0];
 #pragma unroll
-                    for (int i = 0; i < 4; i++) sg = dot4(g4[i], g4[i], sg);
-                }
-                int S = 0;
-#pragma unroll
-                for (int g = 0; g < N / 16; g++) S += __builtin_amdgcn_readlane(sg, g);
-                rho = 1.0f / sqrtf((float)S * kInvN + y.rms_eps);
-                // first router round: nodes 1..15 from LDS, thresholds already loaded
-                int ix = 1;
-                {
-                    int dot = 0;
-                    if (qj < nn1) {
-                        uint32_t wvv[QW];
-                        load_words<QW, QA>(wvv, Ws[l - 1] + qj * N + qk * Q4);
-#pragma unroll
-                        for (int i = 0; i < QW; i++) dot = dot4(wvv[i], qbw[i], dot);
-                    }
-                    dot = sum4(dot);
-                    const bool right = (float)dot * rho > th1[l - 1];
-                    const unsigned long long mask = __ballot(right && qk == 0 && qj < nn1);
-                    int loc = 0;
-                    for (int lev = 0; lev < h1; lev++) loc = 2 * loc + 1 + (int)((mask >> (4 * loc)) & 1ull);
-                    ix = (1 << h1) + (loc - nn1);
-                }
-                const float *thr = y.thr + (size_t)x * y.thr_stride;
-                int base = 1 << h1, d0 = h1;
-                for (int rd = 1; rd < m.n_rounds; rd++) {
-                    const int h = m.round_h[rd];
-                    const int nn = (1 << h) - 1;
-                    const int slot = base + ((ix - (1 << d0)) << h) + qj;
-                    int dot = 0;
-                    float th = 0.0f;
-                    if (qj < nn) {
-                        uint32_t wvv[QW];
-                        load_words<QW, QA>(wvv, y.w + (size_t)slot * N + qk * Q4);
-                        th = thr[slot];
-#pragma unroll
-                        for (int i = 0; i < QW; i++) dot = dot4(wvv[i], qbw[i], dot);
-                    }
-                    dot = sum4(dot);
-                    const bool right = (float)dot * rho > th;
-                    const unsigned long long mask = __ballot(right && qk == 0 && qj < nn);
-                    int loc = 0;
-                    for (int lev = 0; lev < h; lev++) loc = 2 * loc + 1 + (int)((mask >> (4 * loc)) & 1ull);
-                    base += (1 << d0) << h;
-                    d0 += h;
-                    ix = (ix << h) + (loc - nn);
-                }
-                r = ix - E;
+                for (int i = 1; i < LR; i++) th = l - 1 == i ? th1[i] : th;
+                rho = below_and_rho<N>(qbw, qs + (l - 1) * N, y.rms_eps, lane);
+                r = descend<N>(m, y, S.W[l - 1], th, qbw, rho, x, lane);
             }
-
-            // the expert's whole gather record and table row, in one burst
-            const uint8_t *g = y.gath + (size_t)r * y.gath_bytes;
-            uint32_t aw[AW], pw[SPW], uw[4][C];
-            int trow[C];
-            if (lane < NL) {
+            Gather<N> G;
+            gather<N>(G, y, r, x, l > 0, R2, lane);
+            if (l > 0 && R2 > 0) layer_input<N>(zls, S.V[l - 1], y, qbw, rho, lane);
+            wave_sync();
+            int qn[F::C];
+            if (lane < F::NL) update<N>(qn, G, qs + l * N, zls, y, l > 0, R2, m.shift, lane);
+            wave_sync();
+            if (lane < F::NL) {
 #pragma unroll
-                for (int c = 0; c < NA; c++) {
-                    const uint4 v = load16<false>(g + (c * NL + lane) * 16);
-                    aw[4 * c] = v.x; aw[4 * c + 1] = v.y; aw[4 * c + 2] = v.z; aw[4 * c + 3] = v.w;
-                }
-                if (l > 0) {
-#pragma unroll
-                    for (int k4 = 0; k4 < 4; k4++) {
-                        if (k4 < R2 / 4) {
-                            uint32_t tmp[C];
-                            load_words_sel<false, C, 4 * C>(tmp, g + y.off_U + ((size_t)(k4 * NL + lane) * C) * 4);
-#pragma unroll
-                            for (int c = 0; c < C; c++) uw[k4][c] = tmp[c];
-                        }
-                    }
-                }
-                const int16_t *tr = y.table + (size_t)r * y.table_sr + (size_t)x * y.table_sx + C * lane;
-#pragma unroll
-                for (int c = 0; c < C; c++) trow[c] = load_i16<false>(tr + c);
-            }
-            {
-                const uint8_t *pp = g + y.off_P;
-#pragma unroll
-                for (int gi = 0; gi < SP / GP; gi++) {
-                    uint32_t tmp[GP / 4];
-                    load_words_sel<false, GP / 4, GP>(tmp, pp + (gi * 64 + lane) * GP);
-#pragma unroll
-                    for (int i = 0; i < GP / 4; i++) pw[gi * (GP / 4) + i] = tmp[i];
-                }
-            }
-
-            // layer input zl from the LDS copy of V'
-            if (l > 0 && R2 > 0) {
-                uint32_t vv[QW];
-                load_words<QW, QA>(vv, Vs[l - 1] + qj * N + qk * Q4);
-                int a = 0;
-#pragma unroll
-                for (int i = 0; i < QW; i++) a = dot4(vv[i], qbw[i], a);
-                a = sum4(a);
-                if (qk == 0) {
-                    float zf = (float)a * y.mv[qj];
-                    zf = zf * rho;
-                    zls[qj] = (int8_t)clamp127(cvt_rne(zf));
-                }
+                for (int c = 0; c < F::C; c++) qs[l * N + F::C * lane + c] = (int8_t)qn[c];
             }
             wave_sync();
-
-            int qn[C];
-            if (lane < NL) {
-                const int blk0 = (C * lane / BLK) * BLK;
-                uint32_t qv[BLK / 4];
-                load_words<BLK / 4, BLK>(qv, qs + l * N + blk0);
-                uint32_t qp[BLK / 2];
-#pragma unroll
-                for (int i = 0; i < BLK / 4; i++) { qp[2 * i] = pair16(qv[i], 0); qp[2 * i + 1] = pair16(qv[i], 2); }
-                int acc[C];
-#pragma unroll
-                for (int c = 0; c < C; c++) {
-                    int a = 0;
-#pragma unroll
-                    for (int p = 0; p < BLK / 2; p++) a = dot2(aw[c * (BLK / 2) + p], qp[p], a);
-                    acc[c] = wadd((a + (1 << (m.shift - 1))) >> m.shift, trow[c]);
-                }
-                if (l > 0 && R2 > 0) {
-                    int d[C];
-#pragma unroll
-                    for (int c = 0; c < C; c++) d[c] = 0;
-#pragma unroll
-                    for (int k4 = 0; k4 < 4; k4++) {
-                        if (k4 < R2 / 4) {
-                            const uint32_t zw = ((const uint32_t *)zls)[k4];
-#pragma unroll
-                            for (int c = 0; c < C; c++) d[c] = dot4(uw[k4][c], zw, d[c]);
-                        }
-                    }
-#pragma unroll
-                    for (int c = 0; c < C; c++) acc[c] = wadd(acc[c], cvt_rne((float)d[c] * y.layer_input_scale));
-                }
-#pragma unroll
-                for (int c = 0; c < C; c++) qn[c] = sat8(acc[c]);
-            }
-            wave_sync();
-            if (lane < NL) {
-#pragma unroll
-                for (int c = 0; c < C; c++) qs[l * N + C * lane + c] = (int8_t)qn[c];
-            }
-            wave_sync();
-
-            {
-                uint32_t qv[SPW];
-                load_words<SPW, (SP % 16 == 0 ? 16 : (SP % 8 == 0 ? 8 : 4))>(qv, qs + l * N + rk * SP);
-                int z = 0;
-#pragma unroll
-                for (int i = 0; i < SPW; i++) z = dot4(pw[i], qv[i], z);
-                z = group_sum<RL>(z);
-                if (rk == 0) zqs[rj] = (int8_t)clamp127(cvt_rne((float)z * y.readout_scale));
-            }
+            readout<N>(zqs, G, qs + l * N, y, lane);
             wave_sync();
             if (4 * lane < VP) {
-                uint32_t zw[2];
-                load_words<2, 16>(zw, zqs);
-                uint32_t qq[8];
-                load_words<8, 16>(qq, Qs[l] + 4 * lane * R);
+                float term[4];
+                unembed_terms(term, zqs, S.Q[l], y.unembed_scale, lane);
 #pragma unroll
-                for (int u = 0; u < 4; u++) {
-                    int d = dot4(qq[2 * u], zw[0], 0);
-                    d = dot4(qq[2 * u + 1], zw[1], d);
-                    lg[u] = lg[u] + (float)d * y.unembed_scale;
-                }
+                for (int u = 0; u < 4; u++) lg[u] = lg[u] + term[u];
             }
             if (leaves && lane == 0) leaves[((size_t)s * T + t) * L + l] = r;
-            if (digest) {
-                unsigned long long f = 0;
-                if (lane < NL) {
-#pragma unroll
-                    for (int c = 0; c < C; c++)
-                        f += (unsigned long long)((uint8_t)qn[c] + 1u) *
-                             ((unsigned long long)(2 * (C * lane + c) + 1) * kDigestCoord);
-                }
-                f = wave_sum_u64(f);
-                dg = dg * kDigestMul + ((unsigned long long)(uint32_t)r * kDigestLeaf + f + (unsigned long long)l);
-            }
+            if (digest) dg = dg * kDigestMul + digest_term<N>(qn, r, l, lane);
             wave_sync();
         }
 
-        if (logits) {
-            float *o = logits + ((size_t)s * T + t) * V;
-            if ((V & 3) == 0 && 4 * lane + 3 < V) {
-                *(float4 *)(o + 4 * lane) = make_float4(lg[0], lg[1], lg[2], lg[3]);
-            } else {
-#pragma unroll
-                for (int u = 0; u < 4; u++)
-                    if (4 * lane + u < V) o[4 * lane + u] = lg[u];
-            }
-        }
+        if (logits) store_logits(logits + ((size_t)s * T + t) * V, lg, V, lane);
         if (states) {
             int8_t *so = states + ((size_t)s * T + t) * L * N;
             for (int i = lane; i < L * N; i += 64) so[i] = qs[i];
@@ -318,6 +401,128 @@ __global__ __launch_bounds__(64 * kFastWaves) __attribute__((amdgpu_waves_per_eu
     wave_sync();
     for (int i = lane; i < L * N; i += 64) st[i] = qs[i];
     if (digest && lane == 0) digest[s] = dg;
+}
+
+// ----------------------------------------------------------------------------------------------- pipe_kernel
+
+template <int N, int L>
+__global__ __launch_bounds__(64 * L) __attribute__((amdgpu_waves_per_eu(4))) void pipe_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
+                                                      int T, int8_t *__restrict__ state, float *__restrict__ logits,
+                                                      int32_t *__restrict__ leaves, int8_t *__restrict__ states,
+                                                      unsigned long long *__restrict__ digest) {
+    using F = Fast<N>;
+    __shared__ __attribute__((aligned(16))) SharedTables<N, L> S;
+    __shared__ __attribute__((aligned(16))) int8_t qbuf[L][2][N];            // layer l after token t: [l][t & 1]
+    __shared__ __attribute__((aligned(16))) float lgs[L][256];               // logits of token t: row t % L
+    __shared__ __attribute__((aligned(16))) unsigned long long dterm[L][L];  // digest terms of token t: row t % L
+    __shared__ __attribute__((aligned(16))) int8_t zlw[L][16];
+    __shared__ __attribute__((aligned(16))) int8_t zqw[L][16];
+    __shared__ int stop_t;                                                   // first token out of range
+
+    const int tid = threadIdx.x, l = tid >> 6, lane = tid & 63;
+    const int s = blockIdx.x;
+    const int V = m.V, VP = m.VP, R2 = m.R2;
+    load_tables<N, L>(S, m, tid, 64 * L);
+    const YggDevLayer &y = m.layers[l];
+    int8_t *st = state + ((size_t)s * L + l) * N;
+    for (int i = lane; i < N; i += 64) qbuf[l][1][i] = st[i];     // the state before token 0
+    if (lane < 16) zlw[l][lane] = 0;
+    if (tid == 0) stop_t = T;
+    __syncthreads();
+
+    const int32_t *tok = tokens + (size_t)s * T;
+    const int qj = lane >> 2;
+    const int nn1 = (1 << m.round_h[0]) - 1;
+    unsigned long long dg = (digest && l == L - 1) ? digest[s] : 0ull;
+    // loaded a tick ahead: the first-round thresholds (routed layers) or the gather record (token layer)
+    float th0 = 0.0f;
+    Gather<N> G0;
+    if (T > 0) {
+        const int x0 = tok[0];
+        if (x0 >= 0 && x0 < V) {
+            if (l > 0 && qj < nn1) th0 = y.thr[(size_t)x0 * y.thr_stride + qj];
+            if (l == 0) gather<N>(G0, y, x0, x0, false, R2, lane);
+        }
+    }
+
+    for (int k = 0; k < T + L - 1; k++) {
+        const int t = k - l;
+        if (t >= 0 && t < T && t < stop_t) {
+            const int x = tok[t];
+            const bool ok = x >= 0 && x < V;
+            if (l == 0 && !ok && lane == 0) {
+                atomicOr(m.err, 1u);
+                stop_t = t;
+            }
+            if (ok) {
+                int r = x;
+                float rho = 0.0f;
+                uint32_t qbw[F::QW];
+                Gather<N> G;
+                if (l > 0) {
+                    rho = below_and_rho<N>(qbw, qbuf[l - 1][t & 1], y.rms_eps, lane);
+                    r = descend<N>(m, y, S.W[l - 1], th0, qbw, rho, x, lane);
+                    gather<N>(G, y, r, x, true, R2, lane);
+                    if (R2 > 0) layer_input<N>(zlw[l], S.V[l - 1], y, qbw, rho, lane);
+                } else {
+                    G = G0;
+                }
+                if (t + 1 < T) {
+                    const int xn = tok[t + 1];
+                    if (xn >= 0 && xn < V) {
+                        if (l > 0 && qj < nn1) th0 = y.thr[(size_t)xn * y.thr_stride + qj];
+                        if (l == 0) gather<N>(G0, y, xn, xn, false, R2, lane);
+                    }
+                }
+                wave_sync();
+                int qn[F::C];
+                if (lane < F::NL) {
+                    update<N>(qn, G, qbuf[l][(t + 1) & 1], zlw[l], y, l > 0, R2, m.shift, lane);
+#pragma unroll
+                    for (int c = 0; c < F::C; c++) qbuf[l][t & 1][F::C * lane + c] = (int8_t)qn[c];
+                }
+                wave_sync();
+                readout<N>(zqw[l], G, qbuf[l][t & 1], y, lane);
+                wave_sync();
+                float *lr = lgs[t % L];
+                if (4 * lane < VP) {
+                    float term[4];
+                    unembed_terms(term, zqw[l], S.Q[l], y.unembed_scale, lane);
+#pragma unroll
+                    for (int u = 0; u < 4; u++) {
+                        const float base = l == 0 ? m.output_bias[4 * lane + u] : lr[4 * lane + u];
+                        lr[4 * lane + u] = base + term[u];
+                    }
+                }
+                if (leaves && lane == 0) leaves[((size_t)s * T + t) * L + l] = r;
+                if (states) {
+                    int8_t *so = states + (((size_t)s * T + t) * L + l) * N;
+                    for (int i = lane; i < N; i += 64) so[i] = qbuf[l][t & 1][i];
+                }
+                if (digest) {
+                    const unsigned long long f = digest_term<N>(qn, r, l, lane);
+                    if (lane == 0) dterm[t % L][l] = f;
+                }
+                if (l == L - 1) {
+                    wave_sync();
+                    if (logits) {
+                        float lg[4];
+#pragma unroll
+                        for (int u = 0; u < 4; u++) lg[u] = 4 * lane + u < VP ? lr[4 * lane + u] : 0.0f;
+                        store_logits(logits + ((size_t)s * T + t) * V, lg, V, lane);
+                    }
+                    if (digest) {
+#pragma unroll
+                        for (int j = 0; j < L; j++) dg = dg * kDigestMul + dterm[t % L][j];
+                    }
+                }
+            }
+        }
+        __syncthreads();
+    }
+    const int te = T < stop_t ? T : stop_t;                          // tokens processed
+    for (int i = lane; i < N; i += 64) st[i] = qbuf[l][(te + 1) & 1][i];
+    if (digest && l == L - 1 && lane == 0) digest[s] = dg;
 }
 
 }  // namespace ygg

@@ -33,6 +33,26 @@ hipError_t launch_fast(const YggDevModel &m, const int32_t *tokens, int B, int T
     if (L == 1) return launch_fast<N, 1>; if (L == 2) return launch_fast<N, 2>; \
     if (L == 3) return launch_fast<N, 3>; if (L == 4) return launch_fast<N, 4>;
 
+template <int N, int L>
+hipError_t launch_pipe(const YggDevModel &m, const int32_t *tokens, int B, int T, int8_t *state, float *logits,
+                       int32_t *leaves, int8_t *states, unsigned long long *digest, hipStream_t stream) {
+    hipLaunchKernelGGL((pipe_kernel<N, L>), dim3(B), dim3(64 * L), 0, stream, m, tokens, B, T, state, logits, leaves,
+                       states, digest);
+    return hipGetLastError();
+}
+
+#define YGG_P(N) \
+    if (L == 1) return launch_pipe<N, 1>; if (L == 2) return launch_pipe<N, 2>; \
+    if (L == 3) return launch_pipe<N, 3>; if (L == 4) return launch_pipe<N, 4>;
+
+// the layer-pipelined kernel for few streams (same shapes as the specialised one)
+Launcher find_pipe_launcher(int n, int L) {
+    if (n == 64) { YGG_P(64) }
+    if (n == 96) { YGG_P(96) }
+    if (n == 128) { YGG_P(128) }
+    return nullptr;
+}
+
 // the specialised kernel: readout rank 8, block 16, layer-input rank <= 16, table storage, tensor scales, L <= 4
 Launcher find_fast_launcher(int n, int L) {
     if (n == 64) { YGG_L(64) }
