@@ -239,3 +239,19 @@ def test_graph_replay(hip, c12):
         _ = torch.randn(1000, device=eager.device).sum()   # eager work between replays
         torch.cuda.synchronize()
         assert torch.equal(le, lgr) and torch.equal(se, sg), t
+
+
+def test_unsplittable_transition_uses_general_kernel(hip, model_dir, monkeypatch):
+    """A transition entry above 32639 has no signed-byte split (A16 = 256 hi + lo); such a model runs on the general
+    kernel, still exactly."""
+    monkeypatch.delenv("YGG_KERNEL", raising=False)
+    spec = synth.ModelSpec(64, 16, 5, 27, 3)
+    layers = synth.random_layers(spec, 4)
+    layers[1].transition[3, 0, 2, 5] = 32700
+    path = model_dir / "unsplit.bin"
+    from yggdrasil_amd import fmt
+    fmt.write(layers, synth.output_bias(spec.vocab), path)
+    model = hip.load(path)
+    assert model.info.kernel == 0 and model.info.pipe_max_streams == 0
+    x = synth.uniform_tokens(spec.vocab, 6, 32, 1)
+    _compare(_gpu_run(model, x), Oracle(path).run(x, states=True))

@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <climits>
 #include <cstdarg>
 #include <cstdio>
@@ -263,8 +264,40 @@ void block_rows(const uint8_t *w, int n, const RoundPlan &p, int8_t *out) {
     });
 }
 
-// File record of one expert -> its gather record (layout in ygg_layout.h).
-void relayout_expert(const FileArrays &fa, const FileLayer &fy, const GatherLayout &gl, bool routed,
+template <class F> void parallel_for(int64_t count, F f) {
+    int nt = (int)std::min<int64_t>(std::max(1u, std::thread::hardware_concurrency()), 16);
+    if (count < 256) nt = 1;
+    std::vector<std::thread> th;
+    for (int k = 0; k < nt; k++)
+        th.emplace_back([=]() {
+            for (int64_t i = count * k / nt; i < count * (k + 1) / nt; i++) f(i);
+        });
+    for (auto &t : th) t.join();
+}
+
+// A16 = 256 hi + lo with hi, lo signed bytes: lo = ((v + 128) mod 256) - 128, hi = (v - lo) / 256; it exists for
+// every v <= 32639
+inline int8_t split_lo(int v) { return (int8_t)(((v + 128) & 255) - 128); }
+inline int8_t split_hi(int v) { return (int8_t)((v - split_lo(v)) / 256); }
+
+// Does every transition entry of every layer split into signed bytes (the specialised kernels need it)?
+bool transitions_split(const FileArrays &fa, const std::vector<FileLayer> &fl) {
+    std::atomic<bool> ok{true};
+    const int n = fa.n, blk = fa.blk;
+    for (size_t l = 0; l < fl.size() && ok; l++) {
+        const FileLayer &y = fl[l];
+        const int64_t E = l == 0 ? fa.V : ((int64_t)1 << fa.D);
+        parallel_for(E, [&](int64_t e) {
+            const uint8_t *A = y.rec + e * y.record_bytes + y.off_A;
+            for (int64_t k = 0; k < (int64_t)n * blk; k++)
+                if (rd16(A + 2 * k) > 32639) { ok = false; return; }
+        });
+    }
+    return ok;
+}
+
+// File record of one expert -> its gather record (layout in ygg_layout.h). split: A16 rows as hi bytes then lo bytes.
+void relayout_expert(const FileArrays &fa, const FileLayer &fy, const GatherLayout &gl, bool routed, bool split,
                      const uint8_t *frec, uint8_t *g) {
     const int n = fa.n, blk = fa.blk, R = fa.R, R2 = fa.R2, K = fa.K;
     const int C = lanes_c(n), NL = n / C;
@@ -275,8 +308,14 @@ void relayout_expert(const FileArrays &fa, const FileLayer &fy, const GatherLayo
             const int i = C * l + c, g16 = i / 16, rr = i % 16;
             for (int j = 0; j < blk; j++) {
                 const int16_t v = rd16(A + (((size_t)(g16 * (blk / 2) + j / 2) * 16 + rr) * 2 + (j & 1)) * 2);
-                const int byte = (c * blk + j) * 2, chunk = byte / 16, within = byte % 16;
-                memcpy(g + ((size_t)chunk * NL + l) * 16 + within, &v, 2);
+                if (split) {
+                    const int hb = c * 2 * blk + j, lb = hb + blk;
+                    g[((size_t)(hb / 16) * NL + l) * 16 + hb % 16] = (uint8_t)split_hi(v);
+                    g[((size_t)(lb / 16) * NL + l) * 16 + lb % 16] = (uint8_t)split_lo(v);
+                } else {
+                    const int byte = (c * blk + j) * 2, chunk = byte / 16, within = byte % 16;
+                    memcpy(g + ((size_t)chunk * NL + l) * 16 + within, &v, 2);
+                }
             }
         }
     // P: lane l -> row j = l / RL, coordinates [(l % RL) SP, +SP); file R = 8: [n/8][16][4], R >= 16: [R/16][n/4][16][4]
@@ -311,16 +350,6 @@ void relayout_expert(const FileArrays &fa, const FileLayer &fy, const GatherLayo
     }
 }
 
-template <class F> void parallel_for(int64_t count, F f) {
-    int nt = (int)std::min<int64_t>(std::max(1u, std::thread::hardware_concurrency()), 16);
-    if (count < 256) nt = 1;
-    std::vector<std::thread> th;
-    for (int k = 0; k < nt; k++)
-        th.emplace_back([=]() {
-            for (int64_t i = count * k / nt; i < count * (k + 1) / nt; i++) f(i);
-        });
-    for (auto &t : th) t.join();
-}
 
 }  // namespace
 
@@ -362,7 +391,8 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     const char *kenv = getenv("YGG_KERNEL");
     const std::string kmode = kenv ? kenv : "";
     ygg::Launcher fast = nullptr, pipe = nullptr;
-    if (kmode != "generic" && R == 8 && fa.blk == 16 && R2 <= 16 && !factored && !group && L <= 4 && VP <= 256) {
+    if (kmode != "generic" && R == 8 && fa.blk == 16 && R2 <= 16 && !factored && !group && L <= 4 && VP <= 256 &&
+        transitions_split(fa, fl)) {
         fast = ygg::find_fast_launcher(n, L);
         if (kmode != "fast") pipe = ygg::find_pipe_launcher(n, L);
     }
@@ -420,8 +450,9 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
         const int El = routed ? E : V;
         uint8_t *gath = H + p.gath.off;
         const GatherLayout gl = p.gl;
-        parallel_for(El, [&, gath, gl, routed](int64_t e) {
-            relayout_expert(fa, y, gl, routed, y.rec + e * y.record_bytes, gath + e * gl.bytes);
+        const bool split = fast != nullptr;
+        parallel_for(El, [&, gath, gl, routed, split](int64_t e) {
+            relayout_expert(fa, y, gl, routed, split, y.rec + e * y.record_bytes, gath + e * gl.bytes);
         });
         if (!y.vt) {
             int16_t *tb = (int16_t *)(H + p.table.off);

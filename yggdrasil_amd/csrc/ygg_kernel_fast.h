@@ -87,16 +87,11 @@ template <int N>
 __device__ __forceinline__ float below_and_rho(uint32_t (&qbw)[Fast<N>::QW], const int8_t *qb, float eps, int lane) {
     using F = Fast<N>;
     load_words<F::QW, F::QA>(qbw, qb + (lane & 3) * F::Q4);
-    int sg = 0;
-    if (lane < N / 16) {
-        uint32_t g4[4];
-        load_words<4, 16>(g4, qb + 16 * lane);
-#pragma unroll
-        for (int i = 0; i < 4; i++) sg = dot4(g4[i], g4[i], sg);
-    }
+    // the 4 lanes of every quad hold the whole state between them: exact sum of squares by a quad sum
     int S = 0;
 #pragma unroll
-    for (int g = 0; g < N / 16; g++) S += __builtin_amdgcn_readlane(sg, g);
+    for (int i = 0; i < F::QW; i++) S = dot4(qbw[i], qbw[i], S);
+    S = sum4(S);
     return 1.0f / sqrtf((float)S * F::kInvN + eps);
 }
 
@@ -208,25 +203,26 @@ __device__ __forceinline__ void layer_input(int8_t *zls, const int8_t *V0, const
 }
 
 // new state rows of this lane: sat8(((A16 q_old + 2^(s-1)) >> s) + T_r[x] + rint(f32(U'_r zl) m_ul))
-// (cpu/ygg.cpp:311-389); qold is the layer's state before the token (LDS)
+// (cpu/ygg.cpp:311-389); qold is the layer's state before the token (LDS). A row is stored as hi and lo signed bytes
+// with A16 = 256 hi + lo, so A16 q = 256 (hi q) + (lo q) exactly, two v_dot4 chains on the raw int8 state.
 template <int N>
 __device__ __forceinline__ void update(int (&qn)[Fast<N>::C], const Gather<N> &G, const int8_t *qold,
                                        const int8_t *zls, const YggDevLayer &y, bool routed, int R2, int shift,
                                        int lane) {
     using F = Fast<N>;
-    constexpr int BLK = F::BLK, C = F::C;
+    constexpr int BLK = F::BLK, C = F::C, RW = BLK / 4;     // dwords of one row's hi (and of its lo) bytes
     const int blk0 = (C * lane / BLK) * BLK;
-    uint32_t qv[BLK / 4];
-    load_words<BLK / 4, BLK>(qv, qold + blk0);
-    uint32_t qp[BLK / 2];
-#pragma unroll
-    for (int i = 0; i < BLK / 4; i++) { qp[2 * i] = pair16(qv[i], 0); qp[2 * i + 1] = pair16(qv[i], 2); }
+    uint32_t qv[RW];
+    load_words<RW, BLK>(qv, qold + blk0);
     int acc[C];
 #pragma unroll
     for (int c = 0; c < C; c++) {
         int a = 0;
 #pragma unroll
-        for (int p = 0; p < BLK / 2; p++) a = dot2(G.aw[c * (BLK / 2) + p], qp[p], a);
+        for (int i = 0; i < RW; i++) a = dot4(G.aw[c * 2 * RW + i], qv[i], a);
+        a <<= 8;
+#pragma unroll
+        for (int i = 0; i < RW; i++) a = dot4(G.aw[c * 2 * RW + RW + i], qv[i], a);
         acc[c] = wadd((a + (1 << (shift - 1))) >> shift, G.trow[c]);
     }
     if (routed && R2 > 0) {

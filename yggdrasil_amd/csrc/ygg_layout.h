@@ -18,7 +18,9 @@
 //
 // Gather record of one expert (gath_bytes, a multiple of 128):
 //   A   at 0:      16-byte chunks, chunk c of lane l at (c NL + l) 16. A lane's bytes are its C rows in order, each
-//                  row the b int16 of that row inside its diagonal block (columns in block order).
+//                  row the b int16 of that row inside its diagonal block (columns in block order). Models run by
+//                  the specialised kernels (ygg_kernel_fast.h) store each row instead as b signed bytes hi followed
+//                  by b signed bytes lo with A16 = 256 hi + lo, so the transition is two v_dot4 on the int8 state.
 //   P   at off_P:  granules of GP bytes (16, 8 or 4: the largest dividing SP), granule g of lane l at
 //                  off_P + (g 64 + l) GP. A lane's bytes are P[j][i] (s8) for its row j and coordinates i in order.
 //   U'  at off_U:  for k4 < R2/4: lane l's C dwords at off_U + ((k4 NL + l) C + c) 4; dword c holds
