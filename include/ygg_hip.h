@@ -86,8 +86,16 @@ int ygg_step(const ygg_model *m, const int32_t *d_tokens, const int8_t *d_state_
 int ygg_run(const ygg_model *m, const int32_t *d_tokens, int B, int T, int8_t *d_state, float *d_logits,
             int32_t *d_leaves, int8_t *d_states, uint64_t *d_digest, void *stream);
 
+/* Score T tokens of each of B streams without writing logits: the reference's `ygg score` (cpu/ygg.cpp:500-519) for
+   B streams at once. Per token, in double: mx = max_c lg[c], se = sum_c exp(lg[c] - mx), and
+   d_nll[b] += log(se) + mx - lg[target] (cpu/ygg.cpp:514-516; se is summed as a tree over classes, not in class
+   order). d_tokens, d_targets (B, T) int32; d_state (B, L, n) int8 in and out; d_nll (B) double in and out. A
+   target outside [0, vocab) adds nothing and sets bit 1 of the error word. */
+int ygg_score(const ygg_model *m, const int32_t *d_tokens, const int32_t *d_targets, int B, int T, int8_t *d_state,
+              double *d_nll, void *stream);
+
 /* Wait for `stream`, then return and clear the model's error word: bit 0 set when a kernel met a token outside
-   [0, vocab) since the last call. */
+   [0, vocab), bit 1 when ygg_score met a target outside it, since the last call. */
 int ygg_take_errors(const ygg_model *m, void *stream, uint32_t *errors);
 
 /* Message of the last failed call on this thread ("" if none). */

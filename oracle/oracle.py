@@ -162,3 +162,28 @@ def ref_time(model_path, tokens_1d: np.ndarray, seg: int = 2000, warm: int = 100
         if cpu is not None:
             cmd = ["taskset", "-c", str(cpu)] + cmd
         return subprocess.run(cmd, check=True, capture_output=True, text=True).stdout.strip()
+
+
+def ref_score(model_path, x: np.ndarray, y: np.ndarray) -> float:
+    """`ygg score` of the reference kernel (cpu/ygg.cpp:500-519): bits per token of targets y given inputs x (B, T),
+    zero state per row, as the printed bpc (6 decimals)."""
+    x = np.ascontiguousarray(x, np.int32)
+    y = np.ascontiguousarray(y, np.int32)
+    B, T = x.shape
+    with tempfile.TemporaryDirectory() as tmp:
+        xf, yf = os.path.join(tmp, "x.i32"), os.path.join(tmp, "y.i32")
+        x.tofile(xf)
+        y.tofile(yf)
+        out = subprocess.run([str(REF_YGG), "score", str(model_path), xf, yf, str(B), str(T)], check=True,
+                             capture_output=True, text=True).stdout
+    return float(out.split("bpc=")[1].split()[0])
+
+
+def nll_bits(logits: np.ndarray, targets: np.ndarray) -> np.ndarray:
+    """Bits per row of targets (B, T) under logits (B, T, V), the formula of the reference's score mode
+    (cpu/ygg.cpp:514-516) in float64: log(sum exp(lg - max)) + max - lg[y]."""
+    lg = logits.astype(np.float64)
+    mx = lg.max(-1)
+    se = np.exp(lg - mx[..., None]).sum(-1)
+    ly = np.take_along_axis(lg, targets[..., None].astype(np.int64), -1)[..., 0]
+    return (np.log(se) + mx - ly).sum(-1) / np.log(2.0)

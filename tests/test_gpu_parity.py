@@ -255,3 +255,44 @@ def test_unsplittable_transition_uses_general_kernel(hip, model_dir, monkeypatch
     assert model.info.kernel == 0 and model.info.pipe_max_streams == 0
     x = synth.uniform_tokens(spec.vocab, 6, 32, 1)
     _compare(_gpu_run(model, x), Oracle(path).run(x, states=True))
+
+
+def test_score_fused(hip, model_dir, kernel_env):
+    """score(): the fused float64 negative log-likelihood equals the reference formula on the oracle's logits (to
+    float64 rounding of a differently ordered sum) and the reference kernel's own `ygg score` bits per token."""
+    from oracle import oracle as O
+    spec = synth.ModelSpec(128, 16, 10, 256, 4, router="gauss")
+    path = model_dir / "c4small_gauss.bin"
+    if not path.exists():
+        synth.write_model(spec, 11, path)
+    w = synth.zipf_bytes(24, 65, 8)
+    model = hip.load(path)
+    _expect_kernel(model, kernel_env)
+    bits = model.score(w)
+    ref = O.Oracle(path).run(w[:, :-1])
+    want = O.nll_bits(ref["logits"], w[:, 1:])
+    np.testing.assert_allclose(bits, want, rtol=1e-12, atol=1e-9)
+    if O.have_ref():
+        bpc = O.ref_score(path, w[:, :-1], w[:, 1:])
+        assert abs(bits.sum() / w[:, 1:].size - bpc) < 1e-6, (bits.sum() / w[:, 1:].size, bpc)
+    # carried state: two halves scored from the state after the first equal the whole
+    import torch
+    first = model.run(w[:, :32], logits=False)
+    part = model.score(w[:, 32:], state=first["state"])
+    np.testing.assert_allclose(O.nll_bits(ref["logits"][:, 32:], w[:, 33:]), part, rtol=1e-12, atol=1e-9)
+    torch.cuda.synchronize()
+
+
+def test_score_bad_target(hip, c12):
+    import torch
+    from yggdrasil_amd import _lib
+    model = hip.load(c12)
+    x = torch.as_tensor(synth.CONFIGS[2].make_tokens(2, 5), device=model.device).contiguous()
+    y = x.clone()
+    y[0, 2] = 300
+    st = model.init_state(2)
+    nll = torch.zeros(2, dtype=torch.float64, device=model.device)
+    p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    _lib.check(_lib.lib().ygg_score(model._h, p(x), p(y), 2, 5, p(st), p(nll),
+                                    ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)))
+    assert model.take_errors() == 2

@@ -262,3 +262,16 @@ def test_errors(tmp_path):
         O.Oracle(p)
     with pytest.raises(O.OracleError, match="out of range"):
         O.Oracle(good).run(np.array([[0, spec.vocab]], np.int32))
+
+
+@pytest.mark.skipif(not O.have_ref(), reason="reference kernel not built in oracle/_ref")
+def test_score_formula_matches_reference(tmp_path):
+    """nll_bits (the oracle's float64 score formula) on the oracle's logits against the reference kernel's own
+    `ygg score` (cpu/ygg.cpp:500-519), which prints bits per token to 6 decimals."""
+    spec = synth.KERNEL_CASES[0]
+    path = tmp_path / "m.bin"
+    synth.write_model(spec, 3, path)
+    w = synth.uniform_tokens(spec.vocab, 6, 41, 4)
+    lg = O.Oracle(path).run(w[:, :-1])["logits"]
+    bits = O.nll_bits(lg, w[:, 1:])
+    assert abs(bits.sum() / w[:, 1:].size - O.ref_score(path, w[:, :-1], w[:, 1:])) < 1e-6

@@ -14,11 +14,11 @@ import torch  # noqa: F401  (must precede the CDLL below, see the module docstri
 LIB_PATH = Path(__file__).resolve().parent / "libygg_hip.so"
 
 # every entry point of include/ygg_hip.h
-SYMBOLS = ("ygg_load", "ygg_load_blob", "ygg_model_info", "ygg_free", "ygg_step", "ygg_run", "ygg_take_errors",
-           "ygg_last_error", "ygg_version")
+SYMBOLS = ("ygg_load", "ygg_load_blob", "ygg_model_info", "ygg_free", "ygg_step", "ygg_run", "ygg_score",
+           "ygg_take_errors", "ygg_last_error", "ygg_version")
 
 ERRORS = {1: "io", 2: "format", 3: "limits", 4: "nomem", 5: "arg", 6: "token", 7: "device"}
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 
 class YggInfo(ctypes.Structure):
@@ -57,6 +57,7 @@ def lib() -> ctypes.CDLL:
     L.ygg_free.restype = None
     L.ygg_step.argtypes = [vp, vp, vp, vp, vp, vp, i32, vp]
     L.ygg_run.argtypes = [vp, vp, i32, i32, vp, vp, vp, vp, vp, vp]
+    L.ygg_score.argtypes = [vp, vp, vp, i32, i32, vp, vp, vp]
     L.ygg_take_errors.argtypes = [vp, vp, ctypes.POINTER(ctypes.c_uint32)]
     L.ygg_last_error.argtypes = []
     L.ygg_last_error.restype = ctypes.c_char_p

@@ -20,7 +20,7 @@
 namespace ygg {
 // kernel launchers, one per (d_state, block, readout rank); defined in ygg_kernels_*.hip
 typedef hipError_t (*Launcher)(const YggDevModel &, const int32_t *, int, int, int8_t *, float *, int32_t *, int8_t *,
-                               unsigned long long *, hipStream_t);
+                               unsigned long long *, const int32_t *, double *, hipStream_t);
 Launcher find_launcher(int n, int blk, int R);
 Launcher find_fast_launcher(int n, int L);
 Launcher find_pipe_launcher(int n, int L);
@@ -589,7 +589,7 @@ struct DeviceGuard {
 
 extern "C" {
 
-int ygg_version(void) { return 3; }
+int ygg_version(void) { return 4; }
 
 const char *ygg_last_error(void) { return g_err.c_str(); }
 
@@ -652,7 +652,21 @@ int ygg_run(const ygg_model *m, const int32_t *d_tokens, int B, int T, int8_t *d
     HIP_TRY(g.set(m->device));
     // the pipelined kernel overlaps the layers of consecutive tokens, so it needs more than one token per launch
     ygg::Launcher k = (m->launch_pipe && B <= m->pipe_max_streams && T > 1) ? m->launch_pipe : m->launch;
-    HIP_TRY(k(m->dev, d_tokens, B, T, d_state, d_logits, d_leaves, d_states, (unsigned long long *)d_digest,
+    HIP_TRY(k(m->dev, d_tokens, B, T, d_state, d_logits, d_leaves, d_states, (unsigned long long *)d_digest, nullptr,
+              nullptr, (hipStream_t)stream));
+    return YGG_OK;
+}
+
+int ygg_score(const ygg_model *m, const int32_t *d_tokens, const int32_t *d_targets, int B, int T, int8_t *d_state,
+              double *d_nll, void *stream) {
+    if (!m) return fail(YGG_ERR_ARG, "model is NULL");
+    if (B < 0 || T < 0) return fail(YGG_ERR_ARG, "negative B (%d) or T (%d)", B, T);
+    if (B == 0) return YGG_OK;
+    if (!d_state || !d_nll || (T > 0 && (!d_tokens || !d_targets))) return fail(YGG_ERR_ARG, "NULL buffer");
+    DeviceGuard g;
+    HIP_TRY(g.set(m->device));
+    ygg::Launcher k = (m->launch_pipe && B <= m->pipe_max_streams && T > 1) ? m->launch_pipe : m->launch;
+    HIP_TRY(k(m->dev, d_tokens, B, T, d_state, nullptr, nullptr, nullptr, nullptr, d_targets, d_nll,
               (hipStream_t)stream));
     return YGG_OK;
 }
@@ -670,7 +684,8 @@ int ygg_step(const ygg_model *m, const int32_t *d_tokens, const int8_t *d_state_
                                (hipStream_t)stream));
     // one token: the per-stream kernel (a one-token launch cannot overlap layers), or the pipelined one when forced
     ygg::Launcher k = (m->launch_pipe && m->pipe_max_streams == INT32_MAX) ? m->launch_pipe : m->launch;
-    HIP_TRY(k(m->dev, d_tokens, B, 1, d_state_out, d_logits, d_leaves, nullptr, nullptr, (hipStream_t)stream));
+    HIP_TRY(k(m->dev, d_tokens, B, 1, d_state_out, d_logits, d_leaves, nullptr, nullptr, nullptr, nullptr,
+              (hipStream_t)stream));
     return YGG_OK;
 }
 

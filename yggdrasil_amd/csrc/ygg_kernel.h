@@ -53,6 +53,37 @@ __device__ __forceinline__ unsigned long long wave_sum_u64(unsigned long long v)
     return v;
 }
 
+__device__ __forceinline__ float wave_max_f32(float v) {
+    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+__device__ __forceinline__ double wave_sum_f64(double v) {
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+// -log softmax(lg)[y] in double, the reference's score mode (cpu/ygg.cpp:514-516): mx = max_c lg[c],
+// se = sum_c exp(lg[c] - mx), log(se) + mx - lg[y]. lg: classes [4 lane, 4 lane + 4) of this lane, V classes; y is
+// uniform and in range. The sum over classes runs as a tree over lanes instead of in class order, so se can differ
+// from the reference's in its last bits.
+__device__ __forceinline__ double token_nll(const float (&lg)[4], int V, int y, int lane) {
+    float mx = -__builtin_huge_valf();
+#pragma unroll
+    for (int u = 0; u < 4; u++)
+        if (4 * lane + u < V) mx = fmaxf(mx, lg[u]);
+    mx = wave_max_f32(mx);
+    double se = 0.0;
+#pragma unroll
+    for (int u = 0; u < 4; u++)
+        if (4 * lane + u < V) se += exp((double)lg[u] - (double)mx);
+    se = wave_sum_f64(se);
+    float ly = lg[0];
+#pragma unroll
+    for (int u = 1; u < 4; u++) ly = (y & 3) == u ? lg[u] : ly;
+    ly = __shfl(ly, y >> 2);
+    return log(se) + (double)mx - (double)ly;
+}
+
 // _mm512_cvtps_epi32 in round-to-nearest-even: NaN and |x| >= 2^31 give INT32_MIN (cpu/ygg.cpp:292 and others)
 __device__ __forceinline__ int cvt_rne(float x) {
     return (x >= -2147483648.0f && x < 2147483648.0f) ? (int)__builtin_rintf(x) : (int)0x80000000;
@@ -135,7 +166,8 @@ template <int N, int BLK, int R>
 __global__ __launch_bounds__(64) void run_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int T,
                                                  int8_t *__restrict__ state, float *__restrict__ logits,
                                                  int32_t *__restrict__ leaves, int8_t *__restrict__ states,
-                                                 unsigned long long *__restrict__ digest) {
+                                                 unsigned long long *__restrict__ digest,
+                                                 const int32_t *__restrict__ targets, double *__restrict__ nll) {
     constexpr int C = Lanes<N>::C, NL = Lanes<N>::NL;
     constexpr int Q4 = N / 4, QW = Q4 / 4;                       // quad-lane chunk of a row
     constexpr int QA = (Q4 % 16 == 0) ? 16 : 8;                  // its alignment
@@ -160,6 +192,7 @@ __global__ __launch_bounds__(64) void run_kernel(const YggDevModel m, const int3
     for (int i = lane; i < YGG_MAX_RANK; i += 64) zls[i] = 0;
     __syncthreads();
     unsigned long long dg = digest ? digest[s] : 0ull;
+    double nacc = 0.0;
     const int32_t *tok = tokens + (size_t)s * T;
     int x_next = T > 0 ? tok[0] : 0;
 
@@ -400,6 +433,11 @@ __global__ __launch_bounds__(64) void run_kernel(const YggDevModel m, const int3
                     if (4 * lane + u < V) o[4 * lane + u] = lg[u];
             }
         }
+        if (nll) {
+            const int yv = targets[(size_t)s * T + t];
+            if (yv >= 0 && yv < V) nacc += token_nll(lg, V, yv, lane);
+            else if (lane == 0) atomicOr(m.err, 2u);
+        }
         if (states) {
             int8_t *so = states + ((size_t)s * T + t) * L * N;
             for (int i = lane; i < L * N; i += 64) so[i] = qs[i];
@@ -408,6 +446,7 @@ __global__ __launch_bounds__(64) void run_kernel(const YggDevModel m, const int3
     __syncthreads();
     for (int i = lane; i < L * N; i += 64) st[i] = qs[i];
     if (digest && lane == 0) digest[s] = dg;
+    if (nll && lane == 0) nll[s] += nacc;
 }
 
 }  // namespace ygg

@@ -304,7 +304,8 @@ template <int N, int L>
 __global__ __launch_bounds__(64 * kFastWaves) __attribute__((amdgpu_waves_per_eu(4)))
 void fast_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B, int T, int8_t *__restrict__ state,
                  float *__restrict__ logits, int32_t *__restrict__ leaves, int8_t *__restrict__ states,
-                 unsigned long long *__restrict__ digest) {
+                 unsigned long long *__restrict__ digest, const int32_t *__restrict__ targets,
+                 double *__restrict__ nll) {
     using F = Fast<N>;
     constexpr int W = kFastWaves, LR = L > 1 ? L - 1 : 1;
     __shared__ __attribute__((aligned(16))) SharedTables<N, L> S;
@@ -330,6 +331,7 @@ void fast_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
     if (lane < 16) zls[lane] = 0;
     wave_sync();
     unsigned long long dg = digest ? digest[s] : 0ull;
+    double nacc = 0.0;
     const int32_t *tok = tokens + (size_t)s * T;
     int x_next = T > 0 ? tok[0] : 0;
 
@@ -389,6 +391,11 @@ void fast_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
         }
 
         if (logits) store_logits(logits + ((size_t)s * T + t) * V, lg, V, lane);
+        if (nll) {
+            const int yv = targets[(size_t)s * T + t];
+            if (yv >= 0 && yv < V) nacc += token_nll(lg, V, yv, lane);
+            else if (lane == 0) atomicOr(m.err, 2u);
+        }
         if (states) {
             int8_t *so = states + ((size_t)s * T + t) * L * N;
             for (int i = lane; i < L * N; i += 64) so[i] = qs[i];
@@ -397,6 +404,7 @@ void fast_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
     wave_sync();
     for (int i = lane; i < L * N; i += 64) st[i] = qs[i];
     if (digest && lane == 0) digest[s] = dg;
+    if (nll && lane == 0) nll[s] += nacc;
 }
 
 // ----------------------------------------------------------------------------------------------- pipe_kernel
@@ -405,7 +413,8 @@ template <int N, int L>
 __global__ __launch_bounds__(64 * L) __attribute__((amdgpu_waves_per_eu(4))) void pipe_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
                                                       int T, int8_t *__restrict__ state, float *__restrict__ logits,
                                                       int32_t *__restrict__ leaves, int8_t *__restrict__ states,
-                                                      unsigned long long *__restrict__ digest) {
+                                                      unsigned long long *__restrict__ digest,
+                                                      const int32_t *__restrict__ targets, double *__restrict__ nll) {
     using F = Fast<N>;
     __shared__ __attribute__((aligned(16))) SharedTables<N, L> S;
     __shared__ __attribute__((aligned(16))) int8_t qbuf[L][2][N];            // layer l after token t: [l][t & 1]
@@ -430,6 +439,7 @@ __global__ __launch_bounds__(64 * L) __attribute__((amdgpu_waves_per_eu(4))) voi
     const int qj = lane >> 2;
     const int nn1 = (1 << m.round_h[0]) - 1;
     unsigned long long dg = (digest && l == L - 1) ? digest[s] : 0ull;
+    double nacc = 0.0;
     // loaded a tick ahead: the first-round thresholds (routed layers) or the gather record (token layer)
     float th0 = 0.0f;
     Gather<N> G0;
@@ -501,11 +511,14 @@ __global__ __launch_bounds__(64 * L) __attribute__((amdgpu_waves_per_eu(4))) voi
                 }
                 if (l == L - 1) {
                     wave_sync();
-                    if (logits) {
-                        float lg[4];
+                    float lg[4];
 #pragma unroll
-                        for (int u = 0; u < 4; u++) lg[u] = 4 * lane + u < VP ? lr[4 * lane + u] : 0.0f;
-                        store_logits(logits + ((size_t)s * T + t) * V, lg, V, lane);
+                    for (int u = 0; u < 4; u++) lg[u] = 4 * lane + u < VP ? lr[4 * lane + u] : 0.0f;
+                    if (logits) store_logits(logits + ((size_t)s * T + t) * V, lg, V, lane);
+                    if (nll) {
+                        const int yv = targets[(size_t)s * T + t];
+                        if (yv >= 0 && yv < V) nacc += token_nll(lg, V, yv, lane);
+                        else if (lane == 0) atomicOr(m.err, 2u);
                     }
                     if (digest) {
 #pragma unroll
@@ -519,6 +532,7 @@ __global__ __launch_bounds__(64 * L) __attribute__((amdgpu_waves_per_eu(4))) voi
     const int te = T < stop_t ? T : stop_t;                          // tokens processed
     for (int i = lane; i < N; i += 64) st[i] = qbuf[l][(te + 1) & 1][i];
     if (digest && l == L - 1 && lane == 0) digest[s] = dg;
+    if (nll && l == L - 1 && lane == 0) nll[s] += nacc;
 }
 
 }  // namespace ygg

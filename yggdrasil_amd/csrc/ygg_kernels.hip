@@ -6,13 +6,14 @@
 namespace ygg {
 
 typedef hipError_t (*Launcher)(const YggDevModel &, const int32_t *, int, int, int8_t *, float *, int32_t *, int8_t *,
-                               unsigned long long *, hipStream_t);
+                               unsigned long long *, const int32_t *, double *, hipStream_t);
 
 template <int N, int BLK, int R>
 hipError_t launch(const YggDevModel &m, const int32_t *tokens, int B, int T, int8_t *state, float *logits,
-                  int32_t *leaves, int8_t *states, unsigned long long *digest, hipStream_t stream) {
+                  int32_t *leaves, int8_t *states, unsigned long long *digest, const int32_t *targets, double *nll,
+                  hipStream_t stream) {
     hipLaunchKernelGGL((run_kernel<N, BLK, R>), dim3(B), dim3(64), 0, stream, m, tokens, T, state, logits, leaves,
-                       states, digest);
+                       states, digest, targets, nll);
     return hipGetLastError();
 }
 
@@ -23,9 +24,10 @@ hipError_t launch(const YggDevModel &m, const int32_t *tokens, int B, int T, int
 
 template <int N, int L>
 hipError_t launch_fast(const YggDevModel &m, const int32_t *tokens, int B, int T, int8_t *state, float *logits,
-                       int32_t *leaves, int8_t *states, unsigned long long *digest, hipStream_t stream) {
+                       int32_t *leaves, int8_t *states, unsigned long long *digest, const int32_t *targets,
+                       double *nll, hipStream_t stream) {
     hipLaunchKernelGGL((fast_kernel<N, L>), dim3((B + kFastWaves - 1) / kFastWaves), dim3(64 * kFastWaves), 0, stream,
-                       m, tokens, B, T, state, logits, leaves, states, digest);
+                       m, tokens, B, T, state, logits, leaves, states, digest, targets, nll);
     return hipGetLastError();
 }
 
@@ -35,9 +37,10 @@ hipError_t launch_fast(const YggDevModel &m, const int32_t *tokens, int B, int T
 
 template <int N, int L>
 hipError_t launch_pipe(const YggDevModel &m, const int32_t *tokens, int B, int T, int8_t *state, float *logits,
-                       int32_t *leaves, int8_t *states, unsigned long long *digest, hipStream_t stream) {
+                       int32_t *leaves, int8_t *states, unsigned long long *digest, const int32_t *targets,
+                       double *nll, hipStream_t stream) {
     hipLaunchKernelGGL((pipe_kernel<N, L>), dim3(B), dim3(64 * L), 0, stream, m, tokens, B, T, state, logits, leaves,
-                       states, digest);
+                       states, digest, targets, nll);
     return hipGetLastError();
 }
 

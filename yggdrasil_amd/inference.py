@@ -175,23 +175,20 @@ class Yggdrasil:
 
     # ------------------------------------------------------------------------------------------------ consumers
     @torch.no_grad()
-    def score(self, tokens, state: Optional[torch.Tensor] = None, batch: int = 1024, chunk: int = 256) -> np.ndarray:
+    def score(self, tokens, state: Optional[torch.Tensor] = None, batch: int = 1024) -> np.ndarray:
         """Bits of tokens[:, 1:] given the tokens before them, per row of tokens (B, L), as float64 (B,).
-        Rows start from state, or from zero (yggdrasil/inference.py:179-188); the log-softmax is taken in float64
-        as the reference's score mode (cpu/ygg.cpp:513-516)."""
+        Rows start from state, or from zero (yggdrasil/inference.py:179-188). One fused launch per batch of rows: the
+        step and the float64 log-softmax of the reference's score mode (cpu/ygg.cpp:513-516), no logits written."""
         tokens = np.atleast_2d(np.asarray(tokens, np.int64))
         out = []
         for i in range(0, len(tokens), batch):
             x = self._tokens(tokens[i:i + batch])
             B, Lw = x.shape
-            st = self.init_state(B) if state is None else self._check_state(state[i:i + B], B)
+            st = self.init_state(B) if state is None else self._check_state(state[i:i + B], B).clone()
             nll = torch.zeros(B, dtype=torch.float64, device=self.device)
-            for t0 in range(0, Lw - 1, chunk):
-                t1 = min(Lw - 1, t0 + chunk)
-                r = self.run(x[:, t0:t1], st)
-                st = r["state"]
-                lp = torch.log_softmax(r["logits"].double(), -1)
-                nll -= lp.gather(2, x[:, t0 + 1:t1 + 1, None].long())[..., 0].sum(1)
+            if Lw > 1:
+                xin, tgt = x[:, :-1].contiguous(), x[:, 1:].contiguous()
+                check(_lib.lib().ygg_score(self._h, _ptr(xin), _ptr(tgt), B, Lw - 1, _ptr(st), _ptr(nll), _stream()))
             out.append((nll / LN2).cpu().numpy())
         return np.concatenate(out) if out else np.zeros(0)
 
