@@ -94,6 +94,18 @@ int ygg_run(const ygg_model *m, const int32_t *d_tokens, int B, int T, int8_t *d
 int ygg_score(const ygg_model *m, const int32_t *d_tokens, const int32_t *d_targets, int B, int T, int8_t *d_state,
               double *d_nll, void *stream);
 
+/* Sample n tokens for each of B streams in one launch, every sampled token fed straight back as the next input: the
+   generate loop of yggdrasil/inference.py:190-202 (and yggdrasil/inference_triton.py:229-248) after its prompt.
+   Step t consumes x_t (x_0 = d_first[b], then x_t = d_out[b, t-1]) from d_state and samples d_out[b, t] from its
+   logits: temperature 0 takes the first class of maximal logit (argmax); otherwise classes whose logit is below the
+   top_k-th largest are dropped (top_k 0: none) and class c is drawn with probability proportional to
+   exp((lg[c] - max) / temperature), by inverse CDF over classes in order with a 24-bit uniform that depends only on
+   (seed, b, t). d_first (B) int32; d_state (B, L, n) int8 in and out (left after consuming x_0 .. x_{n-1});
+   d_out (B, n) int32; d_logits (B, n, vocab) f32 or NULL. A first token outside [0, vocab) sets bit 0 of the error
+   word and leaves that stream's d_out unwritten. */
+int ygg_generate(const ygg_model *m, const int32_t *d_first, int B, int n, int8_t *d_state, float temperature,
+                 int top_k, uint64_t seed, int32_t *d_out, float *d_logits, void *stream);
+
 /* Wait for `stream`, then return and clear the model's error word: bit 0 set when a kernel met a token outside
    [0, vocab), bit 1 when ygg_score met a target outside it, since the last call. */
 int ygg_take_errors(const ygg_model *m, void *stream, uint32_t *errors);

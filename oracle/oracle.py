@@ -121,6 +121,45 @@ def digest_of(leaves: np.ndarray, states: np.ndarray, init=None) -> np.ndarray:
     return d
 
 
+_M64 = (1 << 64) - 1
+
+
+def mix64(z: int) -> int:
+    """SplitMix64's output function (Steele, Lea, Flood, "Fast splittable pseudorandom number generators", 2014) on
+    the state after one increment: the first output of splitmix64 seeded z."""
+    z = (z + 0x9E3779B97F4A7C15) & _M64
+    z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & _M64
+    z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & _M64
+    return z ^ (z >> 31)
+
+
+def sample_uniform(seed: int, b: int, t: int) -> float:
+    """The uniform in [0, 1) that ygg_generate draws for stream b at step t: the top 24 bits of
+    mix64(seed ^ mix64(b << 32 | t)) / 2^24."""
+    r = mix64((seed & _M64) ^ mix64(((b << 32) | t) & _M64))
+    return (r >> 40) / float(1 << 24)
+
+
+def sample(logits: np.ndarray, temperature: float, top_k: int, u: float):
+    """The class ygg_generate takes from the logits (V,) of one step given its uniform u, in float64: temperature 0
+    -> the first maximal class (argmax, yggdrasil/inference.py:102-104); else classes below the top_k-th largest logit
+    are dropped (yggdrasil/inference.py:105-106) and the first class whose running sum of exp((lg - max) / temperature)
+    exceeds u times the total is taken (inverse CDF). Returns (class, margin): margin is the distance of u times the
+    total to the nearest running sum, relative to the total; a float32 implementation may differ where it is tiny."""
+    lg = np.asarray(logits, np.float64)
+    if temperature == 0:
+        return int(np.argmax(lg)), 1.0
+    keep = np.ones(lg.shape, bool)
+    if 0 < top_k < lg.size:
+        keep = lg >= np.sort(lg)[-top_k]
+    w = np.where(keep, np.exp((lg - lg.max()) / temperature), 0.0)
+    cdf = np.cumsum(w)
+    target = u * cdf[-1]
+    idx = np.nonzero((cdf > target) & (w > 0))[0]
+    c = int(idx[0]) if idx.size else int(np.nonzero(w > 0)[0][-1])
+    return c, float(np.min(np.abs(cdf[w > 0] - target)) / cdf[-1])
+
+
 def have_ref() -> bool:
     return REF_YGG.exists() and REF_DUMP.exists()
 

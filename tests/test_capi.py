@@ -65,6 +65,7 @@ def test_bad_arguments(lib):
     assert L.ygg_run(None, None, 1, 1, None, None, None, None, None, None) == 5
     assert L.ygg_step(None, None, None, None, None, None, 1, None) == 5
     assert L.ygg_take_errors(None, None, None) == 5
+    assert L.ygg_generate(None, None, 1, 1, None, 0.0, 0, 0, None, None, None) == 5
     assert L.ygg_load(b"/nonexistent/model.bin", 0, ctypes.byref(h)) == 1
     assert b"cannot open" in L.ygg_last_error()
     L.ygg_free(None)

@@ -275,3 +275,55 @@ def test_score_formula_matches_reference(tmp_path):
     lg = O.Oracle(path).run(w[:, :-1])["logits"]
     bits = O.nll_bits(lg, w[:, 1:])
     assert abs(bits.sum() / w[:, 1:].size - O.ref_score(path, w[:, :-1], w[:, 1:])) < 1e-6
+
+
+# ---------------------------------------------------------------------------------------------- sampler (generate)
+def test_mix64_is_splitmix64():
+    """mix64 is SplitMix64's output: the published first outputs of splitmix64 seeded 1234567."""
+    want = [6457827717110365317, 3203168211198807973, 9817491932198370423, 4593380528125082431,
+            16408922859458223821]
+    s, got = 1234567, []
+    for _ in want:
+        got.append(O.mix64(s))
+        s = (s + 0x9E3779B97F4A7C15) & ((1 << 64) - 1)
+    assert got == want
+
+
+def test_sample_uniform_range_and_spread():
+    u = np.array([O.sample_uniform(5, b, t) for b in range(200) for t in range(20)])
+    assert u.min() >= 0 and u.max() < 1
+    assert abs(u.mean() - 0.5) < 0.02 and abs(u.var() - 1 / 12) < 0.01
+    assert len(np.unique(u)) > 3990       # distinct per (b, t)
+    assert O.sample_uniform(5, 1, 2) != O.sample_uniform(6, 1, 2)
+
+
+def test_sample_greedy_and_top1():
+    lg = np.array([0.5, 2.0, -1.0, 2.0, 1.5], np.float32)
+    assert O.sample(lg, 0.0, 0, 0.99)[0] == 1          # first maximal class, like argmax
+    for u in (0.0, 0.3, 0.999):
+        assert O.sample(lg[[0, 2, 3, 4]], 1.0, 1, u)[0] == 2   # top_k 1 keeps only the (unique) maximum
+    # inverse CDF over classes in order: u below the first class's share takes class 0
+    assert O.sample(np.zeros(4), 1.0, 0, 0.0)[0] == 0
+    assert O.sample(np.zeros(4), 1.0, 0, 0.26)[0] == 1
+    assert O.sample(np.zeros(4), 1.0, 0, 0.99)[0] == 3
+
+
+@pytest.mark.parametrize("temperature,top_k", [(1.0, 0), (0.6, 0), (1.3, 7)])
+def test_sample_distribution(temperature, top_k):
+    """Draws over many streams follow softmax(lg / temperature) restricted to the top_k classes (chi-square)."""
+    from scipy import stats
+    rng = np.random.default_rng(3)
+    lg = rng.normal(0, 1.5, 24).astype(np.float32)
+    n = 40000
+    draws = np.array([O.sample(lg, temperature, top_k, O.sample_uniform(11, b, 3))[0] for b in range(n)])
+    p = np.exp((lg.astype(np.float64) - lg.max()) / temperature)
+    if top_k:
+        p[lg < np.sort(lg)[-top_k]] = 0
+        assert set(np.unique(draws)) <= set(np.nonzero(p)[0])
+    p /= p.sum()
+    cnt = np.bincount(draws, minlength=lg.size)
+    big = p * n >= 5
+    f_obs = np.append(cnt[big], cnt[~big].sum())
+    f_exp = np.append(p[big] * n, p[~big].sum() * n)
+    keep = f_exp > 0
+    assert stats.chisquare(f_obs[keep], f_exp[keep]).pvalue > 1e-3

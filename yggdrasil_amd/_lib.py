@@ -15,10 +15,10 @@ LIB_PATH = Path(__file__).resolve().parent / "libygg_hip.so"
 
 # every entry point of include/ygg_hip.h
 SYMBOLS = ("ygg_load", "ygg_load_blob", "ygg_model_info", "ygg_free", "ygg_step", "ygg_run", "ygg_score",
-           "ygg_take_errors", "ygg_last_error", "ygg_version")
+           "ygg_generate", "ygg_take_errors", "ygg_last_error", "ygg_version")
 
 ERRORS = {1: "io", 2: "format", 3: "limits", 4: "nomem", 5: "arg", 6: "token", 7: "device"}
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 
 class YggInfo(ctypes.Structure):
@@ -58,6 +58,7 @@ def lib() -> ctypes.CDLL:
     L.ygg_step.argtypes = [vp, vp, vp, vp, vp, vp, i32, vp]
     L.ygg_run.argtypes = [vp, vp, i32, i32, vp, vp, vp, vp, vp, vp]
     L.ygg_score.argtypes = [vp, vp, vp, i32, i32, vp, vp, vp]
+    L.ygg_generate.argtypes = [vp, vp, i32, i32, vp, ctypes.c_float, i32, ctypes.c_uint64, vp, vp, vp]
     L.ygg_take_errors.argtypes = [vp, vp, ctypes.POINTER(ctypes.c_uint32)]
     L.ygg_last_error.argtypes = []
     L.ygg_last_error.restype = ctypes.c_char_p

@@ -19,8 +19,7 @@
 
 namespace ygg {
 // kernel launchers, one per (d_state, block, readout rank); defined in ygg_kernels_*.hip
-typedef hipError_t (*Launcher)(const YggDevModel &, const int32_t *, int, int, int8_t *, float *, int32_t *, int8_t *,
-                               unsigned long long *, const int32_t *, double *, hipStream_t);
+typedef hipError_t (*Launcher)(const YggDevModel &, const int32_t *, int, int, int8_t *, const YggIO &, hipStream_t);
 Launcher find_launcher(int n, int blk, int R);
 Launcher find_fast_launcher(int n, int L);
 Launcher find_pipe_launcher(int n, int L);
@@ -589,7 +588,7 @@ struct DeviceGuard {
 
 extern "C" {
 
-int ygg_version(void) { return 4; }
+int ygg_version(void) { return 5; }
 
 const char *ygg_last_error(void) { return g_err.c_str(); }
 
@@ -652,8 +651,12 @@ int ygg_run(const ygg_model *m, const int32_t *d_tokens, int B, int T, int8_t *d
     HIP_TRY(g.set(m->device));
     // the pipelined kernel overlaps the layers of consecutive tokens, so it needs more than one token per launch
     ygg::Launcher k = (m->launch_pipe && B <= m->pipe_max_streams && T > 1) ? m->launch_pipe : m->launch;
-    HIP_TRY(k(m->dev, d_tokens, B, T, d_state, d_logits, d_leaves, d_states, (unsigned long long *)d_digest, nullptr,
-              nullptr, (hipStream_t)stream));
+    YggIO io{};
+    io.logits = d_logits;
+    io.leaves = d_leaves;
+    io.states = d_states;
+    io.digest = (unsigned long long *)d_digest;
+    HIP_TRY(k(m->dev, d_tokens, B, T, d_state, io, (hipStream_t)stream));
     return YGG_OK;
 }
 
@@ -666,8 +669,32 @@ int ygg_score(const ygg_model *m, const int32_t *d_tokens, const int32_t *d_targ
     DeviceGuard g;
     HIP_TRY(g.set(m->device));
     ygg::Launcher k = (m->launch_pipe && B <= m->pipe_max_streams && T > 1) ? m->launch_pipe : m->launch;
-    HIP_TRY(k(m->dev, d_tokens, B, T, d_state, nullptr, nullptr, nullptr, nullptr, d_targets, d_nll,
-              (hipStream_t)stream));
+    YggIO io{};
+    io.targets = d_targets;
+    io.nll = d_nll;
+    HIP_TRY(k(m->dev, d_tokens, B, T, d_state, io, (hipStream_t)stream));
+    return YGG_OK;
+}
+
+int ygg_generate(const ygg_model *m, const int32_t *d_first, int B, int n, int8_t *d_state, float temperature,
+                 int top_k, uint64_t seed, int32_t *d_out, float *d_logits, void *stream) {
+    if (!m) return fail(YGG_ERR_ARG, "model is NULL");
+    if (B < 0 || n < 0) return fail(YGG_ERR_ARG, "negative B (%d) or n (%d)", B, n);
+    if (!(temperature >= 0.0f) || temperature == __builtin_huge_valf())
+        return fail(YGG_ERR_ARG, "temperature %g: finite and >= 0", (double)temperature);
+    if (top_k < 0) return fail(YGG_ERR_ARG, "negative top_k (%d)", top_k);
+    if (B == 0 || n == 0) return YGG_OK;
+    if (!d_first || !d_state || !d_out) return fail(YGG_ERR_ARG, "NULL buffer");
+    DeviceGuard g;
+    HIP_TRY(g.set(m->device));
+    // every token needs all layers of the one before it: the per-stream kernel, never the layer-pipelined one
+    YggIO io{};
+    io.logits = d_logits;
+    io.gen = d_out;
+    io.temperature = temperature;
+    io.top_k = top_k;
+    io.seed = (unsigned long long)seed;
+    HIP_TRY(m->launch(m->dev, d_first, B, n, d_state, io, (hipStream_t)stream));
     return YGG_OK;
 }
 
@@ -684,8 +711,10 @@ int ygg_step(const ygg_model *m, const int32_t *d_tokens, const int8_t *d_state_
                                (hipStream_t)stream));
     // one token: the per-stream kernel (a one-token launch cannot overlap layers), or the pipelined one when forced
     ygg::Launcher k = (m->launch_pipe && m->pipe_max_streams == INT32_MAX) ? m->launch_pipe : m->launch;
-    HIP_TRY(k(m->dev, d_tokens, B, 1, d_state_out, d_logits, d_leaves, nullptr, nullptr, nullptr, nullptr,
-              (hipStream_t)stream));
+    YggIO io{};
+    io.logits = d_logits;
+    io.leaves = d_leaves;
+    HIP_TRY(k(m->dev, d_tokens, B, 1, d_state_out, io, (hipStream_t)stream));
     return YGG_OK;
 }
 

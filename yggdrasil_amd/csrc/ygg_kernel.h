@@ -84,6 +84,101 @@ __device__ __forceinline__ double token_nll(const float (&lg)[4], int V, int y, 
     return log(se) + (double)mx - (double)ly;
 }
 
+__device__ __forceinline__ int wave_min_i32(int v) {
+    for (int o = 32; o >= 1; o >>= 1) v = min(v, __shfl_xor(v, o));
+    return v;
+}
+__device__ __forceinline__ int wave_sum_i32(int v) {
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+__device__ __forceinline__ float wave_sum_f32(float v) {
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+// inclusive prefix sum over lanes
+__device__ __forceinline__ float wave_scan_f32(float v, int lane) {
+    for (int o = 1; o < 64; o <<= 1) {
+        const float u = __shfl_up(v, o);
+        if (lane >= o) v += u;
+    }
+    return v;
+}
+// SplitMix64's output function (Steele, Lea, Flood 2014): a 64-bit mixer for counter-based random numbers
+__device__ __forceinline__ unsigned long long mix64(unsigned long long z) {
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+// order-preserving map of a float to an unsigned key
+__device__ __forceinline__ uint32_t fkey(float f) {
+    const uint32_t u = __float_as_uint(f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// The next token from the logits of one stream (4 classes per lane, V classes; the sampling of
+// yggdrasil/inference.py:102-107 and yggdrasil/inference_triton.py:236-242): temperature 0 takes the first maximal
+// class; otherwise classes below the top_k-th largest logit are dropped and a class is drawn with probability
+// proportional to exp((lg - max) / temperature), by inverse CDF with a uniform from (seed, stream, step).
+__device__ __forceinline__ int sample_token(const float (&lg)[4], int V, float temperature, int top_k,
+                                            unsigned long long seed, int s, int t, int lane) {
+    bool valid[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) valid[u] = 4 * lane + u < V;
+    float mx = -__builtin_huge_valf();
+#pragma unroll
+    for (int u = 0; u < 4; u++)
+        if (valid[u]) mx = fmaxf(mx, lg[u]);
+    mx = wave_max_f32(mx);
+    if (temperature <= 0.0f) {
+        int idx = 0x7fffffff;
+#pragma unroll
+        for (int u = 0; u < 4; u++)
+            if (valid[u] && lg[u] == mx) idx = min(idx, 4 * lane + u);
+        return wave_min_i32(idx);
+    }
+    // the top_k-th largest logit, by a radix search over order-preserving keys
+    uint32_t kth = 0;
+    if (top_k > 0 && top_k < V) {
+        uint32_t key[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) key[u] = fkey(lg[u]);
+        for (int b = 31; b >= 0; b--) {
+            const uint32_t cand = kth | (1u << b);
+            int c = 0;
+#pragma unroll
+            for (int u = 0; u < 4; u++) c += (valid[u] && key[u] >= cand) ? 1 : 0;
+            if (wave_sum_i32(c) >= top_k) kth = cand;
+        }
+    }
+    float w[4], part = 0.0f;
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const bool keep = valid[u] && fkey(lg[u]) >= kth;
+        w[u] = keep ? expf((lg[u] - mx) / temperature) : 0.0f;
+        part += w[u];
+    }
+    const float incl = wave_scan_f32(part, lane);
+    const float total = __shfl(incl, 63);
+    const unsigned long long r = mix64(seed ^ mix64(((unsigned long long)s << 32) | (unsigned)t));
+    const float target = (float)(r >> 40) * (1.0f / 16777216.0f) * total;
+    // the first class whose running sum exceeds the target (the last kept class when rounding leaves none)
+    float run = incl - part;
+    int pick = 0x7fffffff, last = -1;
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        run += w[u];
+        if (w[u] > 0.0f) {
+            last = 4 * lane + u;
+            if (run > target && pick == 0x7fffffff) pick = 4 * lane + u;
+        }
+    }
+    pick = wave_min_i32(pick);
+    if (pick == 0x7fffffff) pick = -wave_min_i32(-last);
+    return pick;
+}
+
 // _mm512_cvtps_epi32 in round-to-nearest-even: NaN and |x| >= 2^31 give INT32_MIN (cpu/ygg.cpp:292 and others)
 __device__ __forceinline__ int cvt_rne(float x) {
     return (x >= -2147483648.0f && x < 2147483648.0f) ? (int)__builtin_rintf(x) : (int)0x80000000;
@@ -162,12 +257,16 @@ constexpr unsigned long long kDigestMul = 0x100000001B3ull;
 constexpr unsigned long long kDigestLeaf = 0xD6E8FEB86659FD93ull;
 constexpr unsigned long long kDigestCoord = 0x9E3779B97F4A7C15ull;
 
-template <int N, int BLK, int R>
+// GEN: sample the next input from the logits of every token (io.gen), instead of reading it from tokens
+template <int N, int BLK, int R, bool GEN>
 __global__ __launch_bounds__(64) void run_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int T,
-                                                 int8_t *__restrict__ state, float *__restrict__ logits,
-                                                 int32_t *__restrict__ leaves, int8_t *__restrict__ states,
-                                                 unsigned long long *__restrict__ digest,
-                                                 const int32_t *__restrict__ targets, double *__restrict__ nll) {
+                                                 int8_t *__restrict__ state, const YggIO io) {
+    float *__restrict__ logits = io.logits;
+    int32_t *__restrict__ leaves = io.leaves;
+    int8_t *__restrict__ states = io.states;
+    unsigned long long *__restrict__ digest = io.digest;
+    const int32_t *__restrict__ targets = io.targets;
+    double *__restrict__ nll = io.nll;
     constexpr int C = Lanes<N>::C, NL = Lanes<N>::NL;
     constexpr int Q4 = N / 4, QW = Q4 / 4;                       // quad-lane chunk of a row
     constexpr int QA = (Q4 % 16 == 0) ? 16 : 8;                  // its alignment
@@ -193,12 +292,12 @@ __global__ __launch_bounds__(64) void run_kernel(const YggDevModel m, const int3
     __syncthreads();
     unsigned long long dg = digest ? digest[s] : 0ull;
     double nacc = 0.0;
-    const int32_t *tok = tokens + (size_t)s * T;
+    const int32_t *tok = tokens + (size_t)s * (GEN ? 1 : T);
     int x_next = T > 0 ? tok[0] : 0;
 
     for (int t = 0; t < T; t++) {
         const int x = x_next;
-        if (t + 1 < T) x_next = tok[t + 1];
+        if (!GEN && t + 1 < T) x_next = tok[t + 1];
         if (x < 0 || x >= V) {
             if (lane == 0) atomicOr(m.err, 1u);
             break;
@@ -437,6 +536,10 @@ __global__ __launch_bounds__(64) void run_kernel(const YggDevModel m, const int3
             const int yv = targets[(size_t)s * T + t];
             if (yv >= 0 && yv < V) nacc += token_nll(lg, V, yv, lane);
             else if (lane == 0) atomicOr(m.err, 2u);
+        }
+        if (GEN) {
+            x_next = sample_token(lg, V, io.temperature, io.top_k, io.seed, s, t, lane);
+            if (lane == 0) io.gen[(size_t)s * T + t] = x_next;
         }
         if (states) {
             int8_t *so = states + ((size_t)s * T + t) * L * N;

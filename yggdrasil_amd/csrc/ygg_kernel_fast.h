@@ -300,12 +300,17 @@ __device__ __forceinline__ void store_logits(float *o, const float (&lg)[4], int
 
 // ----------------------------------------------------------------------------------------------- fast_kernel
 
-template <int N, int L>
+// GEN: sample the next input from the logits of every token (io.gen), instead of reading it from tokens
+template <int N, int L, bool GEN>
 __global__ __launch_bounds__(64 * kFastWaves) __attribute__((amdgpu_waves_per_eu(4)))
 void fast_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B, int T, int8_t *__restrict__ state,
-                 float *__restrict__ logits, int32_t *__restrict__ leaves, int8_t *__restrict__ states,
-                 unsigned long long *__restrict__ digest, const int32_t *__restrict__ targets,
-                 double *__restrict__ nll) {
+                 const YggIO io) {
+    float *__restrict__ logits = io.logits;
+    int32_t *__restrict__ leaves = io.leaves;
+    int8_t *__restrict__ states = io.states;
+    unsigned long long *__restrict__ digest = io.digest;
+    const int32_t *__restrict__ targets = io.targets;
+    double *__restrict__ nll = io.nll;
     using F = Fast<N>;
     constexpr int W = kFastWaves, LR = L > 1 ? L - 1 : 1;
     __shared__ __attribute__((aligned(16))) SharedTables<N, L> S;
@@ -332,12 +337,12 @@ void fast_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
     wave_sync();
     unsigned long long dg = digest ? digest[s] : 0ull;
     double nacc = 0.0;
-    const int32_t *tok = tokens + (size_t)s * T;
+    const int32_t *tok = tokens + (size_t)s * (GEN ? 1 : T);
     int x_next = T > 0 ? tok[0] : 0;
 
     for (int t = 0; t < T; t++) {
         const int x = x_next;
-        if (t + 1 < T) x_next = tok[t + 1];
+        if (!GEN && t + 1 < T) x_next = tok[t + 1];
         if (x < 0 || x >= V) {
             if (lane == 0) atomicOr(m.err, 1u);
             break;
@@ -396,6 +401,10 @@ void fast_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
             if (yv >= 0 && yv < V) nacc += token_nll(lg, V, yv, lane);
             else if (lane == 0) atomicOr(m.err, 2u);
         }
+        if (GEN) {
+            x_next = sample_token(lg, V, io.temperature, io.top_k, io.seed, s, t, lane);
+            if (lane == 0) io.gen[(size_t)s * T + t] = x_next;
+        }
         if (states) {
             int8_t *so = states + ((size_t)s * T + t) * L * N;
             for (int i = lane; i < L * N; i += 64) so[i] = qs[i];
@@ -410,11 +419,16 @@ void fast_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
 // ----------------------------------------------------------------------------------------------- pipe_kernel
 
 template <int N, int L>
-__global__ __launch_bounds__(64 * L) __attribute__((amdgpu_waves_per_eu(4))) void pipe_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
-                                                      int T, int8_t *__restrict__ state, float *__restrict__ logits,
-                                                      int32_t *__restrict__ leaves, int8_t *__restrict__ states,
-                                                      unsigned long long *__restrict__ digest,
-                                                      const int32_t *__restrict__ targets, double *__restrict__ nll) {
+__global__ __launch_bounds__(64 * L) __attribute__((amdgpu_waves_per_eu(4)))
+void pipe_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B, int T, int8_t *__restrict__ state,
+                 const YggIO io) {
+    // generation needs every layer of a token before the next one; the dispatcher never sends it here
+    float *__restrict__ logits = io.logits;
+    int32_t *__restrict__ leaves = io.leaves;
+    int8_t *__restrict__ states = io.states;
+    unsigned long long *__restrict__ digest = io.digest;
+    const int32_t *__restrict__ targets = io.targets;
+    double *__restrict__ nll = io.nll;
     using F = Fast<N>;
     __shared__ __attribute__((aligned(16))) SharedTables<N, L> S;
     __shared__ __attribute__((aligned(16))) int8_t qbuf[L][2][N];            // layer l after token t: [l][t & 1]

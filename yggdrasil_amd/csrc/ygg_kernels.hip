@@ -5,15 +5,15 @@
 
 namespace ygg {
 
-typedef hipError_t (*Launcher)(const YggDevModel &, const int32_t *, int, int, int8_t *, float *, int32_t *, int8_t *,
-                               unsigned long long *, const int32_t *, double *, hipStream_t);
+typedef hipError_t (*Launcher)(const YggDevModel &, const int32_t *, int, int, int8_t *, const YggIO &, hipStream_t);
 
 template <int N, int BLK, int R>
-hipError_t launch(const YggDevModel &m, const int32_t *tokens, int B, int T, int8_t *state, float *logits,
-                  int32_t *leaves, int8_t *states, unsigned long long *digest, const int32_t *targets, double *nll,
-                  hipStream_t stream) {
-    hipLaunchKernelGGL((run_kernel<N, BLK, R>), dim3(B), dim3(64), 0, stream, m, tokens, T, state, logits, leaves,
-                       states, digest, targets, nll);
+hipError_t launch(const YggDevModel &m, const int32_t *tokens, int B, int T, int8_t *state, const YggIO &io,
+                       hipStream_t stream) {
+    if (io.gen)
+        hipLaunchKernelGGL((run_kernel<N, BLK, R, true>), dim3(B), dim3(64), 0, stream, m, tokens, T, state, io);
+    else
+        hipLaunchKernelGGL((run_kernel<N, BLK, R, false>), dim3(B), dim3(64), 0, stream, m, tokens, T, state, io);
     return hipGetLastError();
 }
 
@@ -23,11 +23,13 @@ hipError_t launch(const YggDevModel &m, const int32_t *tokens, int B, int T, int
     if (blk == 8) { YGG_R(N, 8) } if (blk == 16) { YGG_R(N, 16) }
 
 template <int N, int L>
-hipError_t launch_fast(const YggDevModel &m, const int32_t *tokens, int B, int T, int8_t *state, float *logits,
-                       int32_t *leaves, int8_t *states, unsigned long long *digest, const int32_t *targets,
-                       double *nll, hipStream_t stream) {
-    hipLaunchKernelGGL((fast_kernel<N, L>), dim3((B + kFastWaves - 1) / kFastWaves), dim3(64 * kFastWaves), 0, stream,
-                       m, tokens, B, T, state, logits, leaves, states, digest, targets, nll);
+hipError_t launch_fast(const YggDevModel &m, const int32_t *tokens, int B, int T, int8_t *state, const YggIO &io,
+                       hipStream_t stream) {
+    const dim3 grid((B + kFastWaves - 1) / kFastWaves), block(64 * kFastWaves);
+    if (io.gen)
+        hipLaunchKernelGGL((fast_kernel<N, L, true>), grid, block, 0, stream, m, tokens, B, T, state, io);
+    else
+        hipLaunchKernelGGL((fast_kernel<N, L, false>), grid, block, 0, stream, m, tokens, B, T, state, io);
     return hipGetLastError();
 }
 
@@ -36,11 +38,9 @@ hipError_t launch_fast(const YggDevModel &m, const int32_t *tokens, int B, int T
     if (L == 3) return launch_fast<N, 3>; if (L == 4) return launch_fast<N, 4>;
 
 template <int N, int L>
-hipError_t launch_pipe(const YggDevModel &m, const int32_t *tokens, int B, int T, int8_t *state, float *logits,
-                       int32_t *leaves, int8_t *states, unsigned long long *digest, const int32_t *targets,
-                       double *nll, hipStream_t stream) {
-    hipLaunchKernelGGL((pipe_kernel<N, L>), dim3(B), dim3(64 * L), 0, stream, m, tokens, B, T, state, logits, leaves,
-                       states, digest, targets, nll);
+hipError_t launch_pipe(const YggDevModel &m, const int32_t *tokens, int B, int T, int8_t *state, const YggIO &io,
+                       hipStream_t stream) {
+    hipLaunchKernelGGL((pipe_kernel<N, L>), dim3(B), dim3(64 * L), 0, stream, m, tokens, B, T, state, io);
     return hipGetLastError();
 }
 

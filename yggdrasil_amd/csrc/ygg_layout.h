@@ -76,6 +76,21 @@ struct YggDevModel {
     YggDevLayer layers[YGG_MAX_LAYERS];
 };
 
+// Optional inputs and outputs of one launch of a step kernel (null: not read or written).
+struct YggIO {
+    float *logits;                  // (B, T, V) f32
+    int32_t *leaves;                // (B, T, L)
+    int8_t *states;                 // (B, T, L, n) after every token
+    unsigned long long *digest;     // (B) in and out
+    const int32_t *targets;         // score: (B, T) targets
+    double *nll;                    // score: (B) in and out
+    int32_t *gen;                   // generate: (B, T) the token sampled after every step, which is the next input;
+                                    // the launch's tokens are then one first token per stream
+    float temperature;              // generate: 0 = greedy (first maximal class)
+    int32_t top_k;                  // generate: keep classes at least the k-th largest logit (0: all)
+    unsigned long long seed;        // generate
+};
+
 // Compile-time lane constants of a d_state N, readout rank R.
 template <int N> struct Lanes {
     static constexpr int C = N <= 64 ? 1 : (N <= 128 ? 2 : 4);

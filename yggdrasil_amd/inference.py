@@ -193,28 +193,34 @@ class Yggdrasil:
         return np.concatenate(out) if out else np.zeros(0)
 
     @torch.no_grad()
-    def generate(self, prompt, n: int, temperature: float = 1.0, top_k: int = 0, seed: int = 0):
+    def generate(self, prompt, n: int, temperature: float = 1.0, top_k: int = 0, seed: int = 0,
+                 return_logits: bool = False):
         """Prompt (L,) or (B, L), L >= 1, followed by n sampled tokens. temperature 0: greedy
-        (yggdrasil/inference.py:190-202, yggdrasil/inference_triton.py:229-248)."""
+        (yggdrasil/inference.py:190-202, yggdrasil/inference_triton.py:229-248). The prompt but its last token goes
+        through one ygg_run launch; the n sampled tokens come from one ygg_generate launch that samples on the device
+        and feeds each token back as the next input. Draws depend on (seed, row, position) only, so a row samples the
+        same tokens whatever the batch around it. return_logits: also the logits (B, n, classes) each token was
+        sampled from."""
         prompt = np.asarray(prompt, np.int64)
+        if prompt.ndim not in (1, 2) or prompt.shape[-1] < 1:
+            raise ValueError("prompt must be (L,) or (B, L) with L >= 1")
+        if n < 0:
+            raise ValueError(f"n = {n} < 0")
+        if not (temperature >= 0 and math.isfinite(temperature)):
+            raise ValueError(f"temperature {temperature}: finite and >= 0")
+        if top_k < 0:
+            raise ValueError(f"top_k {top_k} < 0")
         x = self._tokens(np.atleast_2d(prompt))
-        r = self.run(x)
-        state, logits = r["state"], r["logits"][:, -1]
-        gen = torch.Generator(self.device).manual_seed(seed)
-        out = [x.long()]
-        for i in range(n):
-            if temperature == 0:
-                tok = logits.argmax(-1)
-            else:
-                lg = logits
-                if top_k:
-                    lg = lg.masked_fill(lg < lg.topk(top_k, -1).values[:, -1:], -float("inf"))
-                tok = torch.multinomial(torch.softmax(lg / temperature, -1), 1, generator=gen)[:, 0]
-            out.append(tok[:, None])
-            if i + 1 < n:
-                logits, state = self.step(tok, state)
-        res = torch.cat(out, 1).cpu().numpy()
-        return res[0] if prompt.ndim == 1 else res
+        B = x.shape[0]
+        st = self.run(x[:, :-1], logits=False)["state"] if x.shape[1] > 1 else self.init_state(B)
+        toks = torch.empty(B, n, dtype=torch.int32, device=self.device)
+        lg = torch.empty(B, n, self.vocab, dtype=torch.float32, device=self.device) if return_logits else None
+        first = x[:, -1].contiguous()
+        check(_lib.lib().ygg_generate(self._h, _ptr(first), B, n, _ptr(st), ctypes.c_float(temperature), int(top_k),
+                                      ctypes.c_uint64(seed & (2 ** 64 - 1)), _ptr(toks), _ptr(lg), _stream()))
+        res = torch.cat([x, toks], 1).long().cpu().numpy()
+        res = res[0] if prompt.ndim == 1 else res
+        return (res, lg) if return_logits else res
 
 
 def load(path, backend: str = "hip", **kw) -> Yggdrasil:
