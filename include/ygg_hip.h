@@ -50,7 +50,8 @@ typedef struct {
                                   rank <= 16, table storage, tensor scales, <= 4 layers); YGG_KERNEL=generic at load
                                   time forces 0 */
     int32_t pipe_max_streams;  /* ygg_run calls with B at most this and T > 1 use the layer-pipelined kernel (one
-                                  wavefront per layer, for latency); 0: never. YGG_KERNEL=fast at load time disables
+                                  wavefront per layer, for latency): its resident workgroups (one per stream) per CU
+                                  times the CUs; 0: never. YGG_KERNEL=fast at load time disables
                                   it, =pipe uses it for every call */
     int64_t file_array_bytes;  /* bytes of the file's arrays (the reference's Model::bytes, cpu/ygg.cpp:158, 167) */
     int64_t device_bytes;      /* device memory held by the model */

@@ -23,6 +23,7 @@ typedef hipError_t (*Launcher)(const YggDevModel &, const int32_t *, int, int, i
 Launcher find_launcher(int n, int blk, int R);
 Launcher find_fast_launcher(int n, int L);
 Launcher find_pipe_launcher(int n, int L);
+int pipe_blocks_per_cu(int n, int L);
 }  // namespace ygg
 
 namespace {
@@ -517,8 +518,9 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || cus <= 0) cus = 256;
     ygg_model *m = new ygg_model();
     m->launch_pipe = pipe;
-    // pipe_kernel when all B L wavefronts of a call are resident at once (16 per CU), or always with YGG_KERNEL=pipe
-    m->pipe_max_streams = pipe ? (kmode == "pipe" ? INT32_MAX : 16 * cus / L) : 0;
+    // pipe_kernel when the workgroups of all B streams of a call are resident at once, or always with YGG_KERNEL=pipe
+    const int pipe_per_cu = pipe ? ygg::pipe_blocks_per_cu(n, L) : 0;
+    m->pipe_max_streams = pipe ? (kmode == "pipe" ? INT32_MAX : pipe_per_cu * cus) : 0;
     m->device = device;
     m->arena = arena;
     m->arena_bytes = total;

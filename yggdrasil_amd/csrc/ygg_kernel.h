@@ -179,6 +179,17 @@ __device__ __forceinline__ int sample_token(const float (&lg)[4], int V, float t
     return pick;
 }
 
+// One round of the router descent from its ballot: node j of the round's subtree (breadth-first, j < 2^h - 1) goes
+// right when bit 4 j of mask is set; walk its h <= 4 levels from the root and return the node index reached, in
+// [2^h - 1, 2^(h+1) - 2]. Unrolled on 4 times the node index so that a level is a bit test and a shift-add.
+__device__ __forceinline__ int walk_round(unsigned long long mask, int h) {
+    int l4 = 0;
+#pragma unroll
+    for (int lev = 0; lev < 4; lev++)
+        if (lev < h) l4 = 2 * l4 + (((mask >> l4) & 1ull) ? 8 : 4);
+    return l4 >> 2;
+}
+
 // _mm512_cvtps_epi32 in round-to-nearest-even: NaN and |x| >= 2^31 give INT32_MIN (cpu/ygg.cpp:292 and others)
 __device__ __forceinline__ int cvt_rne(float x) {
     return (x >= -2147483648.0f && x < 2147483648.0f) ? (int)__builtin_rintf(x) : (int)0x80000000;
@@ -293,11 +304,11 @@ __global__ __launch_bounds__(64) void run_kernel(const YggDevModel m, const int3
     unsigned long long dg = digest ? digest[s] : 0ull;
     double nacc = 0.0;
     const int32_t *tok = tokens + (size_t)s * (GEN ? 1 : T);
-    int x_next = T > 0 ? tok[0] : 0;
+    int x_next = T > 0 ? __builtin_amdgcn_readfirstlane(tok[0]) : 0;
 
     for (int t = 0; t < T; t++) {
         const int x = x_next;
-        if (!GEN && t + 1 < T) x_next = tok[t + 1];
+        if (!GEN && t + 1 < T) x_next = __builtin_amdgcn_readfirstlane(tok[t + 1]);
         if (x < 0 || x >= V) {
             if (lane == 0) atomicOr(m.err, 1u);
             break;
@@ -352,8 +363,7 @@ __global__ __launch_bounds__(64) void run_kernel(const YggDevModel m, const int3
                     dot = sum4(dot);
                     const bool right = (float)dot * rho > th;
                     const unsigned long long mask = __ballot(right && qk == 0 && qj < nn);
-                    int loc = 0;
-                    for (int lev = 0; lev < h; lev++) loc = 2 * loc + 1 + (int)((mask >> (4 * loc)) & 1ull);
+                    const int loc = walk_round(mask, h);
                     base += (1 << d0) << h;
                     d0 += h;
                     ix = (ix << h) + (loc - nn);
@@ -538,7 +548,7 @@ __global__ __launch_bounds__(64) void run_kernel(const YggDevModel m, const int3
             else if (lane == 0) atomicOr(m.err, 2u);
         }
         if (GEN) {
-            x_next = sample_token(lg, V, io.temperature, io.top_k, io.seed, s, t, lane);
+            x_next = __builtin_amdgcn_readfirstlane(sample_token(lg, V, io.temperature, io.top_k, io.seed, s, t, lane));
             if (lane == 0) io.gen[(size_t)s * T + t] = x_next;
         }
         if (states) {

@@ -115,8 +115,7 @@ __device__ __forceinline__ int descend(const YggDevModel &m, const YggDevLayer &
         dot = sum4(dot);
         const bool right = (float)dot * rho > th0;
         const unsigned long long mask = __ballot(right && qk == 0 && qj < nn1);
-        int loc = 0;
-        for (int lev = 0; lev < h1; lev++) loc = 2 * loc + 1 + (int)((mask >> (4 * loc)) & 1ull);
+        const int loc = walk_round(mask, h1);
         ix = (1 << h1) + (loc - nn1);
     }
     const float *thr = y.thr + (size_t)x * y.thr_stride;
@@ -137,8 +136,7 @@ __device__ __forceinline__ int descend(const YggDevModel &m, const YggDevLayer &
         dot = sum4(dot);
         const bool right = (float)dot * rho > th;
         const unsigned long long mask = __ballot(right && qk == 0 && qj < nn);
-        int loc = 0;
-        for (int lev = 0; lev < h; lev++) loc = 2 * loc + 1 + (int)((mask >> (4 * loc)) & 1ull);
+        const int loc = walk_round(mask, h);
         base += (1 << d0) << h;
         d0 += h;
         ix = (ix << h) + (loc - nn);
@@ -318,7 +316,8 @@ void fast_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
     __shared__ __attribute__((aligned(16))) int8_t zlw[W][16];
     __shared__ __attribute__((aligned(16))) int8_t zqw[W][16];
 
-    const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63;
+    // the wavefront index, stream, tokens and leaves are uniform over a wavefront: kept in scalar registers
+    const int tid = threadIdx.x, wv = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int s = blockIdx.x * W + wv;
     const int V = m.V, VP = m.VP, R2 = m.R2;
     load_tables<N, L>(S, m, tid, 64 * W);
@@ -338,11 +337,11 @@ void fast_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
     unsigned long long dg = digest ? digest[s] : 0ull;
     double nacc = 0.0;
     const int32_t *tok = tokens + (size_t)s * (GEN ? 1 : T);
-    int x_next = T > 0 ? tok[0] : 0;
+    int x_next = T > 0 ? __builtin_amdgcn_readfirstlane(tok[0]) : 0;
 
     for (int t = 0; t < T; t++) {
         const int x = x_next;
-        if (!GEN && t + 1 < T) x_next = tok[t + 1];
+        if (!GEN && t + 1 < T) x_next = __builtin_amdgcn_readfirstlane(tok[t + 1]);
         if (x < 0 || x >= V) {
             if (lane == 0) atomicOr(m.err, 1u);
             break;
@@ -402,7 +401,7 @@ void fast_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
             else if (lane == 0) atomicOr(m.err, 2u);
         }
         if (GEN) {
-            x_next = sample_token(lg, V, io.temperature, io.top_k, io.seed, s, t, lane);
+            x_next = __builtin_amdgcn_readfirstlane(sample_token(lg, V, io.temperature, io.top_k, io.seed, s, t, lane));
             if (lane == 0) io.gen[(size_t)s * T + t] = x_next;
         }
         if (states) {
@@ -438,7 +437,8 @@ void pipe_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
     __shared__ __attribute__((aligned(16))) int8_t zqw[L][16];
     __shared__ int stop_t;                                                   // first token out of range
 
-    const int tid = threadIdx.x, l = tid >> 6, lane = tid & 63;
+    // the wavefront's layer and the tokens are uniform over a wavefront: kept in scalar registers
+    const int tid = threadIdx.x, l = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int s = blockIdx.x;
     const int V = m.V, VP = m.VP, R2 = m.R2;
     load_tables<N, L>(S, m, tid, 64 * L);
@@ -458,7 +458,7 @@ void pipe_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
     float th0 = 0.0f;
     Gather<N> G0;
     if (T > 0) {
-        const int x0 = tok[0];
+        const int x0 = __builtin_amdgcn_readfirstlane(tok[0]);
         if (x0 >= 0 && x0 < V) {
             if (l > 0 && qj < nn1) th0 = y.thr[(size_t)x0 * y.thr_stride + qj];
             if (l == 0) gather<N>(G0, y, x0, x0, false, R2, lane);
@@ -468,7 +468,7 @@ void pipe_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
     for (int k = 0; k < T + L - 1; k++) {
         const int t = k - l;
         if (t >= 0 && t < T && t < stop_t) {
-            const int x = tok[t];
+            const int x = __builtin_amdgcn_readfirstlane(tok[t]);
             const bool ok = x >= 0 && x < V;
             if (l == 0 && !ok && lane == 0) {
                 atomicOr(m.err, 1u);
@@ -488,7 +488,7 @@ void pipe_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
                     G = G0;
                 }
                 if (t + 1 < T) {
-                    const int xn = tok[t + 1];
+                    const int xn = __builtin_amdgcn_readfirstlane(tok[t + 1]);
                     if (xn >= 0 && xn < V) {
                         if (l > 0 && qj < nn1) th0 = y.thr[(size_t)xn * y.thr_stride + qj];
                         if (l == 0) gather<N>(G0, y, xn, xn, false, R2, lane);

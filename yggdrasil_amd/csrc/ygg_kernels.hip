@@ -56,6 +56,26 @@ Launcher find_pipe_launcher(int n, int L) {
     return nullptr;
 }
 
+template <int N, int L> int pipe_blocks() {
+    int nb = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, reinterpret_cast<const void *>(&pipe_kernel<N, L>), 64 * L,
+                                                     0) != hipSuccess)
+        return 0;
+    return nb;
+}
+
+#define YGG_O(N) \
+    if (L == 1) return pipe_blocks<N, 1>(); if (L == 2) return pipe_blocks<N, 2>(); \
+    if (L == 3) return pipe_blocks<N, 3>(); if (L == 4) return pipe_blocks<N, 4>();
+
+// workgroups of the layer-pipelined kernel (one stream each) resident per CU on the current device
+int pipe_blocks_per_cu(int n, int L) {
+    if (n == 64) { YGG_O(64) }
+    if (n == 96) { YGG_O(96) }
+    if (n == 128) { YGG_O(128) }
+    return 0;
+}
+
 // the specialised kernel: readout rank 8, block 16, layer-input rank <= 16, table storage, tensor scales, L <= 4
 Launcher find_fast_launcher(int n, int L) {
     if (n == 64) { YGG_L(64) }
