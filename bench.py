@@ -116,7 +116,60 @@ def cpu_baseline(path: Path, tokens: np.ndarray, procs: int, streams_per_proc: i
                       f"logits only, no softmax"}
 
 
+def _counter_sums(d: str) -> dict:
+    """rocprofv3 --pmc CSV output under d -> {(dispatch id, kernel name): counter value summed over its rows}."""
+    import csv
+    files = sorted(Path(d).rglob("*counter_collection.csv"))
+    if not files:
+        raise SystemExit(f"no *counter_collection.csv under {d}")
+    out = {}
+    for f in files:
+        for r in csv.DictReader(open(f)):
+            name = r["Kernel_Name"].split("(")[0].strip()
+            k = (int(r["Dispatch_Id"]), name[5:] if name.startswith("void ") else name)
+            out[k] = out.get(k, 0.0) + float(r["Counter_Value"])
+    return out
+
+
+def traffic_summary(fetch_dir, write_dir, copy_fetch_dir, copy_write_dir, copy_bytes, workload, algorithmic):
+    """HBM bytes of the last step-kernel dispatch from two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE; KiB per
+    dispatch), each scaled by bytes moved / counter reading of a plain device copy of copy_bytes."""
+    f, w = _counter_sums(fetch_dir), _counter_sums(write_dir)
+    cf, cw = _counter_sums(copy_fetch_dir), _counter_sums(copy_write_dir)
+    copies_f = [v for (_, n), v in cf.items() if "copyBuffer" in n]
+    copies_w = [v for (_, n), v in cw.items() if "copyBuffer" in n]
+    if not copies_f or not copies_w:
+        raise SystemExit("no copyBuffer dispatch in the calibration runs")
+    ff = copy_bytes / (1024 * float(np.mean(copies_f)))
+    wf = copy_bytes / (1024 * float(np.mean(copies_w)))
+    kf = max(k for k in f if k[1].startswith("ygg::"))
+    kw = max(k for k in w if k[1].startswith("ygg::"))
+    assert kf[1] == kw[1], (kf, kw)
+    fetched, written = f[kf] * 1024 * ff, w[kw] * 1024 * wf
+    doc = {"workload": workload, "kernel": kf[1], "fetch_size_kib": f[kf], "write_size_kib": w[kw],
+           "copy_calibration": {"bytes": copy_bytes, "fetch_size_kib": float(np.mean(copies_f)),
+                                "write_size_kib": float(np.mean(copies_w)), "fetch_factor": round(ff, 4),
+                                "write_factor": round(wf, 4)},
+           "hbm_bytes_per_launch": int(fetched + written), "fetched_bytes": int(fetched),
+           "written_bytes": int(written)}
+    if algorithmic:
+        doc["algorithmic_bytes_per_launch"] = int(algorithmic)
+        doc["traffic_over_algorithmic"] = round((fetched + written) / algorithmic, 3)
+    return doc
+
+
 def main():
+    if len(sys.argv) > 1 and sys.argv[1] == "--traffic":
+        # python bench.py --traffic FETCH_DIR WRITE_DIR COPY_FETCH_DIR COPY_WRITE_DIR COPY_BYTES BENCH_JSON OUT_JSON
+        fd, wd, cfd, cwd, cb, bj, out = sys.argv[2:9]
+        b = json.loads(Path(bj).read_text().strip().splitlines()[-1])
+        wl = b["config"]["workload"].split(" (")[0]
+        doc = traffic_summary(fd, wd, cfd, cwd, int(cb), wl, b["roofline"]["algorithmic_bytes_per_launch"])
+        if doc["kernel"] != b["roofline"]["kernel"]:
+            raise SystemExit(f"profiled kernel {doc['kernel']} is not the bench's {b['roofline']['kernel']}")
+        Path(out).write_text(json.dumps(doc, indent=1) + "\n")
+        print(json.dumps(doc))
+        return
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=5)
@@ -128,7 +181,7 @@ def main():
                                                                                       "ygg_bench")))
     ap.add_argument("--batch1-tokens", type=int, default=8192)
     ap.add_argument("--cpu-procs", type=int, default=16)
-    ap.add_argument("--cpu-streams", type=int, default=64, help="streams per CPU baseline process")
+    ap.add_argument("--cpu-streams", type=int, default=256, help="streams per CPU baseline process")
     ap.add_argument("--no-cpu", action="store_true")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -179,22 +232,32 @@ def main():
         f"{hist.max() / hist.sum():.4f}; compulsory {alg['per_token_compulsory']:.0f} B/token, per-stream "
         f"{alg['per_token_per_stream']:.0f} B/token")
 
-    # timed region: the zero fill of the state is part of each step (one 2 MB fill kernel)
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    # timed region: the zero fill of the state is part of each step (one 2 MB fill kernel); a second pair of events
+    # on the same stream brackets each step kernel alone, for its average duration
+    ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
+    e0, e1 = ev(), ev()
+    ks = [(ev(), ev()) for _ in range(a.steps)]
     torch.cuda.synchronize()
     e0.record(stream)
-    for _ in range(a.steps):
-        launch()
+    for k0, k1 in ks:
+        st.zero_()
+        k0.record(stream)
+        _lib.check(L.ygg_run(model._h, p(x), B, T, p(st), p(logits), None, None, None, sp))
+        k1.record(stream)
     e1.record(stream)
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / a.steps
+    kernel_ms = sum(k0.elapsed_time(k1) for k0, k1 in ks) / a.steps
     tokens_per_s = B * T / (ms / 1e3)
-    achieved = alg["compulsory"] / (ms / 1e3) / 1e9
-    log(f"{a.steps} steps: {ms:.3f} ms/step, {tokens_per_s / 1e6:.2f} M tokens/s, compulsory {achieved:.0f} GB/s "
-        f"({achieved / PEAK_HBM_GBS:.3f} of 8 TB/s), per-stream {alg['per_stream'] / (ms / 1e3) / 1e9:.0f} GB/s")
+    achieved = alg["compulsory"] / (kernel_ms / 1e3) / 1e9
+    log(f"{a.steps} steps: {ms:.3f} ms/step ({kernel_ms:.3f} ms in the step kernel), {tokens_per_s / 1e6:.2f} M "
+        f"tokens/s, compulsory {achieved:.0f} GB/s ({achieved / PEAK_HBM_GBS:.3f} of 8 TB/s), per-stream "
+        f"{alg['per_stream'] / (kernel_ms / 1e3) / 1e9:.0f} GB/s")
 
-    kernel = (f"ygg::fast_kernel<{info.d_state}, {info.n_layers}>" if info.kernel == 1 else
-              f"ygg::run_kernel<{info.d_state}, {info.block_size}, {info.readout_rank}>")
+    pipe = 0 < B <= info.pipe_max_streams and T > 1
+    kernel = (f"ygg::pipe_kernel<{info.d_state}, {info.n_layers}>" if pipe else
+              f"ygg::fast_kernel<{info.d_state}, {info.n_layers}, false>" if info.kernel == 1 else
+              f"ygg::run_kernel<{info.d_state}, {info.block_size}, {info.readout_rank}, false>")
     # HBM bytes per launch measured by rocprofv3 (FETCH_SIZE, WRITE_SIZE, copy-calibrated) for this workload and kernel
     traffic = None
     tf = ROOT / "profiles" / f"traffic_{w.name}.json"
@@ -235,8 +298,8 @@ def main():
                      "algorithmic_bytes_per_launch": alg["compulsory"],
                      "compulsory_bytes_per_token": round(alg["per_token_compulsory"], 1),
                      "per_stream_bytes_per_token": round(alg["per_token_per_stream"], 1),
-                     "per_stream_GBps": round(alg["per_stream"] / (ms / 1e3) / 1e9, 1),
-                     "kernel": kernel},
+                     "per_stream_GBps": round(alg["per_stream"] / (kernel_ms / 1e3) / 1e9, 1),
+                     "kernel": kernel, "kernel_ms": round(kernel_ms, 4)},
         "cpu_baseline": cpu,
         "batch1": batch1,
     }

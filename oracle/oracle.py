@@ -41,6 +41,8 @@ def lib():
         L.yo_info.argtypes = [vp, vp]
         L.yo_run.argtypes = [vp, vp, ctypes.c_int, ctypes.c_int, vp, vp, vp, vp, vp, ctypes.c_int, ctypes.c_char_p,
                              ctypes.c_int]
+        L.yo_run_sums.argtypes = [vp, vp, ctypes.c_int, ctypes.c_int, vp, vp, vp, ctypes.c_int, ctypes.c_char_p,
+                                  ctypes.c_int]
         _lib = L
     return _lib
 
@@ -103,6 +105,30 @@ class Oracle:
             if v is not None:
                 out[k] = v
         return out
+
+
+    def run_sums(self, tokens, state=None, threads=None):
+        """tokens (B, T) -> (digest (B,) uint64, lgsum (B,) uint64, final state): the digest of every leaf and state,
+        and the sum of the f32 bit patterns (as uint32) of every logit, per stream; nothing per token is kept, so it
+        runs at any size."""
+        x = np.ascontiguousarray(tokens, np.int32)
+        B, T = x.shape
+        st = np.zeros((B, self.n_layers, self.n), np.int8) if state is None else \
+            np.array(state, np.int8, copy=True, order="C")
+        dg = np.full(B, DIGEST_INIT, np.uint64)
+        ls = np.zeros(B, np.uint64)
+        err = ctypes.create_string_buffer(512)
+        th = threads or min(os.cpu_count() or 1, 16, max(B, 1))
+        rc = lib().yo_run_sums(self._h, _ptr(x), B, T, _ptr(st), _ptr(dg), _ptr(ls), th, err, 512)
+        if rc:
+            raise OracleError(rc, err.value.decode())
+        return dg, ls, st
+
+
+def logit_bits_sum(logits: np.ndarray) -> np.ndarray:
+    """Per stream, the sum of the f32 bit patterns (as uint32) of logits (B, T, V), as uint64."""
+    b = np.ascontiguousarray(logits, np.float32).view(np.uint32).astype(np.uint64)
+    return b.reshape(b.shape[0], -1).sum(-1, dtype=np.uint64)
 
 
 def digest_of(leaves: np.ndarray, states: np.ndarray, init=None) -> np.ndarray:

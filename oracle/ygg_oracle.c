@@ -339,6 +339,7 @@ typedef struct {
     int32_t *leaves;
     int8_t *states;
     uint64_t *digest;
+    uint64_t *lgsum;
 } job_t;
 
 static void *run_job(void *p) {
@@ -353,6 +354,15 @@ static void *run_job(void *p) {
             const size_t i = (size_t)s * j->T + t;
             step(m, q, j->tokens[i], lg, j->leaves ? j->leaves + i * L : NULL, j->digest ? &dg : NULL);
             if (j->logits) memcpy(j->logits + i * V, lg, sizeof(float) * V);
+            if (j->lgsum) {
+                uint64_t acc = 0;
+                for (int c = 0; c < V; c++) {
+                    uint32_t b;
+                    memcpy(&b, &lg[c], 4);
+                    acc += b;
+                }
+                j->lgsum[s] += acc;
+            }
             if (j->states) memcpy(j->states + i * L * n, q, (size_t)L * n);
         }
         if (j->digest) j->digest[s] = dg;
@@ -360,8 +370,9 @@ static void *run_job(void *p) {
     return NULL;
 }
 
-int yo_run(const yo_model *m, const int32_t *tokens, int B, int T, int8_t *state, float *logits, int32_t *leaves,
-           int8_t *states, uint64_t *digest, int threads, char *err, int errlen) {
+static int run_all(const yo_model *m, const int32_t *tokens, int B, int T, int8_t *state, float *logits,
+                   int32_t *leaves, int8_t *states, uint64_t *digest, uint64_t *lgsum, int threads, char *err,
+                   int errlen) {
     if (B < 0 || T < 0) { set_err(err, errlen, "negative B or T"); return YO_ERR_ARG; }
     for (size_t i = 0; i < (size_t)B * T; i++)
         if (tokens[i] < 0 || tokens[i] >= m->vocab) {
@@ -374,7 +385,7 @@ int yo_run(const yo_model *m, const int32_t *tokens, int B, int T, int8_t *state
     pthread_t *th = (pthread_t *)calloc((size_t)threads, sizeof(pthread_t));
     for (int k = 0; k < threads; k++) {
         jobs[k] = (job_t){m, tokens, B, T, (int)((long)B * k / threads), (int)((long)B * (k + 1) / threads),
-                          state, logits, leaves, states, digest};
+                          state, logits, leaves, states, digest, lgsum};
         if (threads > 1) pthread_create(&th[k], NULL, run_job, &jobs[k]);
         else run_job(&jobs[k]);
     }
@@ -383,6 +394,16 @@ int yo_run(const yo_model *m, const int32_t *tokens, int B, int T, int8_t *state
     free(jobs);
     free(th);
     return YO_OK;
+}
+
+int yo_run(const yo_model *m, const int32_t *tokens, int B, int T, int8_t *state, float *logits, int32_t *leaves,
+           int8_t *states, uint64_t *digest, int threads, char *err, int errlen) {
+    return run_all(m, tokens, B, T, state, logits, leaves, states, digest, NULL, threads, err, errlen);
+}
+
+int yo_run_sums(const yo_model *m, const int32_t *tokens, int B, int T, int8_t *state, uint64_t *digest,
+                uint64_t *lgsum, int threads, char *err, int errlen) {
+    return run_all(m, tokens, B, T, state, NULL, NULL, NULL, digest, lgsum, threads, err, errlen);
 }
 
 uint64_t yo_digest_init(void) { return YO_DIGEST_INIT; }

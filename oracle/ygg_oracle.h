@@ -28,6 +28,10 @@ int yo_info(const yo_model *m, int32_t *out12);
    digest (B) in/out (seed with yo_digest_init()) */
 int yo_run(const yo_model *m, const int32_t *tokens, int B, int T, int8_t *state, float *logits, int32_t *leaves,
            int8_t *states, uint64_t *digest, int threads, char *err, int errlen);
+/* Full-size checks: the digest (as yo_run) and lgsum (B) in/out, += the f32 bit patterns (as uint32) of every logit of
+   the stream's tokens, mod 2^64; no per-token outputs are kept. */
+int yo_run_sums(const yo_model *m, const int32_t *tokens, int B, int T, int8_t *state, uint64_t *digest,
+                uint64_t *lgsum, int threads, char *err, int errlen);
 uint64_t yo_digest_init(void);
 
 #ifdef __cplusplus

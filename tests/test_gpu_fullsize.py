@@ -1,0 +1,82 @@
+"""Parity at the benchmark configurations' full sizes: one ygg_run launch over all B streams x T tokens of
+configurations 2-5 (the launch bench.py times, with the kernel the library picks for it), checked against the C oracle
+over every stream and token through two size-independent sums: the digest of every leaf and int8 state (per stream,
+order-sensitive) and the sum of the f32 bit patterns of every logit (per stream). Both are exact integer checks: one
+differing leaf, state byte or logit bit changes them.
+
+Config 1 (one stream of 4096 tokens) is checked token by token in test_gpu_parity.py.
+"""
+import os
+import time
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from yggdrasil_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+def _model(cfg: int) -> Path:
+    w = synth.CONFIGS[cfg]
+    cache = Path(os.environ.get("YGG_BENCH_DIR", "/tmp/ygg_bench"))
+    cache.mkdir(parents=True, exist_ok=True)
+    p = cache / f"{w.name}_seed{w.model_seed}.bin"
+    if not p.exists():
+        tmp = p.with_suffix(".tmp")
+        synth.write_model(w.spec, w.model_seed, tmp)
+        os.replace(tmp, p)
+    return p
+
+
+def _gpu_sums(model, x: np.ndarray):
+    """One launch over all of x; per-stream digest and logit bit sums."""
+    import torch
+    B, T = x.shape
+    xt = torch.as_tensor(x, device=model.device).contiguous()
+    r = model.run(xt, digest=True)
+    torch.cuda.synchronize()
+    assert model.take_errors() == 0
+    lg = r["logits"]
+    sums = torch.empty(B, dtype=torch.int64, device=model.device)
+    step = max(1, (1 << 28) // max(1, T * model.vocab))
+    for b0 in range(0, B, step):
+        bits = lg[b0:b0 + step].view(torch.int32).to(torch.int64) & 0xFFFFFFFF
+        sums[b0:b0 + step] = bits.sum(dim=(1, 2))
+    torch.cuda.synchronize()
+    out = (r["digest"].cpu().numpy().view(np.uint64), sums.cpu().numpy().astype(np.uint64),
+           r["state"].cpu().numpy())
+    del r, lg
+    torch.cuda.empty_cache()
+    return out
+
+
+@pytest.mark.timeout(900)
+@pytest.mark.parametrize("cfg", [2, 3, 5, 4])
+def test_full_size_digest(cfg):
+    from yggdrasil_amd.inference import Yggdrasil
+    w = synth.CONFIGS[cfg]
+    path = _model(cfg)
+    x = w.make_tokens()
+    B, T = x.shape
+    model = Yggdrasil.load(path)
+    kind = ("pipe" if B <= model.info.pipe_max_streams else "fast") if model.info.kernel == 1 else "generic"
+    _say(f"config {cfg}: {B} x {T}, kernel {kind}")
+    t0 = time.time()
+    dg, ls, st = _gpu_sums(model, x)
+    model.close()
+    _say(f"config {cfg}: GPU done in {time.time() - t0:.1f}s; oracle on {min(os.cpu_count() or 1, 16)} threads")
+    t0 = time.time()
+    rdg, rls, rst = O.Oracle(path).run_sums(x)
+    _say(f"config {cfg}: oracle done in {time.time() - t0:.1f}s")
+    np.testing.assert_array_equal(st, rst)
+    bad = np.nonzero(dg != rdg)[0]
+    assert bad.size == 0, f"digest differs on {bad.size} of {B} streams, first {bad[:8].tolist()}"
+    bad = np.nonzero(ls != rls)[0]
+    assert bad.size == 0, f"logit sums differ on {bad.size} of {B} streams, first {bad[:8].tolist()}"

@@ -327,3 +327,18 @@ def test_sample_distribution(temperature, top_k):
     f_exp = np.append(p[big] * n, p[~big].sum() * n)
     keep = f_exp > 0
     assert stats.chisquare(f_obs[keep], f_exp[keep]).pvalue > 1e-3
+
+
+def test_run_sums_equal_run(tmp_path):
+    """The full-size checksum run equals the digest and the logit bit sums of the per-token run."""
+    spec = synth.KERNEL_CASES[3]
+    p = tmp_path / "m.bin"
+    synth.write_model(spec, synth.KERNEL_SEED, p)
+    o = O.Oracle(p)
+    x = synth.kernel_tokens(spec.vocab)
+    full = o.run(x, digest=True)
+    dg, ls, st = o.run_sums(x)
+    np.testing.assert_array_equal(dg, full["digest"])
+    np.testing.assert_array_equal(ls, O.logit_bits_sum(full["logits"]))
+    np.testing.assert_array_equal(st, full["state"])
+    assert (ls > 0).all()

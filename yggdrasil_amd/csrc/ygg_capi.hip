@@ -398,7 +398,24 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     }
     if (fast) launch = fast;
 
-    const RoundPlan rplan = round_plan(L > 1 ? fa.D : 0);
+    RoundPlan rplan = round_plan(L > 1 ? fa.D : 0);
+    // YGG_ROUNDS=h0,h1,...: an explicit plan for the specialised kernels (every round 1..4 levels, sum D)
+    if (const char *rs = getenv("YGG_ROUNDS"); rs && fast && L > 1 && strchr(rs, ',')) {
+        RoundPlan p;
+        int sum = 0;
+        bool ok = true;
+        for (const char *c = rs; *c && p.n < YGG_MAX_ROUNDS;) {
+            const int h = atoi(c);
+            ok = ok && h >= 1 && h <= 4;
+            p.h[p.n++] = h;
+            sum += h;
+            c = strchr(c, ',');
+            if (!c) break;
+            c++;
+        }
+        if (!ok || sum != fa.D) return fail(YGG_ERR_ARG, "YGG_ROUNDS=%s: not a plan for depth %d", rs, fa.D);
+        rplan = p;
+    }
     const int64_t slots = plan_slots(rplan);
     // device arena plan: every array 256-byte aligned
     struct Piece { size_t off, bytes; };

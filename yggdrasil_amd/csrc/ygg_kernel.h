@@ -270,7 +270,7 @@ constexpr unsigned long long kDigestCoord = 0x9E3779B97F4A7C15ull;
 
 // GEN: sample the next input from the logits of every token (io.gen), instead of reading it from tokens
 template <int N, int BLK, int R, bool GEN>
-__global__ __launch_bounds__(64) void run_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int T,
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void run_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int T,
                                                  int8_t *__restrict__ state, const YggIO io) {
     float *__restrict__ logits = io.logits;
     int32_t *__restrict__ leaves = io.leaves;

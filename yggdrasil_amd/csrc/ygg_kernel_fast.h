@@ -123,7 +123,8 @@ __device__ __forceinline__ int descend(const YggDevModel &m, const YggDevLayer &
     for (int rd = 1; rd < m.n_rounds; rd++) {
         const int h = m.round_h[rd];
         const int nn = (1 << h) - 1;
-        const int slot = base + ((ix - (1 << d0)) << h) + qj;
+        const int blk = base + ((ix - (1 << d0)) << h);
+        const int slot = blk + qj;
         int dot = 0;
         float th = 0.0f;
         if (qj < nn) {
@@ -135,8 +136,7 @@ __device__ __forceinline__ int descend(const YggDevModel &m, const YggDevLayer &
         }
         dot = sum4(dot);
         const bool right = (float)dot * rho > th;
-        const unsigned long long mask = __ballot(right && qk == 0 && qj < nn);
-        const int loc = walk_round(mask, h);
+        const int loc = walk_round(__ballot(right && qk == 0 && qj < nn), h);
         base += (1 << d0) << h;
         d0 += h;
         ix = (ix << h) + (loc - nn);
