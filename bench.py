@@ -72,7 +72,8 @@ def cpu_baseline(path: Path, tokens: np.ndarray, procs: int, streams_per_proc: i
     binary is absent or the host lacks AVX-512 VNNI."""
     from oracle import oracle as O
     B, T = tokens.shape
-    procs = max(1, min(procs, B // max(1, streams_per_proc)))
+    procs = max(1, min(procs, B))
+    streams_per_proc = max(1, min(streams_per_proc, B // procs))
     ref_ok = O.REF_YGG.exists() and "avx512_vnni" in cpu_flags()
     if ref_ok:
         with tempfile.TemporaryDirectory() as tmp:
