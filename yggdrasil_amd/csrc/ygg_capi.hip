@@ -548,7 +548,11 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     d.L = L; d.N = n; d.BLK = fa.blk; d.V = V; d.VP = VP; d.D = fa.D; d.E = E; d.R = R; d.R2 = R2; d.K = fa.K;
     d.shift = fa.shift;
     d.n_rounds = rplan.n;
-    for (int r = 0; r < YGG_MAX_ROUNDS; r++) d.round_h[r] = rplan.h[r];
+    d.round_pack = 0;
+    for (int r = 0; r < YGG_MAX_ROUNDS; r++) {
+        d.round_h[r] = rplan.h[r];
+        d.round_pack |= (uint64_t)(rplan.h[r] & 15) << (4 * r);
+    }
     d.output_bias = (const float *)at(p_bias);
     d.err = (uint32_t *)at(p_err);
     for (int l = 0; l < L; l++) {

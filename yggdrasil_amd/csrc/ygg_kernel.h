@@ -180,15 +180,32 @@ __device__ __forceinline__ int sample_token(const float (&lg)[4], int V, float t
 }
 
 // One round of the router descent from its ballot: node j of the round's subtree (breadth-first, j < 2^h - 1) goes
-// right when bit 4 j of mask is set; walk its h <= 4 levels from the root and return the node index reached, in
-// [2^h - 1, 2^(h+1) - 2]. Unrolled on 4 times the node index so that a level is a bit test and a shift-add.
+// right when bit 4 j of mask is set, and bits of nodes j >= 2^h - 1 are clear. Returns the node index reached after
+// h <= 4 levels, in [2^h - 1, 2^(h+1) - 2]. The walk always takes 4 levels on l4 = 4 node (a bit test, a select and
+// a shift-add in scalar registers per level); past level h it only goes left (clear bits), so
+// loc_h + 1 = (loc_4 + 1) >> (4 - h).
 __device__ __forceinline__ int walk_round(unsigned long long mask, int h) {
-    int l4 = 0;
-#pragma unroll
-    for (int lev = 0; lev < 4; lev++)
-        if (lev < h) l4 = 2 * l4 + (((mask >> l4) & 1ull) ? 8 : 4);
-    return l4 >> 2;
+    unsigned l4 = 0, t;
+    asm("s_bitcmp1_b64 %2, %0\n\t"
+        "s_cselect_b32 %1, 8, 4\n\t"
+        "s_lshl1_add_u32 %0, %0, %1\n\t"
+        "s_bitcmp1_b64 %2, %0\n\t"
+        "s_cselect_b32 %1, 8, 4\n\t"
+        "s_lshl1_add_u32 %0, %0, %1\n\t"
+        "s_bitcmp1_b64 %2, %0\n\t"
+        "s_cselect_b32 %1, 8, 4\n\t"
+        "s_lshl1_add_u32 %0, %0, %1\n\t"
+        "s_bitcmp1_b64 %2, %0\n\t"
+        "s_cselect_b32 %1, 8, 4\n\t"
+        "s_lshl1_add_u32 %0, %0, %1"
+        : "+s"(l4), "=&s"(t)
+        : "s"(mask)
+        : "scc");
+    return (int)(((l4 >> 2) + 1) >> (4 - h)) - 1;
 }
+
+// the lanes whose pred holds, as a wavefront-uniform 64-bit mask
+__device__ __forceinline__ unsigned long long lane_mask(bool pred) { return __builtin_amdgcn_ballot_w64(pred); }
 
 // _mm512_cvtps_epi32 in round-to-nearest-even: NaN and |x| >= 2^31 give INT32_MIN (cpu/ygg.cpp:292 and others)
 __device__ __forceinline__ int cvt_rne(float x) {
@@ -362,8 +379,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void ru
                     }
                     dot = sum4(dot);
                     const bool right = (float)dot * rho > th;
-                    const unsigned long long mask = __ballot(right && qk == 0 && qj < nn);
-                    const int loc = walk_round(mask, h);
+                    const int loc = walk_round(lane_mask(right && qk == 0 && qj < nn), h);
                     base += (1 << d0) << h;
                     d0 += h;
                     ix = (ix << h) + (loc - nn);

@@ -114,14 +114,13 @@ __device__ __forceinline__ int descend(const YggDevModel &m, const YggDevLayer &
         }
         dot = sum4(dot);
         const bool right = (float)dot * rho > th0;
-        const unsigned long long mask = __ballot(right && qk == 0 && qj < nn1);
-        const int loc = walk_round(mask, h1);
+        const int loc = walk_round(lane_mask(right && qk == 0 && qj < nn1), h1);
         ix = (1 << h1) + (loc - nn1);
     }
     const float *thr = y.thr + (size_t)x * y.thr_stride;
     int base = 1 << h1, d0 = h1;
     for (int rd = 1; rd < m.n_rounds; rd++) {
-        const int h = m.round_h[rd];
+        const int h = (m.round_pack >> (4 * rd)) & 15;
         const int nn = (1 << h) - 1;
         const int blk = base + ((ix - (1 << d0)) << h);
         const int slot = blk + qj;
@@ -136,7 +135,7 @@ __device__ __forceinline__ int descend(const YggDevModel &m, const YggDevLayer &
         }
         dot = sum4(dot);
         const bool right = (float)dot * rho > th;
-        const int loc = walk_round(__ballot(right && qk == 0 && qj < nn), h);
+        const int loc = walk_round(lane_mask(right && qk == 0 && qj < nn), h);
         base += (1 << d0) << h;
         d0 += h;
         ix = (ix << h) + (loc - nn);

@@ -71,6 +71,7 @@ struct YggDevLayer {
 struct YggDevModel {
     int32_t L, N, BLK, V, VP, D, E, R, R2, K, shift;
     int32_t n_rounds, round_h[YGG_MAX_ROUNDS];   // router descent plan
+    uint64_t round_pack;        // round_h[r] in bits 4 r .. 4 r + 3 (rounds 0 .. 15)
     const float *output_bias;   // [VP]
     uint32_t *err;              // error word (bit 0: token out of range)
     YggDevLayer layers[YGG_MAX_LAYERS];
