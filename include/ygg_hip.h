@@ -47,8 +47,8 @@ typedef struct {
     int32_t group;             /* group scales present */
     int32_t device;            /* HIP device holding the weights */
     int32_t kernel;            /* step kernel in use: 0 general, 1 specialised (readout rank 8, block 16, layer-input
-                                  rank <= 16, table storage, tensor scales, <= 4 layers); YGG_KERNEL=generic at load
-                                  time forces 0 */
+                                  rank 16, table storage, tensor scales, <= 4 layers, A16 entries <= 32639, each
+                                  layer's tables under 4 GiB); YGG_KERNEL=generic at load time forces 0 */
     int32_t pipe_max_streams;  /* ygg_run calls with B at most this and T > 1 use the layer-pipelined kernel (one
                                   wavefront per layer, for latency): its resident workgroups (one per stream) per CU
                                   times the CUs; 0: never. YGG_KERNEL=fast at load time disables

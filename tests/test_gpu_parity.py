@@ -63,7 +63,7 @@ def test_kernel_case(hip, model_dir, ci, kernel_env):
     x = synth.kernel_tokens(spec.vocab)
     ref = Oracle(path).run(x, states=True)
     model = hip.load(path)
-    common = spec.readout_rank == 8 and spec.block_size == 16 and spec.layer_input_rank <= 16 and \
+    common = spec.readout_rank == 8 and spec.block_size == 16 and (spec.layer_input_rank == 16 or spec.n_layers == 1) and \
         not spec.input_rank and not spec.group and spec.n_layers <= 4 and spec.d_state <= 128
     if common:
         _expect_kernel(model, kernel_env)

@@ -391,8 +391,10 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     const char *kenv = getenv("YGG_KERNEL");
     const std::string kmode = kenv ? kenv : "";
     ygg::Launcher fast = nullptr, pipe = nullptr;
-    if (kmode != "generic" && R == 8 && fa.blk == 16 && R2 <= 16 && !factored && !group && L <= 4 && VP <= 256 &&
-        transitions_split(fa, fl)) {
+    // (layer-input rank 16 exactly, and every routed layer's table and gather records addressable in 32 bits)
+    const bool small_tables = (int64_t)E * V * n * 2 < ((int64_t)1 << 32) && (int64_t)E * 64 * n < ((int64_t)1 << 32);
+    if (kmode != "generic" && R == 8 && fa.blk == 16 && (R2 == 16 || L == 1) && !factored && !group && L <= 4 &&
+        VP <= 256 && small_tables && transitions_split(fa, fl)) {
         fast = ygg::find_fast_launcher(n, L);
         if (kmode != "fast") pipe = ygg::find_pipe_launcher(n, L);
     }

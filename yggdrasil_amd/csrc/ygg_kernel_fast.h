@@ -1,4 +1,4 @@
-// Two kernels for the common shape: readout rank 8, block 16, layer-input rank <= 16, table storage, one scale per
+// Two kernels for the common shape: readout rank 8, block 16, layer-input rank 16, table storage, one scale per
 // tensor, at most 4 layers (every benchmark configuration). Same arithmetic and lane mapping as run_kernel
 // (ygg_kernel.h); the per-layer pieces below are shared by both.
 //
@@ -145,10 +145,10 @@ __device__ __forceinline__ int descend(const YggDevModel &m, const YggDevLayer &
 
 // the expert's whole gather record and table row, in one burst
 template <int N>
-__device__ __forceinline__ void gather(Gather<N> &G, const YggDevLayer &y, int r, int x, bool routed, int R2,
-                                       int lane) {
+__device__ __forceinline__ void gather(Gather<N> &G, const YggDevLayer &y, int r, int x, bool routed, int lane) {
     using F = Fast<N>;
-    const uint8_t *g = y.gath + (size_t)r * y.gath_bytes;
+    // a layer's records and tables lie within 4 GiB (checked at load): 32-bit offsets
+    const uint8_t *g = y.gath + (uint32_t)r * (uint32_t)y.gath_bytes;
     if (lane < F::NL) {
 #pragma unroll
         for (int c = 0; c < F::NA; c++) {
@@ -158,15 +158,14 @@ __device__ __forceinline__ void gather(Gather<N> &G, const YggDevLayer &y, int r
         if (routed) {
 #pragma unroll
             for (int k4 = 0; k4 < 4; k4++) {
-                if (k4 < R2 / 4) {
-                    uint32_t tmp[F::C];
-                    load_words<F::C, 4 * F::C>(tmp, g + y.off_U + ((size_t)(k4 * F::NL + lane) * F::C) * 4);
+                uint32_t tmp[F::C];
+                load_words<F::C, 4 * F::C>(tmp, g + y.off_U + ((k4 * F::NL + lane) * F::C) * 4);
 #pragma unroll
-                    for (int c = 0; c < F::C; c++) G.uw[k4][c] = tmp[c];
-                }
+                for (int c = 0; c < F::C; c++) G.uw[k4][c] = tmp[c];
             }
         }
-        const int16_t *tr = y.table + (size_t)r * y.table_sr + (size_t)x * y.table_sx + F::C * lane;
+        const int16_t *tr = y.table + ((uint32_t)r * (uint32_t)y.table_sr + (uint32_t)x * (uint32_t)y.table_sx) +
+                            F::C * lane;
 #pragma unroll
         for (int c = 0; c < F::C; c++) G.trow[c] = tr[c];
     }
@@ -204,8 +203,7 @@ __device__ __forceinline__ void layer_input(int8_t *zls, const int8_t *V0, const
 // with A16 = 256 hi + lo, so A16 q = 256 (hi q) + (lo q) exactly, two v_dot4 chains on the raw int8 state.
 template <int N>
 __device__ __forceinline__ void update(int (&qn)[Fast<N>::C], const Gather<N> &G, const int8_t *qold,
-                                       const int8_t *zls, const YggDevLayer &y, bool routed, int R2, int shift,
-                                       int lane) {
+                                       const int8_t *zls, const YggDevLayer &y, bool routed, int shift, int lane) {
     using F = Fast<N>;
     constexpr int BLK = F::BLK, C = F::C, RW = BLK / 4;     // dwords of one row's hi (and of its lo) bytes
     const int blk0 = (C * lane / BLK) * BLK;
@@ -222,17 +220,15 @@ __device__ __forceinline__ void update(int (&qn)[Fast<N>::C], const Gather<N> &G
         for (int i = 0; i < RW; i++) a = dot4(G.aw[c * 2 * RW + RW + i], qv[i], a);
         acc[c] = wadd((a + (1 << (shift - 1))) >> shift, G.trow[c]);
     }
-    if (routed && R2 > 0) {
+    if (routed) {
         int d[C];
 #pragma unroll
         for (int c = 0; c < C; c++) d[c] = 0;
 #pragma unroll
         for (int k4 = 0; k4 < 4; k4++) {
-            if (k4 < R2 / 4) {
-                const uint32_t zw = ((const uint32_t *)zls)[k4];
+            const uint32_t zw = ((const uint32_t *)zls)[k4];
 #pragma unroll
-                for (int c = 0; c < C; c++) d[c] = dot4(G.uw[k4][c], zw, d[c]);
-            }
+            for (int c = 0; c < C; c++) d[c] = dot4(G.uw[k4][c], zw, d[c]);
         }
 #pragma unroll
         for (int c = 0; c < C; c++) acc[c] = wadd(acc[c], cvt_rne((float)d[c] * y.layer_input_scale));
@@ -318,7 +314,7 @@ void fast_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
     // the wavefront index, stream, tokens and leaves are uniform over a wavefront: kept in scalar registers
     const int tid = threadIdx.x, wv = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int s = blockIdx.x * W + wv;
-    const int V = m.V, VP = m.VP, R2 = m.R2;
+    const int V = m.V, VP = m.VP;
     load_tables<N, L>(S, m, tid, 64 * W);
     __syncthreads();
     if (s >= B) return;
@@ -369,11 +365,11 @@ void fast_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
                 r = descend<N>(m, y, S.W[l - 1], th, qbw, rho, x, lane);
             }
             Gather<N> G;
-            gather<N>(G, y, r, x, l > 0, R2, lane);
-            if (l > 0 && R2 > 0) layer_input<N>(zls, S.V[l - 1], y, qbw, rho, lane);
+            gather<N>(G, y, r, x, l > 0, lane);
+            if (l > 0) layer_input<N>(zls, S.V[l - 1], y, qbw, rho, lane);
             wave_sync();
             int qn[F::C];
-            if (lane < F::NL) update<N>(qn, G, qs + l * N, zls, y, l > 0, R2, m.shift, lane);
+            if (lane < F::NL) update<N>(qn, G, qs + l * N, zls, y, l > 0, m.shift, lane);
             wave_sync();
             if (lane < F::NL) {
 #pragma unroll
@@ -439,7 +435,7 @@ void pipe_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
     // the wavefront's layer and the tokens are uniform over a wavefront: kept in scalar registers
     const int tid = threadIdx.x, l = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int s = blockIdx.x;
-    const int V = m.V, VP = m.VP, R2 = m.R2;
+    const int V = m.V, VP = m.VP;
     load_tables<N, L>(S, m, tid, 64 * L);
     const YggDevLayer &y = m.layers[l];
     int8_t *st = state + ((size_t)s * L + l) * N;
@@ -460,7 +456,7 @@ void pipe_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
         const int x0 = __builtin_amdgcn_readfirstlane(tok[0]);
         if (x0 >= 0 && x0 < V) {
             if (l > 0 && qj < nn1) th0 = y.thr[(size_t)x0 * y.thr_stride + qj];
-            if (l == 0) gather<N>(G0, y, x0, x0, false, R2, lane);
+            if (l == 0) gather<N>(G0, y, x0, x0, false, lane);
         }
     }
 
@@ -481,8 +477,8 @@ void pipe_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
                 if (l > 0) {
                     rho = below_and_rho<N>(qbw, qbuf[l - 1][t & 1], y.rms_eps, lane);
                     r = descend<N>(m, y, S.W[l - 1], th0, qbw, rho, x, lane);
-                    gather<N>(G, y, r, x, true, R2, lane);
-                    if (R2 > 0) layer_input<N>(zlw[l], S.V[l - 1], y, qbw, rho, lane);
+                    gather<N>(G, y, r, x, true, lane);
+                    layer_input<N>(zlw[l], S.V[l - 1], y, qbw, rho, lane);
                 } else {
                     G = G0;
                 }
@@ -490,13 +486,13 @@ void pipe_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
                     const int xn = __builtin_amdgcn_readfirstlane(tok[t + 1]);
                     if (xn >= 0 && xn < V) {
                         if (l > 0 && qj < nn1) th0 = y.thr[(size_t)xn * y.thr_stride + qj];
-                        if (l == 0) gather<N>(G0, y, xn, xn, false, R2, lane);
+                        if (l == 0) gather<N>(G0, y, xn, xn, false, lane);
                     }
                 }
                 wave_sync();
                 int qn[F::C];
                 if (lane < F::NL) {
-                    update<N>(qn, G, qbuf[l][(t + 1) & 1], zlw[l], y, l > 0, R2, m.shift, lane);
+                    update<N>(qn, G, qbuf[l][(t + 1) & 1], zlw[l], y, l > 0, m.shift, lane);
 #pragma unroll
                     for (int c = 0; c < F::C; c++) qbuf[l][t & 1][F::C * lane + c] = (int8_t)qn[c];
                 }
