@@ -55,6 +55,7 @@ template <int N, int L> struct SharedTables {
     int8_t Q[L][256 * 8];
     int8_t W[LR][15 * N];
     int8_t V[LR][16 * N];
+    float mv[LR][16];
 };
 
 template <int N, int L>
@@ -73,12 +74,9 @@ __device__ __forceinline__ void load_tables(SharedTables<N, L> &S, const YggDevM
         uint32_t *wd = (uint32_t *)S.W[l - 1];
         for (int i = tid; i < 15 * N / 4; i += nthreads) wd[i] = i < rows * N / 4 ? ws[i] : 0u;
         uint32_t *vd = (uint32_t *)S.V[l - 1];
-        if (m.R2 > 0) {
-            const uint32_t *vs = (const uint32_t *)y.vl;
-            for (int i = tid; i < 16 * N / 4; i += nthreads) vd[i] = vs[i];
-        } else {
-            for (int i = tid; i < 16 * N / 4; i += nthreads) vd[i] = 0u;
-        }
+        const uint32_t *vs = (const uint32_t *)y.vl;
+        for (int i = tid; i < 16 * N / 4; i += nthreads) vd[i] = vs[i];
+        if (tid < 16) S.mv[l - 1][tid] = y.mv[tid];
     }
 }
 
@@ -179,9 +177,10 @@ __device__ __forceinline__ void gather(Gather<N> &G, const YggDevLayer &y, int r
     }
 }
 
-// zl[k] = clamp(rint((f32(V'_k . q_below) m_v[k]) rho), +-127) into LDS (cpu/ygg.cpp:285-296)
+// zl[k] = clamp(rint((f32(V'_k . q_below) m_v[k]) rho), +-127) into LDS (cpu/ygg.cpp:285-296); V0 and mv0 are the
+// layer's V' rows and m_v in LDS
 template <int N>
-__device__ __forceinline__ void layer_input(int8_t *zls, const int8_t *V0, const YggDevLayer &y,
+__device__ __forceinline__ void layer_input(int8_t *zls, const int8_t *V0, const float *mv0,
                                             const uint32_t (&qbw)[Fast<N>::QW], float rho, int lane) {
     using F = Fast<N>;
     const int qk = lane & 3, qj = lane >> 2;
@@ -192,7 +191,7 @@ __device__ __forceinline__ void layer_input(int8_t *zls, const int8_t *V0, const
     for (int i = 0; i < F::QW; i++) a = dot4(vv[i], qbw[i], a);
     a = sum4(a);
     if (qk == 0) {
-        float zf = (float)a * y.mv[qj];
+        float zf = (float)a * mv0[qj];
         zf = zf * rho;
         zls[qj] = (int8_t)clamp127(cvt_rne(zf));
     }
@@ -366,7 +365,7 @@ void fast_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
             }
             Gather<N> G;
             gather<N>(G, y, r, x, l > 0, lane);
-            if (l > 0) layer_input<N>(zls, S.V[l - 1], y, qbw, rho, lane);
+            if (l > 0) layer_input<N>(zls, S.V[l - 1], S.mv[l - 1], qbw, rho, lane);
             wave_sync();
             int qn[F::C];
             if (lane < F::NL) update<N>(qn, G, qs + l * N, zls, y, l > 0, m.shift, lane);
@@ -478,7 +477,7 @@ void pipe_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
                     rho = below_and_rho<N>(qbw, qbuf[l - 1][t & 1], y.rms_eps, lane);
                     r = descend<N>(m, y, S.W[l - 1], th0, qbw, rho, x, lane);
                     gather<N>(G, y, r, x, true, lane);
-                    layer_input<N>(zlw[l], S.V[l - 1], y, qbw, rho, lane);
+                    layer_input<N>(zlw[l], S.V[l - 1], S.mv[l - 1], qbw, rho, lane);
                 } else {
                     G = G0;
                 }
