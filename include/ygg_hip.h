@@ -111,6 +111,49 @@ int ygg_generate(const ygg_model *m, const int32_t *d_first, int B, int n, int8_
    [0, vocab), bit 1 when ygg_score met a target outside it, since the last call. */
 int ygg_take_errors(const ygg_model *m, void *stream, uint32_t *errors);
 
+/* ---- The float step (yggdrasil/inference.py:42-74): the inference model of a float checkpoint (.npz), in f32 (the
+   serving precision of the Triton backend, yggdrasil/inference_triton.py) or f64 (the precision cpu/export.py
+   calibrates in). The host (Python) reads the checkpoint and precomputes T_r[x] and A_r as yggdrasil/inference.py:
+   145-155 does; every array below is row-major float64 on the host. */
+typedef struct ygg_fmodel ygg_fmodel;
+
+typedef struct {
+    const double *table;            /* token layer [V][n], row x = T_x[x]; routed [E][V][n] */
+    const double *transition;       /* [E][n/b][b][b] A_r, or NULL (experts without transitions) */
+    const double *readout;          /* [E][R][n] P_r */
+    const double *unembed;          /* [classes][R] Q */
+    const double *router_embed;     /* routed: [V][F] */
+    const double *router_weight;    /* routed: [2^D - 1][F + n] (router_state) or [2^D - 1][F] */
+    const double *router_bias;      /* routed: [2^D - 1] */
+    const double *layer_input_down; /* routed, R2 > 0: [R2][n] V' */
+    const double *layer_input_proj; /* routed, R2 > 0: [E][n][R2] U'_r */
+} ygg_float_layer;
+
+typedef struct {
+    int32_t n_layers, d_state, block_size, vocab, classes, router_depth, readout_rank, layer_input_rank;
+    int32_t router_token_dim;       /* F */
+    int32_t router_state;           /* 1: the router also reads rms(h_below) */
+    const double *output_bias;      /* [classes] */
+    ygg_float_layer layers[8];
+} ygg_float_desc;
+
+/* Copy a float model to `device` in `precision` 32 (f32) or 64 (f64). Limits: n <= 256 and a multiple of 16,
+   classes <= 256, R and R2 <= 64, F <= 256, D <= 20, <= 8 layers. */
+int ygg_float_load(const ygg_float_desc *desc, int precision, int device, ygg_fmodel **out);
+
+/* T tokens for each of B streams: d_state (B, L, n) in and out and d_logits (B, T, classes) in the model's precision
+   (float or double); d_leaves (B, T, L) int32 or NULL; d_stats (L x (3 + n/16 + R)) double or NULL, zero-filled by
+   the caller: per layer the running maxima of |h|, |V' rms(h_below)|, |P_r h|, |h| per 16 coordinates and |P_r h|
+   per row, the calibration statistics of cpu/export.py:117-153. A token outside [0, vocab) stops its stream and sets
+   bit 0 of the model's error word. */
+int ygg_float_run(const ygg_fmodel *m, const int32_t *d_tokens, int B, int T, void *d_state, void *d_logits,
+                  int32_t *d_leaves, double *d_stats, void *stream);
+
+/* Wait for `stream`, then return and clear the float model's error word (bit 0: a token outside [0, vocab)). */
+int ygg_float_take_errors(const ygg_fmodel *m, void *stream, uint32_t *errors);
+
+void ygg_float_free(ygg_fmodel *m);
+
 /* Message of the last failed call on this thread ("" if none). */
 const char *ygg_last_error(void);
 

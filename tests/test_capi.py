@@ -66,6 +66,14 @@ def test_bad_arguments(lib):
     assert L.ygg_step(None, None, None, None, None, None, 1, None) == 5
     assert L.ygg_take_errors(None, None, None) == 5
     assert L.ygg_generate(None, None, 1, 1, None, 0.0, 0, 0, None, None, None) == 5
+    assert L.ygg_float_load(None, 32, 0, ctypes.byref(h)) == 5
+    assert L.ygg_float_run(None, None, 1, 1, None, None, None, None, None) == 5
+    d = lib.FloatDesc()
+    assert L.ygg_float_load(ctypes.byref(d), 16, 0, ctypes.byref(h)) == 5      # precision
+    d.n_layers, d.d_state, d.block_size, d.vocab, d.classes, d.readout_rank = 2, 72, 8, 16, 16, 8
+    assert L.ygg_float_load(ctypes.byref(d), 32, 0, ctypes.byref(h)) == 3      # d_state not a multiple of 16
+    assert b"unsupported shape" in L.ygg_last_error()
+    L.ygg_float_free(None)
     assert L.ygg_load(b"/nonexistent/model.bin", 0, ctypes.byref(h)) == 1
     assert b"cannot open" in L.ygg_last_error()
     L.ygg_free(None)

@@ -54,7 +54,7 @@ def test_container_round_trip(tmp_path):
     # offsets are 64-aligned
     data = np.fromfile(path, np.uint8)
     base = fmt.round_up(fmt.HEADER_STRUCT.size + h["n_arrays"] * fmt.ENTRY_STRUCT.size, 64)
-    for a in mf.arrays.values():
+    for a in fmt.parse(data).arrays.values():       # views of `data`: offsets from its start
         assert (a.__array_interface__["data"][0] - data.__array_interface__["data"][0] - base) % 64 == 0
 
 

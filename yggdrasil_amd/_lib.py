@@ -15,10 +15,25 @@ LIB_PATH = Path(__file__).resolve().parent / "libygg_hip.so"
 
 # every entry point of include/ygg_hip.h
 SYMBOLS = ("ygg_load", "ygg_load_blob", "ygg_model_info", "ygg_free", "ygg_step", "ygg_run", "ygg_score",
-           "ygg_generate", "ygg_take_errors", "ygg_last_error", "ygg_version")
+           "ygg_generate", "ygg_take_errors", "ygg_float_load", "ygg_float_run", "ygg_float_take_errors",
+           "ygg_float_free", "ygg_last_error", "ygg_version")
 
 ERRORS = {1: "io", 2: "format", 3: "limits", 4: "nomem", 5: "arg", 6: "token", 7: "device"}
-ABI_VERSION = 5
+ABI_VERSION = 6
+
+
+class FloatLayer(ctypes.Structure):
+    """ygg_float_layer: host float64 arrays of one layer (NULL where absent)."""
+    _fields_ = [(name, ctypes.c_void_p) for name in (
+        "table", "transition", "readout", "unembed", "router_embed", "router_weight", "router_bias",
+        "layer_input_down", "layer_input_proj")]
+
+
+class FloatDesc(ctypes.Structure):
+    """ygg_float_desc."""
+    _fields_ = [(name, ctypes.c_int32) for name in (
+        "n_layers", "d_state", "block_size", "vocab", "classes", "router_depth", "readout_rank", "layer_input_rank",
+        "router_token_dim", "router_state")] + [("output_bias", ctypes.c_void_p), ("layers", FloatLayer * 8)]
 
 
 class YggInfo(ctypes.Structure):
@@ -60,6 +75,11 @@ def lib() -> ctypes.CDLL:
     L.ygg_score.argtypes = [vp, vp, vp, i32, i32, vp, vp, vp]
     L.ygg_generate.argtypes = [vp, vp, i32, i32, vp, ctypes.c_float, i32, ctypes.c_uint64, vp, vp, vp]
     L.ygg_take_errors.argtypes = [vp, vp, ctypes.POINTER(ctypes.c_uint32)]
+    L.ygg_float_load.argtypes = [ctypes.POINTER(FloatDesc), i32, i32, ctypes.POINTER(vp)]
+    L.ygg_float_run.argtypes = [vp, vp, i32, i32, vp, vp, vp, vp, vp]
+    L.ygg_float_take_errors.argtypes = [vp, vp, ctypes.POINTER(ctypes.c_uint32)]
+    L.ygg_float_free.argtypes = [vp]
+    L.ygg_float_free.restype = None
     L.ygg_last_error.argtypes = []
     L.ygg_last_error.restype = ctypes.c_char_p
     L.ygg_version.argtypes = []

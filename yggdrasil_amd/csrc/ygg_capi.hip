@@ -611,9 +611,14 @@ struct DeviceGuard {
 
 }  // namespace
 
+namespace ygg {
+// the thread's last error, for the other sources of the library
+int set_error(int code, const char *msg) { return fail(code, "%s", msg); }
+}  // namespace ygg
+
 extern "C" {
 
-int ygg_version(void) { return 5; }
+int ygg_version(void) { return 6; }
 
 const char *ygg_last_error(void) { return g_err.c_str(); }
 

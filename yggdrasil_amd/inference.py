@@ -60,11 +60,15 @@ class Yggdrasil:
     @classmethod
     def load(cls, path, backend: str = "hip", **kw):
         """From an int8 model file (YGG1, cpu/export.py). backend "hip": the fused gfx950 step; kw device, graph
-        (replay one captured step per batch size, as the Triton backend's cuda_graph)."""
+        (replay one captured step per batch size, as the Triton backend's cuda_graph). A float checkpoint (.npz) loads
+        the float step instead (yggdrasil_amd.float_model.FloatYggdrasil; kw device, precision 32 or 64)."""
         if backend != "hip":
             raise ValueError(f"backend {backend!r}: hip")
         if not Path(path).exists():
             raise FileNotFoundError(path)
+        if str(path).endswith(".npz"):
+            from .float_model import FloatYggdrasil
+            return FloatYggdrasil.load(path, backend=backend, **kw)
         try:
             _lib.lib()
         except ImportError as e:
