@@ -49,22 +49,46 @@ template <int N> struct Gather {
     int trow[Fast<N>::C];
 };
 
-// the workgroup's LDS copies of Q (all layers), V' and the first-round router rows (routed layers)
+// A quad lane's share of an n-byte row: for n = 128 the 16-byte chunks at qk 16 and 64 + qk 16, with LDS rows
+// kLdsRow = 192 bytes apart, so that the 16 quads of a wavefront reading 16 rows hit 64 distinct banks (contiguous
+// 32-byte quarters of 128-byte rows put rows j and j + 2 on the same banks); otherwise the contiguous quarter qk Q4.
+template <int N> constexpr int kLdsRow = N == 128 ? 192 : N;
+
+template <int N>
+__device__ __forceinline__ void quad_share(uint32_t (&w)[Fast<N>::QW], const int8_t *row, int qk) {
+    using F = Fast<N>;
+    if constexpr (N == 128) {
+        uint32_t a[4], b[4];
+        load_words<4, 16>(a, row + qk * 16);
+        load_words<4, 16>(b, row + 64 + qk * 16);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            w[i] = a[i];
+            w[4 + i] = b[i];
+        }
+    } else {
+        load_words<F::QW, F::QA>(w, row + qk * F::Q4);
+    }
+}
+
+// the workgroup's LDS copies of Q (all layers), V' and the first-round router rows (routed layers). Q is held in two
+// planes of 1 KiB: lane l's classes 4l, 4l + 1 at 16 l in plane 0 and 4l + 2, 4l + 3 at 16 l in plane 1.
 template <int N, int L> struct SharedTables {
     static constexpr int LR = L > 1 ? L - 1 : 1;
     int8_t Q[L][256 * 8];
-    int8_t W[LR][15 * N];
-    int8_t V[LR][16 * N];
+    int8_t W[LR][15 * kLdsRow<N>];
+    int8_t V[LR][16 * kLdsRow<N>];
     float mv[LR][16];
 };
 
 template <int N, int L>
 __device__ __forceinline__ void load_tables(SharedTables<N, L> &S, const YggDevModel &m, int tid, int nthreads) {
+    constexpr int RW = N / 4, SW = kLdsRow<N> / 4;   // dwords per row in memory and in LDS
 #pragma unroll
     for (int l = 0; l < L; l++) {
-        const uint32_t *src = (const uint32_t *)m.layers[l].Q;
-        uint32_t *dst = (uint32_t *)S.Q[l];
-        for (int i = tid; i < m.VP * 8 / 4; i += nthreads) dst[i] = src[i];
+        const uint4 *src = (const uint4 *)m.layers[l].Q;
+        uint4 *dst = (uint4 *)S.Q[l];
+        for (int k = tid; k < m.VP * 8 / 16; k += nthreads) dst[(k & 1) * 64 + (k >> 1)] = src[k];
     }
 #pragma unroll
     for (int l = 1; l < L; l++) {
@@ -72,10 +96,10 @@ __device__ __forceinline__ void load_tables(SharedTables<N, L> &S, const YggDevM
         const int rows = (1 << m.round_h[0]) - 1;     // the first round's block: slots 0 .. 2^h0 - 2
         const uint32_t *ws = (const uint32_t *)y.w;
         uint32_t *wd = (uint32_t *)S.W[l - 1];
-        for (int i = tid; i < 15 * N / 4; i += nthreads) wd[i] = i < rows * N / 4 ? ws[i] : 0u;
+        for (int i = tid; i < 15 * RW; i += nthreads) wd[(i / RW) * SW + i % RW] = i < rows * RW ? ws[i] : 0u;
         uint32_t *vd = (uint32_t *)S.V[l - 1];
         const uint32_t *vs = (const uint32_t *)y.vl;
-        for (int i = tid; i < 16 * N / 4; i += nthreads) vd[i] = vs[i];
+        for (int i = tid; i < 16 * RW; i += nthreads) vd[(i / RW) * SW + i % RW] = vs[i];
         if (tid < 16) S.mv[l - 1][tid] = y.mv[tid];
     }
 }
@@ -84,7 +108,7 @@ __device__ __forceinline__ void load_tables(SharedTables<N, L> &S, const YggDevM
 template <int N>
 __device__ __forceinline__ float below_and_rho(uint32_t (&qbw)[Fast<N>::QW], const int8_t *qb, float eps, int lane) {
     using F = Fast<N>;
-    load_words<F::QW, F::QA>(qbw, qb + (lane & 3) * F::Q4);
+    quad_share<N>(qbw, qb, lane & 3);
     // the 4 lanes of every quad hold the whole state between them: exact sum of squares by a quad sum
     int S = 0;
 #pragma unroll
@@ -106,7 +130,7 @@ __device__ __forceinline__ int descend(const YggDevModel &m, const YggDevLayer &
         int dot = 0;
         if (qj < nn1) {
             uint32_t wv[F::QW];
-            load_words<F::QW, F::QA>(wv, W0 + qj * N + qk * F::Q4);
+            quad_share<N>(wv, W0 + qj * kLdsRow<N>, qk);
 #pragma unroll
             for (int i = 0; i < F::QW; i++) dot = dot4(wv[i], qbw[i], dot);
         }
@@ -126,7 +150,7 @@ __device__ __forceinline__ int descend(const YggDevModel &m, const YggDevLayer &
         float th = 0.0f;
         if (qj < nn) {
             uint32_t wv[F::QW];
-            load_words<F::QW, F::QA>(wv, y.w + (size_t)slot * N + qk * F::Q4);
+            quad_share<N>(wv, y.w + (size_t)slot * N, qk);
             th = thr[slot];
 #pragma unroll
             for (int i = 0; i < F::QW; i++) dot = dot4(wv[i], qbw[i], dot);
@@ -185,7 +209,7 @@ __device__ __forceinline__ void layer_input(int8_t *zls, const int8_t *V0, const
     using F = Fast<N>;
     const int qk = lane & 3, qj = lane >> 2;
     uint32_t vv[F::QW];
-    load_words<F::QW, F::QA>(vv, V0 + qj * N + qk * F::Q4);
+    quad_share<N>(vv, V0 + qj * kLdsRow<N>, qk);
     int a = 0;
 #pragma unroll
     for (int i = 0; i < F::QW; i++) a = dot4(vv[i], qbw[i], a);
@@ -256,8 +280,14 @@ __device__ __forceinline__ void unembed_terms(float (&term)[4], const int8_t *zq
                                               int lane) {
     uint32_t zw[2];
     load_words<2, 16>(zw, zqs);
-    uint32_t qq[8];
-    load_words<8, 16>(qq, Qs + 4 * lane * 8);
+    uint32_t qq[8], q0[4], q1[4];
+    load_words<4, 16>(q0, Qs + 16 * lane);             // classes 4 lane, 4 lane + 1
+    load_words<4, 16>(q1, Qs + 1024 + 16 * lane);      // classes 4 lane + 2, 4 lane + 3
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        qq[i] = q0[i];
+        qq[4 + i] = q1[i];
+    }
 #pragma unroll
     for (int u = 0; u < 4; u++) {
         int d = dot4(qq[2 * u], zw[0], 0);
