@@ -117,11 +117,18 @@ __device__ __forceinline__ float below_and_rho(uint32_t (&qbw)[Fast<N>::QW], con
     return 1.0f / sqrtf((float)S * F::kInvN + eps);
 }
 
+// nothing to overlap with the first global router round
+struct NoHook {
+    __device__ __forceinline__ void operator()() const {}
+};
+
 // the router descent (cpu/ygg.cpp:271-280) -> leaf index; the first round from the LDS rows W0 and the thresholds
-// th0 (thr[x][slot qj] of that round, loaded by the caller), the others from global memory
-template <int N>
+// th0 (thr[x][slot qj] of that round, loaded by the caller), the others from global memory. hook() runs once, while
+// the loads of the first global round are in flight (or after the descent when there is no such round).
+template <int N, class Hook = NoHook>
 __device__ __forceinline__ int descend(const YggDevModel &m, const YggDevLayer &y, const int8_t *W0, float th0,
-                                       const uint32_t (&qbw)[Fast<N>::QW], float rho, int x, int lane) {
+                                       const uint32_t (&qbw)[Fast<N>::QW], float rho, int x, int lane,
+                                       Hook hook = Hook()) {
     using F = Fast<N>;
     const int qk = lane & 3, qj = lane >> 2;
     const int h1 = m.round_h[0], nn1 = (1 << h1) - 1;
@@ -145,13 +152,17 @@ __device__ __forceinline__ int descend(const YggDevModel &m, const YggDevLayer &
         const int h = (m.round_pack >> (4 * rd)) & 15;
         const int nn = (1 << h) - 1;
         const int blk = base + ((ix - (1 << d0)) << h);
+        // only the quads of the round's nodes load (a quad past them would fetch another cache line)
         const int slot = blk + qj;
-        int dot = 0;
+        uint32_t wv[F::QW];
         float th = 0.0f;
         if (qj < nn) {
-            uint32_t wv[F::QW];
             quad_share<N>(wv, y.w + (size_t)slot * N, qk);
             th = thr[slot];
+        }
+        if (rd == 1) hook();
+        int dot = 0;
+        if (qj < nn) {
 #pragma unroll
             for (int i = 0; i < F::QW; i++) dot = dot4(wv[i], qbw[i], dot);
         }
@@ -162,6 +173,7 @@ __device__ __forceinline__ int descend(const YggDevModel &m, const YggDevLayer &
         d0 += h;
         ix = (ix << h) + (loc - nn);
     }
+    if (m.n_rounds == 1) hook();
     return ix - m.E;
 }
 
@@ -260,19 +272,20 @@ __device__ __forceinline__ void update(int (&qn)[Fast<N>::C], const Gather<N> &G
     for (int c = 0; c < C; c++) qn[c] = sat8(acc[c]);
 }
 
-// zq[j] = clamp(rint(f32(P_r q) m_z), +-127) into LDS (cpu/ygg.cpp:395-420); qnew is the new state (LDS)
+// zq[j] = clamp(rint(f32(P_r q) m_z), +-127) into LDS (cpu/ygg.cpp:395-420); pw the lane's P granules, qnew the new
+// state (LDS)
 template <int N>
-__device__ __forceinline__ void readout(int8_t *zqs, const Gather<N> &G, const int8_t *qnew, const YggDevLayer &y,
-                                        int lane) {
+__device__ __forceinline__ void readout(int8_t *zqs, const uint32_t (&pw)[Fast<N>::SPW], const int8_t *qnew,
+                                        float readout_scale, int lane) {
     using F = Fast<N>;
     const int rj = lane / F::RL, rk = lane % F::RL;
     uint32_t qv[F::SPW];
     load_words<F::SPW, F::SPA>(qv, qnew + rk * F::SP);
     int z = 0;
 #pragma unroll
-    for (int i = 0; i < F::SPW; i++) z = dot4(G.pw[i], qv[i], z);
+    for (int i = 0; i < F::SPW; i++) z = dot4(pw[i], qv[i], z);
     z = group_sum<F::RL>(z);
-    if (rk == 0) zqs[rj] = (int8_t)clamp127(cvt_rne((float)z * y.readout_scale));
+    if (rk == 0) zqs[rj] = (int8_t)clamp127(cvt_rne((float)z * readout_scale));
 }
 
 // f32(Q zq) s_q for the 4 classes of this lane (cpu/ygg.cpp:421-434)
@@ -379,6 +392,27 @@ void fast_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
 #pragma unroll
         for (int u = 0; u < 4; u++) lg[u] = 4 * lane + u < VP ? m.output_bias[4 * lane + u] : 0.0f;
 
+        // The readout of layer l (P_r q -> zq -> Q zq into the logits) is not on the path to layer l + 1, which needs
+        // only the new state: it runs while the loads of layer l + 1's first global router round are in flight
+        // (pl: the layer whose readout is pending, ppw: its P granules). The logits still add layer by layer in order.
+        uint32_t ppw[F::SPW];
+        int pl = -1;
+        auto flush = [&]() {
+            if (pl >= 0) {
+                const YggDevLayer &yp = m.layers[pl];
+                readout<N>(zqs, ppw, qs + pl * N, yp.readout_scale, lane);
+                wave_sync();
+                if (4 * lane < VP) {
+                    float term[4];
+                    unembed_terms(term, zqs, S.Q[pl], yp.unembed_scale, lane);
+#pragma unroll
+                    for (int u = 0; u < 4; u++) lg[u] = lg[u] + term[u];
+                }
+                wave_sync();
+                pl = -1;
+            }
+        };
+
         // not unrolled: an unrolled loop keeps every layer's pointers in scalar registers at once and spills them
 #pragma unroll 1
         for (int l = 0; l < L; l++) {
@@ -391,7 +425,7 @@ void fast_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
 #pragma unroll
                 for (int i = 1; i < LR; i++) th = l - 1 == i ? th1[i] : th;
                 rho = below_and_rho<N>(qbw, qs + (l - 1) * N, y.rms_eps, lane);
-                r = descend<N>(m, y, S.W[l - 1], th, qbw, rho, x, lane);
+                r = descend<N>(m, y, S.W[l - 1], th, qbw, rho, x, lane, flush);
             }
             Gather<N> G;
             gather<N>(G, y, r, x, l > 0, lane);
@@ -405,17 +439,12 @@ void fast_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
                 for (int c = 0; c < F::C; c++) qs[l * N + F::C * lane + c] = (int8_t)qn[c];
             }
             wave_sync();
-            readout<N>(zqs, G, qs + l * N, y, lane);
-            wave_sync();
-            if (4 * lane < VP) {
-                float term[4];
-                unembed_terms(term, zqs, S.Q[l], y.unembed_scale, lane);
-#pragma unroll
-                for (int u = 0; u < 4; u++) lg[u] = lg[u] + term[u];
-            }
             if (leaves && lane == 0) leaves[((size_t)s * T + t) * L + l] = r;
             if (digest) dg = dg * kDigestMul + digest_term<N>(qn, r, l, lane);
-            wave_sync();
+#pragma unroll
+            for (int i = 0; i < F::SPW; i++) ppw[i] = G.pw[i];
+            pl = l;
+            if (l == L - 1) flush();
         }
 
         if (logits) store_logits(logits + ((size_t)s * T + t) * V, lg, V, lane);
@@ -526,7 +555,7 @@ void pipe_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
                     for (int c = 0; c < F::C; c++) qbuf[l][t & 1][F::C * lane + c] = (int8_t)qn[c];
                 }
                 wave_sync();
-                readout<N>(zqw[l], G, qbuf[l][t & 1], y, lane);
+                readout<N>(zqw[l], G.pw, qbuf[l][t & 1], y.readout_scale, lane);
                 wave_sync();
                 float *lr = lgs[t % L];
                 if (4 * lane < VP) {
