@@ -90,6 +90,9 @@ def test_malformed_files(lib, tmp_path):
         "truncated": (data[:len(data) // 2], 2, b"short model file"),
         "d_state": (data[:8] + np.int32(72).tobytes() + data[12:], 3, b"LIMITS"),
         "missing": (data[:i] + b"l1_X" + data[i + 4:], 2, b"missing l1_w"),
+        # an entry whose offset + bytes overflows int64 must not pass the bounds check
+        "overflow": (data[:52 + 32] + np.int64(1 << 62).tobytes() + np.int64(1 << 62).tobytes() + data[52 + 48:], 2,
+                     b"short model file (array"),
     }
     h = ctypes.c_void_p()
     for name, (blob, code, msg) in bad.items():

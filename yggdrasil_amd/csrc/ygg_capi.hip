@@ -82,7 +82,7 @@ int parse(const uint8_t *data, size_t size, FileArrays &fa) {
         memcpy(name, data + 52 + (size_t)i * 48, 32);
         memcpy(&off, data + 52 + (size_t)i * 48 + 32, 8);
         memcpy(&nb, data + 52 + (size_t)i * 48 + 40, 8);
-        if (off < 0 || nb < 0 || off + nb > fa.bytes)
+        if (off < 0 || nb < 0 || off > fa.bytes || nb > fa.bytes - off)
             return fail(YGG_ERR_FORMAT, "short model file (array %s)", name);
         fa.arr[name] = {data + base + off, nb};
     }
