@@ -352,9 +352,23 @@ def run_batch1(model, w, n_tok: int, L, _lib) -> dict:
     torch.cuda.synchronize()
     graph_us = e0.elapsed_time(e1) * 1e3 / n_tok
     same = bool(torch.equal(lg, ref_logits))
+    # (c) greedy generation on the device: one ygg_generate launch samples n_tok tokens, each fed back as the next
+    # input, so no two layers of different tokens overlap (each token waits for the last layer of the one before)
+    out = torch.empty(1, n_tok, dtype=torch.int32, device=dev)
+    st.zero_()
+    _lib.check(L.ygg_generate(model._h, ptr(x1), 1, 64, ptr(st), ctypes.c_float(0.0), 0, ctypes.c_uint64(0),
+                              ptr(out), None, sp))
+    st.zero_()
+    torch.cuda.synchronize()
+    e0.record(stream)
+    _lib.check(L.ygg_generate(model._h, ptr(x1), 1, n_tok, ptr(st), ctypes.c_float(0.0), 0, ctypes.c_uint64(0),
+                              ptr(out), None, sp))
+    e1.record(stream)
+    torch.cuda.synchronize()
+    gen_us = e0.elapsed_time(e1) * 1e3 / n_tok
     return {"tokens": n_tok, "us_per_token_persistent_launch": round(run_us, 3),
             "us_per_token_graph_step": round(graph_us, 3), "graph_steps_per_graph": G,
-            "graph_logits_equal_persistent": same}
+            "graph_logits_equal_persistent": same, "us_per_token_generate_greedy": round(gen_us, 3)}
 
 
 if __name__ == "__main__":

@@ -83,7 +83,8 @@ template <int N, int L> struct SharedTables {
 
 template <int N, int L>
 __device__ __forceinline__ void load_tables(SharedTables<N, L> &S, const YggDevModel &m, int tid, int nthreads) {
-    constexpr int RW = N / 4, SW = kLdsRow<N> / 4;   // dwords per row in memory and in LDS
+    // 16-byte chunks: RC per row in memory, SC per row in LDS
+    constexpr int RC = N / 16, SC = kLdsRow<N> / 16;
 #pragma unroll
     for (int l = 0; l < L; l++) {
         const uint4 *src = (const uint4 *)m.layers[l].Q;
@@ -94,12 +95,13 @@ __device__ __forceinline__ void load_tables(SharedTables<N, L> &S, const YggDevM
     for (int l = 1; l < L; l++) {
         const YggDevLayer &y = m.layers[l];
         const int rows = (1 << m.round_h[0]) - 1;     // the first round's block: slots 0 .. 2^h0 - 2
-        const uint32_t *ws = (const uint32_t *)y.w;
-        uint32_t *wd = (uint32_t *)S.W[l - 1];
-        for (int i = tid; i < 15 * RW; i += nthreads) wd[(i / RW) * SW + i % RW] = i < rows * RW ? ws[i] : 0u;
-        uint32_t *vd = (uint32_t *)S.V[l - 1];
-        const uint32_t *vs = (const uint32_t *)y.vl;
-        for (int i = tid; i < 16 * RW; i += nthreads) vd[(i / RW) * SW + i % RW] = vs[i];
+        const uint4 *ws = (const uint4 *)y.w;
+        uint4 *wd = (uint4 *)S.W[l - 1];
+        for (int k = tid; k < 15 * RC; k += nthreads)
+            wd[(k / RC) * SC + k % RC] = k < rows * RC ? ws[k] : make_uint4(0u, 0u, 0u, 0u);
+        uint4 *vd = (uint4 *)S.V[l - 1];
+        const uint4 *vs = (const uint4 *)y.vl;
+        for (int k = tid; k < 16 * RC; k += nthreads) vd[(k / RC) * SC + k % RC] = vs[k];
         if (tid < 16) S.mv[l - 1][tid] = y.mv[tid];
     }
 }
