@@ -73,6 +73,14 @@ def test_bad_arguments(lib):
     d.n_layers, d.d_state, d.block_size, d.vocab, d.classes, d.readout_rank = 2, 72, 8, 16, 16, 8
     assert L.ygg_float_load(ctypes.byref(d), 32, 0, ctypes.byref(h)) == 3      # d_state not a multiple of 16
     assert b"unsupported shape" in L.ygg_last_error()
+    # a missing array is reported before any device is touched
+    d.d_state, d.router_depth, d.router_token_dim, d.router_state = 64, 2, 4, 1
+    assert L.ygg_float_load(ctypes.byref(d), 32, 0, ctypes.byref(h)) == 5
+    assert b"output_bias is NULL" in L.ygg_last_error()
+    ob = np.zeros(16)
+    d.output_bias = ob.ctypes.data
+    assert L.ygg_float_load(ctypes.byref(d), 64, 0, ctypes.byref(h)) == 5
+    assert b"layer 0 lacks an array" in L.ygg_last_error() and not h.value
     L.ygg_float_free(None)
     assert L.ygg_load(b"/nonexistent/model.bin", 0, ctypes.byref(h)) == 1
     assert b"cannot open" in L.ygg_last_error()

@@ -14,6 +14,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
+#include <new>
 #include <string>
 #include <vector>
 
@@ -264,7 +265,8 @@ template <typename T> int upload(const ygg_float_desc *d, int device, ygg_fmodel
         total += ((size_t)count * sizeof(T) + 255) / 256 * 256;
         return (int)parts.size() - 1;
     };
-    int ob = add(d->output_bias, C);
+    const int ob = add(d->output_bias, C);
+    if (ob < 0) return fail(YGG_ERR_ARG, "float model: output_bias is NULL");
     struct Idx { int table, A, P, Q, emb, W, bias, Vd, Up; };
     std::vector<Idx> idx(L);
     for (int l = 0; l < L; l++) {
@@ -284,7 +286,16 @@ template <typename T> int upload(const ygg_float_desc *d, int device, ygg_fmodel
             (l && R2 && (k.Vd < 0 || k.Up < 0)))
             return fail(YGG_ERR_ARG, "float model: layer %d lacks an array", l);
     }
-    std::vector<uint8_t> host(total, 0);
+    // the description is checked before any device is touched
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= 0) return fail(YGG_ERR_DEVICE, "no HIP device");
+    if (device < 0 || device >= ndev) return fail(YGG_ERR_ARG, "device %d out of range", device);
+    std::vector<uint8_t> host;
+    try {
+        host.assign(total, 0);
+    } catch (const std::bad_alloc &) {
+        return fail(YGG_ERR_NOMEM, "float model: %zu bytes of host staging", total);
+    }
     for (const Part &p : parts) {
         T *dst = (T *)(host.data() + p.off);
         for (int64_t i = 0; i < p.count; i++) dst[i] = (T)p.src[i];
@@ -330,9 +341,6 @@ int ygg_float_load(const ygg_float_desc *d, int precision, int device, ygg_fmode
         d->router_depth > 20 || d->router_token_dim < 0 || d->router_token_dim > kMaxF)))
         return fail(YGG_ERR_LIMITS, "float model: unsupported shape (L %d, n %d, b %d, classes %d, R %d, R2 %d, D %d)",
                     L, n, b, d->classes, d->readout_rank, d->layer_input_rank, d->router_depth);
-    int ndev = 0;
-    if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= 0) return fail(YGG_ERR_DEVICE, "no HIP device");
-    if (device < 0 || device >= ndev) return fail(YGG_ERR_ARG, "device %d out of range", device);
     ygg_fmodel *fm = new ygg_fmodel();
     fm->device = device;
     fm->precision = precision;
