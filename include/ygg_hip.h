@@ -49,10 +49,16 @@ typedef struct {
     int32_t kernel;            /* step kernel in use: 0 general, 1 specialised (readout rank 8, block 16, layer-input
                                   rank 16, table storage, tensor scales, <= 4 layers, A16 entries <= 32639, each
                                   layer's tables under 4 GiB); YGG_KERNEL=generic at load time forces 0 */
-    int32_t pipe_max_streams;  /* ygg_run calls with B at most this and T > 1 use the layer-pipelined kernel (one
-                                  wavefront per layer, for latency): its resident workgroups (one per stream) per CU
-                                  times the CUs; 0: never. YGG_KERNEL=fast at load time disables
+    int32_t pipe_max_streams;  /* ygg_run/ygg_score calls with B at most this and T > 1 use the layer-pipelined kernel
+                                  (one wavefront per layer, for latency): its resident workgroups (one per stream)
+                                  per CU times the CUs; 0: never. YGG_KERNEL=fast or =deep at load time disables
                                   it, =pipe uses it for every call */
+    int32_t deep;              /* 1: the model's router plan allows the deep descent (2 to 4 rounds, the first of at
+                                  least 2 levels, the third and fourth at most 6 levels together) and it is on
+                                  (YGG_DEEP=0 at load time turns it off) */
+    int32_t deep_max_streams;  /* ygg_generate calls of at least 8 tokens with B at most this (the CUs) use the
+                                  one-stream-per-workgroup kernel with the deep descent; 0: never. YGG_KERNEL=deep
+                                  uses it for every call */
     int64_t file_array_bytes;  /* bytes of the file's arrays (the reference's Model::bytes, cpu/ygg.cpp:158, 167) */
     int64_t device_bytes;      /* device memory held by the model */
     int64_t gather_bytes[8];   /* per layer: bytes of one expert's transition, layer-input and readout weights */

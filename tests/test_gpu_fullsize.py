@@ -80,3 +80,63 @@ def test_full_size_digest(cfg):
     assert bad.size == 0, f"digest differs on {bad.size} of {B} streams, first {bad[:8].tolist()}"
     bad = np.nonzero(ls != rls)[0]
     assert bad.size == 0, f"logit sums differ on {bad.size} of {B} streams, first {bad[:8].tolist()}"
+
+
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("cfg", [3, 4])
+def test_few_streams_full_model(cfg, monkeypatch):
+    """The few-stream kernels on the full configuration 3 and 4 models (D = 13 and 14: the deep descent ends in one
+    round of 63 nodes): 6 streams x 40 tokens through the kernel the library picks (layer-pipelined) and greedy
+    generation (the deep kernel), then through the deep kernel forced for every call (one launch, launches of 3
+    tokens, a step loop). Every leaf, state after every token, logit and generated token equals the oracle's."""
+    import torch
+    from yggdrasil_amd.inference import Yggdrasil
+    w = synth.CONFIGS[cfg]
+    path = _model(cfg)
+    x = w.make_tokens(6, 40)
+    orc = O.Oracle(path)
+    ref = orc.run(x, states=True)
+
+    def same(got, what):
+        for k in ("leaves", "states", "logits"):
+            a, b = got[k], ref[k][:, :got[k].shape[1]]
+            assert np.array_equal(a, b), f"config {cfg} {what}: {k} differs at {np.argwhere(a != b)[:4].tolist()}"
+
+    monkeypatch.delenv("YGG_DEEP", raising=False)
+    for k in ("auto", "deep"):
+        if k == "auto":
+            monkeypatch.delenv("YGG_KERNEL", raising=False)
+        else:
+            monkeypatch.setenv("YGG_KERNEL", k)
+        model = Yggdrasil.load(path)
+        assert model.info.deep == 1 and model.info.kernel == 1 and model.info.deep_max_streams > 0
+        _say(f"config {cfg}: 6 x 40, kernel {k}, pipe_max {model.info.pipe_max_streams}, "
+             f"deep_max {model.info.deep_max_streams}")
+        r = model.run(x, leaves=True, states=True)
+        torch.cuda.synchronize()
+        same({key: v.cpu().numpy() for key, v in r.items()}, f"{k} one launch")
+        if k == "auto":
+            # greedy generation of 12 tokens after a 4-token prompt: the oracle's argmax loop
+            out = model.generate(x[:, :4], 12, temperature=0)
+            r0 = orc.run(x[:, :4])
+            lg, st = r0["logits"][:, -1], r0["state"]
+            for i in range(12):
+                tok = lg.argmax(-1).astype(np.int32)
+                assert np.array_equal(out[:, 4 + i], tok), (cfg, i)
+                r1 = orc.run(tok[:, None], state=st)
+                lg, st = r1["logits"][:, 0], r1["state"]
+        else:
+            parts, st = [], None
+            for t0 in range(0, 39, 3):
+                rr = model.run(x[:, t0:t0 + 3], state=st, leaves=True, states=True)
+                parts.append({key: v.cpu().numpy() for key, v in rr.items()})
+                st = rr["state"]
+            same({key: np.concatenate([p[key] for p in parts], 1) for key in ("leaves", "states", "logits")},
+                 "deep 3-token launches")
+            st = model.init_state(6)
+            for t in range(6):
+                lg, st = model.step(x[:, t], st)
+                assert np.array_equal(lg.cpu().numpy(), ref["logits"][:, t]), (cfg, t)
+                assert np.array_equal(st.cpu().numpy(), ref["states"][:, t]), (cfg, t)
+        model.close()
+        torch.cuda.empty_cache()

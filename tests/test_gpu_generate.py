@@ -20,10 +20,12 @@ def _say(msg):
     print(msg, flush=True)
 
 
-@pytest.fixture(params=["fast", "generic"])
+@pytest.fixture(params=["fast", "deep", "generic"])
 def kernel_env(request, monkeypatch):
-    """Generation runs on the per-stream kernels only (the layer-pipelined one overlaps tokens): force each."""
+    """Generation runs on the per-stream kernels only (the layer-pipelined one overlaps tokens): force each (deep: one
+    stream per workgroup with the deep router descent, which the library picks for few streams)."""
     monkeypatch.setenv("YGG_KERNEL", request.param)
+    monkeypatch.delenv("YGG_DEEP", raising=False)
     return request.param
 
 
@@ -39,7 +41,8 @@ def gmodel(model_dir):
 def _load(path, kernel_env):
     from yggdrasil_amd.inference import Yggdrasil
     m = Yggdrasil.load(path)
-    assert m.info.kernel == (1 if kernel_env == "fast" else 0), m.info.kernel
+    assert m.info.kernel == (0 if kernel_env == "generic" else 1), m.info.kernel
+    assert (m.info.deep_max_streams > 0) == (kernel_env in ("deep", "auto")), m.info.deep_max_streams
     return m
 
 
@@ -112,12 +115,13 @@ def test_generate_sampled_replays_through_oracle(gmodel, kernel_env, temperature
     model.close()
 
 
-def test_generate_distribution(gmodel):
+def test_generate_distribution(gmodel, monkeypatch):
     """16384 streams from one prompt, one draw each: frequencies follow softmax(logits / T) over the top_k."""
     import torch
     from scipy import stats
     _say("distribution")
-    model = _load(gmodel, "fast")
+    monkeypatch.delenv("YGG_KERNEL", raising=False)
+    model = _load(gmodel, "auto")
     B = 16384
     prompt = np.tile(synth.zipf_bytes(1, 6, 8), (B, 1))
     for temperature, top_k in ((0.8, 0), (1.2, 6)):
@@ -138,11 +142,12 @@ def test_generate_distribution(gmodel):
     model.close()
 
 
-def test_generate_errors(gmodel):
+def test_generate_errors(gmodel, monkeypatch):
     import ctypes
     import torch
     from yggdrasil_amd import _lib
-    model = _load(gmodel, "fast")
+    monkeypatch.delenv("YGG_KERNEL", raising=False)
+    model = _load(gmodel, "auto")
     with pytest.raises(ValueError):
         model.generate([1, 2], 3, temperature=-1)
     with pytest.raises(ValueError):

@@ -39,11 +39,14 @@ def _compare(got, ref, keys=("leaves", "states", "logits")):
                                  f"gpu {a[tuple(bad[0])]} oracle {b[tuple(bad[0])]}")
 
 
-@pytest.fixture(params=["pipe", "fast", "generic"])
+@pytest.fixture(params=["pipe", "fast", "deep", "generic"])
 def kernel_env(request, monkeypatch):
-    """Load models with one kernel forced (YGG_KERNEL): the layer-pipelined one, the specialised per-stream one, or
-    the general one; the first two apply only to the common shape (readout rank 8, block 16, ...)."""
+    """Load models with one kernel forced for every call (YGG_KERNEL): the layer-pipelined one, the specialised
+    per-stream one (4 streams per workgroup), its one-stream-per-workgroup form with the deep router descent (deep:
+    models whose router plan allows it, else the per-stream one), or the general one; all but the last apply only to
+    the common shape (readout rank 8, block 16, ...)."""
     monkeypatch.setenv("YGG_KERNEL", request.param)
+    monkeypatch.delenv("YGG_DEEP", raising=False)
     return request.param
 
 
@@ -68,7 +71,7 @@ def test_kernel_case(hip, model_dir, ci, kernel_env):
     if common:
         _expect_kernel(model, kernel_env)
     else:
-        assert model.info.kernel == 0 and model.info.pipe_max_streams == 0
+        assert model.info.kernel == 0 and model.info.pipe_max_streams == 0 and model.info.deep_max_streams == 0
     got = _gpu_run(model, x)
     _compare(got, ref)
     np.testing.assert_array_equal(got["state"], ref["state"])
@@ -83,10 +86,30 @@ def c12(model_dir):
     return path
 
 
+def default_plan(D: int) -> list:
+    """The library's default router plan: min(4, D) levels, then the rest in near-equal rounds of at most 4."""
+    if D <= 0:
+        return []
+    h0 = min(4, D)
+    rest = D - h0
+    nr = (rest + 3) // 4
+    return [h0] + [rest // nr + (r < rest % nr) for r in range(nr)]
+
+
+def deep_plan(plan) -> bool:
+    """Plans the deep descent takes: 2 to 4 rounds, the first of >= 2 levels, the third and fourth <= 6 together."""
+    return 2 <= len(plan) <= 4 and plan[0] >= 2 and (len(plan) < 4 or plan[2] + plan[3] <= 6)
+
+
 def _expect_kernel(model, kernel_env):
     """The forced kernel is the one in use (the shapes passed here are all common-shape models)."""
-    assert model.info.kernel == (0 if kernel_env == "generic" else 1), model.info.kernel
-    assert (model.info.pipe_max_streams > 0) == (kernel_env == "pipe"), model.info.pipe_max_streams
+    info = model.info
+    assert info.kernel == (0 if kernel_env == "generic" else 1), info.kernel
+    assert (info.pipe_max_streams > 0) == (kernel_env == "pipe"), info.pipe_max_streams
+    deep = info.n_layers > 1 and deep_plan(default_plan(info.router_depth))
+    if kernel_env != "generic":
+        assert info.deep == deep, info.deep
+    assert (info.deep_max_streams > 0) == (kernel_env == "deep" and deep), info.deep_max_streams
 
 
 def test_config1_full_stream(hip, c12, kernel_env):
@@ -296,3 +319,42 @@ def test_score_bad_target(hip, c12):
     _lib.check(_lib.lib().ygg_score(model._h, p(x), p(y), 2, 5, p(st), p(nll),
                                     ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)))
     assert model.take_errors() == 2
+
+
+@pytest.mark.parametrize("which,plan", [
+    ("c4small", None), ("c4small", "4,4,2"), ("c4small", "2,4,2,2"), ("c4small", "3,3,2,2"), ("c4small", "4,2,3,1"),
+    ("c4small", "4,2,4"), ("c4small", "4,4,1,1"), ("c4small", "1,3,3,3"), ("c4small", "2,2,2,2,2"),
+    ("c12", "2,2,3,3"), ("c12", "4,4,2")])
+def test_deep_descent_plans(hip, model_dir, c12, monkeypatch, which, plan):
+    """Router plans (YGG_ROUNDS) on d = 128 and d = 64 models with D = 10 under the deep descent (one launch of 40
+    tokens, launches of 3 tokens with the state carried) and the layer-pipelined kernel; plans the deep descent does
+    not take (a first round of 1 level, 5 rounds) run the per-stream kernel instead. Leaves, states after every token
+    and logits equal the oracle's."""
+    import torch
+    if which == "c4small":
+        path = model_dir / "c4small_gauss.bin"
+        if not path.exists():
+            synth.write_model(synth.ModelSpec(128, 16, 10, 256, 4, router="gauss"), 11, path)
+    else:
+        path = c12
+    if plan:
+        monkeypatch.setenv("YGG_ROUNDS", plan)
+    monkeypatch.delenv("YGG_DEEP", raising=False)
+    x = synth.zipf_bytes(12, 40, 6)
+    ref = Oracle(path).run(x, states=True)
+    deep = deep_plan([int(h) for h in plan.split(",")] if plan else default_plan(10))
+    for k in ("deep", "pipe"):
+        monkeypatch.setenv("YGG_KERNEL", k)
+        model = hip.load(path)
+        _say(f"{which} plan {plan} kernel {k}: deep {model.info.deep}")
+        assert model.info.deep == deep
+        assert (model.info.deep_max_streams > 0) == (k == "deep" and deep)
+        _compare(_gpu_run(model, x), ref)
+        if k == "deep":
+            parts, st = [], None
+            for t0 in range(0, x.shape[1], 3):
+                parts.append(_gpu_run(model, x[:, t0:t0 + 3], state=st))
+                st = torch.as_tensor(parts[-1]["state"], device=model.device)
+            got = {key: np.concatenate([p[key] for p in parts], 1) for key in ("leaves", "states", "logits")}
+            _compare(got, ref)
+        model.close()

@@ -22,6 +22,7 @@ namespace ygg {
 typedef hipError_t (*Launcher)(const YggDevModel &, const int32_t *, int, int, int8_t *, const YggIO &, hipStream_t);
 Launcher find_launcher(int n, int blk, int R);
 Launcher find_fast_launcher(int n, int L);
+Launcher find_deep_launcher(int n, int L);
 Launcher find_pipe_launcher(int n, int L);
 int pipe_blocks_per_cu(int n, int L);
 }  // namespace ygg
@@ -360,8 +361,11 @@ struct ygg_model {
     void *arena = nullptr;
     size_t arena_bytes = 0;
     ygg::Launcher launch = nullptr;
-    ygg::Launcher launch_pipe = nullptr;   // for calls with B <= pipe_max_streams
+    ygg::Launcher launch_pipe = nullptr;   // T > 1 and B <= pipe_max_streams
     int pipe_max_streams = 0;
+    ygg::Launcher launch_deep = nullptr;   // generate with B <= deep_max_streams (every call when deep_all)
+    int deep_max_streams = 0;
+    bool deep_all = false;
 };
 
 namespace {
@@ -386,18 +390,18 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     for (int l = 1; l < L; l++)
         if ((fl[l].vt != nullptr) != (fl[1].vt != nullptr))
             return fail(YGG_ERR_FORMAT, "model file: mixed table and factored routed layers");
-    // the specialised kernels cover the common shape: fast_kernel for many streams, pipe_kernel (one wavefront per
-    // layer) when the call's B L wavefronts fit on the device at once. YGG_KERNEL=generic|fast|pipe forces one.
+    // the specialised kernels cover the common shape: fast_kernel for many streams; pipe_kernel (one wavefront per
+    // layer) when a call of T > 1 tokens has its B L wavefronts resident at once; generation for few streams on
+    // fast_kernel with one stream per workgroup and the deep router descent. YGG_KERNEL=generic|fast|pipe|deep forces
+    // one for every call; YGG_DEEP=0 turns the deep descent off.
     const char *kenv = getenv("YGG_KERNEL");
     const std::string kmode = kenv ? kenv : "";
-    ygg::Launcher fast = nullptr, pipe = nullptr;
+    ygg::Launcher fast = nullptr;
     // (layer-input rank 16 exactly, and every routed layer's table and gather records addressable in 32 bits)
     const bool small_tables = (int64_t)E * V * n * 2 < ((int64_t)1 << 32) && (int64_t)E * 64 * n < ((int64_t)1 << 32);
     if (kmode != "generic" && R == 8 && fa.blk == 16 && (R2 == 16 || L == 1) && !factored && !group && L <= 4 &&
-        VP <= 256 && small_tables && transitions_split(fa, fl)) {
+        VP <= 256 && small_tables && transitions_split(fa, fl))
         fast = ygg::find_fast_launcher(n, L);
-        if (kmode != "fast") pipe = ygg::find_pipe_launcher(n, L);
-    }
     if (fast) launch = fast;
 
     RoundPlan rplan = round_plan(L > 1 ? fa.D : 0);
@@ -418,6 +422,14 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
         if (!ok || sum != fa.D) return fail(YGG_ERR_ARG, "YGG_ROUNDS=%s: not a plan for depth %d", rs, fa.D);
         rplan = p;
     }
+    // the deep descent: at most 4 rounds, the first of at least 2 levels, the rounds after the second at most 6
+    // levels together (one lane per node)
+    const char *denv = getenv("YGG_DEEP");
+    const bool deep = fast && L > 1 && !(denv && !strcmp(denv, "0")) && rplan.n >= 2 && rplan.n <= 4 &&
+                      rplan.h[0] >= 2 && (rplan.n < 4 || rplan.h[2] + rplan.h[3] <= 6);
+    ygg::Launcher pipe = nullptr, deepk = nullptr;
+    if (fast && kmode != "fast" && kmode != "deep") pipe = ygg::find_pipe_launcher(n, L);
+    if (deep && kmode != "fast" && kmode != "pipe") deepk = ygg::find_deep_launcher(n, L);
     const int64_t slots = plan_slots(rplan);
     // device arena plan: every array 256-byte aligned
     struct Piece { size_t off, bytes; };
@@ -540,6 +552,11 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     // pipe_kernel when the workgroups of all B streams of a call are resident at once, or always with YGG_KERNEL=pipe
     const int pipe_per_cu = pipe ? ygg::pipe_blocks_per_cu(n, L) : 0;
     m->pipe_max_streams = pipe ? (kmode == "pipe" ? INT32_MAX : pipe_per_cu * cus) : 0;
+    // generation with one stream per workgroup while the streams do not outnumber the CUs (for more, the 4 streams
+    // per workgroup of fast_kernel win); YGG_KERNEL=deep takes it for every call
+    m->launch_deep = deepk;
+    m->deep_all = deepk && kmode == "deep";
+    m->deep_max_streams = deepk ? (m->deep_all ? INT32_MAX : cus) : 0;
     m->device = device;
     m->arena = arena;
     m->arena_bytes = total;
@@ -589,11 +606,21 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     I.n_experts = E; I.readout_rank = R; I.layer_input_rank = R2; I.input_rank = fa.K; I.shift = fa.shift;
     I.factored = factored; I.group = group; I.device = device; I.kernel = fast ? 1 : 0;
     I.pipe_max_streams = m->pipe_max_streams;
+    I.deep = deep ? 1 : 0;
+    I.deep_max_streams = m->deep_max_streams;
     I.file_array_bytes = fa.bytes;
     I.device_bytes = (int64_t)total;
     for (int l = 0; l < L; l++) I.gather_bytes[l] = lp[l].gl.bytes;
     *out = m;
     return YGG_OK;
+}
+
+// The kernel of a run/score/step call of B streams and T tokens: the layer-pipelined one for T > 1 when its
+// workgroups fit, else the per-stream kernel (or the deep one when forced for every call).
+ygg::Launcher pick(const ygg_model *m, int B, int T) {
+    if (m->deep_all) return m->launch_deep;
+    if (T > 1 && m->launch_pipe && B <= m->pipe_max_streams) return m->launch_pipe;
+    return m->launch;
 }
 
 struct DeviceGuard {
@@ -618,7 +645,7 @@ int set_error(int code, const char *msg) { return fail(code, "%s", msg); }
 
 extern "C" {
 
-int ygg_version(void) { return 6; }
+int ygg_version(void) { return 7; }
 
 const char *ygg_last_error(void) { return g_err.c_str(); }
 
@@ -680,7 +707,7 @@ int ygg_run(const ygg_model *m, const int32_t *d_tokens, int B, int T, int8_t *d
     DeviceGuard g;
     HIP_TRY(g.set(m->device));
     // the pipelined kernel overlaps the layers of consecutive tokens, so it needs more than one token per launch
-    ygg::Launcher k = (m->launch_pipe && B <= m->pipe_max_streams && T > 1) ? m->launch_pipe : m->launch;
+    ygg::Launcher k = pick(m, B, T);
     YggIO io{};
     io.logits = d_logits;
     io.leaves = d_leaves;
@@ -698,7 +725,7 @@ int ygg_score(const ygg_model *m, const int32_t *d_tokens, const int32_t *d_targ
     if (!d_state || !d_nll || (T > 0 && (!d_tokens || !d_targets))) return fail(YGG_ERR_ARG, "NULL buffer");
     DeviceGuard g;
     HIP_TRY(g.set(m->device));
-    ygg::Launcher k = (m->launch_pipe && B <= m->pipe_max_streams && T > 1) ? m->launch_pipe : m->launch;
+    ygg::Launcher k = pick(m, B, T);
     YggIO io{};
     io.targets = d_targets;
     io.nll = d_nll;
@@ -717,14 +744,17 @@ int ygg_generate(const ygg_model *m, const int32_t *d_first, int B, int n, int8_
     if (!d_first || !d_state || !d_out) return fail(YGG_ERR_ARG, "NULL buffer");
     DeviceGuard g;
     HIP_TRY(g.set(m->device));
-    // every token needs all layers of the one before it: the per-stream kernel, never the layer-pipelined one
+    // every token needs all layers of the one before it: a per-stream kernel, never the layer-pipelined one
+    // (the deep kernel's LDS staging pays off over a few tokens)
+    const ygg::Launcher k = (m->launch_deep && B <= m->deep_max_streams && (n >= 8 || m->deep_all)) ? m->launch_deep
+                                                                                                   : m->launch;
     YggIO io{};
     io.logits = d_logits;
     io.gen = d_out;
     io.temperature = temperature;
     io.top_k = top_k;
     io.seed = (unsigned long long)seed;
-    HIP_TRY(m->launch(m->dev, d_first, B, n, d_state, io, (hipStream_t)stream));
+    HIP_TRY(k(m->dev, d_first, B, n, d_state, io, (hipStream_t)stream));
     return YGG_OK;
 }
 
@@ -739,8 +769,8 @@ int ygg_step(const ygg_model *m, const int32_t *d_tokens, const int8_t *d_state_
     if (d_state_in != d_state_out)
         HIP_TRY(hipMemcpyAsync(d_state_out, d_state_in, (size_t)B * m->dev.L * m->dev.N, hipMemcpyDeviceToDevice,
                                (hipStream_t)stream));
-    // one token: the per-stream kernel (a one-token launch cannot overlap layers), or the pipelined one when forced
-    ygg::Launcher k = (m->launch_pipe && m->pipe_max_streams == INT32_MAX) ? m->launch_pipe : m->launch;
+    // one token: a per-stream kernel (a one-token launch cannot overlap layers), or the pipelined one when forced
+    ygg::Launcher k = (m->launch_pipe && m->pipe_max_streams == INT32_MAX) ? m->launch_pipe : pick(m, B, 1);
     YggIO io{};
     io.logits = d_logits;
     io.leaves = d_leaves;

@@ -204,6 +204,27 @@ __device__ __forceinline__ int walk_round(unsigned long long mask, int h) {
     return (int)(((l4 >> 2) + 1) >> (4 - h)) - 1;
 }
 
+// walk_round for a ballot with node j's bit at bit j (one lane per node)
+__device__ __forceinline__ int walk_bits(unsigned long long mask, int h) {
+    unsigned l = 0, t;
+    asm("s_bitcmp1_b64 %2, %0\n\t"
+        "s_cselect_b32 %1, 2, 1\n\t"
+        "s_lshl1_add_u32 %0, %0, %1\n\t"
+        "s_bitcmp1_b64 %2, %0\n\t"
+        "s_cselect_b32 %1, 2, 1\n\t"
+        "s_lshl1_add_u32 %0, %0, %1\n\t"
+        "s_bitcmp1_b64 %2, %0\n\t"
+        "s_cselect_b32 %1, 2, 1\n\t"
+        "s_lshl1_add_u32 %0, %0, %1\n\t"
+        "s_bitcmp1_b64 %2, %0\n\t"
+        "s_cselect_b32 %1, 2, 1\n\t"
+        "s_lshl1_add_u32 %0, %0, %1"
+        : "+s"(l), "=&s"(t)
+        : "s"(mask)
+        : "scc");
+    return (int)((l + 1) >> (4 - h)) - 1;
+}
+
 // the lanes whose pred holds, as a wavefront-uniform 64-bit mask
 __device__ __forceinline__ unsigned long long lane_mask(bool pred) { return __builtin_amdgcn_ballot_w64(pred); }
 
@@ -310,7 +331,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void ru
 
     const int lane = threadIdx.x;
     const int s = blockIdx.x;
-    const int L = m.L, V = m.V, VP = m.VP, E = m.E, D = m.D, R2 = m.R2, K = m.K;
+    const int L = m.L, V = m.V, VP = m.VP, E = m.E, R2 = m.R2, K = m.K;
     const int qk = lane & 3, qj = lane >> 2;                     // quad lane, quad
     const int rj = lane / RL, rk = lane % RL;                    // readout row, readout lane
 

@@ -3,7 +3,8 @@
 // (ygg_kernel.h); the per-layer pieces below are shared by both.
 //
 // fast_kernel (throughput: many streams): one wavefront per stream runs every layer of every token, 4 streams per
-// workgroup. What every stream reads at every token is in LDS once per workgroup: the unembedding Q of every layer,
+// workgroup. Its DEEP form (generation for few streams: one stream per workgroup) shortens the router descent, see
+// descend_deep. What every stream reads at every token is in LDS once per workgroup: the unembedding Q of every layer,
 // the layer-input down-projection V' of every routed layer and the router rows of the first descent round (nodes
 // 1..15). The thresholds of that round, thr[x][1..15], depend only on the token and are loaded when the token is
 // read. An expert's whole gather record (A16, U', P) and table row are loaded in one burst as soon as the expert is
@@ -179,6 +180,155 @@ __device__ __forceinline__ int descend(const YggDevModel &m, const YggDevLayer &
     return ix - m.E;
 }
 
+// ------------------------------------------------------------------------------------------ deep descent
+// For one stream generating tokens, every router round is a dependent step on the path from one sampled token to the
+// next. The deep descent takes the second round from LDS (its rows staged once per launch, its thresholds loaded
+// with the token) and evaluates the rounds after it (at most two, at most 6 levels together) as one round, so a
+// routed layer's descent has a single dependent global round. It needs a plan of 2 to 4 rounds whose first has at
+// least 2 levels (16-byte aligned threshold blocks).
+
+// The second round's rows of one routed layer in LDS: slot s of the round (s < 2^(h0 + h1) <= 256) at s N. For
+// n = 128 the two 64-byte halves of a row are swapped when bit 1 of s is set: the 16 quads of a wavefront reading
+// 16 consecutive rows then hit 64 distinct banks in every 16-lane group.
+template <int N> constexpr int kR2Slots = 256;
+
+template <int N, int L>
+__device__ __forceinline__ void load_round2(int8_t (*W1)[kR2Slots<N> * N], const YggDevModel &m, int tid,
+                                            int nthreads) {
+    constexpr int RC = N / 16;
+    if (m.n_rounds < 2) return;
+    const int base = 1 << m.round_h[0], count = 1 << (m.round_h[0] + m.round_h[1]);
+#pragma unroll
+    for (int l = 1; l < L; l++) {
+        const uint4 *src = (const uint4 *)(m.layers[l].w + (size_t)base * N);
+        uint4 *dst = (uint4 *)W1[l - 1];
+        for (int k = tid; k < count * RC; k += nthreads) {
+            const int sl = k / RC, c = k % RC;
+            dst[sl * RC + (N == 128 ? c ^ (((sl >> 1) & 1) << 2) : c)] = src[k];
+        }
+    }
+}
+
+// quad_share of slot sl of the LDS second-round rows
+template <int N>
+__device__ __forceinline__ void quad_share_r2(uint32_t (&w)[Fast<N>::QW], const int8_t *row, int qk, int sl) {
+    if constexpr (N == 128) {
+        const int sw = ((sl >> 1) & 1) * 64;
+        uint32_t a[4], b[4];
+        load_words<4, 16>(a, row + qk * 16 + sw);
+        load_words<4, 16>(b, row + qk * 16 + (64 - sw));
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            w[i] = a[i];
+            w[4 + i] = b[i];
+        }
+    } else {
+        quad_share<N>(w, row, qk);
+    }
+}
+
+// The tail round: the rounds after the second as one round with one lane per node (at most 63): lanes
+// [0, 2^h2 - 1) take the third round's block (breadth-first), the next 2^h2 (2^h3 - 1) lanes the 2^h2 fourth-round
+// blocks below it, which lie one after the other; other lanes are off. Lane l's node sits in slot ta + (sub << tsh),
+// sub the index of the second round's end node among the nodes of its depth d2 = h0 + h1. Each lane reads its whole
+// row and forms the dot alone (measured faster here than quads over several passes, whose reductions and shuffles
+// lengthen the chain).
+struct Tail {
+    int ta, tsh;
+    bool on;
+};
+
+__device__ __forceinline__ Tail make_tail(const YggDevModel &m, int lane) {
+    Tail t{0, 0, false};
+    if (m.n_rounds < 3) return t;
+    const int h0 = m.round_h[0], h1 = m.round_h[1], h2 = m.round_h[2], h3 = m.n_rounds > 3 ? m.round_h[3] : 0;
+    const int base2 = (1 << h0) + (1 << (h0 + h1)), base3 = base2 + (1 << (h0 + h1 + h2));
+    const int nn2 = (1 << h2) - 1, nn3 = (1 << h3) - 1;
+    if (lane < nn2) {
+        t = Tail{base2 + lane, h2, true};
+    } else if (nn3 > 0 && lane < nn2 + (nn3 << h2)) {
+        const int q = lane - nn2, c = q / nn3;
+        t = Tail{base3 + (c << h3) + (q - c * nn3), h2 + h3, true};
+    }
+    return t;
+}
+
+// The deep descent -> leaf index. W0/th0 as in descend; W1 the layer's LDS second-round rows and th2 this lane's four
+// second-round thresholds (slots 2^h0 + 4 lane .. + 3 of the token's row); qb the state below (LDS) for the tail's
+// whole-row dots. hook() runs once, while the tail round's loads are in flight (or after the descent).
+template <int N, class Hook = NoHook>
+__device__ __forceinline__ int descend_deep(const YggDevModel &m, const YggDevLayer &y, const int8_t *W0, float th0,
+                                            const int8_t *W1, const float4 &th2, const uint32_t (&qbw)[Fast<N>::QW],
+                                            const int8_t *qb, float rho, int x, int lane, const Tail &tl,
+                                            Hook hook = Hook()) {
+    using F = Fast<N>;
+    const int qk = lane & 3, qj = lane >> 2;
+    const int h0 = m.round_h[0], nn1 = (1 << h0) - 1;
+    int ix;
+    {
+        int dot = 0;
+        if (qj < nn1) {
+            uint32_t wv[F::QW];
+            quad_share<N>(wv, W0 + qj * kLdsRow<N>, qk);
+#pragma unroll
+            for (int i = 0; i < F::QW; i++) dot = dot4(wv[i], qbw[i], dot);
+        }
+        dot = sum4(dot);
+        const bool right = (float)dot * rho > th0;
+        const int loc = walk_round(lane_mask(right && qk == 0 && qj < nn1), h0);
+        ix = (1 << h0) + (loc - nn1);
+    }
+    {
+        const int h = m.round_h[1], nn = (1 << h) - 1;
+        const int sl = ((ix - (1 << h0)) << h) + qj;          // slot within the second round's slots
+        uint32_t wv[F::QW];
+        if (qj < nn) quad_share_r2<N>(wv, W1 + sl * N, qk, sl);
+        // slot sl's threshold is component sl & 3 of lane sl >> 2's th2 (sl < 256)
+        const int src = (sl >> 2) & 63;
+        const float a = __shfl(th2.x, src), b = __shfl(th2.y, src), c = __shfl(th2.z, src), d = __shfl(th2.w, src);
+        const int k = sl & 3;
+        const float th = k == 0 ? a : (k == 1 ? b : (k == 2 ? c : d));
+        int dot = 0;
+        if (qj < nn) {
+#pragma unroll
+            for (int i = 0; i < F::QW; i++) dot = dot4(wv[i], qbw[i], dot);
+        }
+        dot = sum4(dot);
+        const bool right = (float)dot * rho > th;
+        const int loc = walk_round(lane_mask(right && qk == 0 && qj < nn), h);
+        ix = (ix << h) + (loc - nn);
+    }
+    if (m.n_rounds == 2) {
+        hook();
+        return ix - m.E;
+    }
+    {
+        const float *thr = y.thr + (size_t)x * y.thr_stride;
+        const int slot = tl.ta + ((ix - (1 << (h0 + m.round_h[1]))) << tl.tsh);
+        uint32_t rw[N / 4];
+        float th = 0.0f;
+        if (tl.on) {
+            load_words<N / 4, 16>(rw, y.w + (size_t)slot * N);
+            th = thr[slot];
+        }
+        hook();
+        uint32_t qf[N / 4];
+        load_words<N / 4, 16>(qf, qb);
+        int dot = 0;
+#pragma unroll
+        for (int i = 0; i < N / 4; i++) dot = dot4(rw[i], qf[i], dot);
+        const unsigned long long mask = lane_mask(tl.on && (float)dot * rho > th);
+        const int h2 = m.round_h[2], nn2 = (1 << h2) - 1;
+        const int c = walk_bits(mask, h2) - nn2;
+        ix = (ix << h2) + c;
+        if (m.n_rounds == 4) {
+            const int h3 = m.round_h[3], nn3 = (1 << h3) - 1;
+            ix = (ix << h3) + (walk_bits(mask >> (nn2 + c * nn3), h3) - nn3);
+        }
+    }
+    return ix - m.E;
+}
+
 // the expert's whole gather record and table row, in one burst
 template <int N>
 __device__ __forceinline__ void gather(Gather<N> &G, const YggDevLayer &y, int r, int x, bool routed, int lane) {
@@ -337,9 +487,11 @@ __device__ __forceinline__ void store_logits(float *o, const float (&lg)[4], int
 
 // ----------------------------------------------------------------------------------------------- fast_kernel
 
-// GEN: sample the next input from the logits of every token (io.gen), instead of reading it from tokens
-template <int N, int L, bool GEN>
-__global__ __launch_bounds__(64 * kFastWaves) __attribute__((amdgpu_waves_per_eu(4)))
+// GEN: sample the next input from the logits of every token (io.gen), instead of reading it from tokens. DEEP: one
+// stream per workgroup with the deep descent (generation for few streams), else 4 streams per workgroup with
+// descend.
+template <int N, int L, bool GEN, bool DEEP>
+__global__ __launch_bounds__(64 * kFastWaves) __attribute__((amdgpu_waves_per_eu(DEEP ? 1 : 4)))
 void fast_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B, int T, int8_t *__restrict__ state,
                  const YggIO io) {
     float *__restrict__ logits = io.logits;
@@ -349,20 +501,26 @@ void fast_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
     const int32_t *__restrict__ targets = io.targets;
     double *__restrict__ nll = io.nll;
     using F = Fast<N>;
-    constexpr int W = kFastWaves, LR = L > 1 ? L - 1 : 1;
+    constexpr int W = DEEP ? 1 : kFastWaves, LR = L > 1 ? L - 1 : 1;
     __shared__ __attribute__((aligned(16))) SharedTables<N, L> S;
+    __shared__ __attribute__((aligned(16))) int8_t W1s[DEEP ? LR : 1][DEEP ? kR2Slots<N> * N : 16];
     __shared__ __attribute__((aligned(16))) int8_t qsw[W][L * N];
     __shared__ __attribute__((aligned(16))) int8_t zlw[W][16];
     __shared__ __attribute__((aligned(16))) int8_t zqw[W][16];
 
-    // the wavefront index, stream, tokens and leaves are uniform over a wavefront: kept in scalar registers
+    // the wavefront index, stream, tokens and leaves are uniform over a wavefront: kept in scalar registers. With one
+    // stream per workgroup (DEEP) all 4 wavefronts stage the LDS tables and wavefronts 1-3 then leave.
     const int tid = threadIdx.x, wv = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int s = blockIdx.x * W + wv;
     const int V = m.V, VP = m.VP;
-    load_tables<N, L>(S, m, tid, 64 * W);
+    load_tables<N, L>(S, m, tid, 64 * kFastWaves);
+    if constexpr (DEEP) load_round2<N, L>(W1s, m, tid, 64 * kFastWaves);
     __syncthreads();
-    if (s >= B) return;
+    if (wv >= W || s >= B) return;
 
+    Tail tl{};
+    if constexpr (DEEP) tl = make_tail(m, lane);
+    const int n2 = m.n_rounds > 1 ? 1 << (m.round_h[0] + m.round_h[1]) : 0;   // second-round slots
     int8_t *qs = qsw[wv];
     int8_t *zls = zlw[wv];
     int8_t *zqs = zqw[wv];
@@ -390,6 +548,17 @@ void fast_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
 #pragma unroll
         for (int l = 1; l < L; l++)
             th1[l - 1] = qj < nn1 ? m.layers[l].thr[(size_t)x * m.layers[l].thr_stride + qj] : 0.0f;
+        // DEEP: and those of the second round, four per lane (components in separate arrays, which the selects
+        // below keep in registers)
+        float th2x[LR], th2y[LR], th2z[LR], th2w[LR];
+#pragma unroll
+        for (int l = 1; l < L; l++) {
+            float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (DEEP && 4 * lane < n2)
+                v = *(const float4 *)(m.layers[l].thr + (size_t)x * m.layers[l].thr_stride + (1 << m.round_h[0]) +
+                                      4 * lane);
+            th2x[l - 1] = v.x; th2y[l - 1] = v.y; th2z[l - 1] = v.z; th2w[l - 1] = v.w;
+        }
         float lg[4];
 #pragma unroll
         for (int u = 0; u < 4; u++) lg[u] = 4 * lane + u < VP ? m.output_bias[4 * lane + u] : 0.0f;
@@ -427,7 +596,21 @@ void fast_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
 #pragma unroll
                 for (int i = 1; i < LR; i++) th = l - 1 == i ? th1[i] : th;
                 rho = below_and_rho<N>(qbw, qs + (l - 1) * N, y.rms_eps, lane);
-                r = descend<N>(m, y, S.W[l - 1], th, qbw, rho, x, lane, flush);
+                if constexpr (!DEEP) {
+                    r = descend<N>(m, y, S.W[l - 1], th, qbw, rho, x, lane, flush);
+                } else {
+                    float4 t2 = make_float4(th2x[0], th2y[0], th2z[0], th2w[0]);
+#pragma unroll
+                    for (int i = 1; i < LR; i++) {
+                        const bool b = l - 1 == i;
+                        t2.x = b ? th2x[i] : t2.x;
+                        t2.y = b ? th2y[i] : t2.y;
+                        t2.z = b ? th2z[i] : t2.z;
+                        t2.w = b ? th2w[i] : t2.w;
+                    }
+                    r = descend_deep<N>(m, y, S.W[l - 1], th, W1s[DEEP ? l - 1 : 0], t2, qbw, qs + (l - 1) * N,
+                                        rho, x, lane, tl, flush);
+                }
             }
             Gather<N> G;
             gather<N>(G, y, r, x, l > 0, lane);
