@@ -82,29 +82,73 @@ template <int N, int L> struct SharedTables {
     float mv[LR][16];
 };
 
-template <int N, int L>
-__device__ __forceinline__ void load_tables(SharedTables<N, L> &S, const YggDevModel &m, int tid, int nthreads) {
+// Stage the tables with NT threads: every load is issued before the first LDS store, so a launch waits for them
+// once (a load-store loop would wait for each in turn).
+template <int N, int L, int NT>
+__device__ __forceinline__ void load_tables(SharedTables<N, L> &S, const YggDevModel &m, int tid) {
     // 16-byte chunks: RC per row in memory, SC per row in LDS
-    constexpr int RC = N / 16, SC = kLdsRow<N> / 16;
+    constexpr int RC = N / 16, SC = kLdsRow<N> / 16, LR = L > 1 ? L - 1 : 1;
+    constexpr int QK = (128 + NT - 1) / NT;            // Q chunks (at most 128: VP <= 256) per thread and layer
+    constexpr int RK = (31 * RC + NT - 1) / NT;        // first-round rows and V' rows, per thread and routed layer
+    const int qch = m.VP / 2, rows = (1 << m.round_h[0]) - 1;
+    uint4 qv[L][QK], rv[LR][RK];
+    float mvv = 0.0f;
 #pragma unroll
-    for (int l = 0; l < L; l++) {
-        const uint4 *src = (const uint4 *)m.layers[l].Q;
-        uint4 *dst = (uint4 *)S.Q[l];
-        for (int k = tid; k < m.VP * 8 / 16; k += nthreads) dst[(k & 1) * 64 + (k >> 1)] = src[k];
-    }
+    for (int l = 0; l < L; l++)
+#pragma unroll
+        for (int k = 0; k < QK; k++) {
+            const int c = tid + k * NT;
+            qv[l][k] = make_uint4(0u, 0u, 0u, 0u);
+            if (c < qch) qv[l][k] = ((const uint4 *)m.layers[l].Q)[c];
+        }
 #pragma unroll
     for (int l = 1; l < L; l++) {
         const YggDevLayer &y = m.layers[l];
-        const int rows = (1 << m.round_h[0]) - 1;     // the first round's block: slots 0 .. 2^h0 - 2
-        const uint4 *ws = (const uint4 *)y.w;
-        uint4 *wd = (uint4 *)S.W[l - 1];
-        for (int k = tid; k < 15 * RC; k += nthreads)
-            wd[(k / RC) * SC + k % RC] = k < rows * RC ? ws[k] : make_uint4(0u, 0u, 0u, 0u);
-        uint4 *vd = (uint4 *)S.V[l - 1];
-        const uint4 *vs = (const uint4 *)y.vl;
-        for (int k = tid; k < 16 * RC; k += nthreads) vd[(k / RC) * SC + k % RC] = vs[k];
-        if (tid < 16) S.mv[l - 1][tid] = y.mv[tid];
+#pragma unroll
+        for (int k = 0; k < RK; k++) {
+            const int c = tid + k * NT;
+            rv[l - 1][k] = make_uint4(0u, 0u, 0u, 0u);
+            if (c < rows * RC)
+                rv[l - 1][k] = ((const uint4 *)y.w)[c];
+            else if (c >= 15 * RC && c < 31 * RC)
+                rv[l - 1][k] = ((const uint4 *)y.vl)[c - 15 * RC];
+        }
     }
+#pragma unroll
+    for (int l = 1; l < L; l++)
+        if (tid / 16 == l - 1) mvv = m.layers[l].mv[tid % 16];
+#pragma unroll
+    for (int l = 0; l < L; l++)
+#pragma unroll
+        for (int k = 0; k < QK; k++) {
+            const int c = tid + k * NT;
+            if (c < qch) ((uint4 *)S.Q[l])[(c & 1) * 64 + (c >> 1)] = qv[l][k];
+        }
+#pragma unroll
+    for (int l = 1; l < L; l++)
+#pragma unroll
+        for (int k = 0; k < RK; k++) {
+            const int c = tid + k * NT;
+            if (c < 15 * RC)
+                ((uint4 *)S.W[l - 1])[(c / RC) * SC + c % RC] = rv[l - 1][k];
+            else if (c < 31 * RC)
+                ((uint4 *)S.V[l - 1])[((c - 15 * RC) / RC) * SC + (c - 15 * RC) % RC] = rv[l - 1][k];
+        }
+    if (L > 1 && tid < 16 * (L - 1)) S.mv[tid / 16][tid % 16] = mvv;
+}
+
+// Touch every 64-byte line of the kernel argument (the model description, read by scalar loads) at entry: the
+// scalar cache starts each launch cold, and a layer's fields would otherwise first be read when that layer starts
+// (worth 1 us in a launch of one token; launches of many tokens do without).
+// The fields touched lie less than 64 bytes apart and are ones the token loop never reads (format variants, LDS
+// staging sources), so the compiler has nothing to keep live from here on.
+template <int L>
+__device__ __forceinline__ void touch_args(const YggDevModel &m) {
+    asm volatile("; args %0 %1" ::"s"(m.BLK), "s"(m.round_h[12]));
+#pragma unroll
+    for (int l = 0; l < L; l++)
+        asm volatile("; layer args %0 %1 %2 %3 %4" ::"s"(m.layers[l].vl), "s"(m.layers[l].r2b), "s"(m.layers[l].vt),
+                     "s"(m.layers[l].mT), "s"(m.layers[l].off_FS));
 }
 
 // the quad-lane chunk of the state below and rho = 1 / sqrt(mean(q^2) + eps) (cpu/ygg.cpp:248-255)
@@ -192,21 +236,30 @@ __device__ __forceinline__ int descend(const YggDevModel &m, const YggDevLayer &
 // 16 consecutive rows then hit 64 distinct banks in every 16-lane group.
 template <int N> constexpr int kR2Slots = 256;
 
-template <int N, int L>
-__device__ __forceinline__ void load_round2(int8_t (*W1)[kR2Slots<N> * N], const YggDevModel &m, int tid,
-                                            int nthreads) {
-    constexpr int RC = N / 16;
+template <int N, int L, int NT>
+__device__ __forceinline__ void load_round2(int8_t (*W1)[kR2Slots<N> * N], const YggDevModel &m, int tid) {
+    constexpr int RC = N / 16, K = (kR2Slots<N> * RC + NT - 1) / NT, LR = L > 1 ? L - 1 : 1;
     if (m.n_rounds < 2) return;
-    const int base = 1 << m.round_h[0], count = 1 << (m.round_h[0] + m.round_h[1]);
+    const int base = 1 << m.round_h[0], count = (1 << (m.round_h[0] + m.round_h[1])) * RC;
+    // every load first, then the stores
+    uint4 v[LR][K];
 #pragma unroll
     for (int l = 1; l < L; l++) {
         const uint4 *src = (const uint4 *)(m.layers[l].w + (size_t)base * N);
-        uint4 *dst = (uint4 *)W1[l - 1];
-        for (int k = tid; k < count * RC; k += nthreads) {
-            const int sl = k / RC, c = k % RC;
-            dst[sl * RC + (N == 128 ? c ^ (((sl >> 1) & 1) << 2) : c)] = src[k];
+#pragma unroll
+        for (int k = 0; k < K; k++) {
+            const int c = tid + k * NT;
+            v[l - 1][k] = make_uint4(0u, 0u, 0u, 0u);
+            if (c < count) v[l - 1][k] = src[c];
         }
     }
+#pragma unroll
+    for (int l = 1; l < L; l++)
+#pragma unroll
+        for (int k = 0; k < K; k++) {
+            const int c = tid + k * NT, sl = c / RC, q = c % RC;
+            if (c < count) ((uint4 *)W1[l - 1])[sl * RC + (N == 128 ? q ^ (((sl >> 1) & 1) << 2) : q)] = v[l - 1][k];
+        }
 }
 
 // quad_share of slot sl of the LDS second-round rows
@@ -513,10 +566,21 @@ void fast_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
     const int tid = threadIdx.x, wv = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int s = blockIdx.x * W + wv;
     const int V = m.V, VP = m.VP;
-    load_tables<N, L>(S, m, tid, 64 * kFastWaves);
-    if constexpr (DEEP) load_round2<N, L>(W1s, m, tid, 64 * kFastWaves);
+    const bool live = wv < W && s < B;
+    // The stream's first token and its state are read before the LDS tables are staged, so that their loads overlap
+    // (a launch of one token would otherwise wait for them one after the other).
+    const int32_t *tok = tokens + (size_t)s * (GEN ? 1 : T);
+    if constexpr (!DEEP) touch_args<L>(m);     // (measured: the DEEP kernel generated 15% slower with it)
+    int x_next = (live && T > 0) ? __builtin_amdgcn_readfirstlane(tok[0]) : 0;
+    int8_t *st = state + (size_t)s * L * N;
+    constexpr int SB = (L * N + 63) / 64;     // state bytes per lane
+    int sb[SB];
+#pragma unroll
+    for (int k = 0; k < SB; k++) sb[k] = (live && lane + 64 * k < L * N) ? st[lane + 64 * k] : 0;
+    load_tables<N, L, 64 * kFastWaves>(S, m, tid);
+    if constexpr (DEEP) load_round2<N, L, 64 * kFastWaves>(W1s, m, tid);
     __syncthreads();
-    if (wv >= W || s >= B) return;
+    if (!live) return;
 
     Tail tl{};
     if constexpr (DEEP) tl = make_tail(m, lane);
@@ -527,14 +591,13 @@ void fast_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
     const int qj = lane >> 2;
     const int nn1 = (1 << m.round_h[0]) - 1;
 
-    int8_t *st = state + (size_t)s * L * N;
-    for (int i = lane; i < L * N; i += 64) qs[i] = st[i];
+#pragma unroll
+    for (int k = 0; k < SB; k++)
+        if (lane + 64 * k < L * N) qs[lane + 64 * k] = (int8_t)sb[k];
     if (lane < 16) zls[lane] = 0;
     wave_sync();
     unsigned long long dg = digest ? digest[s] : 0ull;
     double nacc = 0.0;
-    const int32_t *tok = tokens + (size_t)s * (GEN ? 1 : T);
-    int x_next = T > 0 ? __builtin_amdgcn_readfirstlane(tok[0]) : 0;
 
     for (int t = 0; t < T; t++) {
         const int x = x_next;
@@ -679,7 +742,7 @@ void pipe_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
     const int tid = threadIdx.x, l = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int s = blockIdx.x;
     const int V = m.V, VP = m.VP;
-    load_tables<N, L>(S, m, tid, 64 * L);
+    load_tables<N, L, 64 * L>(S, m, tid);
     const YggDevLayer &y = m.layers[l];
     int8_t *st = state + ((size_t)s * L + l) * N;
     for (int i = lane; i < N; i += 64) qbuf[l][1][i] = st[i];     // the state before token 0
