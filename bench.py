@@ -255,7 +255,7 @@ def main():
         f"tokens/s, compulsory {achieved:.0f} GB/s ({achieved / PEAK_HBM_GBS:.3f} of 8 TB/s), per-stream "
         f"{alg['per_stream'] / (kernel_ms / 1e3) / 1e9:.0f} GB/s")
 
-    kernel = kernel_name(info, B, T)
+    kernel = model.kernel_name(B, T)
     # HBM bytes per launch measured by rocprofv3 (FETCH_SIZE, WRITE_SIZE, copy-calibrated) for this workload and kernel
     traffic = None
     tf = ROOT / "profiles" / f"traffic_{w.name}.json"
@@ -303,20 +303,6 @@ def main():
     }
     print(json.dumps(out), flush=True)
     model.close()
-
-
-def kernel_name(info, B: int, T: int, gen: bool = False) -> str:
-    """The step kernel a ygg_run (gen: ygg_generate) call of B streams x T tokens launches (the library's choice,
-    ygg_capi.hip `pick` and ygg_generate)."""
-    n, L, g = info.d_state, info.n_layers, "true" if gen else "false"
-    if info.kernel != 1:
-        return f"ygg::run_kernel<{n}, {info.block_size}, {info.readout_rank}, {g}>"
-    forced = info.deep_max_streams == 2 ** 31 - 1
-    if forced or (gen and T >= 8 and 0 < B <= info.deep_max_streams):
-        return f"ygg::fast_kernel<{n}, {L}, {g}, true>"
-    if not gen and T > 1 and 0 < B <= info.pipe_max_streams:
-        return f"ygg::pipe_kernel<{n}, {L}>"
-    return f"ygg::fast_kernel<{n}, {L}, {g}, false>"
 
 
 def run_batch1(model, w, n_tok: int, L, _lib) -> dict:
@@ -377,12 +363,11 @@ def run_batch1(model, w, n_tok: int, L, _lib) -> dict:
     e1.record(stream)
     torch.cuda.synchronize()
     gen_us = e0.elapsed_time(e1) * 1e3 / n_tok
-    info = model.info
     return {"tokens": n_tok, "us_per_token_persistent_launch": round(run_us, 3),
             "us_per_token_graph_step": round(graph_us, 3), "graph_steps_per_graph": G,
             "graph_logits_equal_persistent": same, "us_per_token_generate_greedy": round(gen_us, 3),
-            "kernels": {"persistent_launch": kernel_name(info, 1, n_tok), "graph_step": kernel_name(info, 1, 1),
-                        "generate": kernel_name(info, 1, n_tok, gen=True)}}
+            "kernels": {"persistent_launch": model.kernel_name(1, n_tok), "graph_step": model.kernel_name(1, 1),
+                        "generate": model.kernel_name(1, n_tok, generate=True)}}
 
 
 if __name__ == "__main__":

@@ -163,6 +163,11 @@ void ygg_float_free(ygg_fmodel *m);
 /* Message of the last failed call on this thread ("" if none). */
 const char *ygg_last_error(void);
 
+/* The kernel a call would launch, by the name profilers show for it (e.g. "ygg::fast_kernel<128, 4, false, false>"):
+   generate = 0 for ygg_run/ygg_score/ygg_step (T = 1), 1 for ygg_generate (T = its n); written NUL-terminated into
+   name (len bytes). No counterpart in the reference (its one kernel is the CPU step); for profiles and tests. */
+int ygg_kernel_name(const ygg_model *m, int B, int T, int generate, char *name, size_t len);
+
 /* Library ABI version (bumped when a signature above changes). */
 int ygg_version(void);
 

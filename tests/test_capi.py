@@ -66,6 +66,7 @@ def test_bad_arguments(lib):
     assert L.ygg_step(None, None, None, None, None, None, 1, None) == 5
     assert L.ygg_take_errors(None, None, None) == 5
     assert L.ygg_generate(None, None, 1, 1, None, 0.0, 0, 0, None, None, None) == 5
+    assert L.ygg_kernel_name(None, 1, 1, 0, ctypes.create_string_buffer(8), 8) == 5
     assert L.ygg_float_load(None, 32, 0, ctypes.byref(h)) == 5
     assert L.ygg_float_run(None, None, 1, 1, None, None, None, None, None) == 5
     d = lib.FloatDesc()

@@ -66,8 +66,7 @@ def test_full_size_digest(cfg):
     x = w.make_tokens()
     B, T = x.shape
     model = Yggdrasil.load(path)
-    kind = ("pipe" if B <= model.info.pipe_max_streams else "fast") if model.info.kernel == 1 else "generic"
-    _say(f"config {cfg}: {B} x {T}, kernel {kind}")
+    _say(f"config {cfg}: {B} x {T}, kernel {model.kernel_name(B, T)}")
     t0 = time.time()
     dg, ls, st = _gpu_sums(model, x)
     model.close()

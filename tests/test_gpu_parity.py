@@ -110,6 +110,12 @@ def _expect_kernel(model, kernel_env):
     if kernel_env != "generic":
         assert info.deep == deep, info.deep
     assert (info.deep_max_streams > 0) == (kernel_env == "deep" and deep), info.deep_max_streams
+    name = model.kernel_name(8, 64)
+    want = {"generic": "ygg::run_kernel<", "pipe": "ygg::pipe_kernel<",
+            "fast": "ygg::fast_kernel<", "deep": "ygg::fast_kernel<"}[kernel_env]
+    assert name.startswith(want), name
+    if kernel_env in ("fast", "deep"):
+        assert name.endswith(", false, true>" if kernel_env == "deep" and deep else ", false, false>"), name
 
 
 def test_config1_full_stream(hip, c12, kernel_env):
@@ -358,3 +364,35 @@ def test_deep_descent_plans(hip, model_dir, c12, monkeypatch, which, plan):
             got = {key: np.concatenate([p[key] for p in parts], 1) for key in ("leaves", "states", "logits")}
             _compare(got, ref)
         model.close()
+
+
+def test_default_dispatch(hip, model_dir, monkeypatch):
+    """The kernel the library picks per call (ygg_kernel_name), and parity of the layer-pipelined kernel's capped
+    build, which only calls with more streams than the uncapped build keeps resident reach."""
+    monkeypatch.delenv("YGG_KERNEL", raising=False)
+    monkeypatch.delenv("YGG_DEEP", raising=False)
+    path = model_dir / "c4small_gauss.bin"
+    if not path.exists():
+        synth.write_model(synth.ModelSpec(128, 16, 10, 256, 4, router="gauss"), 11, path)
+    model = hip.load(path)
+    info = model.info
+    assert model.kernel_name(1, 64) == "ygg::pipe_kernel<128, 4, false>"
+    assert model.kernel_name(1, 1) == "ygg::fast_kernel<128, 4, false, false>"
+    assert model.kernel_name(info.pipe_max_streams + 1, 64) == "ygg::fast_kernel<128, 4, false, false>"
+    assert model.kernel_name(1, 100, generate=True) == "ygg::fast_kernel<128, 4, true, true>"
+    assert model.kernel_name(1, 4, generate=True) == "ygg::fast_kernel<128, 4, true, false>"
+    assert model.kernel_name(info.deep_max_streams + 1, 100, generate=True) == "ygg::fast_kernel<128, 4, true, false>"
+    # the smallest batch that runs on the capped build
+    lo, hi = 1, info.pipe_max_streams
+    assert model.kernel_name(hi, 16) == "ygg::pipe_kernel<128, 4, true>"
+    while lo < hi:
+        mid = (lo + hi) // 2
+        if model.kernel_name(mid, 16) == "ygg::pipe_kernel<128, 4, true>":
+            hi = mid
+        else:
+            lo = mid + 1
+    assert lo > 1 and model.kernel_name(lo - 1, 16) == "ygg::pipe_kernel<128, 4, false>"
+    _say(f"capped pipe build from {lo} streams (pipe_max {info.pipe_max_streams})")
+    x = synth.zipf_bytes(lo, 12, 9)
+    _compare(_gpu_run(model, x), Oracle(path).run(x, states=True))
+    model.close()

@@ -16,7 +16,7 @@ LIB_PATH = Path(__file__).resolve().parent / "libygg_hip.so"
 # every entry point of include/ygg_hip.h
 SYMBOLS = ("ygg_load", "ygg_load_blob", "ygg_model_info", "ygg_free", "ygg_step", "ygg_run", "ygg_score",
            "ygg_generate", "ygg_take_errors", "ygg_float_load", "ygg_float_run", "ygg_float_take_errors",
-           "ygg_float_free", "ygg_last_error", "ygg_version")
+           "ygg_float_free", "ygg_kernel_name", "ygg_last_error", "ygg_version")
 
 ERRORS = {1: "io", 2: "format", 3: "limits", 4: "nomem", 5: "arg", 6: "token", 7: "device"}
 ABI_VERSION = 7
@@ -75,6 +75,7 @@ def lib() -> ctypes.CDLL:
     L.ygg_score.argtypes = [vp, vp, vp, i32, i32, vp, vp, vp]
     L.ygg_generate.argtypes = [vp, vp, i32, i32, vp, ctypes.c_float, i32, ctypes.c_uint64, vp, vp, vp]
     L.ygg_take_errors.argtypes = [vp, vp, ctypes.POINTER(ctypes.c_uint32)]
+    L.ygg_kernel_name.argtypes = [vp, i32, i32, i32, ctypes.c_char_p, ctypes.c_size_t]
     L.ygg_float_load.argtypes = [ctypes.POINTER(FloatDesc), i32, i32, ctypes.POINTER(vp)]
     L.ygg_float_run.argtypes = [vp, vp, i32, i32, vp, vp, vp, vp, vp]
     L.ygg_float_take_errors.argtypes = [vp, vp, ctypes.POINTER(ctypes.c_uint32)]

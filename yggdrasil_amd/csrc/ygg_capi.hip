@@ -15,17 +15,8 @@
 #include <vector>
 
 #include "../../include/ygg_hip.h"
+#include "ygg_launch.h"
 #include "ygg_layout.h"
-
-namespace ygg {
-// kernel launchers, one per (d_state, block, readout rank); defined in ygg_kernels_*.hip
-typedef hipError_t (*Launcher)(const YggDevModel &, const int32_t *, int, int, int8_t *, const YggIO &, hipStream_t);
-Launcher find_launcher(int n, int blk, int R);
-Launcher find_fast_launcher(int n, int L);
-Launcher find_deep_launcher(int n, int L);
-Launcher find_pipe_launcher(int n, int L);
-int pipe_blocks_per_cu(int n, int L);
-}  // namespace ygg
 
 namespace {
 
@@ -360,12 +351,14 @@ struct ygg_model {
     int device = 0;
     void *arena = nullptr;
     size_t arena_bytes = 0;
-    ygg::Launcher launch = nullptr;
-    ygg::Launcher launch_pipe = nullptr;   // T > 1 and B <= pipe_max_streams
-    int pipe_max_streams = 0;
-    ygg::Launcher launch_deep = nullptr;   // generate with B <= deep_max_streams (every call when deep_all)
+    ygg::Kernel run;                  // per-stream: fast_kernel (4 streams per workgroup) or run_kernel
+    ygg::Kernel pipe;                 // layer-pipelined, 128-VGPR cap: T > 1 and B <= pipe_max_streams
+    ygg::Kernel pipe_few;             // the same without the cap: B <= pipe_few_max_streams
+    int pipe_max_streams = 0, pipe_few_max_streams = 0;
+    bool pipe_all = false;            // YGG_KERNEL=pipe: every call
+    ygg::Kernel deep;                 // deep descent: generate with B <= deep_max_streams
     int deep_max_streams = 0;
-    bool deep_all = false;
+    bool deep_all = false;            // YGG_KERNEL=deep: every call
 };
 
 namespace {
@@ -374,7 +367,7 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     FileArrays fa;
     if (int rc = parse(data, size, fa)) return rc;
     const int L = fa.n_layers, n = fa.n, V = fa.V, VP = (V + 31) / 32 * 32, E = 1 << fa.D, R = fa.R, R2 = fa.R2;
-    ygg::Launcher launch = ygg::find_launcher(n, fa.blk, R);
+    ygg::Kernel launch = ygg::find_launcher(n, fa.blk, R);
     if (!launch) return fail(YGG_ERR_LIMITS, "no kernel for d_state %d, block %d, readout rank %d", n, fa.blk, R);
     int64_t hb_nb = 0;
     const float *head_b = (const float *)fa.get("head_b", &hb_nb);
@@ -396,7 +389,7 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     // one for every call; YGG_DEEP=0 turns the deep descent off.
     const char *kenv = getenv("YGG_KERNEL");
     const std::string kmode = kenv ? kenv : "";
-    ygg::Launcher fast = nullptr;
+    ygg::Kernel fast;
     // (layer-input rank 16 exactly, and every routed layer's table and gather records addressable in 32 bits)
     const bool small_tables = (int64_t)E * V * n * 2 < ((int64_t)1 << 32) && (int64_t)E * 64 * n < ((int64_t)1 << 32);
     if (kmode != "generic" && R == 8 && fa.blk == 16 && (R2 == 16 || L == 1) && !factored && !group && L <= 4 &&
@@ -427,8 +420,11 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     const char *denv = getenv("YGG_DEEP");
     const bool deep = fast && L > 1 && !(denv && !strcmp(denv, "0")) && rplan.n >= 2 && rplan.n <= 4 &&
                       rplan.h[0] >= 2 && (rplan.n < 4 || rplan.h[2] + rplan.h[3] <= 6);
-    ygg::Launcher pipe = nullptr, deepk = nullptr;
-    if (fast && kmode != "fast" && kmode != "deep") pipe = ygg::find_pipe_launcher(n, L);
+    ygg::Kernel pipe, pipe_few, deepk;
+    if (fast && kmode != "fast" && kmode != "deep") {
+        pipe = ygg::find_pipe_launcher(n, L, true);
+        pipe_few = ygg::find_pipe_launcher(n, L, false);
+    }
     if (deep && kmode != "fast" && kmode != "pipe") deepk = ygg::find_deep_launcher(n, L);
     const int64_t slots = plan_slots(rplan);
     // device arena plan: every array 256-byte aligned
@@ -481,7 +477,7 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
         const int El = routed ? E : V;
         uint8_t *gath = H + p.gath.off;
         const GatherLayout gl = p.gl;
-        const bool split = fast != nullptr;
+        const bool split = static_cast<bool>(fast);
         parallel_for(El, [&, gath, gl, routed, split](int64_t e) {
             relayout_expert(fa, y, gl, routed, split, y.rec + e * y.record_bytes, gath + e * gl.bytes);
         });
@@ -548,19 +544,22 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     int cus = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || cus <= 0) cus = 256;
     ygg_model *m = new ygg_model();
-    m->launch_pipe = pipe;
-    // pipe_kernel when the workgroups of all B streams of a call are resident at once, or always with YGG_KERNEL=pipe
-    const int pipe_per_cu = pipe ? ygg::pipe_blocks_per_cu(n, L) : 0;
-    m->pipe_max_streams = pipe ? (kmode == "pipe" ? INT32_MAX : pipe_per_cu * cus) : 0;
+    // pipe_kernel when the workgroups of all B streams of a call are resident at once (without the VGPR cap while
+    // they fit so), or always with YGG_KERNEL=pipe
+    m->pipe = pipe;
+    m->pipe_few = pipe_few;
+    m->pipe_all = pipe && kmode == "pipe";
+    m->pipe_max_streams = pipe ? (m->pipe_all ? INT32_MAX : ygg::pipe_blocks_per_cu(n, L, true) * cus) : 0;
+    m->pipe_few_max_streams = pipe_few ? ygg::pipe_blocks_per_cu(n, L, false) * cus : 0;
     // generation with one stream per workgroup while the streams do not outnumber the CUs (for more, the 4 streams
     // per workgroup of fast_kernel win); YGG_KERNEL=deep takes it for every call
-    m->launch_deep = deepk;
+    m->deep = deepk;
     m->deep_all = deepk && kmode == "deep";
     m->deep_max_streams = deepk ? (m->deep_all ? INT32_MAX : cus) : 0;
     m->device = device;
     m->arena = arena;
     m->arena_bytes = total;
-    m->launch = launch;
+    m->run = launch;
     uint8_t *A = (uint8_t *)arena;
     auto at = [&](const Piece &p) -> void * { return p.bytes ? A + p.off : nullptr; };
     YggDevModel &d = m->dev;
@@ -615,12 +614,16 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     return YGG_OK;
 }
 
-// The kernel of a run/score/step call of B streams and T tokens: the layer-pipelined one for T > 1 when its
-// workgroups fit, else the per-stream kernel (or the deep one when forced for every call).
-ygg::Launcher pick(const ygg_model *m, int B, int T) {
-    if (m->deep_all) return m->launch_deep;
-    if (T > 1 && m->launch_pipe && B <= m->pipe_max_streams) return m->launch_pipe;
-    return m->launch;
+// The kernel of a call of B streams and T tokens (gen: ygg_generate). Generation: the deep kernel for >= 8 tokens
+// and B <= deep_max_streams, else the per-stream kernel (every token needs all layers of the one before it, so never
+// the layer-pipelined one). Otherwise: the layer-pipelined kernel for T > 1 when its workgroups fit (the uncapped
+// build while they fit so), else the per-stream kernel. A kernel forced by YGG_KERNEL takes every call it can run.
+const ygg::Kernel &pick(const ygg_model *m, int B, int T, bool gen) {
+    if (m->deep_all) return m->deep;
+    if (gen) return (m->deep && B <= m->deep_max_streams && T >= 8) ? m->deep : m->run;
+    if (m->pipe && (m->pipe_all || (T > 1 && B <= m->pipe_max_streams)))
+        return (m->pipe_few && B <= m->pipe_few_max_streams) ? m->pipe_few : m->pipe;
+    return m->run;
 }
 
 struct DeviceGuard {
@@ -707,13 +710,13 @@ int ygg_run(const ygg_model *m, const int32_t *d_tokens, int B, int T, int8_t *d
     DeviceGuard g;
     HIP_TRY(g.set(m->device));
     // the pipelined kernel overlaps the layers of consecutive tokens, so it needs more than one token per launch
-    ygg::Launcher k = pick(m, B, T);
+    const ygg::Kernel &k = pick(m, B, T, false);
     YggIO io{};
     io.logits = d_logits;
     io.leaves = d_leaves;
     io.states = d_states;
     io.digest = (unsigned long long *)d_digest;
-    HIP_TRY(k(m->dev, d_tokens, B, T, d_state, io, (hipStream_t)stream));
+    HIP_TRY(k.fn(m->dev, d_tokens, B, T, d_state, io, (hipStream_t)stream));
     return YGG_OK;
 }
 
@@ -725,11 +728,11 @@ int ygg_score(const ygg_model *m, const int32_t *d_tokens, const int32_t *d_targ
     if (!d_state || !d_nll || (T > 0 && (!d_tokens || !d_targets))) return fail(YGG_ERR_ARG, "NULL buffer");
     DeviceGuard g;
     HIP_TRY(g.set(m->device));
-    ygg::Launcher k = pick(m, B, T);
+    const ygg::Kernel &k = pick(m, B, T, false);
     YggIO io{};
     io.targets = d_targets;
     io.nll = d_nll;
-    HIP_TRY(k(m->dev, d_tokens, B, T, d_state, io, (hipStream_t)stream));
+    HIP_TRY(k.fn(m->dev, d_tokens, B, T, d_state, io, (hipStream_t)stream));
     return YGG_OK;
 }
 
@@ -744,17 +747,14 @@ int ygg_generate(const ygg_model *m, const int32_t *d_first, int B, int n, int8_
     if (!d_first || !d_state || !d_out) return fail(YGG_ERR_ARG, "NULL buffer");
     DeviceGuard g;
     HIP_TRY(g.set(m->device));
-    // every token needs all layers of the one before it: a per-stream kernel, never the layer-pipelined one
-    // (the deep kernel's LDS staging pays off over a few tokens)
-    const ygg::Launcher k = (m->launch_deep && B <= m->deep_max_streams && (n >= 8 || m->deep_all)) ? m->launch_deep
-                                                                                                   : m->launch;
+    const ygg::Kernel &k = pick(m, B, n, true);
     YggIO io{};
     io.logits = d_logits;
     io.gen = d_out;
     io.temperature = temperature;
     io.top_k = top_k;
     io.seed = (unsigned long long)seed;
-    HIP_TRY(k(m->dev, d_first, B, n, d_state, io, (hipStream_t)stream));
+    HIP_TRY(k.fn(m->dev, d_first, B, n, d_state, io, (hipStream_t)stream));
     return YGG_OK;
 }
 
@@ -769,12 +769,20 @@ int ygg_step(const ygg_model *m, const int32_t *d_tokens, const int8_t *d_state_
     if (d_state_in != d_state_out)
         HIP_TRY(hipMemcpyAsync(d_state_out, d_state_in, (size_t)B * m->dev.L * m->dev.N, hipMemcpyDeviceToDevice,
                                (hipStream_t)stream));
-    // one token: a per-stream kernel (a one-token launch cannot overlap layers), or the pipelined one when forced
-    ygg::Launcher k = (m->launch_pipe && m->pipe_max_streams == INT32_MAX) ? m->launch_pipe : pick(m, B, 1);
+    // one token: a per-stream kernel (a one-token launch cannot overlap layers), or a forced one
+    const ygg::Kernel &k = pick(m, B, 1, false);
     YggIO io{};
     io.logits = d_logits;
     io.leaves = d_leaves;
-    HIP_TRY(k(m->dev, d_tokens, B, 1, d_state_out, io, (hipStream_t)stream));
+    HIP_TRY(k.fn(m->dev, d_tokens, B, 1, d_state_out, io, (hipStream_t)stream));
+    return YGG_OK;
+}
+
+int ygg_kernel_name(const ygg_model *m, int B, int T, int generate, char *name, size_t len) {
+    if (!m || !name || len == 0) return fail(YGG_ERR_ARG, "NULL argument");
+    if (B < 0 || T < 0) return fail(YGG_ERR_ARG, "negative B (%d) or T (%d)", B, T);
+    const ygg::Kernel &k = pick(m, B, T, generate != 0);
+    snprintf(name, len, k.name, generate ? "true" : "false");
     return YGG_OK;
 }
 

@@ -718,8 +718,10 @@ void fast_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
 
 // ----------------------------------------------------------------------------------------------- pipe_kernel
 
-template <int N, int L>
-__global__ __launch_bounds__(64 * L) __attribute__((amdgpu_waves_per_eu(4)))
+// CAP: at most 128 VGPRs (4 wavefronts per SIMD: more streams resident, some registers spilled), else as many as
+// the kernel needs (no spills: faster for few streams)
+template <int N, int L, bool CAP>
+__global__ __launch_bounds__(64 * L) __attribute__((amdgpu_waves_per_eu(CAP ? 4 : 1)))
 void pipe_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B, int T, int8_t *__restrict__ state,
                  const YggIO io) {
     // generation needs every layer of a token before the next one; the dispatcher never sends it here

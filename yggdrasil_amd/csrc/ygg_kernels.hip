@@ -2,10 +2,9 @@
 // C-ABI dispatches through. The specialised kernels are instantiated in ygg_kernels_fast.hip and
 // ygg_kernels_deep.hip.
 #include "ygg_kernel.h"
+#include "ygg_launch.h"
 
 namespace ygg {
-
-typedef hipError_t (*Launcher)(const YggDevModel &, const int32_t *, int, int, int8_t *, const YggIO &, hipStream_t);
 
 template <int N, int BLK, int R>
 hipError_t launch(const YggDevModel &m, const int32_t *tokens, int B, int T, int8_t *state, const YggIO &io,
@@ -17,17 +16,22 @@ hipError_t launch(const YggDevModel &m, const int32_t *tokens, int B, int T, int
     return hipGetLastError();
 }
 
+template <int N, int BLK, int R> Kernel kernel() {
+    return make_kernel(launch<N, BLK, R>, "ygg::run_kernel<%d, %d, %d, %%s>", N, BLK, R);
+}
+
 #define YGG_R(N, BLK) \
-    if (R == 8) return launch<N, BLK, 8>; if (R == 16) return launch<N, BLK, 16>; if (R == 32) return launch<N, BLK, 32>;
+    if (R == 8) return kernel<N, BLK, 8>(); if (R == 16) return kernel<N, BLK, 16>(); \
+    if (R == 32) return kernel<N, BLK, 32>();
 #define YGG_B(N) \
     if (blk == 8) { YGG_R(N, 8) } if (blk == 16) { YGG_R(N, 16) }
 
-Launcher find_launcher(int n, int blk, int R) {
+Kernel find_launcher(int n, int blk, int R) {
     if (n == 64) { YGG_B(64) }
     if (n == 96) { YGG_B(96) }
     if (n == 128) { YGG_B(128) }
     if (n == 256) { YGG_B(256) }
-    return nullptr;
+    return Kernel();
 }
 
 }  // namespace ygg

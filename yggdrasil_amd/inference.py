@@ -75,6 +75,13 @@ class Yggdrasil:
             raise ImportError(f"backend='hip' needs the built library ({e})") from e
         return cls(path, **kw)
 
+    def kernel_name(self, B: int, T: int, generate: bool = False) -> str:
+        """The kernel a call of B streams and T tokens launches (generate: `generate` of T tokens), by the name
+        profilers show for it."""
+        buf = ctypes.create_string_buffer(128)
+        check(_lib.lib().ygg_kernel_name(self._h, B, T, int(generate), buf, len(buf)))
+        return buf.value.decode()
+
     def close(self):
         if getattr(self, "_h", None):
             self._graphs.clear()
