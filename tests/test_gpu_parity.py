@@ -115,7 +115,7 @@ def _expect_kernel(model, kernel_env):
             "fast": "ygg::fast_kernel<", "deep": "ygg::fast_kernel<"}[kernel_env]
     assert name.startswith(want), name
     if kernel_env in ("fast", "deep"):
-        assert name.endswith(", false, true>" if kernel_env == "deep" and deep else ", false, false>"), name
+        assert name.endswith(", false, true, false>" if kernel_env == "deep" and deep else ", false, false, false>"), name
 
 
 def test_config1_full_stream(hip, c12, kernel_env):
@@ -368,7 +368,8 @@ def test_deep_descent_plans(hip, model_dir, c12, monkeypatch, which, plan):
 
 def test_default_dispatch(hip, model_dir, monkeypatch):
     """The kernel the library picks per call (ygg_kernel_name), and parity of the layer-pipelined kernel's capped
-    build, which only calls with more streams than the uncapped build keeps resident reach."""
+    build, which only calls with more streams than the uncapped build keeps resident reach (the per-stream kernel's
+    capped build runs configurations 4 and 5 in test_gpu_fullsize.py)."""
     monkeypatch.delenv("YGG_KERNEL", raising=False)
     monkeypatch.delenv("YGG_DEEP", raising=False)
     path = model_dir / "c4small_gauss.bin"
@@ -376,13 +377,16 @@ def test_default_dispatch(hip, model_dir, monkeypatch):
         synth.write_model(synth.ModelSpec(128, 16, 10, 256, 4, router="gauss"), 11, path)
     model = hip.load(path)
     info = model.info
+    fast = "ygg::fast_kernel<128, 4, {}, false, {}>"
     assert model.kernel_name(1, 64) == "ygg::pipe_kernel<128, 4, false>"
-    assert model.kernel_name(1, 1) == "ygg::fast_kernel<128, 4, false, false>"
-    assert model.kernel_name(info.pipe_max_streams + 1, 64) == "ygg::fast_kernel<128, 4, false, false>"
-    assert model.kernel_name(1, 100, generate=True) == "ygg::fast_kernel<128, 4, true, true>"
-    assert model.kernel_name(1, 4, generate=True) == "ygg::fast_kernel<128, 4, true, false>"
-    assert model.kernel_name(info.deep_max_streams + 1, 100, generate=True) == "ygg::fast_kernel<128, 4, true, false>"
-    # the smallest batch that runs on the capped build
+    assert model.kernel_name(1, 1) == fast.format("false", "false")
+    assert model.kernel_name(info.pipe_max_streams + 1, 64) == fast.format("false", "false")
+    assert model.kernel_name(16384, 64) == fast.format("false", "true")
+    assert model.kernel_name(1, 100, generate=True) == "ygg::fast_kernel<128, 4, true, true, false>"
+    assert model.kernel_name(1, 4, generate=True) == fast.format("true", "false")
+    assert model.kernel_name(info.deep_max_streams + 1, 100, generate=True) == fast.format("true", "false")
+    assert model.kernel_name(16384, 100, generate=True) == fast.format("true", "true")
+    # the smallest batch that runs on the capped pipe build
     lo, hi = 1, info.pipe_max_streams
     assert model.kernel_name(hi, 16) == "ygg::pipe_kernel<128, 4, true>"
     while lo < hi:

@@ -351,7 +351,9 @@ struct ygg_model {
     int device = 0;
     void *arena = nullptr;
     size_t arena_bytes = 0;
-    ygg::Kernel run;                  // per-stream: fast_kernel (4 streams per workgroup) or run_kernel
+    ygg::Kernel run;                  // per-stream: fast_kernel (4 streams per workgroup, capped) or run_kernel
+    ygg::Kernel run_few;              // fast_kernel without the VGPR cap: B <= run_few_max_streams[gen]
+    int run_few_max_streams[2] = {0, 0};
     ygg::Kernel pipe;                 // layer-pipelined, 128-VGPR cap: T > 1 and B <= pipe_max_streams
     ygg::Kernel pipe_few;             // the same without the cap: B <= pipe_few_max_streams
     int pipe_max_streams = 0, pipe_few_max_streams = 0;
@@ -394,7 +396,7 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     const bool small_tables = (int64_t)E * V * n * 2 < ((int64_t)1 << 32) && (int64_t)E * 64 * n < ((int64_t)1 << 32);
     if (kmode != "generic" && R == 8 && fa.blk == 16 && (R2 == 16 || L == 1) && !factored && !group && L <= 4 &&
         VP <= 256 && small_tables && transitions_split(fa, fl))
-        fast = ygg::find_fast_launcher(n, L);
+        fast = ygg::find_fast_launcher(n, L, true);
     if (fast) launch = fast;
 
     RoundPlan rplan = round_plan(L > 1 ? fa.D : 0);
@@ -560,6 +562,11 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     m->arena = arena;
     m->arena_bytes = total;
     m->run = launch;
+    // the uncapped per-stream build while every stream of the call is resident with it
+    if (fast) {
+        m->run_few = ygg::find_fast_launcher(n, L, false);
+        for (int g = 0; g < 2; g++) m->run_few_max_streams[g] = ygg::fast_blocks_per_cu(n, L, false, g) * 4 * cus;
+    }
     uint8_t *A = (uint8_t *)arena;
     auto at = [&](const Piece &p) -> void * { return p.bytes ? A + p.off : nullptr; };
     YggDevModel &d = m->dev;
@@ -616,14 +623,15 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
 
 // The kernel of a call of B streams and T tokens (gen: ygg_generate). Generation: the deep kernel for >= 8 tokens
 // and B <= deep_max_streams, else the per-stream kernel (every token needs all layers of the one before it, so never
-// the layer-pipelined one). Otherwise: the layer-pipelined kernel for T > 1 when its workgroups fit (the uncapped
-// build while they fit so), else the per-stream kernel. A kernel forced by YGG_KERNEL takes every call it can run.
+// the layer-pipelined one). Otherwise: the layer-pipelined kernel for T > 1 when its workgroups fit, else the
+// per-stream kernel. Of the two builds of a kernel, the uncapped one while all B streams are resident with it. A
+// kernel forced by YGG_KERNEL takes every call it can run.
 const ygg::Kernel &pick(const ygg_model *m, int B, int T, bool gen) {
     if (m->deep_all) return m->deep;
-    if (gen) return (m->deep && B <= m->deep_max_streams && T >= 8) ? m->deep : m->run;
-    if (m->pipe && (m->pipe_all || (T > 1 && B <= m->pipe_max_streams)))
+    if (gen && m->deep && B <= m->deep_max_streams && T >= 8) return m->deep;
+    if (!gen && m->pipe && (m->pipe_all || (T > 1 && B <= m->pipe_max_streams)))
         return (m->pipe_few && B <= m->pipe_few_max_streams) ? m->pipe_few : m->pipe;
-    return m->run;
+    return (m->run_few && B <= m->run_few_max_streams[gen]) ? m->run_few : m->run;
 }
 
 struct DeviceGuard {

@@ -542,9 +542,11 @@ __device__ __forceinline__ void store_logits(float *o, const float (&lg)[4], int
 
 // GEN: sample the next input from the logits of every token (io.gen), instead of reading it from tokens. DEEP: one
 // stream per workgroup with the deep descent (generation for few streams), else 4 streams per workgroup with
-// descend.
-template <int N, int L, bool GEN, bool DEEP>
-__global__ __launch_bounds__(64 * kFastWaves) __attribute__((amdgpu_waves_per_eu(DEEP ? 1 : 4)))
+// descend. CAP (not DEEP): at most 128 VGPRs, 4 wavefronts per SIMD (the most streams resident, some registers
+// spilled), else up to 256 (no spills; for calls whose streams all fit at the lower occupancy).
+template <int N, int L, bool GEN, bool DEEP, bool CAP>
+__global__ __launch_bounds__(64 * kFastWaves)
+__attribute__((amdgpu_waves_per_eu(DEEP ? 1 : (CAP ? 4 : 2))))
 void fast_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B, int T, int8_t *__restrict__ state,
                  const YggIO io) {
     float *__restrict__ logits = io.logits;

@@ -12,9 +12,9 @@ hipError_t launch_deep(const YggDevModel &m, const int32_t *tokens, int B, int T
     // one stream per workgroup of 4 wavefronts (all stage the LDS tables, one runs the stream)
     const dim3 grid(B), block(64 * kFastWaves);
     if (io.gen)
-        hipLaunchKernelGGL((fast_kernel<N, L, true, true>), grid, block, 0, stream, m, tokens, B, T, state, io);
+        hipLaunchKernelGGL((fast_kernel<N, L, true, true, false>), grid, block, 0, stream, m, tokens, B, T, state, io);
     else
-        hipLaunchKernelGGL((fast_kernel<N, L, false, true>), grid, block, 0, stream, m, tokens, B, T, state, io);
+        hipLaunchKernelGGL((fast_kernel<N, L, false, true, false>), grid, block, 0, stream, m, tokens, B, T, state, io);
     return hipGetLastError();
 }
 
@@ -66,7 +66,7 @@ Kernel find_pipe_launcher(int n, int L, bool cap) { return cap ? pipe_for<true>(
 int pipe_blocks_per_cu(int n, int L, bool cap) { return cap ? occ_for<true>(n, L) : occ_for<false>(n, L); }
 
 template <int N, int L> Kernel deep_k() {
-    return make_kernel(launch_deep<N, L>, "ygg::fast_kernel<%d, %d, %%s, true>", N, L);
+    return make_kernel(launch_deep<N, L>, "ygg::fast_kernel<%d, %d, %%s, true, false>", N, L);
 }
 
 // fast_kernel with the deep descent (2 <= L <= 4)

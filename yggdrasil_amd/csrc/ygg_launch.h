@@ -30,7 +30,8 @@ inline Kernel make_kernel(Launcher fn, const char *fmt, ...) {
 }
 
 Kernel find_launcher(int n, int blk, int R);                // run_kernel (ygg_kernels.hip)
-Kernel find_fast_launcher(int n, int L);                    // fast_kernel, many streams (ygg_kernels_fast.hip)
+Kernel find_fast_launcher(int n, int L, bool cap);          // fast_kernel, 128-VGPR cap or none (ygg_kernels_fast.hip)
+int fast_blocks_per_cu(int n, int L, bool cap, bool gen);   // its resident workgroups (4 streams each) per CU
 Kernel find_deep_launcher(int n, int L);                    // fast_kernel, deep descent (ygg_kernels_deep.hip)
 Kernel find_pipe_launcher(int n, int L, bool cap);          // pipe_kernel, 128-VGPR cap or none (ygg_kernels_deep.hip)
 int pipe_blocks_per_cu(int n, int L, bool cap);             // its resident workgroups per CU
