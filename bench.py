@@ -41,9 +41,20 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def model_path(cfg: int, cache: Path) -> Path:
+def workload(cfg: int, storage: str = "table"):
+    """The configuration's workload; storage "factored" stores its routed inputs factored at rank 64 (the format's
+    other storage, cpu/ygg.cpp:339-358: about 0.78 GB for configuration 4 instead of 3.63 GB)."""
+    import dataclasses
     from yggdrasil_amd import synth
     w = synth.CONFIGS[cfg]
+    if storage == "factored":
+        w = dataclasses.replace(w, name=w.name + "_factored", spec=dataclasses.replace(w.spec, input_rank=64))
+    return w
+
+
+def model_path(cfg: int, cache: Path, storage: str = "table") -> Path:
+    from yggdrasil_amd import synth
+    w = workload(cfg, storage)
     cache.mkdir(parents=True, exist_ok=True)
     p = cache / f"{w.name}_seed{w.model_seed}.bin"
     if not p.exists():
@@ -176,6 +187,8 @@ def main():
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--config", type=int, default=4, choices=[1, 2, 3, 4, 5])
+    ap.add_argument("--storage", default="table", choices=["table", "factored"],
+                    help="routed-layer input storage of the synthetic model (factored: rank 64)")
     ap.add_argument("--streams", type=int, default=0, help="override the configuration's stream count")
     ap.add_argument("--tokens", type=int, default=0, help="override the configuration's tokens per stream")
     ap.add_argument("--cache", default=os.environ.get("YGG_BENCH_DIR", os.path.join(tempfile.gettempdir(),
@@ -195,9 +208,9 @@ def main():
     from yggdrasil_amd.inference import Yggdrasil
     from yggdrasil_amd.roofline import step_bytes
 
-    w = synth.CONFIGS[a.config]
+    w = workload(a.config, a.storage)
     B, T = a.streams or w.streams, a.tokens or w.steps
-    path = model_path(a.config, Path(a.cache))
+    path = model_path(a.config, Path(a.cache), a.storage)
     t0 = time.time()
     model = Yggdrasil.load(path, device="cuda:0")
     info = model.info

@@ -5,7 +5,9 @@ weights that step touches, plus the per-stream inputs and outputs:
 
     sum over routed layers l of
         distinct leaves r        x (2 n b + n R2 + R n)     transition A16, layer-input U', readout P
-        distinct (r, x)          x 2 n                      table row T_r[x] (factored: U_r k n + c_r 2 n + 4)
+                                   (factored: + k n + 2 n + 4, the input projection U_r, bias c_r and scale)
+        distinct (r, x)          x 2 n                      table row T_r[x] (table storage)
+        distinct tokens x        x k                        token code v[x] (factored storage, rank k)
         distinct router nodes    x n                        router rows on the paths taken
         distinct (x, node)       x 4                        thresholds thr[x][node]
     + distinct tokens x          x (2 n b + R n + 2 n)      token layer: A16, P and its own table row
@@ -26,8 +28,8 @@ def step_bytes(leaves: np.ndarray, tokens: np.ndarray, n: int, b: int, R: int, R
     T-token launch, the per-launch state bytes in 'state' and the per-token figures."""
     B, T, L = leaves.shape
     E = 1 << D
-    leaf_w = 2 * n * b + n * R2 + R * n
-    row_w = (factored_rank * n + 2 * n + 4) if factored_rank else 2 * n
+    leaf_w = 2 * n * b + n * R2 + R * n + ((factored_rank * n + 2 * n + 4) if factored_rank else 0)
+    row_w = 0 if factored_rank else 2 * n
     tok_w = 2 * n * b + R * n + 2 * n
     io = B * (4 + 4 * V)
     comp = 0
@@ -41,13 +43,13 @@ def step_bytes(leaves: np.ndarray, tokens: np.ndarray, n: int, b: int, R: int, R
         for l in range(1, L):
             r = leaves[:, t, l].astype(np.int64)
             comp += np.unique(r).size * leaf_w
-            comp += np.unique(r * V + x).size * row_w
+            comp += np.unique(r * V + x).size * row_w + np.unique(x).size * factored_rank
             # the path of leaf r: node at depth d is (r + E) >> (D - d), d = 0 .. D-1
             d = np.arange(D, dtype=np.int64)
             nodes = (r[:, None] + E) >> (D - d)[None, :]
             comp += np.unique(nodes).size * n
             comp += np.unique(x[:, None] * E + nodes).size * 4
-            per += B * (leaf_w + row_w + D * (n + 4))
+            per += B * (leaf_w + row_w + factored_rank + D * (n + 4))
     scale = T / len(steps)
     state = 2 * B * L * n
     comp, per = comp * scale + state, per * scale + state
