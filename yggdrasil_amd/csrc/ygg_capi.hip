@@ -392,11 +392,21 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     const char *kenv = getenv("YGG_KERNEL");
     const std::string kmode = kenv ? kenv : "";
     ygg::Kernel fast;
-    // (layer-input rank 16 exactly, and every routed layer's table and gather records addressable in 32 bits)
-    const bool small_tables = (int64_t)E * V * n * 2 < ((int64_t)1 << 32) && (int64_t)E * 64 * n < ((int64_t)1 << 32);
-    if (kmode != "generic" && R == 8 && fa.blk == 16 && (R2 == 16 || L == 1) && !factored && !group && L <= 4 &&
-        VP <= 256 && small_tables && transitions_split(fa, fl))
-        fast = ygg::find_fast_launcher(n, L, true);
+    // (a shape of YGG_SHAPES, up to 5 layers; a one-layer model has no layer input and runs at any layer-input rank
+    // as 16; every routed layer's table and gather records addressable in 32 bits)
+    auto shape_ok = [](int nn, int rr, int r2) {
+#define YGG_S(N_, R_, R2_) \
+    if (nn == N_ && rr == R_ && r2 == R2_) return true;
+        YGG_SHAPES(YGG_S)
+#undef YGG_S
+        return false;
+    };
+    const int R2f = L == 1 ? 16 : R2;
+    const int64_t rec_bound = (int64_t)n * (2 * fa.blk + R2 + R) + 128;     // gather record bytes, at most
+    const bool small_tables = (int64_t)E * V * n * 2 < ((int64_t)1 << 32) && (int64_t)E * rec_bound < ((int64_t)1 << 32);
+    if (kmode != "generic" && fa.blk == 16 && shape_ok(n, R, R2f) && !factored && !group &&
+        L <= ygg::kMaxFastLayers && VP <= 256 && small_tables && transitions_split(fa, fl))
+        fast = ygg::find_fast_launcher(n, R, R2f, L, true);
     if (fast) launch = fast;
 
     RoundPlan rplan = round_plan(L > 1 ? fa.D : 0);
@@ -424,10 +434,12 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
                       rplan.h[0] >= 2 && (rplan.n < 4 || rplan.h[2] + rplan.h[3] <= 6);
     ygg::Kernel pipe, pipe_few, deepk;
     if (fast && kmode != "fast" && kmode != "deep") {
-        pipe = ygg::find_pipe_launcher(n, L, true);
-        pipe_few = ygg::find_pipe_launcher(n, L, false);
+        pipe = ygg::find_pipe_launcher(n, R, R2f, L, true);
+        pipe_few = ygg::find_pipe_launcher(n, R, R2f, L, false);
     }
-    if (deep && kmode != "fast" && kmode != "pipe") deepk = ygg::find_deep_launcher(n, L);
+    // (the deep kernel exists where its LDS fits a workgroup)
+    const ygg::Kernel deep_avail = deep ? ygg::find_deep_launcher(n, R, R2f, L) : ygg::Kernel();
+    if (kmode != "fast" && kmode != "pipe") deepk = deep_avail;
     const int64_t slots = plan_slots(rplan);
     // device arena plan: every array 256-byte aligned
     struct Piece { size_t off, bytes; };
@@ -551,8 +563,8 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     m->pipe = pipe;
     m->pipe_few = pipe_few;
     m->pipe_all = pipe && kmode == "pipe";
-    m->pipe_max_streams = pipe ? (m->pipe_all ? INT32_MAX : ygg::pipe_blocks_per_cu(n, L, true) * cus) : 0;
-    m->pipe_few_max_streams = pipe_few ? ygg::pipe_blocks_per_cu(n, L, false) * cus : 0;
+    m->pipe_max_streams = pipe ? (m->pipe_all ? INT32_MAX : ygg::pipe_blocks_per_cu(n, R, R2f, L, true) * cus) : 0;
+    m->pipe_few_max_streams = pipe_few ? ygg::pipe_blocks_per_cu(n, R, R2f, L, false) * cus : 0;
     // generation with one stream per workgroup while the streams do not outnumber the CUs (for more, the 4 streams
     // per workgroup of fast_kernel win); YGG_KERNEL=deep takes it for every call
     m->deep = deepk;
@@ -564,8 +576,9 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     m->run = launch;
     // the uncapped per-stream build while every stream of the call is resident with it
     if (fast) {
-        m->run_few = ygg::find_fast_launcher(n, L, false);
-        for (int g = 0; g < 2; g++) m->run_few_max_streams[g] = ygg::fast_blocks_per_cu(n, L, false, g) * 4 * cus;
+        m->run_few = ygg::find_fast_launcher(n, R, R2f, L, false);
+        for (int g = 0; g < 2; g++)
+            m->run_few_max_streams[g] = ygg::fast_blocks_per_cu(n, R, R2f, L, false, g) * 4 * cus;
     }
     uint8_t *A = (uint8_t *)arena;
     auto at = [&](const Piece &p) -> void * { return p.bytes ? A + p.off : nullptr; };
@@ -612,7 +625,7 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     I.n_experts = E; I.readout_rank = R; I.layer_input_rank = R2; I.input_rank = fa.K; I.shift = fa.shift;
     I.factored = factored; I.group = group; I.device = device; I.kernel = fast ? 1 : 0;
     I.pipe_max_streams = m->pipe_max_streams;
-    I.deep = deep ? 1 : 0;
+    I.deep = deep_avail ? 1 : 0;
     I.deep_max_streams = m->deep_max_streams;
     I.file_array_bytes = fa.bytes;
     I.device_bytes = (int64_t)total;

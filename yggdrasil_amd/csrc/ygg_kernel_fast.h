@@ -32,28 +32,39 @@ __device__ __forceinline__ void wave_sync() {
 
 constexpr int kFastWaves = 4;
 
+// constants of a state width N (block 16)
 template <int N> struct Fast {
-    static constexpr int R = 8, BLK = 16;
+    static constexpr int BLK = 16;
     static constexpr int C = Lanes<N>::C, NL = Lanes<N>::NL;
     static constexpr int Q4 = N / 4, QW = Q4 / 4;
     static constexpr int QA = (Q4 % 16 == 0) ? 16 : 8;
-    static constexpr int RL = ReadoutLanes<N, R>::RL, SP = ReadoutLanes<N, R>::SP, GP = ReadoutLanes<N, R>::GP;
-    static constexpr int SPW = SP / 4;
-    static constexpr int SPA = SP % 16 == 0 ? 16 : (SP % 8 == 0 ? 8 : 4);
     static constexpr int AW = C * BLK / 2, NA = AW / 4;
     static constexpr float kInvN = 1.0f / (float)N;
 };
 
+// a specialised shape: state width N, readout rank R, layer-input rank R2 (a multiple of 16)
+template <int N_, int R_, int R2_> struct Shape : Fast<N_> {
+    static constexpr int N = N_, R = R_, R2 = R2_;
+    static constexpr int RL = ReadoutLanes<N, R>::RL, SP = ReadoutLanes<N, R>::SP, GP = ReadoutLanes<N, R>::GP;
+    static constexpr int SPW = SP / 4;
+    static constexpr int SPA = SP % 16 == 0 ? 16 : (SP % 8 == 0 ? 8 : 4);
+    static constexpr int K4 = R2 / 4;      // U' dwords per coordinate
+    static constexpr int RG = R2 / 16;     // passes of 16 V' rows
+    static constexpr int QC = R / 4;       // 16-byte chunks of a lane's 4 unembedding classes
+    static constexpr int ZQ = R > 16 ? R : 16, ZL = R2 > 16 ? R2 : 16;    // LDS bytes of zq and zl
+};
+
 // the per-expert registers of one stream and layer
-template <int N> struct Gather {
-    uint32_t aw[Fast<N>::AW], pw[Fast<N>::SPW], uw[4][Fast<N>::C];
-    int trow[Fast<N>::C];
+template <class SH> struct Gather {
+    uint32_t aw[SH::AW], pw[SH::SPW], uw[SH::K4][SH::C];
+    int trow[SH::C];
 };
 
 // A quad lane's share of an n-byte row: for n = 128 the 16-byte chunks at qk 16 and 64 + qk 16, with LDS rows
 // kLdsRow = 192 bytes apart, so that the 16 quads of a wavefront reading 16 rows hit 64 distinct banks (contiguous
-// 32-byte quarters of 128-byte rows put rows j and j + 2 on the same banks); otherwise the contiguous quarter qk Q4.
-template <int N> constexpr int kLdsRow = N == 128 ? 192 : N;
+// 32-byte quarters of 128-byte rows put rows j and j + 2 on the same banks); otherwise the contiguous quarter qk Q4
+// (n = 256: LDS rows 272 bytes apart, so that 4 consecutive rows start on 4 different 16-byte bank groups).
+template <int N> constexpr int kLdsRow = N == 128 ? 192 : (N == 256 ? 272 : N);
 
 template <int N>
 __device__ __forceinline__ void quad_share(uint32_t (&w)[Fast<N>::QW], const int8_t *row, int qk) {
@@ -72,25 +83,31 @@ __device__ __forceinline__ void quad_share(uint32_t (&w)[Fast<N>::QW], const int
     }
 }
 
-// the workgroup's LDS copies of Q (all layers), V' and the first-round router rows (routed layers). Q is held in two
-// planes of 1 KiB: lane l's classes 4l, 4l + 1 at 16 l in plane 0 and 4l + 2, 4l + 3 at 16 l in plane 1.
-template <int N, int L> struct SharedTables {
+// the workgroup's LDS copies of Q (all layers), V' and the first-round router rows (routed layers). Q is held in
+// R / 4 planes of 1 KiB: the 4 R bytes of lane l's classes 4l .. 4l + 3 (class-major) as 16-byte chunks, chunk p at
+// 16 l in plane p (R = 8: classes 4l, 4l + 1 in plane 0, 4l + 2, 4l + 3 in plane 1).
+template <class SH, int L> struct SharedTables {
     static constexpr int LR = L > 1 ? L - 1 : 1;
-    int8_t Q[L][256 * 8];
-    int8_t W[LR][15 * kLdsRow<N>];
-    int8_t V[LR][16 * kLdsRow<N>];
-    float mv[LR][16];
+    int8_t Q[L][256 * SH::R];
+    int8_t W[LR][15 * kLdsRow<SH::N>];
+    int8_t V[LR][SH::R2 * kLdsRow<SH::N>];
+    float mv[LR][SH::R2];
 };
+
+template <class SH, int L> constexpr int kTablesBytes = (int)sizeof(SharedTables<SH, L>);
 
 // Stage the tables with NT threads: every load is issued before the first LDS store, so a launch waits for them
 // once (a load-store loop would wait for each in turn).
-template <int N, int L, int NT>
-__device__ __forceinline__ void load_tables(SharedTables<N, L> &S, const YggDevModel &m, int tid) {
+template <class SH, int L, int NT>
+__device__ __forceinline__ void load_tables(SharedTables<SH, L> &S, const YggDevModel &m, int tid) {
     // 16-byte chunks: RC per row in memory, SC per row in LDS
+    constexpr int N = SH::N, R2 = SH::R2, QC = SH::QC;
     constexpr int RC = N / 16, SC = kLdsRow<N> / 16, LR = L > 1 ? L - 1 : 1;
-    constexpr int QK = (128 + NT - 1) / NT;            // Q chunks (at most 128: VP <= 256) per thread and layer
-    constexpr int RK = (31 * RC + NT - 1) / NT;        // first-round rows and V' rows, per thread and routed layer
-    const int qch = m.VP / 2, rows = (1 << m.round_h[0]) - 1;
+    constexpr int QK = (16 * SH::R + NT - 1) / NT;     // Q chunks (at most 16 R: VP <= 256) per thread and layer
+    constexpr int VR = 15 + R2;                        // first-round rows and V' rows of a routed layer
+    constexpr int RK = (VR * RC + NT - 1) / NT;        // their chunks per thread
+    static_assert(L == 1 || NT >= R2 * (L - 1), "one thread per m_v entry");
+    const int qch = m.VP * SH::R / 16, rows = (1 << m.round_h[0]) - 1;
     uint4 qv[L][QK], rv[LR][RK];
     float mvv = 0.0f;
 #pragma unroll
@@ -110,19 +127,19 @@ __device__ __forceinline__ void load_tables(SharedTables<N, L> &S, const YggDevM
             rv[l - 1][k] = make_uint4(0u, 0u, 0u, 0u);
             if (c < rows * RC)
                 rv[l - 1][k] = ((const uint4 *)y.w)[c];
-            else if (c >= 15 * RC && c < 31 * RC)
+            else if (c >= 15 * RC && c < VR * RC)
                 rv[l - 1][k] = ((const uint4 *)y.vl)[c - 15 * RC];
         }
     }
 #pragma unroll
     for (int l = 1; l < L; l++)
-        if (tid / 16 == l - 1) mvv = m.layers[l].mv[tid % 16];
+        if (tid / R2 == l - 1) mvv = m.layers[l].mv[tid % R2];
 #pragma unroll
     for (int l = 0; l < L; l++)
 #pragma unroll
         for (int k = 0; k < QK; k++) {
             const int c = tid + k * NT;
-            if (c < qch) ((uint4 *)S.Q[l])[(c & 1) * 64 + (c >> 1)] = qv[l][k];
+            if (c < qch) ((uint4 *)S.Q[l])[(c % QC) * 64 + c / QC] = qv[l][k];
         }
 #pragma unroll
     for (int l = 1; l < L; l++)
@@ -131,10 +148,10 @@ __device__ __forceinline__ void load_tables(SharedTables<N, L> &S, const YggDevM
             const int c = tid + k * NT;
             if (c < 15 * RC)
                 ((uint4 *)S.W[l - 1])[(c / RC) * SC + c % RC] = rv[l - 1][k];
-            else if (c < 31 * RC)
+            else if (c < VR * RC)
                 ((uint4 *)S.V[l - 1])[((c - 15 * RC) / RC) * SC + (c - 15 * RC) % RC] = rv[l - 1][k];
         }
-    if (L > 1 && tid < 16 * (L - 1)) S.mv[tid / 16][tid % 16] = mvv;
+    if (L > 1 && tid < R2 * (L - 1)) S.mv[tid / R2][tid % R2] = mvv;
 }
 
 // Touch every 64-byte line of the kernel argument (the model description, read by scalar loads) at entry: the
@@ -383,9 +400,9 @@ __device__ __forceinline__ int descend_deep(const YggDevModel &m, const YggDevLa
 }
 
 // the expert's whole gather record and table row, in one burst
-template <int N>
-__device__ __forceinline__ void gather(Gather<N> &G, const YggDevLayer &y, int r, int x, bool routed, int lane) {
-    using F = Fast<N>;
+template <class SH>
+__device__ __forceinline__ void gather(Gather<SH> &G, const YggDevLayer &y, int r, int x, bool routed, int lane) {
+    using F = SH;
     // a layer's records and tables lie within 4 GiB (checked at load): 32-bit offsets
     const uint8_t *g = y.gath + (uint32_t)r * (uint32_t)y.gath_bytes;
     if (lane < F::NL) {
@@ -396,7 +413,7 @@ __device__ __forceinline__ void gather(Gather<N> &G, const YggDevLayer &y, int r
         }
         if (routed) {
 #pragma unroll
-            for (int k4 = 0; k4 < 4; k4++) {
+            for (int k4 = 0; k4 < F::K4; k4++) {
                 uint32_t tmp[F::C];
                 load_words<F::C, 4 * F::C>(tmp, g + y.off_U + ((k4 * F::NL + lane) * F::C) * 4);
 #pragma unroll
@@ -420,31 +437,37 @@ __device__ __forceinline__ void gather(Gather<N> &G, const YggDevLayer &y, int r
 
 // zl[k] = clamp(rint((f32(V'_k . q_below) m_v[k]) rho), +-127) into LDS (cpu/ygg.cpp:285-296); V0 and mv0 are the
 // layer's V' rows and m_v in LDS
-template <int N>
+template <class SH>
 __device__ __forceinline__ void layer_input(int8_t *zls, const int8_t *V0, const float *mv0,
-                                            const uint32_t (&qbw)[Fast<N>::QW], float rho, int lane) {
+                                            const uint32_t (&qbw)[Fast<SH::N>::QW], float rho, int lane) {
+    constexpr int N = SH::N;
     using F = Fast<N>;
     const int qk = lane & 3, qj = lane >> 2;
-    uint32_t vv[F::QW];
-    quad_share<N>(vv, V0 + qj * kLdsRow<N>, qk);
-    int a = 0;
+    // pass p: quad j takes row 16 p + j
 #pragma unroll
-    for (int i = 0; i < F::QW; i++) a = dot4(vv[i], qbw[i], a);
-    a = sum4(a);
-    if (qk == 0) {
-        float zf = (float)a * mv0[qj];
-        zf = zf * rho;
-        zls[qj] = (int8_t)clamp127(cvt_rne(zf));
+    for (int p = 0; p < SH::RG; p++) {
+        const int k = 16 * p + qj;
+        uint32_t vv[F::QW];
+        quad_share<N>(vv, V0 + k * kLdsRow<N>, qk);
+        int a = 0;
+#pragma unroll
+        for (int i = 0; i < F::QW; i++) a = dot4(vv[i], qbw[i], a);
+        a = sum4(a);
+        if (qk == 0) {
+            float zf = (float)a * mv0[k];
+            zf = zf * rho;
+            zls[k] = (int8_t)clamp127(cvt_rne(zf));
+        }
     }
 }
 
 // new state rows of this lane: sat8(((A16 q_old + 2^(s-1)) >> s) + T_r[x] + rint(f32(U'_r zl) m_ul))
 // (cpu/ygg.cpp:311-389); qold is the layer's state before the token (LDS). A row is stored as hi and lo signed bytes
 // with A16 = 256 hi + lo, so A16 q = 256 (hi q) + (lo q) exactly, two v_dot4 chains on the raw int8 state.
-template <int N>
-__device__ __forceinline__ void update(int (&qn)[Fast<N>::C], const Gather<N> &G, const int8_t *qold,
+template <class SH>
+__device__ __forceinline__ void update(int (&qn)[SH::C], const Gather<SH> &G, const int8_t *qold,
                                        const int8_t *zls, const YggDevLayer &y, bool routed, int shift, int lane) {
-    using F = Fast<N>;
+    using F = SH;
     constexpr int BLK = F::BLK, C = F::C, RW = BLK / 4;     // dwords of one row's hi (and of its lo) bytes
     const int blk0 = (C * lane / BLK) * BLK;
     uint32_t qv[RW];
@@ -465,7 +488,7 @@ __device__ __forceinline__ void update(int (&qn)[Fast<N>::C], const Gather<N> &G
 #pragma unroll
         for (int c = 0; c < C; c++) d[c] = 0;
 #pragma unroll
-        for (int k4 = 0; k4 < 4; k4++) {
+        for (int k4 = 0; k4 < F::K4; k4++) {
             const uint32_t zw = ((const uint32_t *)zls)[k4];
 #pragma unroll
             for (int c = 0; c < C; c++) d[c] = dot4(G.uw[k4][c], zw, d[c]);
@@ -479,10 +502,10 @@ __device__ __forceinline__ void update(int (&qn)[Fast<N>::C], const Gather<N> &G
 
 // zq[j] = clamp(rint(f32(P_r q) m_z), +-127) into LDS (cpu/ygg.cpp:395-420); pw the lane's P granules, qnew the new
 // state (LDS)
-template <int N>
-__device__ __forceinline__ void readout(int8_t *zqs, const uint32_t (&pw)[Fast<N>::SPW], const int8_t *qnew,
+template <class SH>
+__device__ __forceinline__ void readout(int8_t *zqs, const uint32_t (&pw)[SH::SPW], const int8_t *qnew,
                                         float readout_scale, int lane) {
-    using F = Fast<N>;
+    using F = SH;
     const int rj = lane / F::RL, rk = lane % F::RL;
     uint32_t qv[F::SPW];
     load_words<F::SPW, F::SPA>(qv, qnew + rk * F::SP);
@@ -493,23 +516,26 @@ __device__ __forceinline__ void readout(int8_t *zqs, const uint32_t (&pw)[Fast<N
     if (rk == 0) zqs[rj] = (int8_t)clamp127(cvt_rne((float)z * readout_scale));
 }
 
-// f32(Q zq) s_q for the 4 classes of this lane (cpu/ygg.cpp:421-434)
+// f32(Q zq) s_q for the 4 classes of this lane (cpu/ygg.cpp:421-434); Qs the layer's Q planes
+template <int R>
 __device__ __forceinline__ void unembed_terms(float (&term)[4], const int8_t *zqs, const int8_t *Qs, float scale,
                                               int lane) {
-    uint32_t zw[2];
-    load_words<2, 16>(zw, zqs);
-    uint32_t qq[8], q0[4], q1[4];
-    load_words<4, 16>(q0, Qs + 16 * lane);             // classes 4 lane, 4 lane + 1
-    load_words<4, 16>(q1, Qs + 1024 + 16 * lane);      // classes 4 lane + 2, 4 lane + 3
+    constexpr int QC = R / 4, RW = R / 4;              // 16-byte chunks per lane, dwords per class
+    uint32_t zw[RW];
+    load_words<RW, 16>(zw, zqs);
+    uint32_t qq[4 * QC];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        qq[i] = q0[i];
-        qq[4 + i] = q1[i];
+    for (int p = 0; p < QC; p++) {
+        uint32_t q[4];
+        load_words<4, 16>(q, Qs + 1024 * p + 16 * lane);
+#pragma unroll
+        for (int i = 0; i < 4; i++) qq[4 * p + i] = q[i];
     }
 #pragma unroll
     for (int u = 0; u < 4; u++) {
-        int d = dot4(qq[2 * u], zw[0], 0);
-        d = dot4(qq[2 * u + 1], zw[1], d);
+        int d = 0;
+#pragma unroll
+        for (int i = 0; i < RW; i++) d = dot4(qq[u * RW + i], zw[i], d);
         term[u] = (float)d * scale;
     }
 }
@@ -544,7 +570,7 @@ __device__ __forceinline__ void store_logits(float *o, const float (&lg)[4], int
 // stream per workgroup with the deep descent (generation for few streams), else 4 streams per workgroup with
 // descend. CAP (not DEEP): at most 128 VGPRs, 4 wavefronts per SIMD (the most streams resident, some registers
 // spilled), else up to 256 (no spills; for calls whose streams all fit at the lower occupancy).
-template <int N, int L, bool GEN, bool DEEP, bool CAP>
+template <int N, int R, int R2, int L, bool GEN, bool DEEP, bool CAP>
 __global__ __launch_bounds__(64 * kFastWaves)
 __attribute__((amdgpu_waves_per_eu(DEEP ? 1 : (CAP ? 4 : 2))))
 void fast_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B, int T, int8_t *__restrict__ state,
@@ -555,13 +581,14 @@ void fast_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
     unsigned long long *__restrict__ digest = io.digest;
     const int32_t *__restrict__ targets = io.targets;
     double *__restrict__ nll = io.nll;
-    using F = Fast<N>;
+    using SH = Shape<N, R, R2>;
+    using F = SH;
     constexpr int W = DEEP ? 1 : kFastWaves, LR = L > 1 ? L - 1 : 1;
-    __shared__ __attribute__((aligned(16))) SharedTables<N, L> S;
+    __shared__ __attribute__((aligned(16))) SharedTables<SH, L> S;
     __shared__ __attribute__((aligned(16))) int8_t W1s[DEEP ? LR : 1][DEEP ? kR2Slots<N> * N : 16];
     __shared__ __attribute__((aligned(16))) int8_t qsw[W][L * N];
-    __shared__ __attribute__((aligned(16))) int8_t zlw[W][16];
-    __shared__ __attribute__((aligned(16))) int8_t zqw[W][16];
+    __shared__ __attribute__((aligned(16))) int8_t zlw[W][SH::ZL];
+    __shared__ __attribute__((aligned(16))) int8_t zqw[W][SH::ZQ];
 
     // the wavefront index, stream, tokens and leaves are uniform over a wavefront: kept in scalar registers. With one
     // stream per workgroup (DEEP) all 4 wavefronts stage the LDS tables and wavefronts 1-3 then leave.
@@ -579,7 +606,7 @@ void fast_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
     int sb[SB];
 #pragma unroll
     for (int k = 0; k < SB; k++) sb[k] = (live && lane + 64 * k < L * N) ? st[lane + 64 * k] : 0;
-    load_tables<N, L, 64 * kFastWaves>(S, m, tid);
+    load_tables<SH, L, 64 * kFastWaves>(S, m, tid);
     if constexpr (DEEP) load_round2<N, L, 64 * kFastWaves>(W1s, m, tid);
     __syncthreads();
     if (!live) return;
@@ -596,7 +623,7 @@ void fast_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
 #pragma unroll
     for (int k = 0; k < SB; k++)
         if (lane + 64 * k < L * N) qs[lane + 64 * k] = (int8_t)sb[k];
-    if (lane < 16) zls[lane] = 0;
+    if (lane < SH::ZL) zls[lane] = 0;
     wave_sync();
     unsigned long long dg = digest ? digest[s] : 0ull;
     double nacc = 0.0;
@@ -636,11 +663,11 @@ void fast_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
         auto flush = [&]() {
             if (pl >= 0) {
                 const YggDevLayer &yp = m.layers[pl];
-                readout<N>(zqs, ppw, qs + pl * N, yp.readout_scale, lane);
+                readout<SH>(zqs, ppw, qs + pl * N, yp.readout_scale, lane);
                 wave_sync();
                 if (4 * lane < VP) {
                     float term[4];
-                    unembed_terms(term, zqs, S.Q[pl], yp.unembed_scale, lane);
+                    unembed_terms<R>(term, zqs, S.Q[pl], yp.unembed_scale, lane);
 #pragma unroll
                     for (int u = 0; u < 4; u++) lg[u] = lg[u] + term[u];
                 }
@@ -677,12 +704,12 @@ void fast_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
                                         rho, x, lane, tl, flush);
                 }
             }
-            Gather<N> G;
-            gather<N>(G, y, r, x, l > 0, lane);
-            if (l > 0) layer_input<N>(zls, S.V[l - 1], S.mv[l - 1], qbw, rho, lane);
+            Gather<SH> G;
+            gather<SH>(G, y, r, x, l > 0, lane);
+            if (l > 0) layer_input<SH>(zls, S.V[l - 1], S.mv[l - 1], qbw, rho, lane);
             wave_sync();
             int qn[F::C];
-            if (lane < F::NL) update<N>(qn, G, qs + l * N, zls, y, l > 0, m.shift, lane);
+            if (lane < F::NL) update<SH>(qn, G, qs + l * N, zls, y, l > 0, m.shift, lane);
             wave_sync();
             if (lane < F::NL) {
 #pragma unroll
@@ -722,7 +749,7 @@ void fast_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
 
 // CAP: at most 128 VGPRs (4 wavefronts per SIMD: more streams resident, some registers spilled), else as many as
 // the kernel needs (no spills: faster for few streams)
-template <int N, int L, bool CAP>
+template <int N, int R, int R2, int L, bool CAP>
 __global__ __launch_bounds__(64 * L) __attribute__((amdgpu_waves_per_eu(CAP ? 4 : 1)))
 void pipe_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B, int T, int8_t *__restrict__ state,
                  const YggIO io) {
@@ -733,24 +760,25 @@ void pipe_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
     unsigned long long *__restrict__ digest = io.digest;
     const int32_t *__restrict__ targets = io.targets;
     double *__restrict__ nll = io.nll;
-    using F = Fast<N>;
-    __shared__ __attribute__((aligned(16))) SharedTables<N, L> S;
+    using SH = Shape<N, R, R2>;
+    using F = SH;
+    __shared__ __attribute__((aligned(16))) SharedTables<SH, L> S;
     __shared__ __attribute__((aligned(16))) int8_t qbuf[L][2][N];            // layer l after token t: [l][t & 1]
     __shared__ __attribute__((aligned(16))) float lgs[L][256];               // logits of token t: row t % L
     __shared__ __attribute__((aligned(16))) unsigned long long dterm[L][L];  // digest terms of token t: row t % L
-    __shared__ __attribute__((aligned(16))) int8_t zlw[L][16];
-    __shared__ __attribute__((aligned(16))) int8_t zqw[L][16];
+    __shared__ __attribute__((aligned(16))) int8_t zlw[L][SH::ZL];
+    __shared__ __attribute__((aligned(16))) int8_t zqw[L][SH::ZQ];
     __shared__ int stop_t;                                                   // first token out of range
 
     // the wavefront's layer and the tokens are uniform over a wavefront: kept in scalar registers
     const int tid = threadIdx.x, l = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int s = blockIdx.x;
     const int V = m.V, VP = m.VP;
-    load_tables<N, L, 64 * L>(S, m, tid);
+    load_tables<SH, L, 64 * L>(S, m, tid);
     const YggDevLayer &y = m.layers[l];
     int8_t *st = state + ((size_t)s * L + l) * N;
     for (int i = lane; i < N; i += 64) qbuf[l][1][i] = st[i];     // the state before token 0
-    if (lane < 16) zlw[l][lane] = 0;
+    if (lane < SH::ZL) zlw[l][lane] = 0;
     if (tid == 0) stop_t = T;
     __syncthreads();
 
@@ -759,14 +787,16 @@ void pipe_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
     const int nn1 = (1 << m.round_h[0]) - 1;
     unsigned long long dg = (digest && l == L - 1) ? digest[s] : 0ull;
     double nacc = 0.0;
-    // loaded a tick ahead: the first-round thresholds (routed layers) or the gather record (token layer)
+    // loaded a tick ahead: the first-round thresholds (routed layers) or the gather record (token layer; not for the
+    // largest shape, whose two records in flight would spill: the token layer's chain is the shortest anyway)
+    constexpr bool kAhead = N * R2 < 256 * 64;
     float th0 = 0.0f;
-    Gather<N> G0;
+    Gather<SH> G0;
     if (T > 0) {
         const int x0 = __builtin_amdgcn_readfirstlane(tok[0]);
         if (x0 >= 0 && x0 < V) {
             if (l > 0 && qj < nn1) th0 = y.thr[(size_t)x0 * y.thr_stride + qj];
-            if (l == 0) gather<N>(G0, y, x0, x0, false, lane);
+            if (kAhead && l == 0) gather<SH>(G0, y, x0, x0, false, lane);
         }
     }
 
@@ -783,36 +813,38 @@ void pipe_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
                 int r = x;
                 float rho = 0.0f;
                 uint32_t qbw[F::QW];
-                Gather<N> G;
+                Gather<SH> G;
                 if (l > 0) {
                     rho = below_and_rho<N>(qbw, qbuf[l - 1][t & 1], y.rms_eps, lane);
                     r = descend<N>(m, y, S.W[l - 1], th0, qbw, rho, x, lane);
-                    gather<N>(G, y, r, x, true, lane);
-                    layer_input<N>(zlw[l], S.V[l - 1], S.mv[l - 1], qbw, rho, lane);
-                } else {
+                    gather<SH>(G, y, r, x, true, lane);
+                    layer_input<SH>(zlw[l], S.V[l - 1], S.mv[l - 1], qbw, rho, lane);
+                } else if constexpr (kAhead) {
                     G = G0;
+                } else {
+                    gather<SH>(G, y, x, x, false, lane);
                 }
                 if (t + 1 < T) {
                     const int xn = __builtin_amdgcn_readfirstlane(tok[t + 1]);
                     if (xn >= 0 && xn < V) {
                         if (l > 0 && qj < nn1) th0 = y.thr[(size_t)xn * y.thr_stride + qj];
-                        if (l == 0) gather<N>(G0, y, xn, xn, false, lane);
+                        if (kAhead && l == 0) gather<SH>(G0, y, xn, xn, false, lane);
                     }
                 }
                 wave_sync();
                 int qn[F::C];
                 if (lane < F::NL) {
-                    update<N>(qn, G, qbuf[l][(t + 1) & 1], zlw[l], y, l > 0, m.shift, lane);
+                    update<SH>(qn, G, qbuf[l][(t + 1) & 1], zlw[l], y, l > 0, m.shift, lane);
 #pragma unroll
                     for (int c = 0; c < F::C; c++) qbuf[l][t & 1][F::C * lane + c] = (int8_t)qn[c];
                 }
                 wave_sync();
-                readout<N>(zqw[l], G.pw, qbuf[l][t & 1], y.readout_scale, lane);
+                readout<SH>(zqw[l], G.pw, qbuf[l][t & 1], y.readout_scale, lane);
                 wave_sync();
                 float *lr = lgs[t % L];
                 if (4 * lane < VP) {
                     float term[4];
-                    unembed_terms(term, zqw[l], S.Q[l], y.unembed_scale, lane);
+                    unembed_terms<R>(term, zqw[l], S.Q[l], y.unembed_scale, lane);
 #pragma unroll
                     for (int u = 0; u < 4; u++) {
                         const float base = l == 0 ? m.output_bias[4 * lane + u] : lr[4 * lane + u];

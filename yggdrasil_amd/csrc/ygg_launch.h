@@ -14,7 +14,7 @@ typedef hipError_t (*Launcher)(const YggDevModel &, const int32_t *, int, int, i
 
 struct Kernel {
     Launcher fn = nullptr;
-    char name[64] = {0};
+    char name[80] = {0};
     explicit operator bool() const { return fn != nullptr; }
 };
 
@@ -29,11 +29,20 @@ inline Kernel make_kernel(Launcher fn, const char *fmt, ...) {
     return k;
 }
 
-Kernel find_launcher(int n, int blk, int R);                // run_kernel (ygg_kernels.hip)
-Kernel find_fast_launcher(int n, int L, bool cap);          // fast_kernel, 128-VGPR cap or none (ygg_kernels_fast.hip)
-int fast_blocks_per_cu(int n, int L, bool cap, bool gen);   // its resident workgroups (4 streams each) per CU
-Kernel find_deep_launcher(int n, int L);                    // fast_kernel, deep descent (ygg_kernels_deep.hip)
-Kernel find_pipe_launcher(int n, int L, bool cap);          // pipe_kernel, 128-VGPR cap or none (ygg_kernels_deep.hip)
-int pipe_blocks_per_cu(int n, int L, bool cap);             // its resident workgroups per CU
+// The shapes of the specialised kernels (block 16, table storage, tensor scales): state width, readout rank,
+// layer-input rank, and the most layers. The first three are the benchmark configurations' (and the reference's
+// small models), the last two its medium and large models (configs/{enwik8,hg38}/{medium,large}.yaml).
+#define YGG_SHAPES(X) X(64, 8, 16) X(96, 8, 16) X(128, 8, 16) X(128, 16, 32) X(256, 32, 64)
+constexpr int kMaxFastLayers = 5;
+
+Kernel find_launcher(int n, int blk, int R);                            // run_kernel (ygg_kernels.hip)
+// fast_kernel, 4 streams per workgroup, 128-VGPR cap or none (ygg_kernels_fast.hip); its resident workgroups per CU
+Kernel find_fast_launcher(int n, int R, int R2, int L, bool cap);
+int fast_blocks_per_cu(int n, int R, int R2, int L, bool cap, bool gen);
+// fast_kernel with the deep descent, one stream per workgroup; pipe_kernel, 128-VGPR cap or none
+// (ygg_kernels_deep.hip)
+Kernel find_deep_launcher(int n, int R, int R2, int L);
+Kernel find_pipe_launcher(int n, int R, int R2, int L, bool cap);
+int pipe_blocks_per_cu(int n, int R, int R2, int L, bool cap);
 
 }  // namespace ygg
