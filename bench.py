@@ -41,20 +41,31 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def workload(cfg: int, storage: str = "table"):
+# The reference's trained model shapes (configs/{enwik8,hg38}/{small,medium,large}.yaml: 5 layers, block 16, router
+# depth 10; state width, readout rank, layer-input rank), as synthetic byte models
+REFERENCE_SHAPES = {"small": (64, 8, 16), "medium": (128, 16, 32), "large": (256, 32, 64)}
+
+
+def workload(cfg: int, storage: str = "table", shape: str = ""):
     """The configuration's workload; storage "factored" stores its routed inputs factored at rank 64 (the format's
-    other storage, cpu/ygg.cpp:339-358: about 0.78 GB for configuration 4 instead of 3.63 GB)."""
+    other storage, cpu/ygg.cpp:339-358: about 0.78 GB for configuration 4 instead of 3.63 GB); shape (one of
+    REFERENCE_SHAPES) replaces the configuration's model by a random one of that trained shape (V = 256, Gaussian
+    router, seed 5) and keeps its tokens and stream count."""
     import dataclasses
     from yggdrasil_amd import synth
     w = synth.CONFIGS[cfg]
+    if shape:
+        n, R, R2 = REFERENCE_SHAPES[shape]
+        w = dataclasses.replace(w, name=f"ref_{shape}_d{n}_L5_D10", model_seed=5,
+                                spec=synth.ModelSpec(n, 16, 10, 256, 5, R, R2, router="gauss"))
     if storage == "factored":
         w = dataclasses.replace(w, name=w.name + "_factored", spec=dataclasses.replace(w.spec, input_rank=64))
     return w
 
 
-def model_path(cfg: int, cache: Path, storage: str = "table") -> Path:
+def model_path(cfg: int, cache: Path, storage: str = "table", shape: str = "") -> Path:
     from yggdrasil_amd import synth
-    w = workload(cfg, storage)
+    w = workload(cfg, storage, shape)
     cache.mkdir(parents=True, exist_ok=True)
     p = cache / f"{w.name}_seed{w.model_seed}.bin"
     if not p.exists():
@@ -189,6 +200,8 @@ def main():
     ap.add_argument("--config", type=int, default=4, choices=[1, 2, 3, 4, 5])
     ap.add_argument("--storage", default="table", choices=["table", "factored"],
                     help="routed-layer input storage of the synthetic model (factored: rank 64)")
+    ap.add_argument("--shape", default="", choices=["", *REFERENCE_SHAPES],
+                    help="a model of one of the reference's trained shapes instead of the configuration's")
     ap.add_argument("--streams", type=int, default=0, help="override the configuration's stream count")
     ap.add_argument("--tokens", type=int, default=0, help="override the configuration's tokens per stream")
     ap.add_argument("--cache", default=os.environ.get("YGG_BENCH_DIR", os.path.join(tempfile.gettempdir(),
@@ -208,9 +221,9 @@ def main():
     from yggdrasil_amd.inference import Yggdrasil
     from yggdrasil_amd.roofline import step_bytes
 
-    w = workload(a.config, a.storage)
+    w = workload(a.config, a.storage, a.shape)
     B, T = a.streams or w.streams, a.tokens or w.steps
-    path = model_path(a.config, Path(a.cache), a.storage)
+    path = model_path(a.config, Path(a.cache), a.storage, a.shape)
     t0 = time.time()
     model = Yggdrasil.load(path, device="cuda:0")
     info = model.info

@@ -139,3 +139,27 @@ def test_few_streams_full_model(cfg, monkeypatch):
                 assert np.array_equal(st.cpu().numpy(), ref["states"][:, t]), (cfg, t)
         model.close()
         torch.cuda.empty_cache()
+
+
+@pytest.mark.timeout(600)
+def test_reference_large_shape_full_model():
+    """The reference's largest trained shape (configs/enwik8/large.yaml: 5 layers, d = 256, D = 10, R = 32, R2 = 64;
+    a random 0.68 GB model of the 681 MB published file's size) over 512 streams x 256 Zipf tokens in one launch, on
+    the kernel the library picks, against the C oracle's per-stream digest and logit sums."""
+    from yggdrasil_amd.inference import Yggdrasil
+    cache = Path(os.environ.get("YGG_BENCH_DIR", "/tmp/ygg_bench"))
+    cache.mkdir(parents=True, exist_ok=True)
+    path = cache / "ref_large_d256_L5_D10_seed5.bin"
+    if not path.exists():
+        tmp = path.with_suffix(".tmp")
+        synth.write_model(synth.ModelSpec(256, 16, 10, 256, 5, 32, 64, router="gauss"), 5, tmp)
+        os.replace(tmp, path)
+    x = synth.zipf_bytes(512, 256, 7)
+    model = Yggdrasil.load(path)
+    assert model.info.kernel == 1
+    _say(f"large shape: 512 x 256, kernel {model.kernel_name(512, 256)}")
+    dg, ls, st = _gpu_sums(model, x)
+    model.close()
+    rdg, rls, rst = O.Oracle(path).run_sums(x)
+    np.testing.assert_array_equal(st, rst)
+    assert (dg == rdg).all() and (ls == rls).all()
