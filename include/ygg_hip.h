@@ -46,9 +46,10 @@ typedef struct {
     int32_t factored;          /* routed layers use factored input storage */
     int32_t group;             /* group scales present */
     int32_t device;            /* HIP device holding the weights */
-    int32_t kernel;            /* step kernel in use: 0 general, 1 specialised (readout rank 8, block 16, layer-input
-                                  rank 16, table storage, tensor scales, <= 4 layers, A16 entries <= 32639, each
-                                  layer's tables under 4 GiB); YGG_KERNEL=generic at load time forces 0 */
+    int32_t kernel;            /* step kernel in use: 0 general, 1 specialised (d_state, readout rank, layer-input
+                                  rank one of (64, 8, 16), (96, 8, 16), (128, 8, 16), (128, 16, 32), (256, 32, 64),
+                                  block 16, table storage, tensor scales, <= 5 layers, A16 entries <= 32639, each
+                                  layer's tables and records under 4 GiB); YGG_KERNEL=generic at load time forces 0 */
     int32_t pipe_max_streams;  /* ygg_run/ygg_score calls with B at most this and T > 1 use the layer-pipelined kernel
                                   (one wavefront per layer, for latency): its resident workgroups (one per stream)
                                   per CU times the CUs; 0: never. YGG_KERNEL=fast or =deep at load time disables
