@@ -439,6 +439,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void ru
             // layer input zl from V' (cpu/ygg.cpp:285-296)
             if (l > 0 && R2 > 0) {
                 const int RG = (R2 + 15) >> 4;
+                // (unrolled: the row loads of several passes are in flight together)
+#pragma unroll 4
                 for (int gg = 0; gg < RG; gg++) {
                     const int k = gg * 16 + qj;
                     uint32_t vv[QW];
@@ -483,6 +485,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void ru
                     int d[C];
 #pragma unroll
                     for (int c = 0; c < C; c++) d[c] = 0;
+#pragma unroll 8
                     for (int k4 = 0; k4 < K / 4; k4++) {
                         const uint32_t vw = vx[k4];
                         const uint32_t *up = (const uint32_t *)(fp + ((size_t)(k4 * NL + lane) * C) * 4);
@@ -503,6 +506,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void ru
                     int d[C];
 #pragma unroll
                     for (int c = 0; c < C; c++) d[c] = 0;
+#pragma unroll 8
                     for (int k4 = 0; k4 < R2 / 4; k4++) {
                         const uint32_t zw = ((const uint32_t *)zls)[k4];
                         const uint32_t *up = (const uint32_t *)(up0 + ((size_t)(k4 * NL + lane) * C) * 4);
