@@ -46,11 +46,13 @@ def log(msg):
 REFERENCE_SHAPES = {"small": (64, 8, 16), "medium": (128, 16, 32), "large": (256, 32, 64)}
 
 
-def workload(cfg: int, storage: str = "table", shape: str = ""):
+def workload(cfg: int, storage: str = "table", shape: str = "", scales: str = "tensor"):
     """The configuration's workload; storage "factored" stores its routed inputs factored at rank 64 (the format's
     other storage, cpu/ygg.cpp:339-358: about 0.78 GB for configuration 4 instead of 3.63 GB); shape (one of
     REFERENCE_SHAPES) replaces the configuration's model by a random one of that trained shape (V = 256, Gaussian
-    router, seed 5) and keeps its tokens and stream count."""
+    router, seed 5) and keeps its tokens and stream count; scales "group" gives the model group scales (per-group
+    state scales, per-row readout scales, per-class unembedding scales: the export's other scale mode,
+    cpu/export.py:216-262)."""
     import dataclasses
     from yggdrasil_amd import synth
     w = synth.CONFIGS[cfg]
@@ -60,12 +62,14 @@ def workload(cfg: int, storage: str = "table", shape: str = ""):
                                 spec=synth.ModelSpec(n, 16, 10, 256, 5, R, R2, router="gauss"))
     if storage == "factored":
         w = dataclasses.replace(w, name=w.name + "_factored", spec=dataclasses.replace(w.spec, input_rank=64))
+    if scales == "group":
+        w = dataclasses.replace(w, name=w.name + "_group", spec=dataclasses.replace(w.spec, group=True))
     return w
 
 
-def model_path(cfg: int, cache: Path, storage: str = "table", shape: str = "") -> Path:
+def model_path(cfg: int, cache: Path, storage: str = "table", shape: str = "", scales: str = "tensor") -> Path:
     from yggdrasil_amd import synth
-    w = workload(cfg, storage, shape)
+    w = workload(cfg, storage, shape, scales)
     cache.mkdir(parents=True, exist_ok=True)
     p = cache / f"{w.name}_seed{w.model_seed}.bin"
     if not p.exists():
@@ -202,6 +206,8 @@ def main():
                     help="routed-layer input storage of the synthetic model (factored: rank 64)")
     ap.add_argument("--shape", default="", choices=["", *REFERENCE_SHAPES],
                     help="a model of one of the reference's trained shapes instead of the configuration's")
+    ap.add_argument("--scales", default="tensor", choices=["tensor", "group"],
+                    help="state/readout/unembedding scales of the synthetic model")
     ap.add_argument("--streams", type=int, default=0, help="override the configuration's stream count")
     ap.add_argument("--tokens", type=int, default=0, help="override the configuration's tokens per stream")
     ap.add_argument("--cache", default=os.environ.get("YGG_BENCH_DIR", os.path.join(tempfile.gettempdir(),
@@ -221,9 +227,9 @@ def main():
     from yggdrasil_amd.inference import Yggdrasil
     from yggdrasil_amd.roofline import step_bytes
 
-    w = workload(a.config, a.storage, a.shape)
+    w = workload(a.config, a.storage, a.shape, a.scales)
     B, T = a.streams or w.streams, a.tokens or w.steps
-    path = model_path(a.config, Path(a.cache), a.storage, a.shape)
+    path = model_path(a.config, Path(a.cache), a.storage, a.shape, a.scales)
     t0 = time.time()
     model = Yggdrasil.load(path, device="cuda:0")
     info = model.info
@@ -253,7 +259,7 @@ def main():
     lv = leaves.cpu().numpy()
     del leaves
     alg = step_bytes(lv, x_np, info.d_state, info.block_size, info.readout_rank, info.layer_input_rank,
-                     info.vocab, info.router_depth, info.input_rank if info.factored else 0)
+                     info.vocab, info.router_depth, info.input_rank if info.factored else 0, group=bool(info.group))
     hist = np.bincount(lv[:, :, -1].reshape(-1), minlength=info.n_experts)
     log(f"leaves of the last layer: {np.count_nonzero(hist)} of {info.n_experts} used, max share "
         f"{hist.max() / hist.sum():.4f}; compulsory {alg['per_token_compulsory']:.0f} B/token, per-stream "

@@ -48,8 +48,9 @@ typedef struct {
     int32_t device;            /* HIP device holding the weights */
     int32_t kernel;            /* step kernel in use: 0 general, 1 specialised (d_state, readout rank, layer-input
                                   rank one of (64, 8, 16), (96, 8, 16), (128, 8, 16), (128, 16, 32), (256, 32, 64),
-                                  block 16, table storage, tensor scales, <= 5 layers, A16 entries <= 32639, each
-                                  layer's tables and records under 4 GiB); YGG_KERNEL=generic at load time forces 0 */
+                                  block 16, table storage, tensor scales or group scales (group: d_state 64, 128
+                                  or 256), <= 5 layers, A16 entries <= 32639, each layer's tables and records under
+                                  4 GiB); YGG_KERNEL=generic at load time forces 0 */
     int32_t pipe_max_streams;  /* ygg_run/ygg_score calls with B at most this and T > 1 use the layer-pipelined kernel
                                   (one wavefront per layer, for latency): its resident workgroups (one per stream)
                                   per CU times the CUs; 0: never. YGG_KERNEL=fast or =deep at load time disables
@@ -164,10 +165,12 @@ void ygg_float_free(ygg_fmodel *m);
 /* Message of the last failed call on this thread ("" if none). */
 const char *ygg_last_error(void);
 
-/* The kernel a call would launch, by the name profilers show for it (e.g. "ygg::fast_kernel<128, 4, false, false>"):
-   generate = 0 for ygg_run/ygg_score/ygg_step (T = 1), 1 for ygg_generate (T = its n); written NUL-terminated into
-   name (len bytes). No counterpart in the reference (its one kernel is the CPU step); for profiles and tests. */
-int ygg_kernel_name(const ygg_model *m, int B, int T, int generate, char *name, size_t len);
+/* The kernel a call would launch, by the name profilers show for it (e.g.
+   "ygg::fast_kernel<128, 8, 16, 4, 0, false, true, false>"): mode = 0 for ygg_run without a digest and ygg_step
+   (T = 1), 1 for ygg_generate (T = its n), 2 for ygg_score and ygg_run with a digest (the specialised per-stream
+   kernel has a build per mode); written NUL-terminated into name (len bytes). No counterpart in the reference (its one
+   kernel is the CPU step); for profiles and tests. */
+int ygg_kernel_name(const ygg_model *m, int B, int T, int mode, char *name, size_t len);
 
 /* Library ABI version (bumped when a signature above changes). */
 int ygg_version(void);

@@ -98,8 +98,10 @@ def test_pack_proj_readout_unembed_index():
             assert v == (Q[c, j] if c < 27 else 0)
 
 
-def test_generation_is_deterministic_and_streaming_matches(tmp_path, monkeypatch):
-    spec = synth.ModelSpec(64, 16, 11, 27, 3, router="skew")   # 2048 experts: two chunks per routed layer
+@pytest.mark.parametrize("group", [False, True], ids=["tensor", "group"])
+def test_generation_is_deterministic_and_streaming_matches(tmp_path, monkeypatch, group):
+    # 2048 experts: two chunks per routed layer; group scales add the per-expert readout scale array
+    spec = synth.ModelSpec(64, 16, 11, 27, 3, router="skew", group=group)
     a, b = tmp_path / "a.bin", tmp_path / "b.bin"
     synth.write_model(spec, 5, a)
     # force the chunk-streamed path used for large models

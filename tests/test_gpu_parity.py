@@ -7,6 +7,7 @@ configurations at reduced stream counts, and edge cases (empty batch, zero token
 carried state, graph replay).
 """
 import ctypes
+import dataclasses
 import os
 
 import numpy as np
@@ -91,10 +92,11 @@ SHAPES = {(64, 8, 16), (96, 8, 16), (128, 8, 16), (128, 16, 32), (256, 32, 64)}
 
 def specialised(spec) -> bool:
     """Whether a model runs on the specialised kernels: a shape of SHAPES (a one-layer model at readout rank 8 with
-    any layer-input rank), block 16, table storage, tensor scales, at most 5 layers."""
+    any layer-input rank), block 16, table storage, tensor scales or group scales (state width 64, 128 or 256), at
+    most 5 layers."""
     r2 = 16 if spec.n_layers == 1 else spec.layer_input_rank
     return (spec.d_state, spec.readout_rank, r2) in SHAPES and spec.block_size == 16 and not spec.input_rank and \
-        not spec.group and spec.n_layers <= 5
+        (not spec.group or spec.d_state != 96) and spec.n_layers <= 5
 
 
 def default_plan(D: int) -> list:
@@ -129,8 +131,12 @@ def _expect_kernel(model, kernel_env):
     want = {"generic": "ygg::run_kernel<", "pipe": "ygg::pipe_kernel<",
             "fast": "ygg::fast_kernel<", "deep": "ygg::fast_kernel<"}[kernel_env]
     assert name.startswith(want), name
+    group = "true" if info.group else "false"
     if kernel_env in ("fast", "deep"):
-        assert name.endswith(", false, true, false>" if kernel_env == "deep" and deep else ", false, false, false>"), name
+        descent = "true" if kernel_env == "deep" and deep else "false"
+        assert name.endswith(f", 0, {descent}, false, {group}>"), name
+    if kernel_env == "pipe":
+        assert name.endswith(f", false, {group}>"), name
 
 
 def test_config1_full_stream(hip, c12, kernel_env):
@@ -392,27 +398,73 @@ def test_default_dispatch(hip, model_dir, monkeypatch):
         synth.write_model(synth.ModelSpec(128, 16, 10, 256, 4, router="gauss"), 11, path)
     model = hip.load(path)
     info = model.info
-    fast = "ygg::fast_kernel<128, 8, 16, 4, {}, false, {}>"
-    assert model.kernel_name(1, 64) == "ygg::pipe_kernel<128, 8, 16, 4, false>"
-    assert model.kernel_name(1, 1) == fast.format("false", "false")
-    assert model.kernel_name(info.pipe_max_streams + 1, 64) == fast.format("false", "false")
-    assert model.kernel_name(16384, 64) == fast.format("false", "true")
-    assert model.kernel_name(1, 100, generate=True) == "ygg::fast_kernel<128, 8, 16, 4, true, true, false>"
-    assert model.kernel_name(1, 4, generate=True) == fast.format("true", "false")
-    assert model.kernel_name(info.deep_max_streams + 1, 100, generate=True) == fast.format("true", "false")
-    assert model.kernel_name(16384, 100, generate=True) == fast.format("true", "true")
+    # mode 0: run, 1: generate, 2: score or a run with a digest
+    fast = "ygg::fast_kernel<128, 8, 16, 4, {}, false, {}, false>"
+    assert model.kernel_name(1, 64) == "ygg::pipe_kernel<128, 8, 16, 4, false, false>"
+    assert model.kernel_name(1, 64, score=True) == "ygg::pipe_kernel<128, 8, 16, 4, false, false>"
+    assert model.kernel_name(1, 1) == fast.format(0, "false")
+    assert model.kernel_name(1, 1, score=True) == fast.format(2, "false")
+    assert model.kernel_name(info.pipe_max_streams + 1, 64) == fast.format(0, "false")
+    assert model.kernel_name(16384, 64) == fast.format(0, "true")
+    assert model.kernel_name(16384, 64, score=True) == fast.format(2, "true")
+    assert model.kernel_name(1, 100, generate=True) == "ygg::fast_kernel<128, 8, 16, 4, 1, true, false, false>"
+    assert model.kernel_name(1, 4, generate=True) == fast.format(1, "false")
+    assert model.kernel_name(info.deep_max_streams + 1, 100, generate=True) == fast.format(1, "false")
+    assert model.kernel_name(16384, 100, generate=True) == fast.format(1, "true")
+    from yggdrasil_amd import _lib
+    assert _lib.lib().ygg_kernel_name(model._h, 1, 1, 3, ctypes.create_string_buffer(128), 128) == 5   # bad mode
     # the smallest batch that runs on the capped pipe build
     lo, hi = 1, info.pipe_max_streams
-    assert model.kernel_name(hi, 16) == "ygg::pipe_kernel<128, 8, 16, 4, true>"
+    assert model.kernel_name(hi, 16) == "ygg::pipe_kernel<128, 8, 16, 4, true, false>"
     while lo < hi:
         mid = (lo + hi) // 2
-        if model.kernel_name(mid, 16) == "ygg::pipe_kernel<128, 8, 16, 4, true>":
+        if model.kernel_name(mid, 16) == "ygg::pipe_kernel<128, 8, 16, 4, true, false>":
             hi = mid
         else:
             lo = mid + 1
-    assert lo > 1 and model.kernel_name(lo - 1, 16) == "ygg::pipe_kernel<128, 8, 16, 4, false>"
+    assert lo > 1 and model.kernel_name(lo - 1, 16) == "ygg::pipe_kernel<128, 8, 16, 4, false, false>"
     _say(f"capped pipe build from {lo} streams (pipe_max {info.pipe_max_streams})")
     x = synth.zipf_bytes(lo, 12, 9)
+    _compare(_gpu_run(model, x), Oracle(path).run(x, states=True))
+    model.close()
+
+
+def _smallest_batch(model, T, name, hi):
+    """The smallest stream count (<= hi, which runs on the kernel named) whose calls of T tokens run on it."""
+    lo = 1
+    assert model.kernel_name(hi, T) == name, model.kernel_name(hi, T)
+    while lo < hi:
+        mid = (lo + hi) // 2
+        if model.kernel_name(mid, T) == name:
+            hi = mid
+        else:
+            lo = mid + 1
+    return lo
+
+
+def test_group_scales_capped_builds(hip, model_dir, monkeypatch):
+    """A group-scale model on the capped builds, which only calls with more streams than the uncapped builds keep
+    resident reach: the per-stream kernel (4 tokens per stream) and the layer-pipelined kernel (12 tokens)."""
+    monkeypatch.delenv("YGG_KERNEL", raising=False)
+    monkeypatch.delenv("YGG_DEEP", raising=False)
+    path = model_dir / "c4small_group.bin"
+    if not path.exists():
+        synth.write_model(synth.ModelSpec(128, 16, 10, 256, 4, router="gauss", group=True), 11, path)
+    model = hip.load(path)
+    info = model.info
+    assert info.group
+    fast_capped = "ygg::fast_kernel<128, 8, 16, 4, 0, false, true, true>"
+    lo = _smallest_batch(model, 1, fast_capped, 16384)
+    assert lo > info.pipe_max_streams and model.kernel_name(lo, 4) == fast_capped
+    assert model.kernel_name(lo - 1, 1) == "ygg::fast_kernel<128, 8, 16, 4, 0, false, false, true>"
+    _say(f"capped per-stream group build from {lo} streams")
+    x = synth.zipf_bytes(lo, 4, 5)
+    _compare(_gpu_run(model, x), Oracle(path).run(x, states=True))
+    pipe_capped = "ygg::pipe_kernel<128, 8, 16, 4, true, true>"
+    lo = _smallest_batch(model, 12, pipe_capped, info.pipe_max_streams)
+    assert lo > 1 and model.kernel_name(lo - 1, 12) == "ygg::pipe_kernel<128, 8, 16, 4, false, true>"
+    _say(f"capped pipe group build from {lo} streams (pipe_max {info.pipe_max_streams})")
+    x = synth.zipf_bytes(lo, 12, 6)
     _compare(_gpu_run(model, x), Oracle(path).run(x, states=True))
     model.close()
 
@@ -423,13 +475,15 @@ REFERENCE_SHAPES = {"small": synth.ModelSpec(64, 16, 10, 27, 5, 8, 16), "medium"
                     "large": synth.ModelSpec(256, 16, 10, 27, 5, 32, 64)}
 
 
+@pytest.mark.parametrize("group", [False, True], ids=["tensor", "group"])
 @pytest.mark.parametrize("name", list(REFERENCE_SHAPES))
-def test_reference_model_shapes(hip, model_dir, kernel_env, name):
-    """The reference's trained model shapes on every kernel: leaves, states after every token and logits equal the
-    oracle's (12 streams x 40 tokens; one launch, and for the per-stream kernels a step loop over the first tokens)."""
+def test_reference_model_shapes(hip, model_dir, kernel_env, name, group):
+    """The reference's trained model shapes on every kernel, with tensor or group scales (the export's "auto" picks
+    either): leaves, states after every token and logits equal the oracle's (12 streams x 40 tokens; one launch, and
+    for the per-stream kernels a step loop over the first tokens)."""
     import torch
-    spec = REFERENCE_SHAPES[name]
-    path = model_dir / f"refshape_{name}.bin"
+    spec = dataclasses.replace(REFERENCE_SHAPES[name], group=group)
+    path = model_dir / f"refshape_{name}{'_group' if group else ''}.bin"
     if not path.exists():
         synth.write_model(spec, 13, path)
     x = synth.uniform_tokens(spec.vocab, 12, 40, 3)

@@ -1,5 +1,6 @@
 """The algorithmic (compulsory) byte count behind bench.py's roofline (yggdrasil_amd.roofline.step_bytes), against
-counts by hand: one stream, two streams sharing their leaf or on neighbouring leaves, and factored storage."""
+counts by hand: one stream, two streams sharing their leaf or on neighbouring leaves, factored storage and group
+scales."""
 import numpy as np
 
 from yggdrasil_amd.roofline import step_bytes
@@ -48,3 +49,11 @@ def test_factored_storage():
     want = 2 * (TOK + IO + D * 4 + STATE) + LEAF + fac + D * n + 2 * k
     assert t["compulsory"] == want
     assert t["per_stream"] == 2 * (TOK + IO + LEAF + fac + k + D * (n + 4) + STATE)
+
+
+def test_group_scales():
+    # the R readout row scales (f32) of every distinct expert: the routed leaf and each distinct token's expert
+    t = _bytes([7, 9], [5, 5], group=True)
+    base = _bytes([7, 9], [5, 5])
+    assert t["compulsory"] == base["compulsory"] + 4 * R * 3
+    assert t["per_stream"] == base["per_stream"] + 2 * 4 * R * 2

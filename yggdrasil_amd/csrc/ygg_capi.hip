@@ -352,8 +352,8 @@ struct ygg_model {
     void *arena = nullptr;
     size_t arena_bytes = 0;
     ygg::Kernel run;                  // per-stream: fast_kernel (4 streams per workgroup, capped) or run_kernel
-    ygg::Kernel run_few;              // fast_kernel without the VGPR cap: B <= run_few_max_streams[gen]
-    int run_few_max_streams[2] = {0, 0};
+    ygg::Kernel run_few;              // fast_kernel without the VGPR cap: B <= run_few_max_streams[mode]
+    int run_few_max_streams[3] = {0, 0, 0};
     ygg::Kernel pipe;                 // layer-pipelined, 128-VGPR cap: T > 1 and B <= pipe_max_streams
     ygg::Kernel pipe_few;             // the same without the cap: B <= pipe_few_max_streams
     int pipe_max_streams = 0, pipe_few_max_streams = 0;
@@ -392,8 +392,9 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     const char *kenv = getenv("YGG_KERNEL");
     const std::string kmode = kenv ? kenv : "";
     ygg::Kernel fast;
-    // (a shape of YGG_SHAPES, up to 5 layers; a one-layer model has no layer input and runs at any layer-input rank
-    // as 16; every routed layer's table and gather records addressable in 32 bits)
+    // (a shape of YGG_SHAPES, up to 5 layers, group scales at n of 64, 128 or 256; a one-layer model has no layer
+    // input and runs at any layer-input rank as 16; every routed layer's table and gather records addressable in 32
+    // bits)
     auto shape_ok = [](int nn, int rr, int r2) {
 #define YGG_S(N_, R_, R2_) \
     if (nn == N_ && rr == R_ && r2 == R2_) return true;
@@ -404,9 +405,9 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     const int R2f = L == 1 ? 16 : R2;
     const int64_t rec_bound = (int64_t)n * (2 * fa.blk + R2 + R) + 128;     // gather record bytes, at most
     const bool small_tables = (int64_t)E * V * n * 2 < ((int64_t)1 << 32) && (int64_t)E * rec_bound < ((int64_t)1 << 32);
-    if (kmode != "generic" && fa.blk == 16 && shape_ok(n, R, R2f) && !factored && !group &&
-        L <= ygg::kMaxFastLayers && VP <= 256 && small_tables && transitions_split(fa, fl))
-        fast = ygg::find_fast_launcher(n, R, R2f, L, true);
+    if (kmode != "generic" && fa.blk == 16 && shape_ok(n, R, R2f) && !factored && L <= ygg::kMaxFastLayers &&
+        VP <= 256 && small_tables && transitions_split(fa, fl))
+        fast = ygg::find_fast_launcher(n, R, R2f, L, true, group);
     if (fast) launch = fast;
 
     RoundPlan rplan = round_plan(L > 1 ? fa.D : 0);
@@ -434,11 +435,11 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
                       rplan.h[0] >= 2 && (rplan.n < 4 || rplan.h[2] + rplan.h[3] <= 6);
     ygg::Kernel pipe, pipe_few, deepk;
     if (fast && kmode != "fast" && kmode != "deep") {
-        pipe = ygg::find_pipe_launcher(n, R, R2f, L, true);
-        pipe_few = ygg::find_pipe_launcher(n, R, R2f, L, false);
+        pipe = ygg::find_pipe_launcher(n, R, R2f, L, true, group);
+        pipe_few = ygg::find_pipe_launcher(n, R, R2f, L, false, group);
     }
     // (the deep kernel exists where its LDS fits a workgroup)
-    const ygg::Kernel deep_avail = deep ? ygg::find_deep_launcher(n, R, R2f, L) : ygg::Kernel();
+    const ygg::Kernel deep_avail = deep ? ygg::find_deep_launcher(n, R, R2f, L, group) : ygg::Kernel();
     if (kmode != "fast" && kmode != "pipe") deepk = deep_avail;
     const int64_t slots = plan_slots(rplan);
     // device arena plan: every array 256-byte aligned
@@ -563,8 +564,9 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     m->pipe = pipe;
     m->pipe_few = pipe_few;
     m->pipe_all = pipe && kmode == "pipe";
-    m->pipe_max_streams = pipe ? (m->pipe_all ? INT32_MAX : ygg::pipe_blocks_per_cu(n, R, R2f, L, true) * cus) : 0;
-    m->pipe_few_max_streams = pipe_few ? ygg::pipe_blocks_per_cu(n, R, R2f, L, false) * cus : 0;
+    m->pipe_max_streams =
+        pipe ? (m->pipe_all ? INT32_MAX : ygg::pipe_blocks_per_cu(n, R, R2f, L, true, group) * cus) : 0;
+    m->pipe_few_max_streams = pipe_few ? ygg::pipe_blocks_per_cu(n, R, R2f, L, false, group) * cus : 0;
     // generation with one stream per workgroup while the streams do not outnumber the CUs (for more, the 4 streams
     // per workgroup of fast_kernel win); YGG_KERNEL=deep takes it for every call
     m->deep = deepk;
@@ -576,9 +578,9 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     m->run = launch;
     // the uncapped per-stream build while every stream of the call is resident with it
     if (fast) {
-        m->run_few = ygg::find_fast_launcher(n, R, R2f, L, false);
-        for (int g = 0; g < 2; g++)
-            m->run_few_max_streams[g] = ygg::fast_blocks_per_cu(n, R, R2f, L, false, g) * 4 * cus;
+        m->run_few = ygg::find_fast_launcher(n, R, R2f, L, false, group);
+        for (int md = 0; md < 3; md++)
+            m->run_few_max_streams[md] = ygg::fast_blocks_per_cu(n, R, R2f, L, false, group, md) * 4 * cus;
     }
     uint8_t *A = (uint8_t *)arena;
     auto at = [&](const Piece &p) -> void * { return p.bytes ? A + p.off : nullptr; };
@@ -634,17 +636,19 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     return YGG_OK;
 }
 
-// The kernel of a call of B streams and T tokens (gen: ygg_generate). Generation: the deep kernel for >= 8 tokens
+// The kernel of a call of B streams and T tokens in mode (kModeRun, kModeGenerate: ygg_generate, kModeScore: a
+// digest or NLL). Generation: the deep kernel for >= 8 tokens
 // and B <= deep_max_streams, else the per-stream kernel (every token needs all layers of the one before it, so never
 // the layer-pipelined one). Otherwise: the layer-pipelined kernel for T > 1 when its workgroups fit, else the
 // per-stream kernel. Of the two builds of a kernel, the uncapped one while all B streams are resident with it. A
 // kernel forced by YGG_KERNEL takes every call it can run.
-const ygg::Kernel &pick(const ygg_model *m, int B, int T, bool gen) {
+const ygg::Kernel &pick(const ygg_model *m, int B, int T, int mode) {
+    const bool gen = mode == kModeGenerate;
     if (m->deep_all) return m->deep;
     if (gen && m->deep && B <= m->deep_max_streams && T >= 8) return m->deep;
     if (!gen && m->pipe && (m->pipe_all || (T > 1 && B <= m->pipe_max_streams)))
         return (m->pipe_few && B <= m->pipe_few_max_streams) ? m->pipe_few : m->pipe;
-    return (m->run_few && B <= m->run_few_max_streams[gen]) ? m->run_few : m->run;
+    return (m->run_few && B <= m->run_few_max_streams[mode]) ? m->run_few : m->run;
 }
 
 struct DeviceGuard {
@@ -731,7 +735,7 @@ int ygg_run(const ygg_model *m, const int32_t *d_tokens, int B, int T, int8_t *d
     DeviceGuard g;
     HIP_TRY(g.set(m->device));
     // the pipelined kernel overlaps the layers of consecutive tokens, so it needs more than one token per launch
-    const ygg::Kernel &k = pick(m, B, T, false);
+    const ygg::Kernel &k = pick(m, B, T, d_digest ? kModeScore : kModeRun);
     YggIO io{};
     io.logits = d_logits;
     io.leaves = d_leaves;
@@ -749,7 +753,7 @@ int ygg_score(const ygg_model *m, const int32_t *d_tokens, const int32_t *d_targ
     if (!d_state || !d_nll || (T > 0 && (!d_tokens || !d_targets))) return fail(YGG_ERR_ARG, "NULL buffer");
     DeviceGuard g;
     HIP_TRY(g.set(m->device));
-    const ygg::Kernel &k = pick(m, B, T, false);
+    const ygg::Kernel &k = pick(m, B, T, kModeScore);
     YggIO io{};
     io.targets = d_targets;
     io.nll = d_nll;
@@ -768,7 +772,7 @@ int ygg_generate(const ygg_model *m, const int32_t *d_first, int B, int n, int8_
     if (!d_first || !d_state || !d_out) return fail(YGG_ERR_ARG, "NULL buffer");
     DeviceGuard g;
     HIP_TRY(g.set(m->device));
-    const ygg::Kernel &k = pick(m, B, n, true);
+    const ygg::Kernel &k = pick(m, B, n, kModeGenerate);
     YggIO io{};
     io.logits = d_logits;
     io.gen = d_out;
@@ -791,7 +795,7 @@ int ygg_step(const ygg_model *m, const int32_t *d_tokens, const int8_t *d_state_
         HIP_TRY(hipMemcpyAsync(d_state_out, d_state_in, (size_t)B * m->dev.L * m->dev.N, hipMemcpyDeviceToDevice,
                                (hipStream_t)stream));
     // one token: a per-stream kernel (a one-token launch cannot overlap layers), or a forced one
-    const ygg::Kernel &k = pick(m, B, 1, false);
+    const ygg::Kernel &k = pick(m, B, 1, kModeRun);
     YggIO io{};
     io.logits = d_logits;
     io.leaves = d_leaves;
@@ -799,11 +803,11 @@ int ygg_step(const ygg_model *m, const int32_t *d_tokens, const int8_t *d_state_
     return YGG_OK;
 }
 
-int ygg_kernel_name(const ygg_model *m, int B, int T, int generate, char *name, size_t len) {
+int ygg_kernel_name(const ygg_model *m, int B, int T, int mode, char *name, size_t len) {
     if (!m || !name || len == 0) return fail(YGG_ERR_ARG, "NULL argument");
     if (B < 0 || T < 0) return fail(YGG_ERR_ARG, "negative B (%d) or T (%d)", B, T);
-    const ygg::Kernel &k = pick(m, B, T, generate != 0);
-    snprintf(name, len, k.name, generate ? "true" : "false");
+    if (mode < 0 || mode > 2) return fail(YGG_ERR_ARG, "mode %d: 0 run, 1 generate, 2 score or digest", mode);
+    pick(m, B, T, mode).name_for(mode, name, len);
     return YGG_OK;
 }
 

@@ -20,6 +20,8 @@
 // token layer's gather record and the routed layers' first-round thresholds of the next token are loaded a tick
 // ahead.
 #pragma once
+#include <type_traits>
+
 #include "ygg_kernel.h"
 
 namespace ygg {
@@ -58,6 +60,7 @@ template <int N_, int R_, int R2_> struct Shape : Fast<N_> {
 template <class SH> struct Gather {
     uint32_t aw[SH::AW], pw[SH::SPW], uw[SH::K4][SH::C];
     int trow[SH::C];
+    float mzr;             // group scales: the readout scale of this lane's readout row (m_z of the expert's row)
 };
 
 // A quad lane's share of an n-byte row: for n = 128 the 16-byte chunks at qk 16 and 64 + qk 16, with LDS rows
@@ -95,6 +98,62 @@ template <class SH, int L> struct SharedTables {
 };
 
 template <class SH, int L> constexpr int kTablesBytes = (int)sizeof(SharedTables<SH, L>);
+
+// Models with group scales (cpu/ygg.cpp:257-266, 371-372, 398, 431): per layer the unembedding scale of every class
+// (sqv, or the layer's single scale), per routed layer the layer-input scale of every coordinate (mulv, or the single
+// scale) and the squared group scales of the layer below (r2b); the readout row scales (m_z per expert and row) come
+// with the gather record.
+template <class SH, int L> struct GroupTables {
+    static constexpr int LR = L > 1 ? L - 1 : 1;
+    float sq[L][256];
+    float mul[LR][SH::N];
+    float r2[LR][SH::N / 16];
+};
+
+struct NoGroupTables {
+    int unused;
+};
+template <class SH, int L, bool GROUP>
+using GroupTablesOf = std::conditional_t<GROUP, GroupTables<SH, L>, NoGroupTables>;
+
+template <class SH, int L, int NT>
+__device__ __forceinline__ void load_group_tables(GroupTables<SH, L> &G, const YggDevModel &m, int tid) {
+    constexpr int N = SH::N, LR = L > 1 ? L - 1 : 1;
+    constexpr int SK = (256 + NT - 1) / NT, MK = (N + NT - 1) / NT;
+    float sv[L][SK], mv[LR][MK], rv = 0.0f;
+#pragma unroll
+    for (int l = 0; l < L; l++) {
+        const YggDevLayer &y = m.layers[l];
+#pragma unroll
+        for (int k = 0; k < SK; k++) {
+            const int c = tid + k * NT;
+            sv[l][k] = y.unembed_scale;
+            if (y.sqv && c < m.VP) sv[l][k] = y.sqv[c];
+        }
+    }
+#pragma unroll
+    for (int l = 1; l < L; l++) {
+        const YggDevLayer &y = m.layers[l];
+#pragma unroll
+        for (int k = 0; k < MK; k++) {
+            const int c = tid + k * NT;
+            mv[l - 1][k] = y.layer_input_scale;
+            if (y.mulv && c < N) mv[l - 1][k] = y.mulv[c];
+        }
+        if (y.r2b && tid / (N / 16) == l - 1) rv = y.r2b[tid % (N / 16)];
+    }
+#pragma unroll
+    for (int l = 0; l < L; l++)
+#pragma unroll
+        for (int k = 0; k < SK; k++)
+            if (tid + k * NT < 256) G.sq[l][tid + k * NT] = sv[l][k];
+#pragma unroll
+    for (int l = 1; l < L; l++)
+#pragma unroll
+        for (int k = 0; k < MK; k++)
+            if (tid + k * NT < N) G.mul[l - 1][tid + k * NT] = mv[l - 1][k];
+    if (L > 1 && tid < (N / 16) * (L - 1)) G.r2[tid / (N / 16)][tid % (N / 16)] = rv;
+}
 
 // Stage the tables with NT threads: every load is issued before the first LDS store, so a launch waits for them
 // once (a load-store loop would wait for each in turn).
@@ -179,6 +238,31 @@ __device__ __forceinline__ float below_and_rho(uint32_t (&qbw)[Fast<N>::QW], con
     for (int i = 0; i < F::QW; i++) S = dot4(qbw[i], qbw[i], S);
     S = sum4(S);
     return 1.0f / sqrtf((float)S * F::kInvN + eps);
+}
+
+// rho with group scales: sum over the 16-coordinate groups g, in order, of r2b[g] f32(sum of q^2 over g), then
+// 1 / sqrt(sum / n + eps) (cpu/ygg.cpp:257-266). r2 the layer's r2b (LDS); qbw the quad share as below_and_rho loads
+// it: quad lane k holds group k (n = 64), groups k and 4 + k (n = 128) or groups 4k .. 4k + 3 (n = 256).
+template <int N>
+__device__ __forceinline__ float group_rho(const uint32_t (&qbw)[Fast<N>::QW], const float *r2, float eps) {
+    static_assert(N == 64 || N == 128 || N == 256, "groups whole in a quad lane's share");
+    constexpr int GPL = Fast<N>::QW / 4;        // groups per quad lane
+    int sg[GPL];
+#pragma unroll
+    for (int j = 0; j < GPL; j++) {
+        sg[j] = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) sg[j] = dot4(qbw[4 * j + i], qbw[4 * j + i], sg[j]);
+    }
+    float sum = 0.0f;
+#pragma unroll
+    for (int g = 0; g < N / 16; g++) {
+        // the lane and slot of group g
+        const int ln = N == 128 ? (g & 3) : (N == 256 ? g >> 2 : g);
+        const int j = N == 128 ? (g >> 2) : (N == 256 ? (g & 3) : 0);
+        sum = sum + r2[g] * (float)__builtin_amdgcn_readlane(sg[j], ln);
+    }
+    return 1.0f / sqrtf(sum * Fast<N>::kInvN + eps);
 }
 
 // nothing to overlap with the first global router round
@@ -425,6 +509,7 @@ __device__ __forceinline__ void gather(Gather<SH> &G, const YggDevLayer &y, int 
 #pragma unroll
         for (int c = 0; c < F::C; c++) G.trow[c] = tr[c];
     }
+    G.mzr = y.mz ? y.mz[(uint32_t)r * SH::R + lane / SH::RL] : y.readout_scale;
     const uint8_t *pp = g + y.off_P;
 #pragma unroll
     for (int gi = 0; gi < F::SP / F::GP; gi++) {
@@ -466,7 +551,8 @@ __device__ __forceinline__ void layer_input(int8_t *zls, const int8_t *V0, const
 // with A16 = 256 hi + lo, so A16 q = 256 (hi q) + (lo q) exactly, two v_dot4 chains on the raw int8 state.
 template <class SH>
 __device__ __forceinline__ void update(int (&qn)[SH::C], const Gather<SH> &G, const int8_t *qold,
-                                       const int8_t *zls, const YggDevLayer &y, bool routed, int shift, int lane) {
+                                       const int8_t *zls, const YggDevLayer &y, bool routed, int shift, int lane,
+                                       const float *mul = nullptr) {
     using F = SH;
     constexpr int BLK = F::BLK, C = F::C, RW = BLK / 4;     // dwords of one row's hi (and of its lo) bytes
     const int blk0 = (C * lane / BLK) * BLK;
@@ -494,7 +580,8 @@ __device__ __forceinline__ void update(int (&qn)[SH::C], const Gather<SH> &G, co
             for (int c = 0; c < C; c++) d[c] = dot4(G.uw[k4][c], zw, d[c]);
         }
 #pragma unroll
-        for (int c = 0; c < C; c++) acc[c] = wadd(acc[c], cvt_rne((float)d[c] * y.layer_input_scale));
+        for (int c = 0; c < C; c++)
+            acc[c] = wadd(acc[c], cvt_rne((float)d[c] * (mul ? mul[C * lane + c] : y.layer_input_scale)));
     }
 #pragma unroll
     for (int c = 0; c < C; c++) qn[c] = sat8(acc[c]);
@@ -519,7 +606,7 @@ __device__ __forceinline__ void readout(int8_t *zqs, const uint32_t (&pw)[SH::SP
 // f32(Q zq) s_q for the 4 classes of this lane (cpu/ygg.cpp:421-434); Qs the layer's Q planes
 template <int R>
 __device__ __forceinline__ void unembed_terms(float (&term)[4], const int8_t *zqs, const int8_t *Qs, float scale,
-                                              int lane) {
+                                              int lane, const float *sq = nullptr) {
     constexpr int QC = R / 4, RW = R / 4;              // 16-byte chunks per lane, dwords per class
     uint32_t zw[RW];
     load_words<RW, 16>(zw, zqs);
@@ -536,7 +623,7 @@ __device__ __forceinline__ void unembed_terms(float (&term)[4], const int8_t *zq
         int d = 0;
 #pragma unroll
         for (int i = 0; i < RW; i++) d = dot4(qq[u * RW + i], zw[i], d);
-        term[u] = (float)d * scale;
+        term[u] = (float)d * (sq ? sq[4 * lane + u] : scale);
     }
 }
 
@@ -566,11 +653,14 @@ __device__ __forceinline__ void store_logits(float *o, const float (&lg)[4], int
 
 // ----------------------------------------------------------------------------------------------- fast_kernel
 
-// GEN: sample the next input from the logits of every token (io.gen), instead of reading it from tokens. DEEP: one
+// MODE: kModeRun (logits, leaves, states), kModeScore (also the digest and the NLL: their constants and lane terms
+// take registers the other modes keep for streams) or kModeGenerate (sample the next input from the logits of every
+// token, io.gen, instead of reading it from tokens). DEEP: one
 // stream per workgroup with the deep descent (generation for few streams), else 4 streams per workgroup with
 // descend. CAP (not DEEP): at most 128 VGPRs, 4 wavefronts per SIMD (the most streams resident, some registers
 // spilled), else up to 256 (no spills; for calls whose streams all fit at the lower occupancy).
-template <int N, int R, int R2, int L, bool GEN, bool DEEP, bool CAP>
+// GROUP: the model has group scales (the tables of GroupTables and the experts' readout row scales)
+template <int N, int R, int R2, int L, int MODE, bool DEEP, bool CAP, bool GROUP>
 __global__ __launch_bounds__(64 * kFastWaves)
 __attribute__((amdgpu_waves_per_eu(DEEP ? 1 : (CAP ? 4 : 2))))
 void fast_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B, int T, int8_t *__restrict__ state,
@@ -584,7 +674,9 @@ void fast_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
     using SH = Shape<N, R, R2>;
     using F = SH;
     constexpr int W = DEEP ? 1 : kFastWaves, LR = L > 1 ? L - 1 : 1;
+    constexpr bool GEN = MODE == kModeGenerate, SCORE = MODE == kModeScore;
     __shared__ __attribute__((aligned(16))) SharedTables<SH, L> S;
+    __shared__ __attribute__((aligned(16))) GroupTablesOf<SH, L, GROUP> GT;
     __shared__ __attribute__((aligned(16))) int8_t W1s[DEEP ? LR : 1][DEEP ? kR2Slots<N> * N : 16];
     __shared__ __attribute__((aligned(16))) int8_t qsw[W][L * N];
     __shared__ __attribute__((aligned(16))) int8_t zlw[W][SH::ZL];
@@ -607,6 +699,7 @@ void fast_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
 #pragma unroll
     for (int k = 0; k < SB; k++) sb[k] = (live && lane + 64 * k < L * N) ? st[lane + 64 * k] : 0;
     load_tables<SH, L, 64 * kFastWaves>(S, m, tid);
+    if constexpr (GROUP) load_group_tables<SH, L, 64 * kFastWaves>(GT, m, tid);
     if constexpr (DEEP) load_round2<N, L, 64 * kFastWaves>(W1s, m, tid);
     __syncthreads();
     if (!live) return;
@@ -625,7 +718,7 @@ void fast_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
         if (lane + 64 * k < L * N) qs[lane + 64 * k] = (int8_t)sb[k];
     if (lane < SH::ZL) zls[lane] = 0;
     wave_sync();
-    unsigned long long dg = digest ? digest[s] : 0ull;
+    unsigned long long dg = (SCORE && digest) ? digest[s] : 0ull;
     double nacc = 0.0;
 
     for (int t = 0; t < T; t++) {
@@ -659,15 +752,18 @@ void fast_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
         // only the new state: it runs while the loads of layer l + 1's first global router round are in flight
         // (pl: the layer whose readout is pending, ppw: its P granules). The logits still add layer by layer in order.
         uint32_t ppw[F::SPW];
+        float pmz = 0.0f;
         int pl = -1;
         auto flush = [&]() {
             if (pl >= 0) {
                 const YggDevLayer &yp = m.layers[pl];
-                readout<SH>(zqs, ppw, qs + pl * N, yp.readout_scale, lane);
+                readout<SH>(zqs, ppw, qs + pl * N, GROUP ? pmz : yp.readout_scale, lane);
                 wave_sync();
                 if (4 * lane < VP) {
                     float term[4];
-                    unembed_terms<R>(term, zqs, S.Q[pl], yp.unembed_scale, lane);
+                    const float *sq = nullptr;
+                    if constexpr (GROUP) sq = GT.sq[pl];
+                    unembed_terms<R>(term, zqs, S.Q[pl], yp.unembed_scale, lane, sq);
 #pragma unroll
                     for (int u = 0; u < 4; u++) lg[u] = lg[u] + term[u];
                 }
@@ -688,6 +784,8 @@ void fast_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
 #pragma unroll
                 for (int i = 1; i < LR; i++) th = l - 1 == i ? th1[i] : th;
                 rho = below_and_rho<N>(qbw, qs + (l - 1) * N, y.rms_eps, lane);
+                if constexpr (GROUP)
+                    if (y.r2b) rho = group_rho<N>(qbw, GT.r2[l - 1], y.rms_eps);
                 if constexpr (!DEEP) {
                     r = descend<N>(m, y, S.W[l - 1], th, qbw, rho, x, lane, flush);
                 } else {
@@ -709,7 +807,10 @@ void fast_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
             if (l > 0) layer_input<SH>(zls, S.V[l - 1], S.mv[l - 1], qbw, rho, lane);
             wave_sync();
             int qn[F::C];
-            if (lane < F::NL) update<SH>(qn, G, qs + l * N, zls, y, l > 0, m.shift, lane);
+            const float *mul = nullptr;
+            if constexpr (GROUP)
+                if (l > 0) mul = GT.mul[l - 1];
+            if (lane < F::NL) update<SH>(qn, G, qs + l * N, zls, y, l > 0, m.shift, lane, mul);
             wave_sync();
             if (lane < F::NL) {
 #pragma unroll
@@ -717,15 +818,16 @@ void fast_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
             }
             wave_sync();
             if (leaves && lane == 0) leaves[((size_t)s * T + t) * L + l] = r;
-            if (digest) dg = dg * kDigestMul + digest_term<N>(qn, r, l, lane);
+            if (SCORE && digest) dg = dg * kDigestMul + digest_term<N>(qn, r, l, lane);
 #pragma unroll
             for (int i = 0; i < F::SPW; i++) ppw[i] = G.pw[i];
+            pmz = G.mzr;
             pl = l;
             if (l == L - 1) flush();
         }
 
         if (logits) store_logits(logits + ((size_t)s * T + t) * V, lg, V, lane);
-        if (nll) {
+        if (SCORE && nll) {
             const int yv = targets[(size_t)s * T + t];
             if (yv >= 0 && yv < V) nacc += token_nll(lg, V, yv, lane);
             else if (lane == 0) atomicOr(m.err, 2u);
@@ -741,15 +843,15 @@ void fast_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
     }
     wave_sync();
     for (int i = lane; i < L * N; i += 64) st[i] = qs[i];
-    if (digest && lane == 0) digest[s] = dg;
-    if (nll && lane == 0) nll[s] += nacc;
+    if (SCORE && digest && lane == 0) digest[s] = dg;
+    if (SCORE && nll && lane == 0) nll[s] += nacc;
 }
 
 // ----------------------------------------------------------------------------------------------- pipe_kernel
 
 // CAP: at most 128 VGPRs (4 wavefronts per SIMD: more streams resident, some registers spilled), else as many as
 // the kernel needs (no spills: faster for few streams)
-template <int N, int R, int R2, int L, bool CAP>
+template <int N, int R, int R2, int L, bool CAP, bool GROUP>
 __global__ __launch_bounds__(64 * L) __attribute__((amdgpu_waves_per_eu(CAP ? 4 : 1)))
 void pipe_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B, int T, int8_t *__restrict__ state,
                  const YggIO io) {
@@ -763,6 +865,7 @@ void pipe_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
     using SH = Shape<N, R, R2>;
     using F = SH;
     __shared__ __attribute__((aligned(16))) SharedTables<SH, L> S;
+    __shared__ __attribute__((aligned(16))) GroupTablesOf<SH, L, GROUP> GT;
     __shared__ __attribute__((aligned(16))) int8_t qbuf[L][2][N];            // layer l after token t: [l][t & 1]
     __shared__ __attribute__((aligned(16))) float lgs[L][256];               // logits of token t: row t % L
     __shared__ __attribute__((aligned(16))) unsigned long long dterm[L][L];  // digest terms of token t: row t % L
@@ -775,6 +878,7 @@ void pipe_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
     const int s = blockIdx.x;
     const int V = m.V, VP = m.VP;
     load_tables<SH, L, 64 * L>(S, m, tid);
+    if constexpr (GROUP) load_group_tables<SH, L, 64 * L>(GT, m, tid);
     const YggDevLayer &y = m.layers[l];
     int8_t *st = state + ((size_t)s * L + l) * N;
     for (int i = lane; i < N; i += 64) qbuf[l][1][i] = st[i];     // the state before token 0
@@ -816,6 +920,8 @@ void pipe_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
                 Gather<SH> G;
                 if (l > 0) {
                     rho = below_and_rho<N>(qbw, qbuf[l - 1][t & 1], y.rms_eps, lane);
+                    if constexpr (GROUP)
+                        if (y.r2b) rho = group_rho<N>(qbw, GT.r2[l - 1], y.rms_eps);
                     r = descend<N>(m, y, S.W[l - 1], th0, qbw, rho, x, lane);
                     gather<SH>(G, y, r, x, true, lane);
                     layer_input<SH>(zlw[l], S.V[l - 1], S.mv[l - 1], qbw, rho, lane);
@@ -834,17 +940,22 @@ void pipe_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
                 wave_sync();
                 int qn[F::C];
                 if (lane < F::NL) {
-                    update<SH>(qn, G, qbuf[l][(t + 1) & 1], zlw[l], y, l > 0, m.shift, lane);
+                    const float *mul = nullptr;
+                    if constexpr (GROUP)
+                        if (l > 0) mul = GT.mul[l - 1];
+                    update<SH>(qn, G, qbuf[l][(t + 1) & 1], zlw[l], y, l > 0, m.shift, lane, mul);
 #pragma unroll
                     for (int c = 0; c < F::C; c++) qbuf[l][t & 1][F::C * lane + c] = (int8_t)qn[c];
                 }
                 wave_sync();
-                readout<SH>(zqw[l], G.pw, qbuf[l][t & 1], y.readout_scale, lane);
+                readout<SH>(zqw[l], G.pw, qbuf[l][t & 1], GROUP ? G.mzr : y.readout_scale, lane);
                 wave_sync();
                 float *lr = lgs[t % L];
                 if (4 * lane < VP) {
                     float term[4];
-                    unembed_terms<R>(term, zqw[l], S.Q[l], y.unembed_scale, lane);
+                    const float *sq = nullptr;
+                    if constexpr (GROUP) sq = GT.sq[l];
+                    unembed_terms<R>(term, zqw[l], S.Q[l], y.unembed_scale, lane, sq);
 #pragma unroll
                     for (int u = 0; u < 4; u++) {
                         const float base = l == 0 ? m.output_bias[4 * lane + u] : lr[4 * lane + u];

@@ -1,5 +1,7 @@
-// The kernels the C-ABI launches: one launcher per instantiation, found by shape, with the name a profiler shows for
-// it (a "%s" in the name stands for the GEN argument, "true" in ygg_generate, else "false").
+// The kernels the C-ABI launches: one launcher per instantiation (or per set of mode builds), found by shape, with
+// the name a profiler shows for it. A "%s" in the name stands for the call's mode: the GEN argument of run_kernel
+// ("true" in ygg_generate, else "false") or, for a modal kernel, the MODE argument (kModeRun, kModeGenerate,
+// kModeScore).
 #pragma once
 #include <hip/hip_runtime.h>
 
@@ -14,8 +16,14 @@ typedef hipError_t (*Launcher)(const YggDevModel &, const int32_t *, int, int, i
 
 struct Kernel {
     Launcher fn = nullptr;
-    char name[80] = {0};
+    char name[96] = {0};
+    bool modal = false;     // the launcher picks a build by io_mode(io), the name's "%s" is that mode
     explicit operator bool() const { return fn != nullptr; }
+    // the name of the build a call of this mode runs
+    void name_for(int mode, char *out, size_t len) const {
+        static const char *const modes[3] = {"0", "1", "2"};
+        snprintf(out, len, name, modal ? modes[mode] : (mode == kModeGenerate ? "true" : "false"));
+    }
 };
 
 inline Kernel make_kernel(Launcher fn, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
@@ -29,20 +37,27 @@ inline Kernel make_kernel(Launcher fn, const char *fmt, ...) {
     return k;
 }
 
-// The shapes of the specialised kernels (block 16, table storage, tensor scales): state width, readout rank,
+// k, whose launcher picks a build per mode
+inline Kernel modal(Kernel k) {
+    k.modal = true;
+    return k;
+}
+
+// The shapes of the specialised kernels (block 16, table storage, tensor or group scales): state width, readout rank,
 // layer-input rank, and the most layers. The first three are the benchmark configurations' (and the reference's
 // small models), the last two its medium and large models (configs/{enwik8,hg38}/{medium,large}.yaml).
 #define YGG_SHAPES(X) X(64, 8, 16) X(96, 8, 16) X(128, 8, 16) X(128, 16, 32) X(256, 32, 64)
 constexpr int kMaxFastLayers = 5;
 
 Kernel find_launcher(int n, int blk, int R);                            // run_kernel (ygg_kernels.hip)
+// group: the model has group scales (builds for n of 64, 128 and 256 only)
 // fast_kernel, 4 streams per workgroup, 128-VGPR cap or none (ygg_kernels_fast.hip); its resident workgroups per CU
-Kernel find_fast_launcher(int n, int R, int R2, int L, bool cap);
-int fast_blocks_per_cu(int n, int R, int R2, int L, bool cap, bool gen);
+Kernel find_fast_launcher(int n, int R, int R2, int L, bool cap, bool group);
+int fast_blocks_per_cu(int n, int R, int R2, int L, bool cap, bool group, int mode);
 // fast_kernel with the deep descent, one stream per workgroup; pipe_kernel, 128-VGPR cap or none
 // (ygg_kernels_deep.hip)
-Kernel find_deep_launcher(int n, int R, int R2, int L);
-Kernel find_pipe_launcher(int n, int R, int R2, int L, bool cap);
-int pipe_blocks_per_cu(int n, int R, int R2, int L, bool cap);
+Kernel find_deep_launcher(int n, int R, int R2, int L, bool group);
+Kernel find_pipe_launcher(int n, int R, int R2, int L, bool cap, bool group);
+int pipe_blocks_per_cu(int n, int R, int R2, int L, bool cap, bool group);
 
 }  // namespace ygg

@@ -92,6 +92,15 @@ struct YggIO {
     unsigned long long seed;        // generate
 };
 
+// What a launch computes, from its outputs: the specialised per-stream kernel has a build per mode (the digest and
+// NLL terms cost registers that plain runs keep for streams). Also the mode argument of ygg_kernel_name.
+constexpr int kModeRun = 0;         // logits, leaves, states after every token
+constexpr int kModeGenerate = 1;    // io.gen: each token sampled from the step before
+constexpr int kModeScore = 2;       // io.digest or io.nll
+inline int io_mode(const YggIO &io) {
+    return io.gen ? kModeGenerate : ((io.digest || io.nll) ? kModeScore : kModeRun);
+}
+
 // Compile-time lane constants of a d_state N, readout rank R.
 template <int N> struct Lanes {
     static constexpr int C = N <= 64 ? 1 : (N <= 128 ? 2 : 4);

@@ -75,11 +75,13 @@ class Yggdrasil:
             raise ImportError(f"backend='hip' needs the built library ({e})") from e
         return cls(path, **kw)
 
-    def kernel_name(self, B: int, T: int, generate: bool = False) -> str:
-        """The kernel a call of B streams and T tokens launches (generate: `generate` of T tokens), by the name
-        profilers show for it."""
+    def kernel_name(self, B: int, T: int, generate: bool = False, score: bool = False) -> str:
+        """The kernel a call of B streams and T tokens launches (generate: `generate` of T tokens; score: `score`, or
+        `run` with a digest), by the name profilers show for it."""
+        if generate and score:
+            raise ValueError("generate and score are different calls")
         buf = ctypes.create_string_buffer(128)
-        check(_lib.lib().ygg_kernel_name(self._h, B, T, int(generate), buf, len(buf)))
+        check(_lib.lib().ygg_kernel_name(self._h, B, T, 1 if generate else (2 if score else 0), buf, len(buf)))
         return buf.value.decode()
 
     def close(self):

@@ -13,6 +13,9 @@ weights that step touches, plus the per-stream inputs and outputs:
     + distinct tokens x          x (2 n b + R n + 2 n)      token layer: A16, P and its own table row
     + B x (4 + 4 V)                                         token in, logits out
 
+With group scales every expert also carries its R readout row scales (4 R bytes, per distinct leaf and per distinct
+token for the token layer); the per-class and per-coordinate scale vectors are read once per launch and left out.
+
 and once per launch the int8 state of every stream in and out, 2 B L n. A T-token launch sums the T steps; the
 per-token figure is measured on an evenly spaced sample of the steps (all of them when T <= sample) and multiplied by
 the B T tokens of the launch. The per-stream figure (no deduplication across streams) is reported beside it.
@@ -23,7 +26,7 @@ import numpy as np
 
 
 def step_bytes(leaves: np.ndarray, tokens: np.ndarray, n: int, b: int, R: int, R2: int, V: int, D: int,
-               factored_rank: int = 0, sample: int = 64) -> dict:
+               factored_rank: int = 0, sample: int = 64, group: bool = False) -> dict:
     """leaves (B, T, L) int (layer 0: the token), tokens (B, T) -> dict(compulsory=, per_stream=) bytes of the whole
     T-token launch, the per-launch state bytes in 'state' and the per-token figures."""
     B, T, L = leaves.shape
@@ -31,6 +34,9 @@ def step_bytes(leaves: np.ndarray, tokens: np.ndarray, n: int, b: int, R: int, R
     leaf_w = 2 * n * b + n * R2 + R * n + ((factored_rank * n + 2 * n + 4) if factored_rank else 0)
     row_w = 0 if factored_rank else 2 * n
     tok_w = 2 * n * b + R * n + 2 * n
+    if group:
+        leaf_w += 4 * R
+        tok_w += 4 * R
     io = B * (4 + 4 * V)
     comp = 0
     per = 0

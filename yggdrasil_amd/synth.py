@@ -182,9 +182,14 @@ def write_model(spec: ModelSpec, seed: int, path, bias: Optional[np.ndarray] = N
             arrs += layer_arrays(l, q, hdr)
             continue
         E = V if l == 0 else E_routed
+        pl = probe[l]
         if spec.group:
-            raise NotImplementedError("streamed writing of group-scale models (per-expert readout scales)")
-        la = layer_arrays(l, probe[l], hdr)
+            # the per-expert readout row scales are an array of their own (mzl): one pass over the chunks for them
+            def scales(j0, l=l, E=E):
+                return _experts(spec, seed, l, j0, min(E, j0 + CHUNK), orth)["readout_scale"]
+            with ThreadPoolExecutor(nt) as ex:
+                pl = dataclasses.replace(pl, readout_scale=np.concatenate(list(ex.map(scales, range(0, E, CHUNK)))))
+        la = layer_arrays(l, pl, hdr)
         rec_bytes = int(dict(la)[f"l{l}_meta"][0])
 
         def chunks(l=l, q=q, E=E):
