@@ -53,9 +53,21 @@ __device__ __forceinline__ unsigned long long wave_sum_u64(unsigned long long v)
     return v;
 }
 
+template <int CTRL> __device__ __forceinline__ float dpp_f32(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float lane_f32(float v, int lane) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+// fmaxf over the wavefront (every lane active), returned to every lane: DPP within rows of 16 lanes (quad swaps, the
+// half-row and row mirrors), then the four row maxima from scalar reads. fmaxf ignores NaNs and is exact, so the order
+// of the pairings does not change the result.
 __device__ __forceinline__ float wave_max_f32(float v) {
-    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-    return v;
+    v = fmaxf(v, dpp_f32<0xB1>(v));
+    v = fmaxf(v, dpp_f32<0x4E>(v));
+    v = fmaxf(v, dpp_f32<0x141>(v));
+    v = fmaxf(v, dpp_f32<0x140>(v));
+    return fmaxf(fmaxf(lane_f32(v, 0), lane_f32(v, 16)), fmaxf(lane_f32(v, 32), lane_f32(v, 48)));
 }
 __device__ __forceinline__ double wave_sum_f64(double v) {
     for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
@@ -84,14 +96,6 @@ __device__ __forceinline__ double token_nll(const float (&lg)[4], int V, int y, 
     return log(se) + (double)mx - (double)ly;
 }
 
-__device__ __forceinline__ int wave_min_i32(int v) {
-    for (int o = 32; o >= 1; o >>= 1) v = min(v, __shfl_xor(v, o));
-    return v;
-}
-__device__ __forceinline__ int wave_sum_i32(int v) {
-    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
-    return v;
-}
 __device__ __forceinline__ float wave_sum_f32(float v) {
     for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
     return v;
@@ -132,11 +136,17 @@ __device__ __forceinline__ int sample_token(const float (&lg)[4], int V, float t
         if (valid[u]) mx = fmaxf(mx, lg[u]);
     mx = wave_max_f32(mx);
     if (temperature <= 0.0f) {
-        int idx = 0x7fffffff;
+        // the first maximal class: the lowest lane holding one, then its lowest class (scalar work on ballots)
+        unsigned long long mk[4], any = 0;
 #pragma unroll
-        for (int u = 0; u < 4; u++)
-            if (valid[u] && lg[u] == mx) idx = min(idx, 4 * lane + u);
-        return wave_min_i32(idx);
+        for (int u = 0; u < 4; u++) {
+            mk[u] = __ballot(valid[u] && lg[u] == mx);
+            any |= mk[u];
+        }
+        if (!any) return 0x7fffffff;
+        const int ln = __builtin_ctzll(any);
+        const int u = ((mk[0] >> ln) & 1) ? 0 : (((mk[1] >> ln) & 1) ? 1 : (((mk[2] >> ln) & 1) ? 2 : 3));
+        return 4 * ln + u;
     }
     // the top_k-th largest logit, by a radix search over order-preserving keys
     uint32_t kth = 0;
@@ -146,10 +156,10 @@ __device__ __forceinline__ int sample_token(const float (&lg)[4], int V, float t
         for (int u = 0; u < 4; u++) key[u] = fkey(lg[u]);
         for (int b = 31; b >= 0; b--) {
             const uint32_t cand = kth | (1u << b);
-            int c = 0;
+            int c = 0;     // classes with keys >= cand: population counts of ballots
 #pragma unroll
-            for (int u = 0; u < 4; u++) c += (valid[u] && key[u] >= cand) ? 1 : 0;
-            if (wave_sum_i32(c) >= top_k) kth = cand;
+            for (int u = 0; u < 4; u++) c += __popcll(__ballot(valid[u] && key[u] >= cand));
+            if (c >= top_k) kth = cand;
         }
     }
     float w[4], part = 0.0f;
@@ -174,9 +184,11 @@ __device__ __forceinline__ int sample_token(const float (&lg)[4], int V, float t
             if (run > target && pick == 0x7fffffff) pick = 4 * lane + u;
         }
     }
-    pick = wave_min_i32(pick);
-    if (pick == 0x7fffffff) pick = -wave_min_i32(-last);
-    return pick;
+    // classes grow with the lane: the first lane with a pick holds the smallest, the last with a kept class the largest
+    const unsigned long long pm = __ballot(pick != 0x7fffffff);
+    if (pm) return __builtin_amdgcn_readlane(pick, __builtin_ctzll(pm));
+    const unsigned long long lm = __ballot(last >= 0);
+    return lm ? __builtin_amdgcn_readlane(last, 63 - __builtin_clzll(lm)) : -1;
 }
 
 // One round of the router descent from its ballot: node j of the round's subtree (breadth-first, j < 2^h - 1) goes
