@@ -52,7 +52,7 @@ def test_version_and_info_layout(lib):
     L = lib.lib()
     assert L.ygg_version() == lib.ABI_VERSION
     # ygg_info: 16 int32 + 2 int64 + 8 int64
-    assert ctypes.sizeof(lib.YggInfo) == 18 * 4 + 8 * 10
+    assert ctypes.sizeof(lib.YggInfo) == 20 * 4 + 8 * 10
 
 
 def test_bad_arguments(lib):

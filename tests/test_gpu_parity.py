@@ -40,12 +40,12 @@ def _compare(got, ref, keys=("leaves", "states", "logits")):
                                  f"gpu {a[tuple(bad[0])]} oracle {b[tuple(bad[0])]}")
 
 
-@pytest.fixture(params=["pipe", "fast", "deep", "generic"])
+@pytest.fixture(params=["flow", "pipe", "fast", "deep", "generic"])
 def kernel_env(request, monkeypatch):
-    """Load models with one kernel forced for every call (YGG_KERNEL): the layer-pipelined one, the specialised
-    per-stream one (4 streams per workgroup), its one-stream-per-workgroup form with the deep router descent (deep:
-    models whose router plan allows it, else the per-stream one), or the general one; all but the last apply only to
-    the common shape (readout rank 8, block 16, ...)."""
+    """Load models with one kernel forced for every call (YGG_KERNEL): the tick-pipelined one (flow: models of 2 or
+    more layers, else the per-stream one), the layer-pipelined one, the specialised per-stream one (4 streams per
+    workgroup), its one-stream-per-workgroup form with the deep router descent (deep: models whose router plan allows
+    it, else the per-stream one), or the general one; all but the last apply only to the specialised shapes."""
     monkeypatch.setenv("YGG_KERNEL", request.param)
     monkeypatch.delenv("YGG_DEEP", raising=False)
     return request.param
@@ -114,6 +114,12 @@ def deep_plan(plan) -> bool:
     return 2 <= len(plan) <= 4 and plan[0] >= 2 and (len(plan) < 4 or plan[2] + plan[3] <= 6)
 
 
+def flow_built(info) -> bool:
+    """Models with flow_kernel builds: 2 to 5 layers, router plans of 3 or 4 rounds (depth 9 to 16), not the largest
+    shape."""
+    return info.n_layers > 1 and info.d_state != 256 and info.router_rounds in (3, 4)
+
+
 def _expect_kernel(model, kernel_env):
     """The forced kernel is the one in use (the shapes passed here are all common-shape models)."""
     info = model.info
@@ -127,10 +133,16 @@ def _expect_kernel(model, kernel_env):
             assert info.deep == 1
     deep = bool(info.deep)
     assert (info.deep_max_streams > 0) == (kernel_env == "deep" and deep), info.deep_max_streams
+    assert (info.flow_max_streams > 0) == (kernel_env == "flow" and flow_built(info)), info.flow_max_streams
     name = model.kernel_name(8, 64)
-    want = {"generic": "ygg::run_kernel<", "pipe": "ygg::pipe_kernel<",
-            "fast": "ygg::fast_kernel<", "deep": "ygg::fast_kernel<"}[kernel_env]
+    want = {"generic": "ygg::run_kernel<", "pipe": "ygg::pipe_kernel<", "fast": "ygg::fast_kernel<",
+            "deep": "ygg::fast_kernel<", "flow": "ygg::flow_kernel<"}[kernel_env]
+    if kernel_env == "flow" and not flow_built(info):
+        want = "ygg::fast_kernel<"
     assert name.startswith(want), name
+    if want == "ygg::flow_kernel<":
+        assert name.endswith(", true>" if info.group else ", false>"), name
+        return
     group = "true" if info.group else "false"
     if kernel_env in ("fast", "deep"):
         descent = "true" if kernel_env == "deep" and deep else "false"
@@ -398,10 +410,16 @@ def test_default_dispatch(hip, model_dir, monkeypatch):
         synth.write_model(synth.ModelSpec(128, 16, 10, 256, 4, router="gauss"), 11, path)
     model = hip.load(path)
     info = model.info
-    # mode 0: run, 1: generate, 2: score or a run with a digest
+    # mode 0: run, 1: generate, 2: score or a run with a digest; D = 10: a plan of 3 rounds
     fast = "ygg::fast_kernel<128, 8, 16, 4, {}, false, {}, false>"
-    assert model.kernel_name(1, 64) == "ygg::pipe_kernel<128, 8, 16, 4, false, false>"
-    assert model.kernel_name(1, 64, score=True) == "ygg::pipe_kernel<128, 8, 16, 4, false, false>"
+    flow = "ygg::flow_kernel<128, 8, 16, 4, 3, {}, false>"
+    assert info.router_rounds == 3 and 0 < info.flow_max_streams < info.pipe_max_streams
+    assert model.kernel_name(1, 64) == flow.format(0)
+    assert model.kernel_name(1, 64, score=True) == flow.format(2)
+    assert model.kernel_name(info.flow_max_streams, 32) == flow.format(0)
+    assert model.kernel_name(1, 31) == "ygg::pipe_kernel<128, 8, 16, 4, false, false>"
+    assert model.kernel_name(info.flow_max_streams + 1, 64) == "ygg::pipe_kernel<128, 8, 16, 4, true, false>" or \
+        model.kernel_name(info.flow_max_streams + 1, 64) == "ygg::pipe_kernel<128, 8, 16, 4, false, false>"
     assert model.kernel_name(1, 1) == fast.format(0, "false")
     assert model.kernel_name(1, 1, score=True) == fast.format(2, "false")
     assert model.kernel_name(info.pipe_max_streams + 1, 64) == fast.format(0, "false")

@@ -29,7 +29,8 @@ ARCH = "gfx950"
 HIPCC_FLAGS = ["--offload-arch=" + ARCH, "-O3", "-std=c++17", "-ffp-contract=off", "-fPIC",
                "-mcode-object-version=5", "-Wall", "-Wno-unused-result",
                "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
-SOURCES = ["ygg_kernels.hip", "ygg_kernels_fast.hip", "ygg_kernels_deep.hip", "ygg_capi.hip", "ygg_float.hip"]
+SOURCES = ["ygg_kernels.hip", "ygg_kernels_fast.hip", "ygg_kernels_deep.hip", "ygg_kernels_flow.hip", "ygg_capi.hip",
+           "ygg_float.hip"]
 
 
 def hipcc() -> str:

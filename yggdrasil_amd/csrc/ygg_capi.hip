@@ -361,6 +361,9 @@ struct ygg_model {
     ygg::Kernel deep;                 // deep descent: generate with B <= deep_max_streams
     int deep_max_streams = 0;
     bool deep_all = false;            // YGG_KERNEL=deep: every call
+    ygg::Kernel flow;                 // router rounds and updates pipelined over ticks: T > 1, B <= flow_max_streams
+    int flow_max_streams = 0;
+    bool flow_all = false;            // YGG_KERNEL=flow: every call but generation
 };
 
 namespace {
@@ -385,10 +388,11 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     for (int l = 1; l < L; l++)
         if ((fl[l].vt != nullptr) != (fl[1].vt != nullptr))
             return fail(YGG_ERR_FORMAT, "model file: mixed table and factored routed layers");
-    // the specialised kernels cover the common shape: fast_kernel for many streams; pipe_kernel (one wavefront per
-    // layer) when a call of T > 1 tokens has its B L wavefronts resident at once; generation for few streams on
-    // fast_kernel with one stream per workgroup and the deep router descent. YGG_KERNEL=generic|fast|pipe|deep forces
-    // one for every call; YGG_DEEP=0 turns the deep descent off.
+    // the specialised kernels cover the common shape: fast_kernel for many streams; flow_kernel (one wavefront per
+    // layer, router rounds and updates pipelined over ticks), else pipe_kernel (one wavefront per layer), when a call
+    // of T > 1 tokens has its B L wavefronts resident at once; generation for few streams on fast_kernel with one
+    // stream per workgroup and the deep router descent. YGG_KERNEL=generic|fast|pipe|deep|flow forces one for every
+    // call it can run; YGG_DEEP=0 turns the deep descent off, YGG_FLOW=0 flow_kernel.
     const char *kenv = getenv("YGG_KERNEL");
     const std::string kmode = kenv ? kenv : "";
     ygg::Kernel fast;
@@ -433,14 +437,18 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     const char *denv = getenv("YGG_DEEP");
     const bool deep = fast && L > 1 && !(denv && !strcmp(denv, "0")) && rplan.n >= 2 && rplan.n <= 4 &&
                       rplan.h[0] >= 2 && (rplan.n < 4 || rplan.h[2] + rplan.h[3] <= 6);
-    ygg::Kernel pipe, pipe_few, deepk;
-    if (fast && kmode != "fast" && kmode != "deep") {
+    ygg::Kernel pipe, pipe_few, deepk, flowk;
+    if (fast && kmode != "fast" && kmode != "deep" && kmode != "flow") {
         pipe = ygg::find_pipe_launcher(n, R, R2f, L, true, group);
         pipe_few = ygg::find_pipe_launcher(n, R, R2f, L, false, group);
     }
+    // the tick-pipelined kernel: plans of 3 or 4 rounds (YGG_FLOW=0: off)
+    const char *fenv = getenv("YGG_FLOW");
+    if (fast && L > 1 && (kmode == "" || kmode == "flow") && !(fenv && !strcmp(fenv, "0")))
+        flowk = ygg::find_flow_launcher(n, R, R2f, L, rplan.n, group);
     // (the deep kernel exists where its LDS fits a workgroup)
     const ygg::Kernel deep_avail = deep ? ygg::find_deep_launcher(n, R, R2f, L, group) : ygg::Kernel();
-    if (kmode != "fast" && kmode != "pipe") deepk = deep_avail;
+    if (kmode != "fast" && kmode != "pipe" && kmode != "flow") deepk = deep_avail;
     const int64_t slots = plan_slots(rplan);
     // device arena plan: every array 256-byte aligned
     struct Piece { size_t off, bytes; };
@@ -572,6 +580,11 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     m->deep = deepk;
     m->deep_all = deepk && kmode == "deep";
     m->deep_max_streams = deepk ? (m->deep_all ? INT32_MAX : cus) : 0;
+    // flow_kernel for T > 1 while every stream's workgroup is resident (or always with YGG_KERNEL=flow)
+    m->flow = flowk;
+    m->flow_all = flowk && kmode == "flow";
+    m->flow_max_streams =
+        flowk ? (m->flow_all ? INT32_MAX : ygg::flow_blocks_per_cu(n, R, R2f, L, rplan.n, group) * cus) : 0;
     m->device = device;
     m->arena = arena;
     m->arena_bytes = total;
@@ -629,6 +642,8 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     I.pipe_max_streams = m->pipe_max_streams;
     I.deep = deep_avail ? 1 : 0;
     I.deep_max_streams = m->deep_max_streams;
+    I.flow_max_streams = m->flow_max_streams;
+    I.router_rounds = L > 1 ? rplan.n : 0;
     I.file_array_bytes = fa.bytes;
     I.device_bytes = (int64_t)total;
     for (int l = 0; l < L; l++) I.gather_bytes[l] = lp[l].gl.bytes;
@@ -636,16 +651,21 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     return YGG_OK;
 }
 
+// flow_kernel's pipeline fills over (L - 1)(P + 1) + 2 ticks (up to 17 at 4 layers and 4 rounds): calls of fewer
+// tokens run faster on pipe_kernel (measured break-even about 24 tokens on configuration 4's model)
+constexpr int kFlowMinTokens = 32;
+
 // The kernel of a call of B streams and T tokens in mode (kModeRun, kModeGenerate: ygg_generate, kModeScore: a
-// digest or NLL). Generation: the deep kernel for >= 8 tokens
-// and B <= deep_max_streams, else the per-stream kernel (every token needs all layers of the one before it, so never
-// the layer-pipelined one). Otherwise: the layer-pipelined kernel for T > 1 when its workgroups fit, else the
-// per-stream kernel. Of the two builds of a kernel, the uncapped one while all B streams are resident with it. A
-// kernel forced by YGG_KERNEL takes every call it can run.
+// digest or NLL). Generation: the deep kernel for >= 8 tokens and B <= deep_max_streams, else the per-stream kernel
+// (every token needs all layers of the one before it, so never a layer-pipelined one). Otherwise: the tick-pipelined
+// kernel for T >= kFlowMinTokens when its workgroups fit, the layer-pipelined kernel for T > 1 when its workgroups
+// fit, else the per-stream kernel. Of the two builds of a kernel, the uncapped one while all B streams are resident
+// with it. A kernel forced by YGG_KERNEL takes every call it can run.
 const ygg::Kernel &pick(const ygg_model *m, int B, int T, int mode) {
     const bool gen = mode == kModeGenerate;
     if (m->deep_all) return m->deep;
     if (gen && m->deep && B <= m->deep_max_streams && T >= 8) return m->deep;
+    if (!gen && m->flow && (m->flow_all || (T >= kFlowMinTokens && B <= m->flow_max_streams))) return m->flow;
     if (!gen && m->pipe && (m->pipe_all || (T > 1 && B <= m->pipe_max_streams)))
         return (m->pipe_few && B <= m->pipe_few_max_streams) ? m->pipe_few : m->pipe;
     return (m->run_few && B <= m->run_few_max_streams[mode]) ? m->run_few : m->run;
@@ -673,7 +693,7 @@ int set_error(int code, const char *msg) { return fail(code, "%s", msg); }
 
 extern "C" {
 
-int ygg_version(void) { return 7; }
+int ygg_version(void) { return 8; }
 
 const char *ygg_last_error(void) { return g_err.c_str(); }
 

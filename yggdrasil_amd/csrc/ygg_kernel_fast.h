@@ -59,9 +59,15 @@ template <int N_, int R_, int R2_> struct Shape : Fast<N_> {
 // the per-expert registers of one stream and layer
 template <class SH> struct Gather {
     uint32_t aw[SH::AW], pw[SH::SPW], uw[SH::K4][SH::C];
-    int trow[SH::C];
+    // the table row's C int16 entries of this lane as loaded: packed in pairs (C >= 2) or one sign-extended entry
+    // (C = 1); unpacked where the update reads them, so that nothing waits for the load in between
+    int trw[(SH::C + 1) / 2];
     float mzr;             // group scales: the readout scale of this lane's readout row (m_z of the expert's row)
 };
+template <class SH> __device__ __forceinline__ int table_entry(const Gather<SH> &G, int c) {
+    if constexpr (SH::C == 1) return G.trw[0];
+    else return (c & 1) ? (G.trw[c >> 1] >> 16) : (int)(int16_t)(G.trw[c >> 1] & 0xffff);
+}
 
 // A quad lane's share of an n-byte row: for n = 128 the 16-byte chunks at qk 16 and 64 + qk 16, with LDS rows
 // kLdsRow = 192 bytes apart, so that the 16 quads of a wavefront reading 16 rows hit 64 distinct banks (contiguous
@@ -506,8 +512,12 @@ __device__ __forceinline__ void gather(Gather<SH> &G, const YggDevLayer &y, int 
         }
         const int16_t *tr = y.table + ((uint32_t)r * (uint32_t)y.table_sr + (uint32_t)x * (uint32_t)y.table_sx) +
                             F::C * lane;
+        if constexpr (F::C == 1) {
+            G.trw[0] = tr[0];
+        } else {
 #pragma unroll
-        for (int c = 0; c < F::C; c++) G.trow[c] = tr[c];
+            for (int c = 0; c < F::C / 2; c++) G.trw[c] = (int)((const uint32_t *)tr)[c];
+        }
     }
     G.mzr = y.mz ? y.mz[(uint32_t)r * SH::R + lane / SH::RL] : y.readout_scale;
     const uint8_t *pp = g + y.off_P;
@@ -567,7 +577,7 @@ __device__ __forceinline__ void update(int (&qn)[SH::C], const Gather<SH> &G, co
         a <<= 8;
 #pragma unroll
         for (int i = 0; i < RW; i++) a = dot4(G.aw[c * 2 * RW + RW + i], qv[i], a);
-        acc[c] = wadd((a + (1 << (shift - 1))) >> shift, G.trow[c]);
+        acc[c] = wadd((a + (1 << (shift - 1))) >> shift, table_entry(G, c));
     }
     if (routed) {
         int d[C];
@@ -995,6 +1005,319 @@ void pipe_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
     for (int i = lane; i < N; i += 64) st[i] = qbuf[l][(te + 1) & 1][i];
     if (digest && l == L - 1 && lane == 0) digest[s] = dg;
     if (nll && l == L - 1 && lane == 0) nll[s] += nacc;
+}
+
+
+// ----------------------------------------------------------------------------------------------- flow_kernel
+// Scoring with the tokens known, one stream per workgroup, one wavefront per layer, as a software pipeline over ticks.
+// Of layer l's work on token t only the update is on the layer's own recurrence (q_l(t) needs q_l(t - 1)): the router
+// rounds and the gather need just the layer below at the same token. So a routed layer runs as stages, one per router
+// round and one for the update, a tick apart: a round's row and threshold loads are issued in one tick and consumed in
+// the next, the record a tick before its update, and the ticks are separated by barriers that wait for LDS only, so
+// the global loads of every stage stay in flight across them. A tick then costs the stages' arithmetic, not their
+// chain of memory round trips (pipe_kernel does each layer's whole chain in one tick).
+//
+// Schedule (P router rounds, o_l the tick of layer l's update of token 0): the token layer gathers token t at tick t
+// (two record buffers) and updates it at tick o_0 + t = 2 + t; routed layer l runs round j of token t at tick
+// o_(l-1) + 1 + t + j (round 0 from the LDS rows, its thresholds loaded a tick before) and, in the tick of its last
+// round, first updates the token before it and then issues this token's record, so a record has a whole tick of
+// rounds to arrive; it updates at tick o_l + t, o_l = o_(l-1) + P + 1. States live in a ring per layer (slot (t + 1)
+// mod QR after token t, slot 0 the state before token 0); logits add up layer by layer, in order, in a ring over the
+// tokens in flight.
+//
+// Every stage runs in every tick, on a clamped token and valid tree nodes while the pipeline fills and drains, and
+// only its stores are conditional: the registers carried from tick to tick are then written once per tick in
+// straight-line code, so the loads that fill them are waited for where the next tick reads them and nowhere else.
+// Tokens come through the scalar cache (their wait counter is not the vector loads').
+constexpr int kFlowStates = 8;     // state ring slots per layer (> the rounds)
+template <int L, int P> constexpr int kFlowLogits = (L - 1) * (P + 1) + 1;   // tokens in flight between layers
+constexpr int kFlowToken0 = 2;     // tick of the token layer's update of token 0 (its records issued two ticks ahead)
+
+template <class SH, int L, int P, bool GROUP> struct FlowShared {
+    alignas(16) SharedTables<SH, L> S;
+    alignas(16) GroupTablesOf<SH, L, GROUP> GT;
+    alignas(16) int8_t qring[L][kFlowStates][SH::N];
+    alignas(16) float lgs[kFlowLogits<L, P>][256];
+    alignas(16) unsigned long long dterm[kFlowLogits<L, P>][L];
+    alignas(16) int8_t zlw[L][2][SH::ZL];
+    alignas(16) int8_t zqw[L][SH::ZQ];
+    int stop_t;
+};
+// (not the largest shape: its 32 KiB record per layer and token alone takes 132 VGPRs, and the stages' row shares on
+// top of it spill)
+template <int N, int R, int R2, int L, int P, bool GROUP>
+constexpr bool kFlowFits =
+    L >= 2 && N * R2 < 256 * 64 && sizeof(FlowShared<Shape<N, R, R2>, L, P, GROUP>) <= 160 * 1024;
+
+// a wavefront-uniform 32-bit load through the scalar cache, waited for at once (it leaves the vector loads in flight)
+__device__ __forceinline__ int scalar_load(const int32_t *p) {
+    const unsigned long long a = (unsigned long long)p;
+    const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)a), hi = __builtin_amdgcn_readfirstlane((unsigned)(a >> 32));
+    const int32_t *q = (const int32_t *)(((unsigned long long)hi << 32) | lo);
+    int v;
+    asm volatile("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(q) : "memory");
+    return v;
+}
+
+// the barrier between ticks: LDS writes done and visible, global loads left in flight
+__device__ __forceinline__ void flow_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// one router round from the loaded row shares (quad qj holds node qj's dot product): the node index ix at the round's
+// start (heap numbering) -> at its end
+template <int N>
+__device__ __forceinline__ int round_step(const uint32_t (&wv)[Fast<N>::QW], const uint32_t (&qbw)[Fast<N>::QW],
+                                          float rho, float th, int ix, int h, int lane) {
+    const int qk = lane & 3, qj = lane >> 2, nn = (1 << h) - 1;
+    int dot = 0;
+#pragma unroll
+    for (int i = 0; i < Fast<N>::QW; i++) dot = dot4(wv[i], qbw[i], dot);
+    dot = sum4(dot);
+    const bool right = (float)dot * rho > th;
+    return (ix << h) + (walk_round(lane_mask(right && qk == 0 && qj < nn), h) - nn);
+}
+
+// the update of token t by layer l (its record G arrived during the last ticks), its readout into the logits of token
+// t, and the outputs; the last layer completes the token. It computes whether ok or not (the record is then read in
+// every tick, so no path leaves its loads pending) and stores only for a token of the stream (ok).
+template <class SH, int L, int P, bool SCORE, bool GROUP>
+__device__ __forceinline__ void flow_update(FlowShared<SH, L, P, GROUP> &sh, const YggDevModel &m,
+                                            const YggDevLayer &y, const Gather<SH> &G, const float (&bias)[4],
+                                            int l, int t, bool ok, int r, int s, int T, const YggIO &io,
+                                            unsigned long long &dg, double &nacc, int lane) {
+    using F = SH;
+    constexpr int N = SH::N, QM = kFlowStates - 1, LG = kFlowLogits<L, P>;
+    const int V = m.V, VP = m.VP;
+    t = ok ? t : 0;
+    int8_t *qnew = sh.qring[l][(t + 1) & QM];
+    int qn[F::C];
+    if (lane < F::NL) {
+        const float *mul = nullptr;
+        if constexpr (GROUP)
+            if (l > 0) mul = sh.GT.mul[l - 1];
+        update<SH>(qn, G, sh.qring[l][t & QM], sh.zlw[l][t & 1], y, l > 0, m.shift, lane, mul);
+        if (ok) {
+#pragma unroll
+            for (int c = 0; c < F::C; c++) qnew[F::C * lane + c] = (int8_t)qn[c];
+        }
+    }
+    wave_sync();
+    readout<SH>(sh.zqw[l], G.pw, qnew, GROUP ? G.mzr : y.readout_scale, lane);
+    wave_sync();
+    if (!ok) return;
+    float *lr = sh.lgs[t % LG];
+    if (4 * lane < VP) {
+        float term[4];
+        const float *sq = nullptr;
+        if constexpr (GROUP) sq = sh.GT.sq[l];
+        unembed_terms<SH::R>(term, sh.zqw[l], sh.S.Q[l], y.unembed_scale, lane, sq);
+#pragma unroll
+        for (int u = 0; u < 4; u++) lr[4 * lane + u] = (l == 0 ? bias[u] : lr[4 * lane + u]) + term[u];
+    }
+    if (io.leaves && lane == 0) io.leaves[((size_t)s * T + t) * L + l] = r;
+    if (io.states) {
+        int8_t *so = io.states + (((size_t)s * T + t) * L + l) * N;
+        for (int i = lane; i < N; i += 64) so[i] = qnew[i];
+    }
+    if (SCORE && io.digest) {
+        const unsigned long long f = digest_term<N>(qn, r, l, lane);
+        if (lane == 0) sh.dterm[t % LG][l] = f;
+    }
+    if (l == L - 1) {
+        wave_sync();
+        float lg[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) lg[u] = 4 * lane + u < VP ? lr[4 * lane + u] : 0.0f;
+        if (io.logits) store_logits(io.logits + ((size_t)s * T + t) * V, lg, V, lane);
+        if (SCORE && io.nll) {
+            const int yv = scalar_load(io.targets + (size_t)s * T + t);
+            if (yv >= 0 && yv < V) nacc += token_nll(lg, V, yv, lane);
+            else if (lane == 0) atomicOr(m.err, 2u);
+        }
+        if (SCORE && io.digest) {
+#pragma unroll
+            for (int j = 0; j < L; j++) dg = dg * kDigestMul + sh.dterm[t % LG][j];
+        }
+    }
+}
+
+// MODE: kModeRun (logits, leaves, states) or kModeScore (also the digest and the NLL)
+template <int N, int R, int R2, int L, int P, int MODE, bool GROUP>
+__global__ __launch_bounds__(64 * L) __attribute__((amdgpu_waves_per_eu(1)))
+void flow_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B, int T, int8_t *__restrict__ state,
+                 const YggIO io) {
+    using SH = Shape<N, R, R2>;
+    using F = SH;
+    constexpr int QM = kFlowStates - 1;
+    constexpr bool SCORE = MODE == kModeScore;
+    __shared__ __attribute__((aligned(16))) FlowShared<SH, L, P, GROUP> sh;
+
+    const int tid = threadIdx.x, l = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int qk = lane & 3, qj = lane >> 2;
+    const int s = blockIdx.x;
+    const int V = m.V, VP = m.VP;
+    load_tables<SH, L, 64 * L>(sh.S, m, tid);
+    if constexpr (GROUP) load_group_tables<SH, L, 64 * L>(sh.GT, m, tid);
+    const YggDevLayer &y = m.layers[l];
+    int8_t *st = state + ((size_t)s * L + l) * N;
+    for (int i = lane; i < N; i += 64) sh.qring[l][0][i] = st[i];     // the state before token 0
+    if (lane < SH::ZL) {
+        sh.zlw[l][0][lane] = 0;
+        sh.zlw[l][1][lane] = 0;
+    }
+    if (tid == 0) sh.stop_t = T;
+    float bias[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) bias[u] = 4 * lane + u < VP ? m.output_bias[4 * lane + u] : 0.0f;
+    __syncthreads();
+
+    const int ticks = (kFlowToken0 + (L - 1) * (P + 1) + T + 1) & ~1;      // (even: the token layer runs 2 a loop)
+    const int32_t *tok = tokens + (size_t)s * T;
+    // the token at an index clamped into the stream (stages on tokens outside the stream or the vocabulary still run,
+    // on token 0, and store nothing)
+    auto token_at = [&](int t) { return scalar_load(tok + (t < 0 ? 0 : (t < T ? t : T - 1))); };
+    unsigned long long dg = (SCORE && io.digest && l == L - 1) ? io.digest[s] : 0ull;
+    double nacc = 0.0;
+    Gather<SH> G;
+    // everything loaded so far has arrived: no value from before the ticks is waited for inside them
+    __builtin_amdgcn_s_waitcnt(0);
+
+    if (T > 0 && l == 0) {
+        // ---- the token layer: the record of token k at tick k into buffer k & 1, its update at tick k + 2
+        Gather<SH> G1;
+        int gx0 = 0, gx1 = 0;
+        auto tick = [&](int k, Gather<SH> &Gk, int &gxk) {
+            const int stop = __builtin_amdgcn_readfirstlane(sh.stop_t);
+            const int xn = token_at(k);
+            const int t = k - kFlowToken0;
+            bool ok = t >= 0 && t < T && t < stop;
+            if (ok && (gxk < 0 || gxk >= V)) {
+                if (lane == 0) {
+                    atomicOr(m.err, 1u);
+                    sh.stop_t = t;
+                }
+                ok = false;
+            }
+            flow_update<SH, L, P, SCORE, GROUP>(sh, m, y, Gk, bias, 0, t, ok, gxk, s, T, io, dg, nacc, lane);
+            gxk = xn;
+            const int xg = (xn < 0 || xn >= V) ? 0 : xn;
+            gather<SH>(Gk, y, xg, xg, false, lane);
+            flow_barrier();
+        };
+        for (int k = 0; k < ticks; k += 2) {
+            tick(k, G, gx0);
+            tick(k + 1, G1, gx1);
+        }
+    } else if (T > 0) {
+        // ---- a routed layer: its router plan (round j: rh[j] levels from slot rb[j], subtrees at depth rd[j])
+        int rh[P], rb[P], rd[P];
+        {
+            int base = 1 << m.round_h[0], d0 = m.round_h[0];
+            rh[0] = m.round_h[0];
+            rb[0] = 0;
+            rd[0] = 0;
+#pragma unroll
+            for (int j = 1; j < P; j++) {
+                rh[j] = (m.round_pack >> (4 * j)) & 15;
+                rb[j] = base;
+                rd[j] = d0;
+                base += (1 << d0) << rh[j];
+                d0 += rh[j];
+            }
+        }
+        const int o_prev = kFlowToken0 + (l - 1) * (P + 1);      // tick of the layer below's update of token 0
+        const int nn0 = (1 << rh[0]) - 1;
+        const int8_t *w0 = sh.S.W[l - 1] + (qj < nn0 ? qj : nn0 - 1) * kLdsRow<N>;
+        // carried from tick to tick: each pending round's row shares, threshold, node, rho and token (round j's
+        // inputs, loaded by round j - 1; th[0] the first round's thresholds), the record of the next update and its
+        // leaf
+        uint32_t wv[P][F::QW];
+        float th[P], rhos[P];
+        int ixs[P], xs[P];
+#pragma unroll
+        for (int j = 0; j < P; j++) {
+            th[j] = 0.0f;
+            rhos[j] = 0.0f;
+            ixs[j] = 1 << rd[j];
+            xs[j] = 0;
+#pragma unroll
+            for (int i = 0; i < F::QW; i++) wv[j][i] = 0u;
+        }
+        int gr = 0;
+        for (int k = 0; k < ticks; k++) {
+            const int stop = __builtin_amdgcn_readfirstlane(sh.stop_t);
+            const int t0 = k - o_prev;                            // the token whose first-round thresholds load now
+            const int xr = token_at(t0);
+            // ---- router rounds, the last first (each consumes what the one before it loaded last tick)
+            int lx = 0, lr = 0, lt = 0;
+            float lrho = 0.0f;
+#pragma unroll
+            for (int j = P - 1; j >= 0; j--) {
+                const int t = k - o_prev - 1 - j;
+                uint32_t qbw[F::QW];
+                int ix, x;
+                float rho;
+                if (j == 0) {
+                    x = xs[0];
+                    rho = below_and_rho<N>(qbw, sh.qring[l - 1][(t + 1) & QM], y.rms_eps, lane);
+                    if constexpr (GROUP)
+                        if (y.r2b) rho = group_rho<N>(qbw, sh.GT.r2[l - 1], y.rms_eps);
+                    uint32_t w[F::QW];
+                    quad_share<N>(w, w0, qk);
+                    ix = round_step<N>(w, qbw, rho, th[0], 1, rh[0], lane);
+                } else {
+                    x = xs[j];
+                    rho = rhos[j];
+                    quad_share<N>(qbw, sh.qring[l - 1][(t + 1) & QM], qk);
+                    ix = round_step<N>(wv[j], qbw, rho, th[j], ixs[j], rh[j], lane);
+                }
+                if (j + 1 < P) {
+                    // the next round's row shares and thresholds, for next tick (quads past the round's nodes
+                    // read its last node's row: no extra cache line)
+                    const int jn = j + 1 < P ? j + 1 : P - 1;     // (constant once unrolled)
+                    const int nn = (1 << rh[jn]) - 1;
+                    const int slot = rb[jn] + ((ix - (1 << rd[jn])) << rh[jn]) + (qj < nn ? qj : nn - 1);
+                    quad_share<N>(wv[jn], y.w + (size_t)slot * N, qk);
+                    th[jn] = y.thr[(size_t)x * y.thr_stride + slot];
+                    ixs[jn] = ix;
+                    rhos[jn] = rho;
+                    xs[jn] = x;
+                } else {
+                    lt = t;
+                    lx = x;
+                    lr = ix - m.E;
+                    lrho = rho;
+                }
+            }
+            // ---- the update of token k - o_prev - P - 1 (its record arrived during the rounds), then the record of
+            // the leaf just reached, for next tick, and its layer input
+            {
+                const int t = k - o_prev - P - 1;
+                flow_update<SH, L, P, SCORE, GROUP>(sh, m, y, G, bias, l, t, t >= 0 && t < T && t < stop, gr, s, T, io, dg,
+                                             nacc, lane);
+            }
+            gr = lr;
+            gather<SH>(G, y, lr, lx, true, lane);
+            if (lt >= 0 && lt < T && lt < stop) {
+                uint32_t qbw[F::QW];
+                quad_share<N>(qbw, sh.qring[l - 1][(lt + 1) & QM], qk);
+                layer_input<SH>(sh.zlw[l][lt & 1], sh.S.V[l - 1], sh.S.mv[l - 1], qbw, lrho, lane);
+            }
+            // ---- the first round's thresholds of token t0, for next tick
+            const int x0 = (xr < 0 || xr >= V) ? 0 : xr;
+            th[0] = y.thr[(size_t)x0 * y.thr_stride + (qj < nn0 ? qj : nn0 - 1)];
+            xs[0] = x0;
+            flow_barrier();
+        }
+    }
+    __syncthreads();
+    const int te = T < sh.stop_t ? T : sh.stop_t;                    // tokens processed
+    for (int i = lane; i < N; i += 64) st[i] = sh.qring[l][te & QM][i];
+    if (SCORE && io.digest && l == L - 1 && lane == 0) io.digest[s] = dg;
+    if (SCORE && io.nll && l == L - 1 && lane == 0) io.nll[s] += nacc;
 }
 
 }  // namespace ygg
