@@ -1017,20 +1017,25 @@ void pipe_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
 // the global loads of every stage stay in flight across them. A tick then costs the stages' arithmetic, not their
 // chain of memory round trips (pipe_kernel does each layer's whole chain in one tick).
 //
+// Waves: the token layer has one; a routed layer two, a descent wave (its router rounds, the layer input) and an update
+// wave (the record, the update, the readout), which share a SIMD's issue slots with other layers' waves and so overlap
+// each other's LDS and arithmetic latencies.
+//
 // Schedule (P router rounds, o_l the tick of layer l's update of token 0): the token layer gathers token t at tick t
-// (two record buffers) and updates it at tick o_0 + t = 2 + t; routed layer l runs round j of token t at tick
-// o_(l-1) + 1 + t + j (round 0 from the LDS rows, its thresholds loaded a tick before) and, in the tick of its last
-// round, first updates the token before it and then issues this token's record, so a record has a whole tick of
-// rounds to arrive; it updates at tick o_l + t, o_l = o_(l-1) + P + 1. States live in a ring per layer (slot (t + 1)
-// mod QR after token t, slot 0 the state before token 0); logits add up layer by layer, in order, in a ring over the
-// tokens in flight.
+// (two record buffers) and updates it at tick o_0 + t = 2 + t; routed layer l's descent wave runs round j of token t at
+// tick o_(l-1) + 1 + t + j (round 0 from the LDS rows, its thresholds loaded a tick before) and leaves the leaf and the
+// layer input in LDS after round P - 1; its update wave issues the token's record the tick after and updates it the
+// tick after that (two record buffers: a record has a whole tick to arrive), o_l = o_(l-1) + P + 2. States live in a
+// ring per layer (slot (t + 1) mod QR after token t, slot 0 the state before token 0); logits add up layer by layer,
+// in order, in a ring over the tokens in flight.
 //
 // Every stage runs in every tick, on a clamped token and valid tree nodes while the pipeline fills and drains, and
 // only its stores are conditional: the registers carried from tick to tick are then written once per tick in
 // straight-line code, so the loads that fill them are waited for where the next tick reads them and nowhere else.
 // Tokens come through the scalar cache (their wait counter is not the vector loads').
 constexpr int kFlowStates = 8;     // state ring slots per layer (> the rounds)
-template <int L, int P> constexpr int kFlowLogits = (L - 1) * (P + 1) + 1;   // tokens in flight between layers
+template <int L, int P> constexpr int kFlowLogits = (L - 1) * (P + 2) + 1;   // tokens in flight between layers
+template <int L> constexpr int kFlowWaves = 2 * L - 1;
 constexpr int kFlowToken0 = 2;     // tick of the token layer's update of token 0 (its records issued two ticks ahead)
 
 template <class SH, int L, int P, bool GROUP> struct FlowShared {
@@ -1039,8 +1044,9 @@ template <class SH, int L, int P, bool GROUP> struct FlowShared {
     alignas(16) int8_t qring[L][kFlowStates][SH::N];
     alignas(16) float lgs[kFlowLogits<L, P>][256];
     alignas(16) unsigned long long dterm[kFlowLogits<L, P>][L];
-    alignas(16) int8_t zlw[L][2][SH::ZL];
+    alignas(16) int8_t zlw[L][4][SH::ZL];                 // layer input of token t: [l][t & 3]
     alignas(16) int8_t zqw[L][SH::ZQ];
+    int leafx[L][2][2];                                   // leaf and token of token t: [l][t & 1]
     int stop_t;
 };
 // (not the largest shape: its 32 KiB record per layer and token alone takes 132 VGPRs, and the stages' row shares on
@@ -1098,7 +1104,7 @@ __device__ __forceinline__ void flow_update(FlowShared<SH, L, P, GROUP> &sh, con
         const float *mul = nullptr;
         if constexpr (GROUP)
             if (l > 0) mul = sh.GT.mul[l - 1];
-        update<SH>(qn, G, sh.qring[l][t & QM], sh.zlw[l][t & 1], y, l > 0, m.shift, lane, mul);
+        update<SH>(qn, G, sh.qring[l][t & QM], sh.zlw[l][t & 3], y, l > 0, m.shift, lane, mul);
         if (ok) {
 #pragma unroll
             for (int c = 0; c < F::C; c++) qnew[F::C * lane + c] = (int8_t)qn[c];
@@ -1146,27 +1152,33 @@ __device__ __forceinline__ void flow_update(FlowShared<SH, L, P, GROUP> &sh, con
 
 // MODE: kModeRun (logits, leaves, states) or kModeScore (also the digest and the NLL)
 template <int N, int R, int R2, int L, int P, int MODE, bool GROUP>
-__global__ __launch_bounds__(64 * L) __attribute__((amdgpu_waves_per_eu(1)))
+__global__ __launch_bounds__(64 * kFlowWaves<L>) __attribute__((amdgpu_waves_per_eu(1)))
 void flow_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B, int T, int8_t *__restrict__ state,
                  const YggIO io) {
     using SH = Shape<N, R, R2>;
     using F = SH;
-    constexpr int QM = kFlowStates - 1;
+    constexpr int QM = kFlowStates - 1, NT = 64 * kFlowWaves<L>;
     constexpr bool SCORE = MODE == kModeScore;
     __shared__ __attribute__((aligned(16))) FlowShared<SH, L, P, GROUP> sh;
 
-    const int tid = threadIdx.x, l = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    // wave 0: the token layer; waves 2 l - 1 and 2 l: routed layer l's descent and update waves
+    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int l = (w + 1) >> 1;
+    const bool descent = (w & 1) != 0;
     const int qk = lane & 3, qj = lane >> 2;
     const int s = blockIdx.x;
     const int V = m.V, VP = m.VP;
-    load_tables<SH, L, 64 * L>(sh.S, m, tid);
-    if constexpr (GROUP) load_group_tables<SH, L, 64 * L>(sh.GT, m, tid);
+    load_tables<SH, L, NT>(sh.S, m, tid);
+    if constexpr (GROUP) load_group_tables<SH, L, NT>(sh.GT, m, tid);
     const YggDevLayer &y = m.layers[l];
     int8_t *st = state + ((size_t)s * L + l) * N;
-    for (int i = lane; i < N; i += 64) sh.qring[l][0][i] = st[i];     // the state before token 0
-    if (lane < SH::ZL) {
-        sh.zlw[l][0][lane] = 0;
-        sh.zlw[l][1][lane] = 0;
+    if (!descent) {
+        for (int i = lane; i < N; i += 64) sh.qring[l][0][i] = st[i];     // the state before token 0
+        if (lane < SH::ZL) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) sh.zlw[l][j][lane] = 0;
+        }
+        if (lane < 4) sh.leafx[l][lane >> 1][lane & 1] = 0;
     }
     if (tid == 0) sh.stop_t = T;
     float bias[4];
@@ -1174,45 +1186,68 @@ void flow_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
     for (int u = 0; u < 4; u++) bias[u] = 4 * lane + u < VP ? m.output_bias[4 * lane + u] : 0.0f;
     __syncthreads();
 
-    const int ticks = (kFlowToken0 + (L - 1) * (P + 1) + T + 1) & ~1;      // (even: the token layer runs 2 a loop)
+    const int ticks = (kFlowToken0 + (L - 1) * (P + 2) + T + 1) & ~1;      // (even: some waves run 2 a loop)
+    const int o_prev = kFlowToken0 + (l - 1) * (P + 2);                   // the layer below's update of token 0
     const int32_t *tok = tokens + (size_t)s * T;
     // the token at an index clamped into the stream (stages on tokens outside the stream or the vocabulary still run,
     // on token 0, and store nothing)
     auto token_at = [&](int t) { return scalar_load(tok + (t < 0 ? 0 : (t < T ? t : T - 1))); };
-    unsigned long long dg = (SCORE && io.digest && l == L - 1) ? io.digest[s] : 0ull;
+    unsigned long long dg = (SCORE && io.digest && l == L - 1 && !descent) ? io.digest[s] : 0ull;
     double nacc = 0.0;
-    Gather<SH> G;
     // everything loaded so far has arrived: no value from before the ticks is waited for inside them
     __builtin_amdgcn_s_waitcnt(0);
 
     if (T > 0 && l == 0) {
-        // ---- the token layer: the record of token k at tick k into buffer k & 1, its update at tick k + 2
-        Gather<SH> G1;
+        // ---- the token layer: the record of token k at tick k into buffer k & 1, its update at tick k + 2 (before
+        // that tick's record refills the buffer)
+        Gather<SH> G0, G1;
         int gx0 = 0, gx1 = 0;
-        auto tick = [&](int k, Gather<SH> &Gk, int &gxk) {
+        auto tick = [&](int k, Gather<SH> &G, int &gx) {
             const int stop = __builtin_amdgcn_readfirstlane(sh.stop_t);
             const int xn = token_at(k);
             const int t = k - kFlowToken0;
             bool ok = t >= 0 && t < T && t < stop;
-            if (ok && (gxk < 0 || gxk >= V)) {
+            if (ok && (gx < 0 || gx >= V)) {
                 if (lane == 0) {
                     atomicOr(m.err, 1u);
                     sh.stop_t = t;
                 }
                 ok = false;
             }
-            flow_update<SH, L, P, SCORE, GROUP>(sh, m, y, Gk, bias, 0, t, ok, gxk, s, T, io, dg, nacc, lane);
-            gxk = xn;
+            flow_update<SH, L, P, SCORE, GROUP>(sh, m, y, G, bias, 0, t, ok, gx, s, T, io, dg, nacc, lane);
+            gx = xn;
             const int xg = (xn < 0 || xn >= V) ? 0 : xn;
-            gather<SH>(Gk, y, xg, xg, false, lane);
+            gather<SH>(G, y, xg, xg, false, lane);
             flow_barrier();
         };
         for (int k = 0; k < ticks; k += 2) {
-            tick(k, G, gx0);
+            tick(k, G0, gx0);
             tick(k + 1, G1, gx1);
         }
+    } else if (T > 0 && !descent) {
+        // ---- a routed layer's update wave: at tick k the record of token k - o_prev - P - 1 (its leaf left by the
+        // descent wave last tick) into buffer k & 1, then the update of the token before it from the other buffer
+        const int o_g = o_prev + P + 1;
+        Gather<SH> G0, G1;
+        int gr0 = 0, gr1 = 0;
+        auto tick = [&](int k, Gather<SH> &Gg, int &grg, const Gather<SH> &Gu, int gru) {
+            const int stop = __builtin_amdgcn_readfirstlane(sh.stop_t);
+            const int tg = k - o_g;
+            const int *lx = sh.leafx[l][tg & 1];
+            const int r = __builtin_amdgcn_readfirstlane(lx[0]), x = __builtin_amdgcn_readfirstlane(lx[1]);
+            grg = r;
+            gather<SH>(Gg, y, r, x, true, lane);
+            const int t = tg - 1;
+            flow_update<SH, L, P, SCORE, GROUP>(sh, m, y, Gu, bias, l, t, t >= 0 && t < T && t < stop, gru, s, T, io,
+                                                dg, nacc, lane);
+            flow_barrier();
+        };
+        for (int k = 0; k < ticks; k += 2) {
+            tick(k, G0, gr0, G1, gr1);
+            tick(k + 1, G1, gr1, G0, gr0);
+        }
     } else if (T > 0) {
-        // ---- a routed layer: its router plan (round j: rh[j] levels from slot rb[j], subtrees at depth rd[j])
+        // ---- a descent wave: its router plan (round j: rh[j] levels from slot rb[j], subtrees at depth rd[j])
         int rh[P], rb[P], rd[P];
         {
             int base = 1 << m.round_h[0], d0 = m.round_h[0];
@@ -1228,12 +1263,10 @@ void flow_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
                 d0 += rh[j];
             }
         }
-        const int o_prev = kFlowToken0 + (l - 1) * (P + 1);      // tick of the layer below's update of token 0
         const int nn0 = (1 << rh[0]) - 1;
         const int8_t *w0 = sh.S.W[l - 1] + (qj < nn0 ? qj : nn0 - 1) * kLdsRow<N>;
         // carried from tick to tick: each pending round's row shares, threshold, node, rho and token (round j's
-        // inputs, loaded by round j - 1; th[0] the first round's thresholds), the record of the next update and its
-        // leaf
+        // inputs, loaded by round j - 1; th[0] the first round's thresholds)
         uint32_t wv[P][F::QW];
         float th[P], rhos[P];
         int ixs[P], xs[P];
@@ -1246,7 +1279,6 @@ void flow_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
 #pragma unroll
             for (int i = 0; i < F::QW; i++) wv[j][i] = 0u;
         }
-        int gr = 0;
         for (int k = 0; k < ticks; k++) {
             const int stop = __builtin_amdgcn_readfirstlane(sh.stop_t);
             const int t0 = k - o_prev;                            // the token whose first-round thresholds load now
@@ -1265,9 +1297,9 @@ void flow_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
                     rho = below_and_rho<N>(qbw, sh.qring[l - 1][(t + 1) & QM], y.rms_eps, lane);
                     if constexpr (GROUP)
                         if (y.r2b) rho = group_rho<N>(qbw, sh.GT.r2[l - 1], y.rms_eps);
-                    uint32_t w[F::QW];
-                    quad_share<N>(w, w0, qk);
-                    ix = round_step<N>(w, qbw, rho, th[0], 1, rh[0], lane);
+                    uint32_t wr[F::QW];
+                    quad_share<N>(wr, w0, qk);
+                    ix = round_step<N>(wr, qbw, rho, th[0], 1, rh[0], lane);
                 } else {
                     x = xs[j];
                     rho = rhos[j];
@@ -1292,19 +1324,15 @@ void flow_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
                     lrho = rho;
                 }
             }
-            // ---- the update of token k - o_prev - P - 1 (its record arrived during the rounds), then the record of
-            // the leaf just reached, for next tick, and its layer input
-            {
-                const int t = k - o_prev - P - 1;
-                flow_update<SH, L, P, SCORE, GROUP>(sh, m, y, G, bias, l, t, t >= 0 && t < T && t < stop, gr, s, T, io, dg,
-                                             nacc, lane);
-            }
-            gr = lr;
-            gather<SH>(G, y, lr, lx, true, lane);
+            // ---- the leaf reached and its layer input, for the update wave
             if (lt >= 0 && lt < T && lt < stop) {
+                if (lane == 0) {
+                    sh.leafx[l][lt & 1][0] = lr;
+                    sh.leafx[l][lt & 1][1] = lx;
+                }
                 uint32_t qbw[F::QW];
                 quad_share<N>(qbw, sh.qring[l - 1][(lt + 1) & QM], qk);
-                layer_input<SH>(sh.zlw[l][lt & 1], sh.S.V[l - 1], sh.S.mv[l - 1], qbw, lrho, lane);
+                layer_input<SH>(sh.zlw[l][lt & 3], sh.S.V[l - 1], sh.S.mv[l - 1], qbw, lrho, lane);
             }
             // ---- the first round's thresholds of token t0, for next tick
             const int x0 = (xr < 0 || xr >= V) ? 0 : xr;
@@ -1314,10 +1342,12 @@ void flow_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
         }
     }
     __syncthreads();
-    const int te = T < sh.stop_t ? T : sh.stop_t;                    // tokens processed
-    for (int i = lane; i < N; i += 64) st[i] = sh.qring[l][te & QM][i];
-    if (SCORE && io.digest && l == L - 1 && lane == 0) io.digest[s] = dg;
-    if (SCORE && io.nll && l == L - 1 && lane == 0) io.nll[s] += nacc;
+    if (!descent) {
+        const int te = T < sh.stop_t ? T : sh.stop_t;                // tokens processed
+        for (int i = lane; i < N; i += 64) st[i] = sh.qring[l][te & QM][i];
+        if (SCORE && io.digest && l == L - 1 && lane == 0) io.digest[s] = dg;
+        if (SCORE && io.nll && l == L - 1 && lane == 0) io.nll[s] += nacc;
+    }
 }
 
 }  // namespace ygg

@@ -13,10 +13,10 @@ template <int N, int R, int R2, int L, int P, bool GROUP>
 hipError_t launch_flow(const YggDevModel &m, const int32_t *tokens, int B, int T, int8_t *state, const YggIO &io,
                        hipStream_t stream) {
     if (io_mode(io) == kModeScore)
-        hipLaunchKernelGGL((flow_kernel<N, R, R2, L, P, kModeScore, GROUP>), dim3(B), dim3(64 * L), 0, stream, m,
+        hipLaunchKernelGGL((flow_kernel<N, R, R2, L, P, kModeScore, GROUP>), dim3(B), dim3(64 * kFlowWaves<L>), 0, stream, m,
                            tokens, B, T, state, io);
     else
-        hipLaunchKernelGGL((flow_kernel<N, R, R2, L, P, kModeRun, GROUP>), dim3(B), dim3(64 * L), 0, stream, m,
+        hipLaunchKernelGGL((flow_kernel<N, R, R2, L, P, kModeRun, GROUP>), dim3(B), dim3(64 * kFlowWaves<L>), 0, stream, m,
                            tokens, B, T, state, io);
     return hipGetLastError();
 }
@@ -37,7 +37,7 @@ template <int N, int R, int R2, int L, int P, bool GROUP> int flow_blocks() {
     if constexpr (kFlowBuilt<N, R, R2, L, P, GROUP>) {
         int nb = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                &nb, reinterpret_cast<const void *>(&flow_kernel<N, R, R2, L, P, kModeRun, GROUP>), 64 * L, 0) !=
+                &nb, reinterpret_cast<const void *>(&flow_kernel<N, R, R2, L, P, kModeRun, GROUP>), 64 * kFlowWaves<L>, 0) !=
             hipSuccess)
             return 0;
         return nb;
