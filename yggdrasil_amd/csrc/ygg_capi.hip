@@ -470,7 +470,9 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
         p.gath = plan((size_t)El * p.gl.bytes);
         p.table = y.vt ? Piece{0, 0} : plan(2 * (size_t)n * (routed ? (size_t)E * V : (size_t)V));
         p.Q = plan((size_t)VP * R);
-        p.mz = y.mzl ? plan(4 * (size_t)El * R) : Piece{0, 0};
+        // (models with group scales get the array in every layer, holding the layer's scale where the file has none:
+        // the kernels then read a row scale without a branch)
+        p.mz = (y.mzl || group) ? plan(4 * (size_t)El * R) : Piece{0, 0};
         p.sqv = y.sqv ? plan(4 * (size_t)VP) : Piece{0, 0};
         if (routed) {
             p.w = plan((size_t)slots * n);
@@ -522,6 +524,9 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
             const int W = R == 8 ? 16 : R;
             for (int e = 0; e < El; e++)
                 for (int j = 0; j < R; j++) mz[(size_t)e * R + j] = y.mzl[(size_t)e * W + (R == 8 ? 2 * j : j)];
+        } else if (group) {
+            float *mz = (float *)(H + p.mz.off);
+            for (size_t i = 0; i < (size_t)El * R; i++) mz[i] = y.scal[0];
         }
         if (y.sqv) memcpy(H + p.sqv.off, y.sqv, 4 * (size_t)VP);
         if (routed) {

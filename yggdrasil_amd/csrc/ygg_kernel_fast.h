@@ -490,7 +490,8 @@ __device__ __forceinline__ int descend_deep(const YggDevModel &m, const YggDevLa
 }
 
 // the expert's whole gather record and table row, in one burst
-template <class SH>
+// MZ: the model has group scales (the expert's readout row scales, in every layer)
+template <class SH, bool MZ = false>
 __device__ __forceinline__ void gather(Gather<SH> &G, const YggDevLayer &y, int r, int x, bool routed, int lane) {
     using F = SH;
     // a layer's records and tables lie within 4 GiB (checked at load): 32-bit offsets
@@ -519,7 +520,9 @@ __device__ __forceinline__ void gather(Gather<SH> &G, const YggDevLayer &y, int 
             for (int c = 0; c < F::C / 2; c++) G.trw[c] = (int)((const uint32_t *)tr)[c];
         }
     }
-    G.mzr = y.mz ? y.mz[(uint32_t)r * SH::R + lane / SH::RL] : y.readout_scale;
+    // (a model with group scales has the row scales in every layer; without, the readout scale is the layer's)
+    if constexpr (MZ) G.mzr = y.mz[(uint32_t)r * SH::R + lane / SH::RL];
+    else G.mzr = 0.0f;
     const uint8_t *pp = g + y.off_P;
 #pragma unroll
     for (int gi = 0; gi < F::SP / F::GP; gi++) {
@@ -559,7 +562,8 @@ __device__ __forceinline__ void layer_input(int8_t *zls, const int8_t *V0, const
 // new state rows of this lane: sat8(((A16 q_old + 2^(s-1)) >> s) + T_r[x] + rint(f32(U'_r zl) m_ul))
 // (cpu/ygg.cpp:311-389); qold is the layer's state before the token (LDS). A row is stored as hi and lo signed bytes
 // with A16 = 256 hi + lo, so A16 q = 256 (hi q) + (lo q) exactly, two v_dot4 chains on the raw int8 state.
-template <class SH>
+// MUL: per-coordinate layer-input scales at mul (group scales; LDS), else the layer's one scale
+template <class SH, bool MUL = false>
 __device__ __forceinline__ void update(int (&qn)[SH::C], const Gather<SH> &G, const int8_t *qold,
                                        const int8_t *zls, const YggDevLayer &y, bool routed, int shift, int lane,
                                        const float *mul = nullptr) {
@@ -591,7 +595,7 @@ __device__ __forceinline__ void update(int (&qn)[SH::C], const Gather<SH> &G, co
         }
 #pragma unroll
         for (int c = 0; c < C; c++)
-            acc[c] = wadd(acc[c], cvt_rne((float)d[c] * (mul ? mul[C * lane + c] : y.layer_input_scale)));
+            acc[c] = wadd(acc[c], cvt_rne((float)d[c] * (MUL ? mul[C * lane + c] : y.layer_input_scale)));
     }
 #pragma unroll
     for (int c = 0; c < C; c++) qn[c] = sat8(acc[c]);
@@ -613,8 +617,9 @@ __device__ __forceinline__ void readout(int8_t *zqs, const uint32_t (&pw)[SH::SP
     if (rk == 0) zqs[rj] = (int8_t)clamp127(cvt_rne((float)z * readout_scale));
 }
 
-// f32(Q zq) s_q for the 4 classes of this lane (cpu/ygg.cpp:421-434); Qs the layer's Q planes
-template <int R>
+// f32(Q zq) s_q for the 4 classes of this lane (cpu/ygg.cpp:421-434); Qs the layer's Q planes. SQ: per-class
+// scales at sq (group scales; LDS), else scale
+template <int R, bool SQ = false>
 __device__ __forceinline__ void unembed_terms(float (&term)[4], const int8_t *zqs, const int8_t *Qs, float scale,
                                               int lane, const float *sq = nullptr) {
     constexpr int QC = R / 4, RW = R / 4;              // 16-byte chunks per lane, dwords per class
@@ -633,7 +638,7 @@ __device__ __forceinline__ void unembed_terms(float (&term)[4], const int8_t *zq
         int d = 0;
 #pragma unroll
         for (int i = 0; i < RW; i++) d = dot4(qq[u * RW + i], zw[i], d);
-        term[u] = (float)d * (sq ? sq[4 * lane + u] : scale);
+        term[u] = (float)d * (SQ ? sq[4 * lane + u] : scale);
     }
 }
 
@@ -773,7 +778,7 @@ void fast_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
                     float term[4];
                     const float *sq = nullptr;
                     if constexpr (GROUP) sq = GT.sq[pl];
-                    unembed_terms<R>(term, zqs, S.Q[pl], yp.unembed_scale, lane, sq);
+                    unembed_terms<R, GROUP>(term, zqs, S.Q[pl], yp.unembed_scale, lane, sq);
 #pragma unroll
                     for (int u = 0; u < 4; u++) lg[u] = lg[u] + term[u];
                 }
@@ -813,14 +818,13 @@ void fast_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
                 }
             }
             Gather<SH> G;
-            gather<SH>(G, y, r, x, l > 0, lane);
+            gather<SH, GROUP>(G, y, r, x, l > 0, lane);
             if (l > 0) layer_input<SH>(zls, S.V[l - 1], S.mv[l - 1], qbw, rho, lane);
             wave_sync();
             int qn[F::C];
             const float *mul = nullptr;
-            if constexpr (GROUP)
-                if (l > 0) mul = GT.mul[l - 1];
-            if (lane < F::NL) update<SH>(qn, G, qs + l * N, zls, y, l > 0, m.shift, lane, mul);
+            if constexpr (GROUP) mul = GT.mul[l > 0 ? l - 1 : 0];
+            if (lane < F::NL) update<SH, GROUP>(qn, G, qs + l * N, zls, y, l > 0, m.shift, lane, mul);
             wave_sync();
             if (lane < F::NL) {
 #pragma unroll
@@ -910,7 +914,7 @@ void pipe_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
         const int x0 = __builtin_amdgcn_readfirstlane(tok[0]);
         if (x0 >= 0 && x0 < V) {
             if (l > 0 && qj < nn1) th0 = y.thr[(size_t)x0 * y.thr_stride + qj];
-            if (kAhead && l == 0) gather<SH>(G0, y, x0, x0, false, lane);
+            if (kAhead && l == 0) gather<SH, GROUP>(G0, y, x0, x0, false, lane);
         }
     }
 
@@ -933,27 +937,26 @@ void pipe_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
                     if constexpr (GROUP)
                         if (y.r2b) rho = group_rho<N>(qbw, GT.r2[l - 1], y.rms_eps);
                     r = descend<N>(m, y, S.W[l - 1], th0, qbw, rho, x, lane);
-                    gather<SH>(G, y, r, x, true, lane);
+                    gather<SH, GROUP>(G, y, r, x, true, lane);
                     layer_input<SH>(zlw[l], S.V[l - 1], S.mv[l - 1], qbw, rho, lane);
                 } else if constexpr (kAhead) {
                     G = G0;
                 } else {
-                    gather<SH>(G, y, x, x, false, lane);
+                    gather<SH, GROUP>(G, y, x, x, false, lane);
                 }
                 if (t + 1 < T) {
                     const int xn = __builtin_amdgcn_readfirstlane(tok[t + 1]);
                     if (xn >= 0 && xn < V) {
                         if (l > 0 && qj < nn1) th0 = y.thr[(size_t)xn * y.thr_stride + qj];
-                        if (kAhead && l == 0) gather<SH>(G0, y, xn, xn, false, lane);
+                        if (kAhead && l == 0) gather<SH, GROUP>(G0, y, xn, xn, false, lane);
                     }
                 }
                 wave_sync();
                 int qn[F::C];
                 if (lane < F::NL) {
                     const float *mul = nullptr;
-                    if constexpr (GROUP)
-                        if (l > 0) mul = GT.mul[l - 1];
-                    update<SH>(qn, G, qbuf[l][(t + 1) & 1], zlw[l], y, l > 0, m.shift, lane, mul);
+                    if constexpr (GROUP) mul = GT.mul[l > 0 ? l - 1 : 0];
+                    update<SH, GROUP>(qn, G, qbuf[l][(t + 1) & 1], zlw[l], y, l > 0, m.shift, lane, mul);
 #pragma unroll
                     for (int c = 0; c < F::C; c++) qbuf[l][t & 1][F::C * lane + c] = (int8_t)qn[c];
                 }
@@ -965,7 +968,7 @@ void pipe_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
                     float term[4];
                     const float *sq = nullptr;
                     if constexpr (GROUP) sq = GT.sq[l];
-                    unembed_terms<R>(term, zqw[l], S.Q[l], y.unembed_scale, lane, sq);
+                    unembed_terms<R, GROUP>(term, zqw[l], S.Q[l], y.unembed_scale, lane, sq);
 #pragma unroll
                     for (int u = 0; u < 4; u++) {
                         const float base = l == 0 ? m.output_bias[4 * lane + u] : lr[4 * lane + u];
@@ -1102,9 +1105,8 @@ __device__ __forceinline__ void flow_update(FlowShared<SH, L, P, GROUP> &sh, con
     int qn[F::C];
     if (lane < F::NL) {
         const float *mul = nullptr;
-        if constexpr (GROUP)
-            if (l > 0) mul = sh.GT.mul[l - 1];
-        update<SH>(qn, G, sh.qring[l][t & QM], sh.zlw[l][t & 3], y, l > 0, m.shift, lane, mul);
+        if constexpr (GROUP) mul = sh.GT.mul[l > 0 ? l - 1 : 0];
+        update<SH, GROUP>(qn, G, sh.qring[l][t & QM], sh.zlw[l][t & 3], y, l > 0, m.shift, lane, mul);
         if (ok) {
 #pragma unroll
             for (int c = 0; c < F::C; c++) qnew[F::C * lane + c] = (int8_t)qn[c];
@@ -1119,7 +1121,7 @@ __device__ __forceinline__ void flow_update(FlowShared<SH, L, P, GROUP> &sh, con
         float term[4];
         const float *sq = nullptr;
         if constexpr (GROUP) sq = sh.GT.sq[l];
-        unembed_terms<SH::R>(term, sh.zqw[l], sh.S.Q[l], y.unembed_scale, lane, sq);
+        unembed_terms<SH::R, GROUP>(term, sh.zqw[l], sh.S.Q[l], y.unembed_scale, lane, sq);
 #pragma unroll
         for (int u = 0; u < 4; u++) lr[4 * lane + u] = (l == 0 ? bias[u] : lr[4 * lane + u]) + term[u];
     }
@@ -1217,7 +1219,7 @@ void flow_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
             flow_update<SH, L, P, SCORE, GROUP>(sh, m, y, G, bias, 0, t, ok, gx, s, T, io, dg, nacc, lane);
             gx = xn;
             const int xg = (xn < 0 || xn >= V) ? 0 : xn;
-            gather<SH>(G, y, xg, xg, false, lane);
+            gather<SH, GROUP>(G, y, xg, xg, false, lane);
             flow_barrier();
         };
         for (int k = 0; k < ticks; k += 2) {
@@ -1236,7 +1238,7 @@ void flow_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
             const int *lx = sh.leafx[l][tg & 1];
             const int r = __builtin_amdgcn_readfirstlane(lx[0]), x = __builtin_amdgcn_readfirstlane(lx[1]);
             grg = r;
-            gather<SH>(Gg, y, r, x, true, lane);
+            gather<SH, GROUP>(Gg, y, r, x, true, lane);
             const int t = tg - 1;
             flow_update<SH, L, P, SCORE, GROUP>(sh, m, y, Gu, bias, l, t, t >= 0 && t < T && t < stop, gru, s, T, io,
                                                 dg, nacc, lane);
