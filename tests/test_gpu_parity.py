@@ -115,9 +115,9 @@ def deep_plan(plan) -> bool:
 
 
 def flow_built(info) -> bool:
-    """Models with flow_kernel builds: 2 to 5 layers, router plans of 3 or 4 rounds (depth 9 to 16), not the largest
-    shape."""
-    return info.n_layers > 1 and info.d_state != 256 and info.router_rounds in (3, 4)
+    """Models with flow_kernel builds: 2 to 5 layers (the largest shape 2 to 4), router plans of 3 or 4 rounds (depth 9
+    to 16)."""
+    return info.n_layers > 1 and info.router_rounds in (3, 4) and not (info.d_state == 256 and info.n_layers == 5)
 
 
 def _expect_kernel(model, kernel_env):
@@ -483,6 +483,25 @@ def test_group_scales_capped_builds(hip, model_dir, monkeypatch):
     assert lo > 1 and model.kernel_name(lo - 1, 12) == "ygg::pipe_kernel<128, 8, 16, 4, false, true>"
     _say(f"capped pipe group build from {lo} streams (pipe_max {info.pipe_max_streams})")
     x = synth.zipf_bytes(lo, 12, 6)
+    _compare(_gpu_run(model, x), Oracle(path).run(x, states=True))
+    model.close()
+
+
+@pytest.mark.parametrize("group", [False, True], ids=["tensor", "group"])
+def test_large_shape_flow(hip, model_dir, monkeypatch, group):
+    """The largest shape at 4 layers on flow_kernel, by the default dispatch (its descent waves compute the U'z
+    products and keep V' in registers): leaves, states after every token and logits equal the oracle's."""
+    monkeypatch.delenv("YGG_KERNEL", raising=False)
+    monkeypatch.delenv("YGG_FLOW", raising=False)
+    spec = synth.ModelSpec(256, 16, 10, 27, 4, 32, 64, group=group)
+    path = model_dir / f"large4{'_group' if group else ''}.bin"
+    if not path.exists():
+        synth.write_model(spec, 17, path)
+    model = hip.load(path)
+    name = model.kernel_name(12, 40)
+    _say(f"large shape, 4 layers, {'group' if group else 'tensor'}: {name}")
+    assert name == f"ygg::flow_kernel<256, 32, 64, 4, 3, 0, {'true' if group else 'false'}>", name
+    x = synth.uniform_tokens(spec.vocab, 12, 40, 4)
     _compare(_gpu_run(model, x), Oracle(path).run(x, states=True))
     model.close()
 

@@ -95,11 +95,12 @@ __device__ __forceinline__ void quad_share(uint32_t (&w)[Fast<N>::QW], const int
 // the workgroup's LDS copies of Q (all layers), V' and the first-round router rows (routed layers). Q is held in
 // R / 4 planes of 1 KiB: the 4 R bytes of lane l's classes 4l .. 4l + 3 (class-major) as 16-byte chunks, chunk p at
 // 16 l in plane p (R = 8: classes 4l, 4l + 1 in plane 0, 4l + 2, 4l + 3 in plane 1).
-template <class SH, int L> struct SharedTables {
+// WITHV = false: V' stays out of LDS (its user keeps the rows in registers)
+template <class SH, int L, bool WITHV = true> struct SharedTables {
     static constexpr int LR = L > 1 ? L - 1 : 1;
     int8_t Q[L][256 * SH::R];
     int8_t W[LR][15 * kLdsRow<SH::N>];
-    int8_t V[LR][SH::R2 * kLdsRow<SH::N>];
+    int8_t V[WITHV ? LR : 1][WITHV ? SH::R2 * kLdsRow<SH::N> : 16];
     float mv[LR][SH::R2];
 };
 
@@ -163,13 +164,13 @@ __device__ __forceinline__ void load_group_tables(GroupTables<SH, L> &G, const Y
 
 // Stage the tables with NT threads: every load is issued before the first LDS store, so a launch waits for them
 // once (a load-store loop would wait for each in turn).
-template <class SH, int L, int NT>
-__device__ __forceinline__ void load_tables(SharedTables<SH, L> &S, const YggDevModel &m, int tid) {
+template <class SH, int L, int NT, bool WITHV = true>
+__device__ __forceinline__ void load_tables(SharedTables<SH, L, WITHV> &S, const YggDevModel &m, int tid) {
     // 16-byte chunks: RC per row in memory, SC per row in LDS
     constexpr int N = SH::N, R2 = SH::R2, QC = SH::QC;
     constexpr int RC = N / 16, SC = kLdsRow<N> / 16, LR = L > 1 ? L - 1 : 1;
     constexpr int QK = (16 * SH::R + NT - 1) / NT;     // Q chunks (at most 16 R: VP <= 256) per thread and layer
-    constexpr int VR = 15 + R2;                        // first-round rows and V' rows of a routed layer
+    constexpr int VR = 15 + (WITHV ? R2 : 0);          // first-round rows and V' rows of a routed layer
     constexpr int RK = (VR * RC + NT - 1) / NT;        // their chunks per thread
     static_assert(L == 1 || NT >= R2 * (L - 1), "one thread per m_v entry");
     const int qch = m.VP * SH::R / 16, rows = (1 << m.round_h[0]) - 1;
@@ -213,7 +214,7 @@ __device__ __forceinline__ void load_tables(SharedTables<SH, L> &S, const YggDev
             const int c = tid + k * NT;
             if (c < 15 * RC)
                 ((uint4 *)S.W[l - 1])[(c / RC) * SC + c % RC] = rv[l - 1][k];
-            else if (c < VR * RC)
+            else if (WITHV && c < VR * RC)
                 ((uint4 *)S.V[l - 1])[((c - 15 * RC) / RC) * SC + (c - 15 * RC) % RC] = rv[l - 1][k];
         }
     if (L > 1 && tid < R2 * (L - 1)) S.mv[tid / R2][tid % R2] = mvv;
@@ -490,8 +491,9 @@ __device__ __forceinline__ int descend_deep(const YggDevModel &m, const YggDevLa
 }
 
 // the expert's whole gather record and table row, in one burst
-// MZ: the model has group scales (the expert's readout row scales, in every layer)
-template <class SH, bool MZ = false>
+// MZ: the model has group scales (the expert's readout row scales, in every layer). UW = false: not U' (its user
+// has the layer-input term from elsewhere)
+template <class SH, bool MZ = false, bool UW = true>
 __device__ __forceinline__ void gather(Gather<SH> &G, const YggDevLayer &y, int r, int x, bool routed, int lane) {
     using F = SH;
     // a layer's records and tables lie within 4 GiB (checked at load): 32-bit offsets
@@ -502,7 +504,7 @@ __device__ __forceinline__ void gather(Gather<SH> &G, const YggDevLayer &y, int 
             const uint4 v = *(const uint4 *)(g + (c * F::NL + lane) * 16);
             G.aw[4 * c] = v.x; G.aw[4 * c + 1] = v.y; G.aw[4 * c + 2] = v.z; G.aw[4 * c + 3] = v.w;
         }
-        if (routed) {
+        if (UW && routed) {
 #pragma unroll
             for (int k4 = 0; k4 < F::K4; k4++) {
                 uint32_t tmp[F::C];
@@ -559,14 +561,70 @@ __device__ __forceinline__ void layer_input(int8_t *zls, const int8_t *V0, const
     }
 }
 
+// layer_input with V' in registers: vr[p] the quad share of row 16 p + qj (loaded once by load_vrows)
+template <class SH>
+__device__ __forceinline__ void load_vrows(uint32_t (&vr)[SH::RG][Fast<SH::N>::QW], const YggDevLayer &y, int lane) {
+    constexpr int N = SH::N;
+    const int qk = lane & 3, qj = lane >> 2;
+#pragma unroll
+    for (int p = 0; p < SH::RG; p++) quad_share<N>(vr[p], y.vl + (size_t)(16 * p + qj) * N, qk);
+}
+template <class SH>
+__device__ __forceinline__ void layer_input_regs(int8_t *zls, const uint32_t (&vr)[SH::RG][Fast<SH::N>::QW],
+                                                 const float *mv0, const uint32_t (&qbw)[Fast<SH::N>::QW], float rho,
+                                                 int lane) {
+    using F = Fast<SH::N>;
+    const int qk = lane & 3, qj = lane >> 2;
+#pragma unroll
+    for (int p = 0; p < SH::RG; p++) {
+        const int k = 16 * p + qj;
+        int a = 0;
+#pragma unroll
+        for (int i = 0; i < F::QW; i++) a = dot4(vr[p][i], qbw[i], a);
+        a = sum4(a);
+        if (qk == 0) {
+            float zf = (float)a * mv0[k];
+            zf = zf * rho;
+            zls[k] = (int8_t)clamp127(cvt_rne(zf));
+        }
+    }
+}
+
+// this lane's share of expert r's U' (the layout the gather record holds) and its products with zl
+template <class SH>
+__device__ __forceinline__ void load_uw(uint32_t (&uw)[SH::K4][SH::C], const YggDevLayer &y, int r, int lane) {
+    using F = SH;
+    const uint8_t *g = y.gath + (uint32_t)r * (uint32_t)y.gath_bytes + y.off_U;
+    const int ln = lane < F::NL ? lane : F::NL - 1;
+#pragma unroll
+    for (int k4 = 0; k4 < F::K4; k4++) {
+        uint32_t tmp[F::C];
+        load_words<F::C, 4 * F::C>(tmp, g + ((k4 * F::NL + ln) * F::C) * 4);
+#pragma unroll
+        for (int c = 0; c < F::C; c++) uw[k4][c] = tmp[c];
+    }
+}
+template <class SH>
+__device__ __forceinline__ void uw_products(int (&d)[SH::C], const uint32_t (&uw)[SH::K4][SH::C], const int8_t *zls) {
+#pragma unroll
+    for (int c = 0; c < SH::C; c++) d[c] = 0;
+#pragma unroll
+    for (int k4 = 0; k4 < SH::K4; k4++) {
+        const uint32_t zw = ((const uint32_t *)zls)[k4];
+#pragma unroll
+        for (int c = 0; c < SH::C; c++) d[c] = dot4(uw[k4][c], zw, d[c]);
+    }
+}
+
 // new state rows of this lane: sat8(((A16 q_old + 2^(s-1)) >> s) + T_r[x] + rint(f32(U'_r zl) m_ul))
 // (cpu/ygg.cpp:311-389); qold is the layer's state before the token (LDS). A row is stored as hi and lo signed bytes
 // with A16 = 256 hi + lo, so A16 q = 256 (hi q) + (lo q) exactly, two v_dot4 chains on the raw int8 state.
-// MUL: per-coordinate layer-input scales at mul (group scales; LDS), else the layer's one scale
-template <class SH, bool MUL = false>
+// MUL: per-coordinate layer-input scales at mul (group scales; LDS), else the layer's one scale. PRE: the products
+// U'_r zl of this lane's coordinates come computed, at dpre (LDS), instead of from G.uw and zls
+template <class SH, bool MUL = false, bool PRE = false>
 __device__ __forceinline__ void update(int (&qn)[SH::C], const Gather<SH> &G, const int8_t *qold,
                                        const int8_t *zls, const YggDevLayer &y, bool routed, int shift, int lane,
-                                       const float *mul = nullptr) {
+                                       const float *mul = nullptr, const int *dpre = nullptr) {
     using F = SH;
     constexpr int BLK = F::BLK, C = F::C, RW = BLK / 4;     // dwords of one row's hi (and of its lo) bytes
     const int blk0 = (C * lane / BLK) * BLK;
@@ -585,13 +643,18 @@ __device__ __forceinline__ void update(int (&qn)[SH::C], const Gather<SH> &G, co
     }
     if (routed) {
         int d[C];
+        if constexpr (PRE) {
 #pragma unroll
-        for (int c = 0; c < C; c++) d[c] = 0;
+            for (int c = 0; c < C; c++) d[c] = dpre[C * lane + c];
+        } else {
 #pragma unroll
-        for (int k4 = 0; k4 < F::K4; k4++) {
-            const uint32_t zw = ((const uint32_t *)zls)[k4];
+            for (int c = 0; c < C; c++) d[c] = 0;
 #pragma unroll
-            for (int c = 0; c < C; c++) d[c] = dot4(G.uw[k4][c], zw, d[c]);
+            for (int k4 = 0; k4 < F::K4; k4++) {
+                const uint32_t zw = ((const uint32_t *)zls)[k4];
+#pragma unroll
+                for (int c = 0; c < C; c++) d[c] = dot4(G.uw[k4][c], zw, d[c]);
+            }
         }
 #pragma unroll
         for (int c = 0; c < C; c++)
@@ -1041,10 +1104,17 @@ template <int L, int P> constexpr int kFlowLogits = (L - 1) * (P + 2) + 1;   // 
 template <int L> constexpr int kFlowWaves = 2 * L - 1;
 constexpr int kFlowToken0 = 2;     // tick of the token layer's update of token 0 (its records issued two ticks ahead)
 
+// BIG: the largest shape, whose 32 KiB record does not fit twice in the update wave's registers: its descent wave
+// keeps V' in registers (not LDS) and computes the U'z products itself, handing them over in dring, so the update
+// wave's records hold A16, P and the table row only
+template <class SH> constexpr bool kFlowBig = SH::N * SH::R2 >= 256 * 64;
 template <class SH, int L, int P, bool GROUP> struct FlowShared {
-    alignas(16) SharedTables<SH, L> S;
+    static constexpr bool BIG = kFlowBig<SH>;
+    static constexpr int QR = (BIG && P < 4) ? 4 : kFlowStates;           // state ring slots (> P)
+    alignas(16) SharedTables<SH, L, !BIG> S;
     alignas(16) GroupTablesOf<SH, L, GROUP> GT;
-    alignas(16) int8_t qring[L][kFlowStates][SH::N];
+    alignas(16) int8_t qring[L][QR][SH::N];
+    alignas(16) int dring[BIG ? L : 1][2][BIG ? SH::N : 4];               // U'z of token t: [l][t & 1]
     alignas(16) float lgs[kFlowLogits<L, P>][256];
     alignas(16) unsigned long long dterm[kFlowLogits<L, P>][L];
     alignas(16) int8_t zlw[L][4][SH::ZL];                 // layer input of token t: [l][t & 3]
@@ -1052,11 +1122,12 @@ template <class SH, int L, int P, bool GROUP> struct FlowShared {
     int leafx[L][2][2];                                   // leaf and token of token t: [l][t & 1]
     int stop_t;
 };
-// (not the largest shape: its 32 KiB record per layer and token alone takes 132 VGPRs, and the stages' row shares on
-// top of it spill)
+// (not the largest shape at 5 layers: 9 wavefronts put 3 on a SIMD, at most 168 VGPRs each, and its descent and
+// update waves then spill; 4.8 us/token at batch 1 against pipe_kernel's 4.3, while at 4 layers, 7 wavefronts, it
+// takes 1.9 against 4.0)
 template <int N, int R, int R2, int L, int P, bool GROUP>
-constexpr bool kFlowFits =
-    L >= 2 && N * R2 < 256 * 64 && sizeof(FlowShared<Shape<N, R, R2>, L, P, GROUP>) <= 160 * 1024;
+constexpr bool kFlowFits = L >= 2 && !(kFlowBig<Shape<N, R, R2>> && kFlowWaves<L> > 8) &&
+                           sizeof(FlowShared<Shape<N, R, R2>, L, P, GROUP>) <= 160 * 1024;
 
 // a wavefront-uniform 32-bit load through the scalar cache, waited for at once (it leaves the vector loads in flight)
 __device__ __forceinline__ int scalar_load(const int32_t *p) {
@@ -1098,7 +1169,8 @@ __device__ __forceinline__ void flow_update(FlowShared<SH, L, P, GROUP> &sh, con
                                             int l, int t, bool ok, int r, int s, int T, const YggIO &io,
                                             unsigned long long &dg, double &nacc, int lane) {
     using F = SH;
-    constexpr int N = SH::N, QM = kFlowStates - 1, LG = kFlowLogits<L, P>;
+    using FS = FlowShared<SH, L, P, GROUP>;
+    constexpr int N = SH::N, QM = FS::QR - 1, LG = kFlowLogits<L, P>;
     const int V = m.V, VP = m.VP;
     t = ok ? t : 0;
     int8_t *qnew = sh.qring[l][(t + 1) & QM];
@@ -1106,7 +1178,9 @@ __device__ __forceinline__ void flow_update(FlowShared<SH, L, P, GROUP> &sh, con
     if (lane < F::NL) {
         const float *mul = nullptr;
         if constexpr (GROUP) mul = sh.GT.mul[l > 0 ? l - 1 : 0];
-        update<SH, GROUP>(qn, G, sh.qring[l][t & QM], sh.zlw[l][t & 3], y, l > 0, m.shift, lane, mul);
+        const int *dpre = nullptr;
+        if constexpr (FS::BIG) dpre = sh.dring[l][t & 1];
+        update<SH, GROUP, FS::BIG>(qn, G, sh.qring[l][t & QM], sh.zlw[l][t & 3], y, l > 0, m.shift, lane, mul, dpre);
         if (ok) {
 #pragma unroll
             for (int c = 0; c < F::C; c++) qnew[F::C * lane + c] = (int8_t)qn[c];
@@ -1159,9 +1233,11 @@ void flow_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
                  const YggIO io) {
     using SH = Shape<N, R, R2>;
     using F = SH;
-    constexpr int QM = kFlowStates - 1, NT = 64 * kFlowWaves<L>;
+    using FS = FlowShared<SH, L, P, GROUP>;
+    constexpr bool BIG = FS::BIG;
+    constexpr int QM = FS::QR - 1, NT = 64 * kFlowWaves<L>;
     constexpr bool SCORE = MODE == kModeScore;
-    __shared__ __attribute__((aligned(16))) FlowShared<SH, L, P, GROUP> sh;
+    __shared__ __attribute__((aligned(16))) FS sh;
 
     // wave 0: the token layer; waves 2 l - 1 and 2 l: routed layer l's descent and update waves
     const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
@@ -1170,7 +1246,7 @@ void flow_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
     const int qk = lane & 3, qj = lane >> 2;
     const int s = blockIdx.x;
     const int V = m.V, VP = m.VP;
-    load_tables<SH, L, NT>(sh.S, m, tid);
+    load_tables<SH, L, NT, !BIG>(sh.S, m, tid);
     if constexpr (GROUP) load_group_tables<SH, L, NT>(sh.GT, m, tid);
     const YggDevLayer &y = m.layers[l];
     int8_t *st = state + ((size_t)s * L + l) * N;
@@ -1238,7 +1314,7 @@ void flow_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
             const int *lx = sh.leafx[l][tg & 1];
             const int r = __builtin_amdgcn_readfirstlane(lx[0]), x = __builtin_amdgcn_readfirstlane(lx[1]);
             grg = r;
-            gather<SH, GROUP>(Gg, y, r, x, true, lane);
+            gather<SH, GROUP, !BIG>(Gg, y, r, x, true, lane);
             const int t = tg - 1;
             flow_update<SH, L, P, SCORE, GROUP>(sh, m, y, Gu, bias, l, t, t >= 0 && t < T && t < stop, gru, s, T, io,
                                                 dg, nacc, lane);
@@ -1267,6 +1343,17 @@ void flow_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
         }
         const int nn0 = (1 << rh[0]) - 1;
         const int8_t *w0 = sh.S.W[l - 1] + (qj < nn0 ? qj : nn0 - 1) * kLdsRow<N>;
+        // BIG: V' in registers, and the U' share of the last leaf reached (its products with zl next tick)
+        uint32_t vr[BIG ? SH::RG : 1][F::QW];
+        uint32_t uwp[BIG ? SH::K4 : 1][F::C];
+        if constexpr (BIG) {
+            load_vrows<SH>(vr, y, lane);
+#pragma unroll
+            for (int k4 = 0; k4 < SH::K4; k4++)
+#pragma unroll
+                for (int c = 0; c < F::C; c++) uwp[k4][c] = 0u;
+            __builtin_amdgcn_s_waitcnt(0);
+        }
         // carried from tick to tick: each pending round's row shares, threshold, node, rho and token (round j's
         // inputs, loaded by round j - 1; th[0] the first round's thresholds)
         uint32_t wv[P][F::QW];
@@ -1334,7 +1421,22 @@ void flow_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
                 }
                 uint32_t qbw[F::QW];
                 quad_share<N>(qbw, sh.qring[l - 1][(lt + 1) & QM], qk);
-                layer_input<SH>(sh.zlw[l][lt & 3], sh.S.V[l - 1], sh.S.mv[l - 1], qbw, lrho, lane);
+                if constexpr (BIG)
+                    layer_input_regs<SH>(sh.zlw[l][lt & 3], vr, sh.S.mv[l - 1], qbw, lrho, lane);
+                else
+                    layer_input<SH>(sh.zlw[l][lt & 3], sh.S.V[l - 1], sh.S.mv[l - 1], qbw, lrho, lane);
+            }
+            if constexpr (BIG) {
+                // ---- the U'z products of the leaf before (its U' arrived during this tick), for the update wave's
+                // next tick; then the U' of the leaf just reached
+                const int tu = lt - 1;
+                int d[F::C];
+                uw_products<SH>(d, uwp, sh.zlw[l][tu & 3]);
+                if (tu >= 0 && tu < T && tu < stop && lane < F::NL) {
+#pragma unroll
+                    for (int c = 0; c < F::C; c++) sh.dring[l][tu & 1][F::C * lane + c] = d[c];
+                }
+                load_uw<SH>(uwp, y, lr, lane);
             }
             // ---- the first round's thresholds of token t0, for next tick
             const int x0 = (xr < 0 || xr >= V) ? 0 : xr;
