@@ -115,9 +115,8 @@ def deep_plan(plan) -> bool:
 
 
 def flow_built(info) -> bool:
-    """Models with flow_kernel builds: 2 to 5 layers (the largest shape 2 to 4), router plans of 3 or 4 rounds (depth 9
-    to 16)."""
-    return info.n_layers > 1 and info.router_rounds in (3, 4) and not (info.d_state == 256 and info.n_layers == 5)
+    """Models with flow_kernel builds: 2 to 5 layers, router plans of 3 or 4 rounds (depth 9 to 16)."""
+    return info.n_layers > 1 and info.router_rounds in (3, 4)
 
 
 def _expect_kernel(model, kernel_env):

@@ -1108,26 +1108,30 @@ constexpr int kFlowToken0 = 2;     // tick of the token layer's update of token 
 // keeps V' in registers (not LDS) and computes the U'z products itself, handing them over in dring, so the update
 // wave's records hold A16, P and the table row only
 template <class SH> constexpr bool kFlowBig = SH::N * SH::R2 >= 256 * 64;
+// VREG: V' in the descent wave's registers (BIG, up to 4 layers: 7 wavefronts leave 256 VGPRs a wave; at 5 layers,
+// 9 wavefronts leave 168, and V' stays in LDS)
+template <class SH, int L> constexpr bool kFlowVreg = kFlowBig<SH> && kFlowWaves<L> <= 8;
+// ZQR (BIG at 5 layers, where LDS is short): each layer leaves its zq row of token t in a ring and the last layer's
+// update wave adds every layer's unembedding term, in layer order, instead of the layers adding theirs to a ring of
+// logit rows
 template <class SH, int L, int P, bool GROUP> struct FlowShared {
-    static constexpr bool BIG = kFlowBig<SH>;
+    static constexpr bool BIG = kFlowBig<SH>, VREG = kFlowVreg<SH, L>, ZQR = BIG && !VREG;
     static constexpr int QR = (BIG && P < 4) ? 4 : kFlowStates;           // state ring slots (> P)
-    alignas(16) SharedTables<SH, L, !BIG> S;
+    static constexpr int LG = kFlowLogits<L, P>;
+    alignas(16) SharedTables<SH, L, !VREG> S;
     alignas(16) GroupTablesOf<SH, L, GROUP> GT;
     alignas(16) int8_t qring[L][QR][SH::N];
     alignas(16) int dring[BIG ? L : 1][2][BIG ? SH::N : 4];               // U'z of token t: [l][t & 1]
-    alignas(16) float lgs[kFlowLogits<L, P>][256];
+    alignas(16) float lgs[ZQR ? 1 : LG][256];
+    alignas(16) int8_t zqr[ZQR ? L : 1][ZQR ? LG : 1][SH::ZQ];             // ZQR: zq of layer l, token t
     alignas(16) unsigned long long dterm[kFlowLogits<L, P>][L];
     alignas(16) int8_t zlw[L][4][SH::ZL];                 // layer input of token t: [l][t & 3]
     alignas(16) int8_t zqw[L][SH::ZQ];
     int leafx[L][2][2];                                   // leaf and token of token t: [l][t & 1]
     int stop_t;
 };
-// (not the largest shape at 5 layers: 9 wavefronts put 3 on a SIMD, at most 168 VGPRs each, and its descent and
-// update waves then spill; 4.8 us/token at batch 1 against pipe_kernel's 4.3, while at 4 layers, 7 wavefronts, it
-// takes 1.9 against 4.0)
 template <int N, int R, int R2, int L, int P, bool GROUP>
-constexpr bool kFlowFits = L >= 2 && !(kFlowBig<Shape<N, R, R2>> && kFlowWaves<L> > 8) &&
-                           sizeof(FlowShared<Shape<N, R, R2>, L, P, GROUP>) <= 160 * 1024;
+constexpr bool kFlowFits = L >= 2 && sizeof(FlowShared<Shape<N, R, R2>, L, P, GROUP>) <= 160 * 1024;
 
 // a wavefront-uniform 32-bit load through the scalar cache, waited for at once (it leaves the vector loads in flight)
 __device__ __forceinline__ int scalar_load(const int32_t *p) {
@@ -1160,6 +1164,43 @@ __device__ __forceinline__ int round_step(const uint32_t (&wv)[Fast<N>::QW], con
     return (ix << h) + (walk_round(lane_mask(right && qk == 0 && qj < nn), h) - nn);
 }
 
+// the per-layer outputs of token t (leaf, state, digest term)
+template <class SH, int L, int P, bool SCORE, bool GROUP>
+__device__ __forceinline__ void flow_outputs(FlowShared<SH, L, P, GROUP> &sh, const YggDevModel &m,
+                                             const int (&qn)[SH::C], const int8_t *qnew, int l, int t, int r, int s,
+                                             int T, const YggIO &io, int lane) {
+    constexpr int N = SH::N, LG = kFlowLogits<L, P>;
+    if (io.leaves && lane == 0) io.leaves[((size_t)s * T + t) * L + l] = r;
+    if (io.states) {
+        int8_t *so = io.states + (((size_t)s * T + t) * L + l) * N;
+        for (int i = lane; i < N; i += 64) so[i] = qnew[i];
+    }
+    if (SCORE && io.digest) {
+        const unsigned long long f = digest_term<N>(qn, r, l, lane);
+        if (lane == 0) sh.dterm[t % LG][l] = f;
+    }
+}
+
+// the last layer completes token t: its logits out, the NLL, the digest of every layer's term in layer order
+template <class SH, int L, int P, bool SCORE, bool GROUP>
+__device__ __forceinline__ void flow_finish(FlowShared<SH, L, P, GROUP> &sh, const YggDevModel &m,
+                                            const float (&lg)[4], int t, int s, int T, const YggIO &io,
+                                            unsigned long long &dg, double &nacc, int lane) {
+    constexpr int LG = kFlowLogits<L, P>;
+    const int V = m.V;
+    wave_sync();
+    if (io.logits) store_logits(io.logits + ((size_t)s * T + t) * V, lg, V, lane);
+    if (SCORE && io.nll) {
+        const int yv = scalar_load(io.targets + (size_t)s * T + t);
+        if (yv >= 0 && yv < V) nacc += token_nll(lg, V, yv, lane);
+        else if (lane == 0) atomicOr(m.err, 2u);
+    }
+    if (SCORE && io.digest) {
+#pragma unroll
+        for (int j = 0; j < L; j++) dg = dg * kDigestMul + sh.dterm[t % LG][j];
+    }
+}
+
 // the update of token t by layer l (its record G arrived during the last ticks), its readout into the logits of token
 // t, and the outputs; the last layer completes the token. It computes whether ok or not (the record is then read in
 // every tick, so no path leaves its loads pending) and stores only for a token of the stream (ok).
@@ -1187,9 +1228,35 @@ __device__ __forceinline__ void flow_update(FlowShared<SH, L, P, GROUP> &sh, con
         }
     }
     wave_sync();
-    readout<SH>(sh.zqw[l], G.pw, qnew, GROUP ? G.mzr : y.readout_scale, lane);
+    // (a token outside the stream reads out into the wave's own row, not the ring slot of a token in flight)
+    int8_t *zq = (FS::ZQR && ok) ? sh.zqr[FS::ZQR ? l : 0][FS::ZQR ? t % LG : 0] : sh.zqw[l];
+    readout<SH>(zq, G.pw, qnew, GROUP ? G.mzr : y.readout_scale, lane);
     wave_sync();
     if (!ok) return;
+    if constexpr (FS::ZQR) {
+        flow_outputs<SH, L, P, SCORE, GROUP>(sh, m, qn, qnew, l, t, r, s, T, io, lane);
+        if (l == L - 1) {
+            // the logits of token t: the bias, then every layer's term in layer order
+            float lg[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) lg[u] = bias[u];
+#pragma unroll 1
+            for (int j = 0; j < L; j++) {
+                const YggDevLayer &yj = m.layers[j];
+                float term[4];
+                const float *sq = nullptr;
+                if constexpr (GROUP) sq = sh.GT.sq[j];
+                unembed_terms<SH::R, GROUP>(term, sh.zqr[FS::ZQR ? j : 0][FS::ZQR ? t % LG : 0], sh.S.Q[j],
+                                            yj.unembed_scale, lane, sq);
+#pragma unroll
+                for (int u = 0; u < 4; u++) lg[u] = lg[u] + term[u];
+            }
+#pragma unroll
+            for (int u = 0; u < 4; u++) lg[u] = 4 * lane + u < VP ? lg[u] : 0.0f;
+            flow_finish<SH, L, P, SCORE, GROUP>(sh, m, lg, t, s, T, io, dg, nacc, lane);
+        }
+        return;
+    }
     float *lr = sh.lgs[t % LG];
     if (4 * lane < VP) {
         float term[4];
@@ -1199,30 +1266,13 @@ __device__ __forceinline__ void flow_update(FlowShared<SH, L, P, GROUP> &sh, con
 #pragma unroll
         for (int u = 0; u < 4; u++) lr[4 * lane + u] = (l == 0 ? bias[u] : lr[4 * lane + u]) + term[u];
     }
-    if (io.leaves && lane == 0) io.leaves[((size_t)s * T + t) * L + l] = r;
-    if (io.states) {
-        int8_t *so = io.states + (((size_t)s * T + t) * L + l) * N;
-        for (int i = lane; i < N; i += 64) so[i] = qnew[i];
-    }
-    if (SCORE && io.digest) {
-        const unsigned long long f = digest_term<N>(qn, r, l, lane);
-        if (lane == 0) sh.dterm[t % LG][l] = f;
-    }
+    flow_outputs<SH, L, P, SCORE, GROUP>(sh, m, qn, qnew, l, t, r, s, T, io, lane);
     if (l == L - 1) {
         wave_sync();
         float lg[4];
 #pragma unroll
         for (int u = 0; u < 4; u++) lg[u] = 4 * lane + u < VP ? lr[4 * lane + u] : 0.0f;
-        if (io.logits) store_logits(io.logits + ((size_t)s * T + t) * V, lg, V, lane);
-        if (SCORE && io.nll) {
-            const int yv = scalar_load(io.targets + (size_t)s * T + t);
-            if (yv >= 0 && yv < V) nacc += token_nll(lg, V, yv, lane);
-            else if (lane == 0) atomicOr(m.err, 2u);
-        }
-        if (SCORE && io.digest) {
-#pragma unroll
-            for (int j = 0; j < L; j++) dg = dg * kDigestMul + sh.dterm[t % LG][j];
-        }
+        flow_finish<SH, L, P, SCORE, GROUP>(sh, m, lg, t, s, T, io, dg, nacc, lane);
     }
 }
 
@@ -1234,7 +1284,7 @@ void flow_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
     using SH = Shape<N, R, R2>;
     using F = SH;
     using FS = FlowShared<SH, L, P, GROUP>;
-    constexpr bool BIG = FS::BIG;
+    constexpr bool BIG = FS::BIG, VREG = FS::VREG;
     constexpr int QM = FS::QR - 1, NT = 64 * kFlowWaves<L>;
     constexpr bool SCORE = MODE == kModeScore;
     __shared__ __attribute__((aligned(16))) FS sh;
@@ -1246,7 +1296,7 @@ void flow_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
     const int qk = lane & 3, qj = lane >> 2;
     const int s = blockIdx.x;
     const int V = m.V, VP = m.VP;
-    load_tables<SH, L, NT, !BIG>(sh.S, m, tid);
+    load_tables<SH, L, NT, !VREG>(sh.S, m, tid);
     if constexpr (GROUP) load_group_tables<SH, L, NT>(sh.GT, m, tid);
     const YggDevLayer &y = m.layers[l];
     int8_t *st = state + ((size_t)s * L + l) * N;
@@ -1344,10 +1394,10 @@ void flow_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
         const int nn0 = (1 << rh[0]) - 1;
         const int8_t *w0 = sh.S.W[l - 1] + (qj < nn0 ? qj : nn0 - 1) * kLdsRow<N>;
         // BIG: V' in registers, and the U' share of the last leaf reached (its products with zl next tick)
-        uint32_t vr[BIG ? SH::RG : 1][F::QW];
+        uint32_t vr[VREG ? SH::RG : 1][F::QW];
         uint32_t uwp[BIG ? SH::K4 : 1][F::C];
         if constexpr (BIG) {
-            load_vrows<SH>(vr, y, lane);
+            if constexpr (VREG) load_vrows<SH>(vr, y, lane);
 #pragma unroll
             for (int k4 = 0; k4 < SH::K4; k4++)
 #pragma unroll
@@ -1421,7 +1471,7 @@ void flow_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
                 }
                 uint32_t qbw[F::QW];
                 quad_share<N>(qbw, sh.qring[l - 1][(lt + 1) & QM], qk);
-                if constexpr (BIG)
+                if constexpr (VREG)
                     layer_input_regs<SH>(sh.zlw[l][lt & 3], vr, sh.S.mv[l - 1], qbw, lrho, lane);
                 else
                     layer_input<SH>(sh.zlw[l][lt & 3], sh.S.V[l - 1], sh.S.mv[l - 1], qbw, lrho, lane);
