@@ -516,8 +516,10 @@ REFERENCE_SHAPES = {"small": synth.ModelSpec(64, 16, 10, 27, 5, 8, 16), "medium"
 def test_reference_model_shapes(hip, model_dir, kernel_env, name, group):
     """The reference's trained model shapes on every kernel, with tensor or group scales (the export's "auto" picks
     either): leaves, states after every token and logits equal the oracle's (12 streams x 40 tokens; one launch, and
-    for the per-stream kernels a step loop over the first tokens)."""
+    for the per-stream kernels a step loop over the first tokens); the fused score equals the reference formula on the
+    oracle's logits and the digest of leaves and states the oracle's."""
     import torch
+    from oracle import oracle as O
     spec = dataclasses.replace(REFERENCE_SHAPES[name], group=group)
     path = model_dir / f"refshape_{name}{'_group' if group else ''}.bin"
     if not path.exists():
@@ -534,5 +536,9 @@ def test_reference_model_shapes(hip, model_dir, kernel_env, name, group):
         lg, st = model.step(x[:, t], st)
         np.testing.assert_array_equal(lg.cpu().numpy(), ref["logits"][:, t])
         np.testing.assert_array_equal(st.cpu().numpy(), ref["states"][:, t])
+    bits = model.score(x)
+    np.testing.assert_allclose(bits, O.nll_bits(ref["logits"][:, :-1], x[:, 1:]), rtol=1e-12, atol=1e-9)
+    dg = model.run(x, logits=False, digest=True)["digest"].cpu().numpy().view(np.uint64)
+    np.testing.assert_array_equal(dg, Oracle(path).run(x, logits=False, leaves=False, digest=True)["digest"])
     torch.cuda.synchronize()
     model.close()

@@ -708,15 +708,17 @@ __device__ __forceinline__ void unembed_terms(float (&term)[4], const int8_t *zq
 template <int N>
 __device__ __forceinline__ unsigned long long digest_term(const int (&qn)[Fast<N>::C], int r, int l, int lane) {
     using F = Fast<N>;
-    unsigned long long f = 0;
+    static_assert(N <= 256, "sum (q_i + 1)(2 i + 1) <= 256 N^2 must fit 32 bits");
+    // sum_i (q_i + 1)(2 i + 1) K mod 2^64 = K sum_i (q_i + 1)(2 i + 1) mod 2^64, and the integer sum is exact in 32
+    // bits: the coordinate multiplier K is applied once, after the wavefront sum
+    uint32_t a = 0;
     if (lane < F::NL) {
 #pragma unroll
-        for (int c = 0; c < F::C; c++)
-            f += (unsigned long long)((uint8_t)qn[c] + 1u) * ((unsigned long long)(2 * (F::C * lane + c) + 1) *
-                                                              kDigestCoord);
+        for (int c = 0; c < F::C; c++) a += ((uint8_t)qn[c] + 1u) * (uint32_t)(2 * (F::C * lane + c) + 1);
     }
-    f = wave_sum_u64(f);
-    return (unsigned long long)(uint32_t)r * kDigestLeaf + f + (unsigned long long)l;
+    a = wave_sum_u32(a);
+    return (unsigned long long)(uint32_t)r * kDigestLeaf + (unsigned long long)a * kDigestCoord +
+           (unsigned long long)l;
 }
 
 __device__ __forceinline__ void store_logits(float *o, const float (&lg)[4], int V, int lane) {
@@ -1114,15 +1116,23 @@ template <class SH, int L> constexpr bool kFlowVreg = kFlowBig<SH> && kFlowWaves
 // ZQR (BIG at 5 layers, where LDS is short): each layer leaves its zq row of token t in a ring and the last layer's
 // update wave adds every layer's unembedding term, in layer order, instead of the layers adding theirs to a ring of
 // logit rows
-template <class SH, int L, int P, bool GROUP> struct FlowShared {
+// Score builds of the form with V' in LDS run the NLL on a wavefront of their own (after the layers' waves): its tick
+// loop holds the double-precision exp and log constants, which in an update wave's loop spill beside the record.
+template <class SH, int L, int MODE>
+constexpr bool kFlowNllWave = MODE == kModeScore && kFlowBig<SH> && !kFlowVreg<SH, L>;
+template <class SH, int L, int MODE> constexpr int kFlowThreads = 64 * (kFlowWaves<L> + (kFlowNllWave<SH, L, MODE> ? 1 : 0));
+
+// SC (score builds): with V' in LDS the finished logits of token t wait in lgs[t & 1] for the NLL wave
+template <class SH, int L, int P, bool GROUP, bool SC> struct FlowShared {
     static constexpr bool BIG = kFlowBig<SH>, VREG = kFlowVreg<SH, L>, ZQR = BIG && !VREG;
     static constexpr int QR = (BIG && P < 4) ? 4 : kFlowStates;           // state ring slots (> P)
     static constexpr int LG = kFlowLogits<L, P>;
+    static constexpr int LGS = ZQR ? (SC ? 2 : 1) : LG;                   // logits slots
     alignas(16) SharedTables<SH, L, !VREG> S;
     alignas(16) GroupTablesOf<SH, L, GROUP> GT;
     alignas(16) int8_t qring[L][QR][SH::N];
     alignas(16) int dring[BIG ? L : 1][2][BIG ? SH::N : 4];               // U'z of token t: [l][t & 1]
-    alignas(16) float lgs[ZQR ? 1 : LG][256];
+    alignas(16) float lgs[LGS][256];
     alignas(16) int8_t zqr[ZQR ? L : 1][ZQR ? LG : 1][SH::ZQ];             // ZQR: zq of layer l, token t
     alignas(16) unsigned long long dterm[kFlowLogits<L, P>][L];
     alignas(16) int8_t zlw[L][4][SH::ZL];                 // layer input of token t: [l][t & 3]
@@ -1131,7 +1141,7 @@ template <class SH, int L, int P, bool GROUP> struct FlowShared {
     int stop_t;
 };
 template <int N, int R, int R2, int L, int P, bool GROUP>
-constexpr bool kFlowFits = L >= 2 && sizeof(FlowShared<Shape<N, R, R2>, L, P, GROUP>) <= 160 * 1024;
+constexpr bool kFlowFits = L >= 2 && sizeof(FlowShared<Shape<N, R, R2>, L, P, GROUP, true>) <= 160 * 1024;
 
 // a wavefront-uniform 32-bit load through the scalar cache, waited for at once (it leaves the vector loads in flight)
 __device__ __forceinline__ int scalar_load(const int32_t *p) {
@@ -1166,7 +1176,7 @@ __device__ __forceinline__ int round_step(const uint32_t (&wv)[Fast<N>::QW], con
 
 // the per-layer outputs of token t (leaf, state, digest term)
 template <class SH, int L, int P, bool SCORE, bool GROUP>
-__device__ __forceinline__ void flow_outputs(FlowShared<SH, L, P, GROUP> &sh, const YggDevModel &m,
+__device__ __forceinline__ void flow_outputs(FlowShared<SH, L, P, GROUP, SCORE> &sh, const YggDevModel &m,
                                              const int (&qn)[SH::C], const int8_t *qnew, int l, int t, int r, int s,
                                              int T, const YggIO &io, int lane) {
     constexpr int N = SH::N, LG = kFlowLogits<L, P>;
@@ -1181,16 +1191,19 @@ __device__ __forceinline__ void flow_outputs(FlowShared<SH, L, P, GROUP> &sh, co
     }
 }
 
-// the last layer completes token t: its logits out, the NLL, the digest of every layer's term in layer order
+// the last layer completes token t: its logits out, the NLL (or, with V' in LDS, the logits for the NLL wave), the
+// digest of every layer's term in layer order
 template <class SH, int L, int P, bool SCORE, bool GROUP>
-__device__ __forceinline__ void flow_finish(FlowShared<SH, L, P, GROUP> &sh, const YggDevModel &m,
+__device__ __forceinline__ void flow_finish(FlowShared<SH, L, P, GROUP, SCORE> &sh, const YggDevModel &m,
                                             const float (&lg)[4], int t, int s, int T, const YggIO &io,
                                             unsigned long long &dg, double &nacc, int lane) {
+    using FS = FlowShared<SH, L, P, GROUP, SCORE>;
     constexpr int LG = kFlowLogits<L, P>;
     const int V = m.V;
+    if (SCORE && FS::ZQR && io.nll) *(float4 *)(sh.lgs[t & 1] + 4 * lane) = make_float4(lg[0], lg[1], lg[2], lg[3]);
     wave_sync();
     if (io.logits) store_logits(io.logits + ((size_t)s * T + t) * V, lg, V, lane);
-    if (SCORE && io.nll) {
+    if (SCORE && !FS::ZQR && io.nll) {
         const int yv = scalar_load(io.targets + (size_t)s * T + t);
         if (yv >= 0 && yv < V) nacc += token_nll(lg, V, yv, lane);
         else if (lane == 0) atomicOr(m.err, 2u);
@@ -1205,12 +1218,12 @@ __device__ __forceinline__ void flow_finish(FlowShared<SH, L, P, GROUP> &sh, con
 // t, and the outputs; the last layer completes the token. It computes whether ok or not (the record is then read in
 // every tick, so no path leaves its loads pending) and stores only for a token of the stream (ok).
 template <class SH, int L, int P, bool SCORE, bool GROUP>
-__device__ __forceinline__ void flow_update(FlowShared<SH, L, P, GROUP> &sh, const YggDevModel &m,
+__device__ __forceinline__ void flow_update(FlowShared<SH, L, P, GROUP, SCORE> &sh, const YggDevModel &m,
                                             const YggDevLayer &y, const Gather<SH> &G, const float (&bias)[4],
                                             int l, int t, bool ok, int r, int s, int T, const YggIO &io,
                                             unsigned long long &dg, double &nacc, int lane) {
     using F = SH;
-    using FS = FlowShared<SH, L, P, GROUP>;
+    using FS = FlowShared<SH, L, P, GROUP, SCORE>;
     constexpr int N = SH::N, QM = FS::QR - 1, LG = kFlowLogits<L, P>;
     const int V = m.V, VP = m.VP;
     t = ok ? t : 0;
@@ -1276,22 +1289,38 @@ __device__ __forceinline__ void flow_update(FlowShared<SH, L, P, GROUP> &sh, con
     }
 }
 
+// the NLL of token t, whose logits the last layer left in lgs[t & 1] last tick (the NLL wave)
+template <class SH, int L, int P, bool GROUP>
+__device__ __forceinline__ void flow_nll(FlowShared<SH, L, P, GROUP, true> &sh, const YggDevModel &m, int t, int s,
+                                         int T, const YggIO &io, double &nacc, int lane) {
+    const int V = m.V, VP = m.VP;
+    const float *lr = sh.lgs[t & 1];
+    float lg[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) lg[u] = 4 * lane + u < VP ? lr[4 * lane + u] : 0.0f;
+    const int yv = scalar_load(io.targets + (size_t)s * T + t);
+    if (yv >= 0 && yv < V) nacc += token_nll(lg, V, yv, lane);
+    else if (lane == 0) atomicOr(m.err, 2u);
+}
+
 // MODE: kModeRun (logits, leaves, states) or kModeScore (also the digest and the NLL)
 template <int N, int R, int R2, int L, int P, int MODE, bool GROUP>
-__global__ __launch_bounds__(64 * kFlowWaves<L>) __attribute__((amdgpu_waves_per_eu(1)))
+__global__ __launch_bounds__((kFlowThreads<Shape<N, R, R2>, L, MODE>)) __attribute__((amdgpu_waves_per_eu(1)))
 void flow_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B, int T, int8_t *__restrict__ state,
                  const YggIO io) {
     using SH = Shape<N, R, R2>;
     using F = SH;
-    using FS = FlowShared<SH, L, P, GROUP>;
+    constexpr bool SCORE = MODE == kModeScore, NLLW = kFlowNllWave<SH, L, MODE>;
+    using FS = FlowShared<SH, L, P, GROUP, SCORE>;
     constexpr bool BIG = FS::BIG, VREG = FS::VREG;
-    constexpr int QM = FS::QR - 1, NT = 64 * kFlowWaves<L>;
-    constexpr bool SCORE = MODE == kModeScore;
+    constexpr int QM = FS::QR - 1, NT = kFlowThreads<SH, L, MODE>;
     __shared__ __attribute__((aligned(16))) FS sh;
 
-    // wave 0: the token layer; waves 2 l - 1 and 2 l: routed layer l's descent and update waves
+    // wave 0: the token layer; waves 2 l - 1 and 2 l: routed layer l's descent and update waves; NLLW: wave 2 L - 1
+    // the NLL (set up as no layer's: descent set, layer 0)
     const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
-    const int l = (w + 1) >> 1;
+    const bool nllw = NLLW && w == 2 * L - 1;
+    const int l = nllw ? 0 : (w + 1) >> 1;
     const bool descent = (w & 1) != 0;
     const int qk = lane & 3, qj = lane >> 2;
     const int s = blockIdx.x;
@@ -1314,7 +1343,8 @@ void flow_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
     for (int u = 0; u < 4; u++) bias[u] = 4 * lane + u < VP ? m.output_bias[4 * lane + u] : 0.0f;
     __syncthreads();
 
-    const int ticks = (kFlowToken0 + (L - 1) * (P + 2) + T + 1) & ~1;      // (even: some waves run 2 a loop)
+    // (even: some waves run 2 a loop; NLLW: one tick more, for the NLL of the last token)
+    const int ticks = (kFlowToken0 + (L - 1) * (P + 2) + T + 1 + (NLLW ? 1 : 0)) & ~1;
     const int o_prev = kFlowToken0 + (l - 1) * (P + 2);                   // the layer below's update of token 0
     const int32_t *tok = tokens + (size_t)s * T;
     // the token at an index clamped into the stream (stages on tokens outside the stream or the vocabulary still run,
@@ -1325,7 +1355,18 @@ void flow_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
     // everything loaded so far has arrived: no value from before the ticks is waited for inside them
     __builtin_amdgcn_s_waitcnt(0);
 
-    if (T > 0 && l == 0) {
+    if (T > 0 && nllw) {
+        // ---- the NLL wave: at tick k the NLL of the token the last layer completed at tick k - 1 (tokens from the
+        // stop on were not completed: the stop only moves to a token the last layer has not reached)
+        if constexpr (NLLW) {
+            for (int k = 0; k < ticks; k++) {
+                const int stop = __builtin_amdgcn_readfirstlane(sh.stop_t);
+                const int tn = k - 1 - kFlowToken0 - (L - 1) * (P + 2);
+                if (io.nll && tn >= 0 && tn < T && tn < stop) flow_nll<SH, L, P, GROUP>(sh, m, tn, s, T, io, nacc, lane);
+                flow_barrier();
+            }
+        }
+    } else if (T > 0 && l == 0) {
         // ---- the token layer: the record of token k at tick k into buffer k & 1, its update at tick k + 2 (before
         // that tick's record refills the buffer)
         Gather<SH> G0, G1;
@@ -1500,8 +1541,9 @@ void flow_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
         const int te = T < sh.stop_t ? T : sh.stop_t;                // tokens processed
         for (int i = lane; i < N; i += 64) st[i] = sh.qring[l][te & QM][i];
         if (SCORE && io.digest && l == L - 1 && lane == 0) io.digest[s] = dg;
-        if (SCORE && io.nll && l == L - 1 && lane == 0) io.nll[s] += nacc;
+        if (SCORE && !NLLW && io.nll && l == L - 1 && lane == 0) io.nll[s] += nacc;
     }
+    if (nllw && io.nll && lane == 0) io.nll[s] += nacc;
 }
 
 }  // namespace ygg

@@ -12,12 +12,13 @@ template <int N> constexpr bool kGroupOk = N != 96;          // group scales nee
 template <int N, int R, int R2, int L, int P, bool GROUP>
 hipError_t launch_flow(const YggDevModel &m, const int32_t *tokens, int B, int T, int8_t *state, const YggIO &io,
                        hipStream_t stream) {
+    using SH = Shape<N, R, R2>;
     if (io_mode(io) == kModeScore)
-        hipLaunchKernelGGL((flow_kernel<N, R, R2, L, P, kModeScore, GROUP>), dim3(B), dim3(64 * kFlowWaves<L>), 0, stream, m,
-                           tokens, B, T, state, io);
+        hipLaunchKernelGGL((flow_kernel<N, R, R2, L, P, kModeScore, GROUP>), dim3(B),
+                           dim3(kFlowThreads<SH, L, kModeScore>), 0, stream, m, tokens, B, T, state, io);
     else
-        hipLaunchKernelGGL((flow_kernel<N, R, R2, L, P, kModeRun, GROUP>), dim3(B), dim3(64 * kFlowWaves<L>), 0, stream, m,
-                           tokens, B, T, state, io);
+        hipLaunchKernelGGL((flow_kernel<N, R, R2, L, P, kModeRun, GROUP>), dim3(B), dim3(kFlowThreads<SH, L, kModeRun>),
+                           0, stream, m, tokens, B, T, state, io);
     return hipGetLastError();
 }
 
@@ -37,7 +38,8 @@ template <int N, int R, int R2, int L, int P, bool GROUP> int flow_blocks() {
     if constexpr (kFlowBuilt<N, R, R2, L, P, GROUP>) {
         int nb = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                &nb, reinterpret_cast<const void *>(&flow_kernel<N, R, R2, L, P, kModeRun, GROUP>), 64 * kFlowWaves<L>, 0) !=
+                &nb, reinterpret_cast<const void *>(&flow_kernel<N, R, R2, L, P, kModeRun, GROUP>),
+                kFlowThreads<Shape<N, R, R2>, L, kModeRun>, 0) !=
             hipSuccess)
             return 0;
         return nb;
