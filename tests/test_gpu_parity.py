@@ -147,7 +147,8 @@ def _expect_kernel(model, kernel_env):
         descent = "true" if kernel_env == "deep" and deep else "false"
         assert name.endswith(f", 0, {descent}, false, {group}>"), name
     if kernel_env == "pipe":
-        assert name.endswith(f", false, {group}>"), name
+        assert name.endswith(f", 0, false, {group}>"), name
+        assert model.kernel_name(8, 64, score=True).endswith(f", 2, false, {group}>")
 
 
 def test_config1_full_stream(hip, c12, kernel_env):
@@ -416,9 +417,9 @@ def test_default_dispatch(hip, model_dir, monkeypatch):
     assert model.kernel_name(1, 64) == flow.format(0)
     assert model.kernel_name(1, 64, score=True) == flow.format(2)
     assert model.kernel_name(info.flow_max_streams, 32) == flow.format(0)
-    assert model.kernel_name(1, 31) == "ygg::pipe_kernel<128, 8, 16, 4, false, false>"
-    assert model.kernel_name(info.flow_max_streams + 1, 64) == "ygg::pipe_kernel<128, 8, 16, 4, true, false>" or \
-        model.kernel_name(info.flow_max_streams + 1, 64) == "ygg::pipe_kernel<128, 8, 16, 4, false, false>"
+    assert model.kernel_name(1, 31) == "ygg::pipe_kernel<128, 8, 16, 4, 0, false, false>"
+    assert model.kernel_name(info.flow_max_streams + 1, 64) == "ygg::pipe_kernel<128, 8, 16, 4, 0, true, false>" or \
+        model.kernel_name(info.flow_max_streams + 1, 64) == "ygg::pipe_kernel<128, 8, 16, 4, 0, false, false>"
     assert model.kernel_name(1, 1) == fast.format(0, "false")
     assert model.kernel_name(1, 1, score=True) == fast.format(2, "false")
     assert model.kernel_name(info.pipe_max_streams + 1, 64) == fast.format(0, "false")
@@ -430,38 +431,45 @@ def test_default_dispatch(hip, model_dir, monkeypatch):
     assert model.kernel_name(16384, 100, generate=True) == fast.format(1, "true")
     from yggdrasil_amd import _lib
     assert _lib.lib().ygg_kernel_name(model._h, 1, 1, 3, ctypes.create_string_buffer(128), 128) == 5   # bad mode
-    # the smallest batch that runs on the capped pipe build
-    lo, hi = 1, info.pipe_max_streams
-    assert model.kernel_name(hi, 16) == "ygg::pipe_kernel<128, 8, 16, 4, true, false>"
-    while lo < hi:
-        mid = (lo + hi) // 2
-        if model.kernel_name(mid, 16) == "ygg::pipe_kernel<128, 8, 16, 4, true, false>":
-            hi = mid
-        else:
-            lo = mid + 1
-    assert lo > 1 and model.kernel_name(lo - 1, 16) == "ygg::pipe_kernel<128, 8, 16, 4, false, false>"
-    _say(f"capped pipe build from {lo} streams (pipe_max {info.pipe_max_streams})")
-    x = synth.zipf_bytes(lo, 12, 9)
-    _compare(_gpu_run(model, x), Oracle(path).run(x, states=True))
+    # the capped pipe build: run calls take it only if the uncapped run build keeps fewer streams resident (without
+    # the NLL's registers it may keep as many); score calls from the smallest batch the uncapped score build cannot
+    assert model.kernel_name(info.pipe_max_streams, 16) in ("ygg::pipe_kernel<128, 8, 16, 4, 0, true, false>",
+                                                            "ygg::pipe_kernel<128, 8, 16, 4, 0, false, false>")
+    _check_capped_pipe_score(model, path, "ygg::pipe_kernel<128, 8, 16, 4, 2, {}, false>", info.pipe_max_streams, 9)
     model.close()
 
 
-def _smallest_batch(model, T, name, hi):
+def _smallest_batch(model, T, name, hi, score=False):
     """The smallest stream count (<= hi, which runs on the kernel named) whose calls of T tokens run on it."""
     lo = 1
-    assert model.kernel_name(hi, T) == name, model.kernel_name(hi, T)
+    assert model.kernel_name(hi, T, score=score) == name, model.kernel_name(hi, T, score=score)
     while lo < hi:
         mid = (lo + hi) // 2
-        if model.kernel_name(mid, T) == name:
+        if model.kernel_name(mid, T, score=score) == name:
             hi = mid
         else:
             lo = mid + 1
     return lo
 
 
+def _check_capped_pipe_score(model, path, name, hi, seed):
+    """Score calls of 11 tokens on the capped pipe build (name: '{}' for the cap), from the smallest batch that takes
+    it: the fused NLL against the reference formula on the oracle's logits, and the digest of leaves and states."""
+    from oracle import oracle as O
+    lo = _smallest_batch(model, 11, name.format("true"), hi, score=True)
+    assert lo > 1 and model.kernel_name(lo - 1, 11, score=True) == name.format("false")
+    _say(f"capped pipe score build from {lo} streams (pipe_max {hi})")
+    x = synth.zipf_bytes(lo, 12, seed)
+    ref = Oracle(path).run(x[:, :-1], digest=True)
+    np.testing.assert_allclose(model.score(x), O.nll_bits(ref["logits"], x[:, 1:]), rtol=1e-12, atol=1e-9)
+    dg = model.run(x[:, :-1], logits=False, digest=True)["digest"].cpu().numpy().view(np.uint64)
+    np.testing.assert_array_equal(dg, ref["digest"])
+
+
 def test_group_scales_capped_builds(hip, model_dir, monkeypatch):
     """A group-scale model on the capped builds, which only calls with more streams than the uncapped builds keep
-    resident reach: the per-stream kernel (4 tokens per stream) and the layer-pipelined kernel (12 tokens)."""
+    resident reach: the per-stream kernel (4 tokens per stream) and the layer-pipelined kernel (score calls of 11
+    tokens)."""
     monkeypatch.delenv("YGG_KERNEL", raising=False)
     monkeypatch.delenv("YGG_DEEP", raising=False)
     path = model_dir / "c4small_group.bin"
@@ -477,12 +485,7 @@ def test_group_scales_capped_builds(hip, model_dir, monkeypatch):
     _say(f"capped per-stream group build from {lo} streams")
     x = synth.zipf_bytes(lo, 4, 5)
     _compare(_gpu_run(model, x), Oracle(path).run(x, states=True))
-    pipe_capped = "ygg::pipe_kernel<128, 8, 16, 4, true, true>"
-    lo = _smallest_batch(model, 12, pipe_capped, info.pipe_max_streams)
-    assert lo > 1 and model.kernel_name(lo - 1, 12) == "ygg::pipe_kernel<128, 8, 16, 4, false, true>"
-    _say(f"capped pipe group build from {lo} streams (pipe_max {info.pipe_max_streams})")
-    x = synth.zipf_bytes(lo, 12, 6)
-    _compare(_gpu_run(model, x), Oracle(path).run(x, states=True))
+    _check_capped_pipe_score(model, path, "ygg::pipe_kernel<128, 8, 16, 4, 2, {}, true>", info.pipe_max_streams, 6)
     model.close()
 
 

@@ -355,8 +355,8 @@ struct ygg_model {
     ygg::Kernel run_few;              // fast_kernel without the VGPR cap: B <= run_few_max_streams[mode]
     int run_few_max_streams[3] = {0, 0, 0};
     ygg::Kernel pipe;                 // layer-pipelined, 128-VGPR cap: T > 1 and B <= pipe_max_streams
-    ygg::Kernel pipe_few;             // the same without the cap: B <= pipe_few_max_streams
-    int pipe_max_streams = 0, pipe_few_max_streams = 0;
+    ygg::Kernel pipe_few;             // the same without the cap: B <= pipe_few_max_streams[mode]
+    int pipe_max_streams = 0, pipe_few_max_streams[3] = {0, 0, 0};
     bool pipe_all = false;            // YGG_KERNEL=pipe: every call
     ygg::Kernel deep;                 // deep descent: generate with B <= deep_max_streams
     int deep_max_streams = 0;
@@ -578,8 +578,11 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     m->pipe_few = pipe_few;
     m->pipe_all = pipe && kmode == "pipe";
     m->pipe_max_streams =
-        pipe ? (m->pipe_all ? INT32_MAX : ygg::pipe_blocks_per_cu(n, R, R2f, L, true, group) * cus) : 0;
-    m->pipe_few_max_streams = pipe_few ? ygg::pipe_blocks_per_cu(n, R, R2f, L, false, group) * cus : 0;
+        pipe ? (m->pipe_all ? INT32_MAX : ygg::pipe_blocks_per_cu(n, R, R2f, L, true, group, kModeRun) * cus) : 0;
+    // (the uncapped builds per mode: the run build, without the NLL's registers, may keep as many resident as the
+    // capped one)
+    for (int md : {kModeRun, kModeScore})
+        m->pipe_few_max_streams[md] = pipe_few ? ygg::pipe_blocks_per_cu(n, R, R2f, L, false, group, md) * cus : 0;
     // generation with one stream per workgroup while the streams do not outnumber the CUs (for more, the 4 streams
     // per workgroup of fast_kernel win); YGG_KERNEL=deep takes it for every call
     m->deep = deepk;
@@ -672,7 +675,7 @@ const ygg::Kernel &pick(const ygg_model *m, int B, int T, int mode) {
     if (gen && m->deep && B <= m->deep_max_streams && T >= 8) return m->deep;
     if (!gen && m->flow && (m->flow_all || (T >= kFlowMinTokens && B <= m->flow_max_streams))) return m->flow;
     if (!gen && m->pipe && (m->pipe_all || (T > 1 && B <= m->pipe_max_streams)))
-        return (m->pipe_few && B <= m->pipe_few_max_streams) ? m->pipe_few : m->pipe;
+        return (m->pipe_few && B <= m->pipe_few_max_streams[mode]) ? m->pipe_few : m->pipe;
     return (m->run_few && B <= m->run_few_max_streams[mode]) ? m->run_few : m->run;
 }
 

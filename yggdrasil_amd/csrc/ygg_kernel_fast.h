@@ -930,17 +930,20 @@ void fast_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
 
 // CAP: at most 128 VGPRs (4 wavefronts per SIMD: more streams resident, some registers spilled), else as many as
 // the kernel needs (no spills: faster for few streams)
-template <int N, int R, int R2, int L, bool CAP, bool GROUP>
+// MODE: kModeRun (logits, leaves, states) or kModeScore (also the digest and the NLL, whose constants the run build
+// does without: its capped builds then fit 128 VGPRs without spills)
+template <int N, int R, int R2, int L, int MODE, bool CAP, bool GROUP>
 __global__ __launch_bounds__(64 * L) __attribute__((amdgpu_waves_per_eu(CAP ? 4 : 1)))
 void pipe_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B, int T, int8_t *__restrict__ state,
                  const YggIO io) {
     // generation needs every layer of a token before the next one; the dispatcher never sends it here
+    constexpr bool SCORE = MODE == kModeScore;
     float *__restrict__ logits = io.logits;
     int32_t *__restrict__ leaves = io.leaves;
     int8_t *__restrict__ states = io.states;
-    unsigned long long *__restrict__ digest = io.digest;
+    unsigned long long *__restrict__ digest = SCORE ? io.digest : nullptr;
     const int32_t *__restrict__ targets = io.targets;
-    double *__restrict__ nll = io.nll;
+    double *__restrict__ nll = SCORE ? io.nll : nullptr;
     using SH = Shape<N, R, R2>;
     using F = SH;
     __shared__ __attribute__((aligned(16))) SharedTables<SH, L> S;

@@ -42,8 +42,12 @@ hipError_t launch_deep(const YggDevModel &m, const int32_t *tokens, int B, int T
 template <int N, int R, int R2, int L, bool CAP, bool GROUP>
 hipError_t launch_pipe(const YggDevModel &m, const int32_t *tokens, int B, int T, int8_t *state, const YggIO &io,
                        hipStream_t stream) {
-    hipLaunchKernelGGL((pipe_kernel<N, R, R2, L, CAP, GROUP>), dim3(B), dim3(64 * L), 0, stream, m, tokens, B, T,
-                       state, io);
+    if (io_mode(io) == kModeScore)
+        hipLaunchKernelGGL((pipe_kernel<N, R, R2, L, kModeScore, CAP, GROUP>), dim3(B), dim3(64 * L), 0, stream, m,
+                           tokens, B, T, state, io);
+    else
+        hipLaunchKernelGGL((pipe_kernel<N, R, R2, L, kModeRun, CAP, GROUP>), dim3(B), dim3(64 * L), 0, stream, m,
+                           tokens, B, T, state, io);
     return hipGetLastError();
 }
 
@@ -53,21 +57,22 @@ template <int N, int R, int R2, int L, bool CAP, bool GROUP> Kernel pipe_k() {
     } else if constexpr (CAP && !kHasCap<N, R, R2>) {
         return pipe_k<N, R, R2, L, false, GROUP>();
     } else {
-        return make_kernel(launch_pipe<N, R, R2, L, CAP, GROUP>, "ygg::pipe_kernel<%d, %d, %d, %d, %s, %s>", N, R, R2,
-                           L, CAP ? "true" : "false", GROUP ? "true" : "false");
+        return modal(make_kernel(launch_pipe<N, R, R2, L, CAP, GROUP>, "ygg::pipe_kernel<%d, %d, %d, %d, %%s, %s, %s>",
+                                 N, R, R2, L, CAP ? "true" : "false", GROUP ? "true" : "false"));
     }
 }
 
-template <int N, int R, int R2, int L, bool CAP, bool GROUP> int pipe_blocks() {
+template <int N, int R, int R2, int L, bool CAP, bool GROUP> int pipe_blocks(int mode) {
     if constexpr (GROUP && !kGroupOk<N>) {
         return 0;
     } else if constexpr (CAP && !kHasCap<N, R, R2>) {
-        return pipe_blocks<N, R, R2, L, false, GROUP>();
+        return pipe_blocks<N, R, R2, L, false, GROUP>(mode);
     } else {
         int nb = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                &nb, reinterpret_cast<const void *>(&pipe_kernel<N, R, R2, L, CAP, GROUP>), 64 * L, 0) != hipSuccess)
-            return 0;
+        const void *f = mode == kModeScore
+                            ? reinterpret_cast<const void *>(&pipe_kernel<N, R, R2, L, kModeScore, CAP, GROUP>)
+                            : reinterpret_cast<const void *>(&pipe_kernel<N, R, R2, L, kModeRun, CAP, GROUP>);
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, f, 64 * L, 0) != hipSuccess) return 0;
         return nb;
     }
 }
@@ -93,15 +98,15 @@ template <int N, int R, int R2, bool CAP, bool GROUP> Kernel pipe_for(int L) {
     return Kernel();
 }
 
-template <int N, int R, int R2, bool CAP, bool GROUP> int pipe_occ(int L) {
+template <int N, int R, int R2, bool CAP, bool GROUP> int pipe_occ(int L, int mode) {
     if (L == 1) {
-        if constexpr (R == 8) return pipe_blocks<N, R, R2, 1, CAP, GROUP>();
+        if constexpr (R == 8) return pipe_blocks<N, R, R2, 1, CAP, GROUP>(mode);
         return 0;
     }
-    if (L == 2) return pipe_blocks<N, R, R2, 2, CAP, GROUP>();
-    if (L == 3) return pipe_blocks<N, R, R2, 3, CAP, GROUP>();
-    if (L == 4) return pipe_blocks<N, R, R2, 4, CAP, GROUP>();
-    if (L == 5) return pipe_blocks<N, R, R2, 5, CAP, GROUP>();
+    if (L == 2) return pipe_blocks<N, R, R2, 2, CAP, GROUP>(mode);
+    if (L == 3) return pipe_blocks<N, R, R2, 3, CAP, GROUP>(mode);
+    if (L == 4) return pipe_blocks<N, R, R2, 4, CAP, GROUP>(mode);
+    if (L == 5) return pipe_blocks<N, R, R2, 5, CAP, GROUP>(mode);
     return 0;
 }
 
@@ -126,11 +131,11 @@ Kernel find_pipe_launcher(int n, int R, int R2, int L, bool cap, bool group) {
 }
 
 // workgroups of that kernel (one stream each) resident per CU on the current device
-int pipe_blocks_per_cu(int n, int R, int R2, int L, bool cap, bool group) {
+int pipe_blocks_per_cu(int n, int R, int R2, int L, bool cap, bool group, int mode) {
 #define YGG_P(N_, R_, R2_) \
     if (n == N_ && R == R_ && R2 == R2_) { \
-        if (group) return cap ? pipe_occ<N_, R_, R2_, true, true>(L) : pipe_occ<N_, R_, R2_, false, true>(L); \
-        return cap ? pipe_occ<N_, R_, R2_, true, false>(L) : pipe_occ<N_, R_, R2_, false, false>(L); \
+        if (group) return cap ? pipe_occ<N_, R_, R2_, true, true>(L, mode) : pipe_occ<N_, R_, R2_, false, true>(L, mode); \
+        return cap ? pipe_occ<N_, R_, R2_, true, false>(L, mode) : pipe_occ<N_, R_, R2_, false, false>(L, mode); \
     }
     YGG_SHAPES(YGG_P)
 #undef YGG_P
