@@ -514,6 +514,38 @@ REFERENCE_SHAPES = {"small": synth.ModelSpec(64, 16, 10, 27, 5, 8, 16), "medium"
                     "large": synth.ModelSpec(256, 16, 10, 27, 5, 32, 64)}
 
 
+def test_score_bad_target_nll_wave(hip, model_dir, monkeypatch):
+    """A target outside the vocabulary in a score call on the largest shape at 5 layers (flow_kernel's score build,
+    whose NLL runs on a wavefront of its own): the call reports error 2 and the other stream's NLL still equals the
+    reference formula on the oracle's logits."""
+    import math
+    import torch
+    from oracle import oracle as O
+    from yggdrasil_amd import _lib
+    monkeypatch.delenv("YGG_KERNEL", raising=False)
+    monkeypatch.delenv("YGG_FLOW", raising=False)
+    spec = REFERENCE_SHAPES["large"]
+    path = model_dir / "refshape_large.bin"
+    if not path.exists():
+        synth.write_model(spec, 13, path)
+    model = hip.load(path)
+    B, T = 2, 40
+    assert model.kernel_name(B, T, score=True) == "ygg::flow_kernel<256, 32, 64, 5, 3, 2, false>"
+    w = synth.uniform_tokens(spec.vocab, B, T + 1, 5)
+    x = torch.as_tensor(w[:, :-1], device=model.device).contiguous()
+    y = torch.as_tensor(w[:, 1:], device=model.device).contiguous()
+    y[0, 7] = 300
+    st = model.init_state(B)
+    nll = torch.zeros(B, dtype=torch.float64, device=model.device)
+    p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    _lib.check(_lib.lib().ygg_score(model._h, p(x), p(y), B, T, p(st), p(nll),
+                                    ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)))
+    assert model.take_errors() == 2
+    want = O.nll_bits(Oracle(path).run(w[1:, :-1])["logits"], w[1:, 1:])[0]
+    np.testing.assert_allclose(nll[1].item() / math.log(2.0), want, rtol=1e-12)
+    model.close()
+
+
 @pytest.mark.parametrize("group", [False, True], ids=["tensor", "group"])
 @pytest.mark.parametrize("name", list(REFERENCE_SHAPES))
 def test_reference_model_shapes(hip, model_dir, kernel_env, name, group):
