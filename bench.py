@@ -91,6 +91,36 @@ def cpu_flags() -> set:
     return set()
 
 
+def host_facts() -> dict:
+    """The host the CPU baseline runs on: its CPU model, logical CPUs, the CPUs this process may use, and whether
+    transparent huge pages are on (the reference allocates its model in huge pages, cpu/ygg.cpp:118-129)."""
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        thp = Path("/sys/kernel/mm/transparent_hugepage/enabled").read_text().strip()
+    except OSError:
+        thp = ""
+    return {"cpu_model": model, "host_logical_cpus": os.cpu_count(),
+            "usable_cpus": len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count(),
+            "thp": thp}
+
+
+# Why the baseline uses at most 16 cores: a one-GPU job on the GPU boxes gets a 16-core share of the host, whatever
+# the host's core count; more pinned processes would share cores with the GPU job's own threads.
+CPU_SHARE = 16
+# The reference binary's target: it is built from cpu/ygg.cpp in the build container (its source does not travel),
+# so for any AVX-512 VNNI host rather than the build host's -march=native.
+REF_MARCH = "-march=x86-64-v4 -mavx512vnni"
+SOFTMAX_NOTE = ("the reference's time mode computes an f32 softmax of every token's logits (cpu/ygg.cpp:61-72, "
+                "552), included in its ns/token; the GPU value writes the logits and computes no softmax")
+
+
 def cpu_baseline(path: Path, tokens: np.ndarray, procs: int, streams_per_proc: int) -> dict:
     """The reference kernel's `time` mode (cpu/ygg.cpp:528-562) on the host: `procs` processes, each pinned to one
     core, each on its own streams_per_proc streams concatenated into one token stream (state carried, f32 softmax
@@ -123,13 +153,15 @@ def cpu_baseline(path: Path, tokens: np.ndarray, procs: int, streams_per_proc: i
             value = sum(1e9 / m for m in mean)
             ntok = streams_per_proc * T
             return {"value": round(value, 1), "unit": "tokens/s", "cores": procs, "kind": "reference",
-                    "sample": f"{procs} pinned processes of `ygg time` (cpu/ygg.cpp, -O3 -march=x86-64-v4 "
-                              f"-mavx512vnni), each {streams_per_proc} streams of the workload concatenated into "
-                              f"{ntok} tokens (first 1000 untimed, state carried, f32 softmax per token included); "
-                              f"value = sum over processes of 1e9 / mean ns/token",
+                    "sample": f"{procs} pinned processes of `ygg time` (cpu/ygg.cpp, -O3 {REF_MARCH}), each "
+                              f"{streams_per_proc} streams of the workload concatenated into {ntok} tokens (first "
+                              f"1000 untimed, state carried, f32 softmax per token included); value = sum over "
+                              f"processes of 1e9 / mean ns/token",
                     "per_core_median_ns_per_token": round(float(np.median(med)), 1),
                     "per_core_tokens_per_s": round(1e9 / float(np.median(med)), 1),
-                    "thp_kB_proc0": int(thp), "wall_s": round(wall, 1)}
+                    "thp_kB_proc0": int(thp), "wall_s": round(wall, 1), "march": REF_MARCH,
+                    "cores_why": f"one pinned process per core of the {CPU_SHARE}-core share a one-GPU job gets on "
+                                 f"the GPU box", "softmax": SOFTMAX_NOTE, **host_facts()}
         log("reference baseline failed: " + " | ".join(o[1].strip()[:200] for o in outs if o[1]))
     # the C oracle (a port), threads over streams
     n = min(B, procs * streams_per_proc)
@@ -140,7 +172,7 @@ def cpu_baseline(path: Path, tokens: np.ndarray, procs: int, streams_per_proc: i
     dt = time.time() - t0
     return {"value": round(n * T / dt, 1), "unit": "tokens/s", "cores": procs, "kind": "port",
             "sample": f"C oracle (oracle/ygg_oracle.c, scalar, -O3) on {n} streams x {T} tokens, {procs} threads; "
-                      f"logits only, no softmax"}
+                      f"logits only, no softmax", **host_facts()}
 
 
 def _counter_sums(d: str) -> dict:
@@ -213,7 +245,7 @@ def main():
     ap.add_argument("--cache", default=os.environ.get("YGG_BENCH_DIR", os.path.join(tempfile.gettempdir(),
                                                                                       "ygg_bench")))
     ap.add_argument("--batch1-tokens", type=int, default=8192)
-    ap.add_argument("--cpu-procs", type=int, default=16)
+    ap.add_argument("--cpu-procs", type=int, default=CPU_SHARE)
     ap.add_argument("--cpu-streams", type=int, default=256, help="streams per CPU baseline process")
     ap.add_argument("--no-cpu", action="store_true")
     a = ap.parse_args()

@@ -9,7 +9,7 @@ from pathlib import Path
 import numpy as np
 import pytest
 
-from yggdrasil_amd import synth
+from yggdrasil_amd import fmt, synth
 
 ROOT = Path(__file__).resolve().parents[1]
 HEADER = ROOT / "include" / "ygg_hip.h"
@@ -109,6 +109,20 @@ def test_malformed_files(lib, tmp_path):
         p.write_bytes(blob)
         assert L.ygg_load(str(p).encode(), 0, ctypes.byref(h)) == code, name
         assert msg in L.ygg_last_error(), (name, L.ygg_last_error())
+        assert not h.value
+    # scales that are not finite (a NaN readout scale, an infinite output bias, a NaN layer-input row scale)
+    arr = np.frombuffer(data, np.uint8)
+    mf = fmt.parse(arr)
+
+    def at(name, k, value):
+        off = mf.arrays[name].__array_interface__["data"][0] - arr.__array_interface__["data"][0] + 4 * k
+        return data[:off] + np.float32(value).tobytes() + data[off + 4:]
+    for name, k, value in (("l1_scal", 0, np.nan), ("head_b", 3, np.inf), ("l1_scal", 2, -np.nan),
+                           ("l0_scal", 1, -np.inf)):
+        p = tmp_path / f"nonfinite_{name}.bin"
+        p.write_bytes(at(name, k, value))
+        assert L.ygg_load(str(p).encode(), 0, ctypes.byref(h)) == 2, name
+        assert b"not finite" in L.ygg_last_error(), (name, L.ygg_last_error())
         assert not h.value
     # a well-formed file gets as far as the device: YGG_ERR_DEVICE without one
     rc = L.ygg_load(str(good).encode(), 0, ctypes.byref(h))

@@ -134,6 +134,107 @@ def test_oracle_rms_and_carry(small):
     np.testing.assert_allclose(np.concatenate([a["logits"], b["logits"]], 1), whole["logits"], rtol=1e-13, atol=1e-13)
 
 
+def _forced(layers, rng):
+    """Router weights 0 and biases +-1: every leaf is fixed whatever the state (see test_oracle_forced_routes)."""
+    for fl in layers[1:]:
+        fl.router_weight = np.zeros_like(fl.router_weight)
+        fl.router_bias = rng.choice([-1.0, 1.0], fl.router_bias.shape)
+
+
+def test_oracle_identity_transition_accumulates(small):
+    """A_r = I and no layer input: every layer's state is the running sum of the table rows it took,
+    h_t = sum_{s <= t} T_{r_s}[x_s]."""
+    layers, ob, spec = _layers(small)
+    rng = np.random.default_rng(5)
+    _forced(layers, rng)
+    for fl in layers:
+        g, b = fl.transition.shape[1], fl.transition.shape[2]
+        fl.transition = np.broadcast_to(np.eye(b), fl.transition.shape).copy()
+        fl.layer_input_down = fl.layer_input_proj = None
+    x = rng.integers(0, spec.vocab, (3, 9))
+    r = FO.run(layers, ob, x)
+    for i, fl in enumerate(layers):
+        acc = np.zeros((3, spec.d_state))
+        for t in range(9):
+            rows = fl.table[x[:, t]] if i == 0 else fl.table[r["leaves"][:, t, i], x[:, t]]
+            acc = acc + rows
+        np.testing.assert_allclose(r["state"][:, i], acc, rtol=1e-12, atol=1e-12)
+
+
+def test_oracle_transition_orientation(small):
+    """One nonzero entry A[block g][row i][column j] = a and no layer input: coordinate g b + i takes a times the
+    previous value of coordinate g b + j, every other coordinate is its table row alone; a transposed A or a wrong
+    block offset moves the term to another coordinate."""
+    layers, ob, spec = _layers(small)
+    rng = np.random.default_rng(6)
+    _forced(layers, rng)
+    b = layers[0].transition.shape[-1]
+    g, i, j, a = 1, 2, 5, 0.75
+    for fl in layers:
+        A = np.zeros_like(fl.transition)
+        A[:, g, i, j] = a
+        fl.transition = A
+        fl.layer_input_down = fl.layer_input_proj = None
+    x = rng.integers(0, spec.vocab, (4, 6))
+    r = FO.run(layers, ob, x)
+    for l, fl in enumerate(layers):
+        prev = np.zeros((4, spec.d_state))
+        for t in range(6):
+            row = fl.table[x[:, t]] if l == 0 else fl.table[r["leaves"][:, t, l], x[:, t]]
+            want = row.copy()
+            want[:, g * b + i] += a * prev[:, g * b + j]
+            got = FO.run(layers, ob, x[:, :t + 1])["state"][:, l]
+            np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-12)
+            prev = want
+
+
+def test_oracle_rank_one_layer_input(small):
+    """V' = e_0 e_k^T (only row 0, column k) and U'_r = c e_m e_0^T, no transitions: a routed layer's state is its
+    table row plus c rms(h_below)[k] at coordinate m, with h_below the layer below after the same token."""
+    layers, ob, spec = _layers(small)
+    rng = np.random.default_rng(7)
+    _forced(layers, rng)
+    k, m, c = 9, 33, -1.25
+    for fl in layers:
+        fl.transition = np.zeros_like(fl.transition)
+        if fl.layer_input_down is not None:
+            Vd = np.zeros_like(fl.layer_input_down)
+            Vd[0, k] = 1.0
+            Up = np.zeros_like(fl.layer_input_proj)
+            Up[:, m, 0] = c
+            fl.layer_input_down, fl.layer_input_proj = Vd, Up
+    assert layers[1].layer_input_down is not None
+    x = rng.integers(0, spec.vocab, (5, 4))
+    r = FO.run(layers, ob, x)
+    st = FO.run(layers, ob, x[:, :3])["state"]
+    for l in range(1, spec.n_layers):
+        below = st[:, l - 1]
+        mean_sq = (below ** 2).mean(-1)
+        want = layers[l].table[r["leaves"][:, 2, l], x[:, 2]].copy()
+        want[:, m] += c * below[:, k] / np.sqrt(mean_sq + 1e-6)
+        np.testing.assert_allclose(st[:, l], want, rtol=1e-12, atol=1e-12)
+
+
+def test_oracle_readout_orientation(small):
+    """P_r = e_j e_k^T (readout row j reads coordinate k) and Q = e_c e_j^T (class c reads readout row j) in every
+    layer: the logits are the output bias plus, at class c only, the sum over layers of h_l[k]."""
+    layers, ob, spec = _layers(small)
+    rng = np.random.default_rng(8)
+    _forced(layers, rng)
+    j, k, c = 3, 17, 11
+    for fl in layers:
+        P = np.zeros_like(fl.readout)
+        P[:, j, k] = 1.0
+        Q = np.zeros_like(fl.unembed)
+        Q[c, j] = 1.0
+        fl.readout, fl.unembed = P, Q
+    x = rng.integers(0, spec.vocab, (3, 5))
+    r = FO.run(layers, ob, x)
+    want = np.broadcast_to(ob.astype(np.float64), (3, len(ob))).copy()
+    want[:, c] += r["state"][:, :, k].sum(-1)
+    np.testing.assert_allclose(r["logits"][:, -1], want, rtol=1e-12, atol=1e-12)
+
+
 # ----------------------------------------------------------------------------------------------- quantisation
 def _golden_setup():
     import importlib.util
@@ -177,3 +278,56 @@ def test_quantize_plants_fail():
            for s in stats]
     q = quantize(layers, bad, 1.0)
     assert not np.array_equal(q[1].table, z["tensor_1.0/1/table"])
+
+
+def test_windows_pair_each_token_with_the_next():
+    from yggdrasil_amd.export import windows
+    ids = np.arange(23)
+    x, y = windows(ids, 5, 10)
+    assert x.shape == y.shape == (4, 5)                     # (23 - 1) // 5 windows
+    np.testing.assert_array_equal(x.ravel(), np.arange(20))
+    np.testing.assert_array_equal(y.ravel(), np.arange(1, 21))
+    x, y = windows(ids, 5, 2)
+    assert x.shape == (2, 5) and y[-1, -1] == 10
+
+
+def test_export_calibrates_on_inputs_and_scores_targets(small, tmp_path, monkeypatch):
+    """export() takes the calibration maxima over the input windows only and compares its candidates by the bits of
+    the targets given the inputs (the reference: calibrate(cx), bpc(int_forward(cx), cy), cpu/export.py:554-561);
+    without targets, (S, T + 1) windows split into inputs [:, :-1] and targets [:, 1:]."""
+    from yggdrasil_amd import export as X
+    spec, p = small
+    seen = {"calib": [], "score": []}
+
+    class NoKernel:
+        def __init__(self, *a, **k):
+            pass
+
+        def close(self):
+            pass
+
+    def fake_calibrate(model, x):
+        seen["calib"].append(np.array(x))
+        return [LayerStats(1.0, 1.0, 1.0, np.ones(spec.d_state // 16), np.ones(8)) for _ in range(spec.n_layers)]
+
+    def fake_bits(q, ob, x, y, F, K):
+        seen["score"].append((np.array(x), np.array(y)))
+        return 1.0
+
+    import torch
+    monkeypatch.setattr(X, "FloatYggdrasil", NoKernel)
+    monkeypatch.setattr(X, "calibrate", fake_calibrate)
+    monkeypatch.setattr(X, "int8_bits", fake_bits)
+    monkeypatch.setattr(torch.cuda, "synchronize", lambda *a: None)
+    rng = np.random.default_rng(0)
+    w = rng.integers(0, spec.vocab, (6, 9))
+    X.export(p, tmp_path / "a.bin", w, hmargin=1.0, state_scale="tensor")
+    np.testing.assert_array_equal(seen["calib"][0], w[:, :-1])
+    np.testing.assert_array_equal(seen["score"][0][0], w[:, :-1])
+    np.testing.assert_array_equal(seen["score"][0][1], w[:, 1:])
+    x, y = X.windows(rng.integers(0, spec.vocab, 100), 8, 4)
+    X.export(p, tmp_path / "b.bin", x, y, hmargin=1.0, state_scale="tensor")
+    np.testing.assert_array_equal(seen["calib"][1], x)
+    np.testing.assert_array_equal(seen["score"][1][1], y)
+    with pytest.raises(ValueError):
+        X.export(p, tmp_path / "c.bin", x, y[:, :-1])

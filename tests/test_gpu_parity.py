@@ -252,6 +252,40 @@ def test_step_in_place_and_edges(hip, c12):
     assert L.ygg_run(model._h, p(xt), -1, 1, p(st), None, None, None, None, s) == 5
 
 
+def test_step_and_run_do_not_wait(hip, c12):
+    """step() and run() return without a host synchronisation (torch's sync debug mode raises on any), with tokens
+    on the GPU and with tokens on the host; a bad token already on the GPU is not read back but reported through the
+    error word, while a bad host token raises before anything is launched."""
+    import torch
+    model = hip.load(c12)
+    x = synth.CONFIGS[2].make_tokens(8, 4)
+    ref = Oracle(c12).run(x, states=True)
+    xd = torch.as_tensor(x, device=model.device)
+    st = model.init_state(8)
+    torch.cuda.synchronize()
+    torch.cuda.set_sync_debug_mode("error")
+    try:
+        lg0, st1 = model.step(xd[:, 0], st)
+        lg1, st2 = model.step(x[:, 1], st1)
+        r = model.run(xd[:, 2:], state=st2)
+        bad = xd[:, 0].clone()
+        bad[3] = 999
+        model.step(bad, model.init_state(8))
+    finally:
+        torch.cuda.set_sync_debug_mode("default")
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(lg0.cpu().numpy(), ref["logits"][:, 0])
+    np.testing.assert_array_equal(lg1.cpu().numpy(), ref["logits"][:, 1])
+    np.testing.assert_array_equal(r["logits"].cpu().numpy(), ref["logits"][:, 2:])
+    np.testing.assert_array_equal(r["state"].cpu().numpy(), ref["state"])
+    assert model.take_errors() == 1
+    with pytest.raises(ValueError):
+        model.step(np.array([0, 1, 2, 3, 999, 5, 6, 7]), st)
+    strict = hip.load(c12, check_tokens=True)
+    with pytest.raises(ValueError):
+        strict.step(bad, strict.init_state(8))
+
+
 def test_bad_token_stops_stream(hip, c12, kernel_env):
     """A token outside [0, V) stops its stream at that token and sets the error word; other streams go on."""
     import torch

@@ -5,6 +5,7 @@
 #include <algorithm>
 #include <atomic>
 #include <climits>
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -118,6 +119,15 @@ struct FileLayer {
     const int8_t *vt = nullptr; int64_t vt_nb = 0;
 };
 
+bool all_finite(const float *p, int64_t count) {
+    for (int64_t i = 0; i < count; i++) {
+        float v;
+        memcpy(&v, p + i, 4);
+        if (!std::isfinite(v)) return false;
+    }
+    return true;
+}
+
 // Binds and size-checks the arrays of layer l (cpu/ygg.cpp:173-202); every array the kernels read is checked to hold
 // the bytes the kernels will read, so a malformed file fails here instead of faulting on the GPU.
 int bind_layer(const FileArrays &fa, int l, FileLayer &y) {
@@ -183,6 +193,29 @@ int bind_layer(const FileArrays &fa, int l, FileLayer &y) {
         y.r2b = (const float *)fa.get(P + "r2b", &y.r2b_nb);
         if (y.r2b && y.r2b_nb < 4LL * (n / 16)) return fail(YGG_ERR_FORMAT, "model file: %sr2b", P.c_str());
     }
+    // Every scale must be a finite number: a NaN or infinite scale would turn every logit of the model into NaN or
+    // infinity, and a sampler fed such logits has no class to pick. (Thresholds may be infinite: an infinite
+    // threshold sends every stream one way at its node.)
+    const struct { const char *tag; const float *p; int64_t count; } scales[] = {
+        {"scal", y.scal, 4},
+        {"mzl", y.mzl, y.mzl ? (int64_t)E * (R == 8 ? 16 : R) : 0},
+        {"sqv", y.sqv, y.sqv ? VP : 0},
+        {"mv", y.mv, y.mv ? 16LL * ((R2 + 15) / 16) : 0},
+        {"mulv", y.mulv, y.mulv ? n : 0},
+        {"r2b", y.r2b, y.r2b ? n / 16 : 0},
+        {"mT", y.mT, y.mT ? n : 0},
+    };
+    for (const auto &sc : scales)
+        if (!all_finite(sc.p, sc.count))
+            return fail(YGG_ERR_FORMAT, "model file: %s%s holds a scale that is not finite", P.c_str(), sc.tag);
+    if (y.vt)
+        for (int64_t e = 0; e < E; e++) {
+            float v;
+            memcpy(&v, y.rec + e * y.record_bytes + y.off_S, 4);
+            if (!std::isfinite(v))
+                return fail(YGG_ERR_FORMAT, "model file: %srec expert %lld has a factored scale that is not finite",
+                            P.c_str(), (long long)e);
+        }
     return YGG_OK;
 }
 
@@ -361,8 +394,8 @@ struct ygg_model {
     ygg::Kernel deep;                 // deep descent: generate with B <= deep_max_streams
     int deep_max_streams = 0;
     bool deep_all = false;            // YGG_KERNEL=deep: every call
-    ygg::Kernel flow;                 // router rounds and updates pipelined over ticks: T > 1, B <= flow_max_streams
-    int flow_max_streams = 0;
+    ygg::Kernel flow;                 // router rounds and updates pipelined over ticks: T > 1, B <= flow_max_streams[mode]
+    int flow_max_streams[3] = {0, 0, 0};
     bool flow_all = false;            // YGG_KERNEL=flow: every call but generation
 };
 
@@ -378,6 +411,7 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     const float *head_b = (const float *)fa.get("head_b", &hb_nb);
     if (!head_b) return fail(YGG_ERR_FORMAT, "missing head_b");
     if (hb_nb < 4LL * VP) return fail(YGG_ERR_FORMAT, "head_b too short");
+    if (!all_finite(head_b, VP)) return fail(YGG_ERR_FORMAT, "model file: head_b holds a bias that is not finite");
     std::vector<FileLayer> fl(L);
     bool factored = false, group = false;
     for (int l = 0; l < L; l++) {
@@ -591,8 +625,10 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     // flow_kernel for T > 1 while every stream's workgroup is resident (or always with YGG_KERNEL=flow)
     m->flow = flowk;
     m->flow_all = flowk && kmode == "flow";
-    m->flow_max_streams =
-        flowk ? (m->flow_all ? INT32_MAX : ygg::flow_blocks_per_cu(n, R, R2f, L, rplan.n, group) * cus) : 0;
+    // (per mode: the score build of the largest shape has one wavefront more; generation never runs on it)
+    for (int md : {kModeRun, kModeScore})
+        m->flow_max_streams[md] =
+            flowk ? (m->flow_all ? INT32_MAX : ygg::flow_blocks_per_cu(n, R, R2f, L, rplan.n, group, md) * cus) : 0;
     m->device = device;
     m->arena = arena;
     m->arena_bytes = total;
@@ -650,7 +686,7 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     I.pipe_max_streams = m->pipe_max_streams;
     I.deep = deep_avail ? 1 : 0;
     I.deep_max_streams = m->deep_max_streams;
-    I.flow_max_streams = m->flow_max_streams;
+    I.flow_max_streams = m->flow_max_streams[kModeRun];
     I.router_rounds = L > 1 ? rplan.n : 0;
     I.file_array_bytes = fa.bytes;
     I.device_bytes = (int64_t)total;
@@ -673,7 +709,7 @@ const ygg::Kernel &pick(const ygg_model *m, int B, int T, int mode) {
     const bool gen = mode == kModeGenerate;
     if (m->deep_all) return m->deep;
     if (gen && m->deep && B <= m->deep_max_streams && T >= 8) return m->deep;
-    if (!gen && m->flow && (m->flow_all || (T >= kFlowMinTokens && B <= m->flow_max_streams))) return m->flow;
+    if (!gen && m->flow && (m->flow_all || (T >= kFlowMinTokens && B <= m->flow_max_streams[mode]))) return m->flow;
     if (!gen && m->pipe && (m->pipe_all || (T > 1 && B <= m->pipe_max_streams)))
         return (m->pipe_few && B <= m->pipe_few_max_streams[mode]) ? m->pipe_few : m->pipe;
     return (m->run_few && B <= m->run_few_max_streams[mode]) ? m->run_few : m->run;

@@ -33,16 +33,21 @@ template <int N, int R, int R2, int L, int P, bool GROUP> Kernel flow_k() {
         return Kernel();
 }
 
-// (resident workgroups of the run build; the score build's registers differ little in what bounds them)
-template <int N, int R, int R2, int L, int P, bool GROUP> int flow_blocks() {
+// resident workgroups per CU of the build of a mode (kModeRun or kModeScore: the score build of the largest shape has
+// a wavefront more, for the NLL, and may fit fewer workgroups)
+template <int N, int R, int R2, int L, int P, int MODE, bool GROUP> int flow_blocks_mode() {
+    int nb = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &nb, reinterpret_cast<const void *>(&flow_kernel<N, R, R2, L, P, MODE, GROUP>),
+            kFlowThreads<Shape<N, R, R2>, L, MODE>, 0) != hipSuccess)
+        return 0;
+    return nb;
+}
+
+template <int N, int R, int R2, int L, int P, bool GROUP> int flow_blocks(int mode) {
     if constexpr (kFlowBuilt<N, R, R2, L, P, GROUP>) {
-        int nb = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                &nb, reinterpret_cast<const void *>(&flow_kernel<N, R, R2, L, P, kModeRun, GROUP>),
-                kFlowThreads<Shape<N, R, R2>, L, kModeRun>, 0) !=
-            hipSuccess)
-            return 0;
-        return nb;
+        return mode == kModeScore ? flow_blocks_mode<N, R, R2, L, P, kModeScore, GROUP>()
+                                  : flow_blocks_mode<N, R, R2, L, P, kModeRun, GROUP>();
     } else {
         return 0;
     }
@@ -56,11 +61,11 @@ template <int N, int R, int R2, int P, bool GROUP> Kernel flow_for(int L) {
     return Kernel();
 }
 
-template <int N, int R, int R2, int P, bool GROUP> int flow_occ(int L) {
-    if (L == 2) return flow_blocks<N, R, R2, 2, P, GROUP>();
-    if (L == 3) return flow_blocks<N, R, R2, 3, P, GROUP>();
-    if (L == 4) return flow_blocks<N, R, R2, 4, P, GROUP>();
-    if (L == 5) return flow_blocks<N, R, R2, 5, P, GROUP>();
+template <int N, int R, int R2, int P, bool GROUP> int flow_occ(int L, int mode) {
+    if (L == 2) return flow_blocks<N, R, R2, 2, P, GROUP>(mode);
+    if (L == 3) return flow_blocks<N, R, R2, 3, P, GROUP>(mode);
+    if (L == 4) return flow_blocks<N, R, R2, 4, P, GROUP>(mode);
+    if (L == 5) return flow_blocks<N, R, R2, 5, P, GROUP>(mode);
     return 0;
 }
 
@@ -70,9 +75,9 @@ template <int N, int R, int R2, bool GROUP> Kernel flow_plan(int L, int P) {
     return Kernel();
 }
 
-template <int N, int R, int R2, bool GROUP> int flow_plan_occ(int L, int P) {
-    if (P == 3) return flow_occ<N, R, R2, 3, GROUP>(L);
-    if (P == 4) return flow_occ<N, R, R2, 4, GROUP>(L);
+template <int N, int R, int R2, bool GROUP> int flow_plan_occ(int L, int P, int mode) {
+    if (P == 3) return flow_occ<N, R, R2, 3, GROUP>(L, mode);
+    if (P == 4) return flow_occ<N, R, R2, 4, GROUP>(L, mode);
     return 0;
 }
 
@@ -85,10 +90,10 @@ Kernel find_flow_launcher(int n, int R, int R2, int L, int P, bool group) {
     return Kernel();
 }
 
-int flow_blocks_per_cu(int n, int R, int R2, int L, int P, bool group) {
+int flow_blocks_per_cu(int n, int R, int R2, int L, int P, bool group, int mode) {
 #define YGG_W(N_, R_, R2_) \
     if (n == N_ && R == R_ && R2 == R2_) \
-        return group ? flow_plan_occ<N_, R_, R2_, true>(L, P) : flow_plan_occ<N_, R_, R2_, false>(L, P);
+        return group ? flow_plan_occ<N_, R_, R2_, true>(L, P, mode) : flow_plan_occ<N_, R_, R2_, false>(L, P, mode);
     YGG_SHAPES(YGG_W)
 #undef YGG_W
     return 0;

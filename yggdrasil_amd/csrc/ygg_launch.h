@@ -60,8 +60,8 @@ Kernel find_deep_launcher(int n, int R, int R2, int L, bool group);
 Kernel find_pipe_launcher(int n, int R, int R2, int L, bool cap, bool group);
 int pipe_blocks_per_cu(int n, int R, int R2, int L, bool cap, bool group, int mode);
 // flow_kernel, one workgroup per stream, for scoring with the tokens known, router plans of P = 3 or 4 rounds
-// (ygg_kernels_flow.hip); its resident workgroups per CU
+// (ygg_kernels_flow.hip); the resident workgroups per CU of its build for a mode (kModeRun or kModeScore)
 Kernel find_flow_launcher(int n, int R, int R2, int L, int P, bool group);
-int flow_blocks_per_cu(int n, int R, int R2, int L, int P, bool group);
+int flow_blocks_per_cu(int n, int R, int R2, int L, int P, bool group, int mode);
 
 }  // namespace ygg

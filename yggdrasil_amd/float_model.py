@@ -268,11 +268,8 @@ class FloatYggdrasil:
         return torch.zeros(batch_size, self.layers, self.n, dtype=self.dtype, device=self.device)
 
     def _tokens(self, tokens):
-        import torch
-        x = torch.as_tensor(tokens, device=self.device).to(torch.int32).contiguous()
-        if x.numel() and (int(x.min()) < 0 or int(x.max()) >= self.vocab):
-            raise ValueError(f"token out of range [0, {self.vocab})")
-        return x
+        from .inference import device_tokens
+        return device_tokens(tokens, self.vocab, self.device)
 
     def run(self, tokens, state=None, logits: bool = True, leaves: bool = False, stats: bool = False) -> dict:
         """T tokens per stream in one launch: tokens (B, T) -> dict(state, logits (B, T, classes), leaves (B, T, L),

@@ -139,32 +139,51 @@ def pack_layer_input_down(Vd: np.ndarray, n: int) -> np.ndarray:
 
 # ----------------------------------------------------------------------------------------------------- header
 
-def header(layers: Sequence[QuantLayer], vocab: int, router_token_dim: int = 0, input_rank: int = 0) -> dict:
-    """HEADER values of layers, checked against LIMITS; ValueError names the failing field (cpu/export.py:353-379)."""
-    q0, routed = layers[0], list(layers[1:])
-    R2 = routed[0].layer_input_proj.shape[2] if routed and routed[0].layer_input_proj is not None else 0
-    fac = [q.factored for q in layers if q.factored is not None]
-    hdr = dict(n_layers=len(layers), d_state=q0.n, block_size=q0.block, vocab=vocab,
-               router_depth=routed[0].depth if routed else 0, readout_rank=q0.readout.shape[1],
-               layer_input_rank=R2, reserved=0, router_token_dim=router_token_dim,
-               input_rank=fac[0].input_proj.shape[2] if fac else input_rank, shift=SHIFT)
+def _layer_input_rank(q: QuantLayer) -> int:
+    return 0 if q.layer_input_proj is None else int(q.layer_input_proj.shape[2])
 
-    def need(ok, field):
-        if not ok:
-            raise ValueError(f"model.bin cannot hold {field} = {hdr.get(field)} (limits {LIMITS})")
-    for k in ("d_state", "block_size", "readout_rank"):
-        need(hdr[k] in LIMITS[k], k)
-    need(R2 % RANK_MULTIPLE == 0 and R2 <= LIMITS["max_layer_input_rank"], "layer_input_rank")
-    need(vocab <= LIMITS["max_vocab"], "vocab")
-    need(1 <= len(layers) <= LIMITS["max_layers"], "n_layers")
-    need(not routed or 1 <= hdr["router_depth"] <= LIMITS["max_router_depth"], "router_depth")
-    need(not fac or (hdr["input_rank"] % RANK_MULTIPLE == 0
-                     and RANK_MULTIPLE <= hdr["input_rank"] <= LIMITS["max_input_rank"]), "input_rank")
-    for q in routed:
-        need(q.depth == hdr["router_depth"], "router_depth")
-        need(q.readout.shape[1] == hdr["readout_rank"], "readout_rank")
-        need((q.layer_input_proj is not None) == bool(R2) and (not R2 or q.layer_input_proj.shape[2] == R2),
-             "layer_input_rank")
+
+def _limit_violations(hdr: dict, layers: Sequence[QuantLayer], factored: bool) -> Iterator[str]:
+    """The header fields whose values a YGG1 file cannot hold, in the order they are checked. Each routed layer must
+    also agree with the header, which is taken from the first one."""
+    for field, allowed in (("d_state", LIMITS["d_state"]), ("block_size", LIMITS["block_size"]),
+                           ("readout_rank", LIMITS["readout_rank"])):
+        if hdr[field] not in allowed:
+            yield field
+    r2, rank = hdr["layer_input_rank"], hdr["input_rank"]
+    if r2 % RANK_MULTIPLE or r2 > LIMITS["max_layer_input_rank"]:
+        yield "layer_input_rank"
+    if hdr["vocab"] > LIMITS["max_vocab"]:
+        yield "vocab"
+    if not 1 <= hdr["n_layers"] <= LIMITS["max_layers"]:
+        yield "n_layers"
+    if hdr["n_layers"] > 1 and not 1 <= hdr["router_depth"] <= LIMITS["max_router_depth"]:
+        yield "router_depth"
+    if factored and (rank % RANK_MULTIPLE or not RANK_MULTIPLE <= rank <= LIMITS["max_input_rank"]):
+        yield "input_rank"
+    for q in layers[1:]:
+        if q.depth != hdr["router_depth"]:
+            yield "router_depth"
+        if q.readout.shape[1] != hdr["readout_rank"]:
+            yield "readout_rank"
+        if _layer_input_rank(q) != r2:
+            yield "layer_input_rank"
+
+
+def header(layers: Sequence[QuantLayer], vocab: int, router_token_dim: int = 0, input_rank: int = 0) -> dict:
+    """The HEADER fields of a file holding layers; ValueError naming the first field outside LIMITS
+    (the checks of cpu/export.py:353-379). The routed-layer fields come from the first routed layer; input_rank is
+    the factored projection's rank when a layer is factored, else the value given."""
+    first, routed = layers[0], layers[1:]
+    fac = next((q.factored for q in layers if q.factored is not None), None)
+    hdr = {"n_layers": len(layers), "d_state": first.n, "block_size": first.block, "vocab": vocab,
+           "router_depth": routed[0].depth if routed else 0, "readout_rank": first.readout.shape[1],
+           "layer_input_rank": _layer_input_rank(routed[0]) if routed else 0, "reserved": 0,
+           "router_token_dim": router_token_dim,
+           "input_rank": fac.input_proj.shape[2] if fac is not None else input_rank, "shift": SHIFT}
+    bad = next(_limit_violations(hdr, layers, fac is not None), None)
+    if bad is not None:
+        raise ValueError(f"YGG1 header field {bad} = {hdr[bad]} is outside the format's limits {LIMITS}")
     return hdr
 
 
@@ -180,86 +199,131 @@ class Streamed:
     chunks: Callable[[], Iterator[np.ndarray]]
 
 
+@dataclasses.dataclass(frozen=True)
+class RecordLayout:
+    """Where the parts of one expert's record lie: (part, byte offset, byte size) in record order, and the record
+    size (the parts' total rounded up to ALIGN). Parts are those of RECORD; a layer has a subset of them."""
+    parts: tuple
+    nbytes: int
+
+    def offset(self, part: str) -> int:
+        return next((o for p, o, _ in self.parts if p == part), -1)
+
+    def meta(self, factored: bool) -> np.ndarray:
+        """l<l>_meta: the record size, then the offset of every RECORD part (-1: absent); the factored parts'
+        offsets only in a factored layer."""
+        tags = RECORD if factored else RECORD[:len(RECORD) - FACTORED_PARTS]
+        return np.array([self.nbytes] + [self.offset(p) for p in tags], np.int32)
+
+
+def record_layout(q: QuantLayer, n: int, R: int, R2: int) -> RecordLayout:
+    """The record of layer q: A16 (2 bytes per entry of n/b blocks of b x b), then the routed layer-input
+    projection U' (n R2 bytes), the readout P (R n bytes), and either its input table (2 n bytes per token the
+    record holds a row for) or the factored projection, bias and scale."""
+    sizes = [("transition", 2 * n * q.block)]
+    if R2 and not q.token_layer:
+        sizes.append(("layer_input_proj", n * R2))
+    sizes.append(("readout", R * n))
+    if q.factored is not None:
+        sizes += [("input_proj", n * q.factored.input_proj.shape[2]), ("bias", 2 * n), ("input_scale", 4)]
+    else:
+        sizes.append(("table", 2 * n * q.table.shape[1]))
+    parts, pos = [], 0
+    for p, s in sizes:
+        parts.append((p, pos, s))
+        pos += s
+    return RecordLayout(tuple(parts), round_up(pos, ALIGN))
+
+
+def _part_bytes(q: QuantLayer, part: str, j0: int, j1: int) -> np.ndarray:
+    """(j1 - j0, bytes) of one record part of experts j0 .. j1 - 1."""
+    if part == "transition":
+        return pack_transition(q.transition[j0:j1])
+    if part == "layer_input_proj":
+        return pack_proj(q.layer_input_proj[j0:j1])
+    if part == "readout":
+        return pack_readout(q.readout[j0:j1])
+    if part == "table":
+        return np.ascontiguousarray(np.asarray(q.table[j0:j1], "<i2")).reshape(j1 - j0, -1).view(np.uint8)
+    fc = q.factored
+    if part == "input_proj":
+        return pack_proj(fc.input_proj[j0:j1])
+    if part == "bias":
+        return np.ascontiguousarray(np.asarray(fc.bias[j0:j1], "<i2")).view(np.uint8)
+    return np.ascontiguousarray(np.asarray(fc.input_scale[j0:j1], f32).reshape(-1, 1)).view(np.uint8)
+
+
+def pack_records(q: QuantLayer, layout: RecordLayout, j0: int, j1: int) -> np.ndarray:
+    """The records of experts j0 .. j1 - 1, zero-padded to layout.nbytes each."""
+    rec = np.zeros((j1 - j0, layout.nbytes), np.uint8)
+    for part, off, size in layout.parts:
+        rec[:, off:off + size] = _part_bytes(q, part, j0, j1)
+    return rec
+
+
+def _router_arrays(q: QuantLayer, n: int, V: int, R2: int) -> list:
+    """(tag, array) of a routed layer ahead of its records, in file order: thresholds (V, 2^D) with the node index
+    as column (column 0 belongs to no node), the optional group and factored arrays, the node weights (2^D, n) as
+    u8 (w + 128, row 0 for no node) and the layer-input down-projection with its row scales (rows padded to 16)."""
+    E = 2 ** q.depth
+    nodes = slice(1, E)
+    thr = np.zeros((V, E), f32)
+    thr[:, nodes] = q.router_threshold
+    out = [("thr", thr)]
+    if q.state_r2 is not None:
+        out.append(("r2b", np.asarray(q.state_r2, f32)))
+    if np.ndim(q.layer_input_scale):
+        out.append(("mulv", np.asarray(q.layer_input_scale, f32)))
+    if q.factored is not None:
+        out += [("vt", np.asarray(q.factored.token_code).astype(np.int8)),
+                ("mT", np.asarray(q.factored.token_scale, f32))]
+    weights = np.full((E, n), 128, np.uint8)
+    weights[nodes] = (np.asarray(q.router_weight, np.int64) + 128).astype(np.uint8)
+    out.append(("w", weights))
+    if R2:
+        scale = np.zeros(round_up(R2, 16), f32)
+        scale[:R2] = q.layer_input_down_scale
+        out += [("vl", pack_layer_input_down(q.layer_input_down, n)), ("mv", scale)]
+    return out
+
+
+def _readout_arrays(q: QuantLayer, V: int, R: int) -> list:
+    """(tag, array) after the records, in file order: Q, the per-class unembedding scales (group scales; zero for
+    padded classes), the per-(expert, row) readout scales (group scales; at R = 8 each row's scale twice, one per
+    kernel lane of the row's two halves) and the four scalars (0 where an array replaces one)."""
+    VP = round_up(V, CLASS_PAD)
+    out = [("Q", pack_unembed(q.unembed, VP))]
+    if np.ndim(q.unembed_scale):
+        per_class = np.zeros(VP, f32)
+        per_class[:V] = q.unembed_scale
+        out.append(("sqv", per_class))
+    if np.ndim(q.readout_scale):
+        rows = np.asarray(q.readout_scale, f32)
+        out.append(("mzl", np.repeat(rows, 2, axis=1) if R == 8 else rows))
+    values = {"readout_scale": q.readout_scale, "unembed_scale": q.unembed_scale, "rms_eps": q.rms_eps,
+              "layer_input_scale": q.layer_input_scale}
+    out.append(("scal", np.array([0 if values[s] is None or np.ndim(values[s]) else values[s] for s in SCALARS],
+                                 f32)))
+    return out
+
+
 def layer_arrays(l: int, q: QuantLayer, hdr: dict, record_chunk: int = 0) -> list:
-    """(name, array) of layer l in file order (the order of cpu/export.py:382-441).
+    """(name, array) of layer l in file order: a routed layer's router arrays, then meta and the expert records,
+    then the readout arrays (the order of cpu/export.py:382-441, which makes the file bytes the reference's).
 
     record_chunk > 0 streams the expert records in chunks of that many experts instead of building them at once."""
     n, V, R, R2 = hdr["d_state"], hdr["vocab"], hdr["readout_rank"], hdr["layer_input_rank"]
-    VP, tag, arrs = round_up(V, CLASS_PAD), f"l{l}_", []
-
-    def add(name, a):
-        arrs.append((tag + name, a if isinstance(a, Streamed) else np.ascontiguousarray(a)))
-    if not q.token_layer:
-        E = 2 ** q.depth
-        thr = np.zeros((V, E), f32)        # heap order from node 1: slot 0 unused
-        thr[:, 1:] = q.router_threshold
-        add("thr", thr)
-        if q.state_r2 is not None:
-            add("r2b", np.asarray(q.state_r2, f32))
-        if np.ndim(q.layer_input_scale):
-            add("mulv", np.asarray(q.layer_input_scale, f32))
-        if q.factored is not None:
-            add("vt", np.asarray(q.factored.token_code).astype(np.int8))
-            add("mT", np.asarray(q.factored.token_scale, f32))
-        w = np.zeros((E, n), np.int64)
-        w[1:] = q.router_weight
-        add("w", (w + 128).astype(np.uint8))
-        if R2:
-            add("vl", pack_layer_input_down(q.layer_input_down, n))
-            mv = np.zeros(round_up(R2, 16), f32)
-            mv[:R2] = q.layer_input_down_scale
-            add("mv", mv)
+    layout = record_layout(q, n, R, R2)
     E = len(q.transition)
-    sizes = {"transition": 2 * n * q.block}
-    if not q.token_layer and R2:
-        sizes["layer_input_proj"] = n * R2
-    sizes["readout"] = R * n
-    if q.factored is not None:
-        k = q.factored.input_proj.shape[2]
-        sizes.update(input_proj=n * k, bias=2 * n, input_scale=4)
-    else:
-        sizes["table"] = q.table.shape[1] * n * 2
-    offset, off = {k: -1 for k in RECORD}, 0
-    for k, s in sizes.items():
-        offset[k] = off
-        off += s
-    record_bytes = round_up(off, ALIGN)
-
-    def records(j0, j1):
-        rec = np.zeros((j1 - j0, record_bytes), np.uint8)
-        parts = {"transition": pack_transition(q.transition[j0:j1])}
-        if "layer_input_proj" in sizes:
-            parts["layer_input_proj"] = pack_proj(q.layer_input_proj[j0:j1])
-        parts["readout"] = pack_readout(q.readout[j0:j1])
-        if q.factored is not None:
-            fc = q.factored
-            parts["input_proj"] = pack_proj(fc.input_proj[j0:j1])
-            parts["bias"] = np.ascontiguousarray(np.asarray(fc.bias[j0:j1], "<i2")).view(np.uint8)
-            parts["input_scale"] = np.ascontiguousarray(np.asarray(fc.input_scale[j0:j1], f32)[:, None]).view(np.uint8)
-        else:
-            parts["table"] = np.ascontiguousarray(np.asarray(q.table[j0:j1], "<i2")).reshape(j1 - j0, -1).view(np.uint8)
-        for k, a in parts.items():
-            rec[:, offset[k]:offset[k] + sizes[k]] = a
-        return rec
-    meta = [record_bytes] + [offset[k] for k in RECORD]
-    add("meta", np.array(meta if q.factored is not None else meta[:-FACTORED_PARTS], np.int32))
     if record_chunk and E > record_chunk:
-        add("rec", Streamed(E * record_bytes,
-                            lambda: (records(j, min(E, j + record_chunk)) for j in range(0, E, record_chunk))))
+        records = Streamed(E * layout.nbytes, lambda: (pack_records(q, layout, j, min(E, j + record_chunk))
+                                                       for j in range(0, E, record_chunk)))
     else:
-        add("rec", records(0, E))
-    add("Q", pack_unembed(q.unembed, VP))
-    if np.ndim(q.unembed_scale):
-        sv = np.zeros(VP, f32)
-        sv[:V] = q.unembed_scale
-        add("sqv", sv)
-    if np.ndim(q.readout_scale):           # R = 8: kernel lane i holds row i / 2
-        add("mzl", np.repeat(np.asarray(q.readout_scale, f32), 2, axis=1) if R == 8
-            else np.asarray(q.readout_scale, f32))
-    scal = dict(readout_scale=q.readout_scale, unembed_scale=q.unembed_scale, rms_eps=q.rms_eps,
-                layer_input_scale=q.layer_input_scale)
-    add("scal", np.array([0 if v is None or np.ndim(v) else v for v in (scal[k] for k in SCALARS)], f32))
-    return arrs
+        records = pack_records(q, layout, 0, E)
+    body = [] if q.token_layer else _router_arrays(q, n, V, R2)
+    body += [("meta", layout.meta(q.factored is not None)), ("rec", records)]
+    body += _readout_arrays(q, V, R)
+    return [(f"l{l}_{tag}", a if isinstance(a, Streamed) else np.ascontiguousarray(a)) for tag, a in body]
 
 
 def write_container(path, hdr: dict, arrs: Sequence) -> int:

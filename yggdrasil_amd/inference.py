@@ -16,6 +16,7 @@ from __future__ import annotations
 
 import ctypes
 import math
+import os
 from pathlib import Path
 from typing import Optional
 
@@ -36,10 +37,34 @@ def _stream():
     return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
 
 
+def device_tokens(tokens, vocab: int, device, check_device: bool = False) -> torch.Tensor:
+    """tokens as a contiguous int32 tensor on device, without waiting for the GPU. Tokens given on the host (arrays,
+    lists, CPU tensors) are checked against [0, vocab) there (ValueError, as the reference rejects a bad token file up
+    front, cpu/ygg.cpp:493-495) and copied through pinned memory, stream-ordered. Tokens already on the GPU are not
+    read back, which would wait for every launch before them: a kernel stops a stream at a token outside [0, vocab)
+    and sets bit 0 of the model's error word (take_errors()). check_device (or YGG_CHECK_TOKENS=1) checks GPU tokens
+    too, at the cost of that wait."""
+    if isinstance(tokens, torch.Tensor) and tokens.device.type == "cuda":
+        x = tokens.to(device=device, dtype=torch.int32).contiguous()
+        if (check_device or os.environ.get("YGG_CHECK_TOKENS") == "1") and x.numel() and \
+                (int(x.min()) < 0 or int(x.max()) >= vocab):
+            raise ValueError(f"token out of range [0, {vocab})")
+        return x
+    a = tokens.numpy() if isinstance(tokens, torch.Tensor) else np.asarray(tokens)
+    if a.dtype.kind not in "iu":
+        raise ValueError(f"tokens must be integers, got {a.dtype}")
+    if a.size and (a.min() < 0 or a.max() >= vocab):
+        raise ValueError(f"token out of range [0, {vocab})")
+    host = torch.from_numpy(np.ascontiguousarray(a, np.int32))
+    if host.numel():
+        host = host.pin_memory()
+    return host.to(device, non_blocking=True)
+
+
 class Yggdrasil:
     """An int8 model on one GPU (the ``hip`` backend)."""
 
-    def __init__(self, path, device=None, graph: bool = False):
+    def __init__(self, path, device=None, graph: bool = False, check_tokens: bool = False):
         if not torch.cuda.is_available():
             raise RuntimeError("backend='hip' needs a ROCm GPU (torch.cuda.is_available() is False)")
         L = _lib.lib()
@@ -55,12 +80,14 @@ class Yggdrasil:
         self.layers, self.n, self.vocab = info.n_layers, info.d_state, info.vocab
         self.classes, self.depth = info.vocab, info.router_depth
         self.graph = graph
+        self.check_tokens = check_tokens
         self._graphs = {}
 
     @classmethod
     def load(cls, path, backend: str = "hip", **kw):
         """From an int8 model file (YGG1, cpu/export.py). backend "hip": the fused gfx950 step; kw device, graph
-        (replay one captured step per batch size, as the Triton backend's cuda_graph). A float checkpoint (.npz) loads
+        (replay one captured step per batch size, as the Triton backend's cuda_graph), check_tokens (also range-check
+        tokens that are already on the GPU, which waits for the stream). A float checkpoint (.npz) loads
         the float step instead (yggdrasil_amd.float_model.FloatYggdrasil; kw device, precision 32 or 64)."""
         if backend != "hip":
             raise ValueError(f"backend {backend!r}: hip")
@@ -102,14 +129,9 @@ class Yggdrasil:
         return torch.zeros(batch_size, self.layers, self.n, dtype=torch.int8, device=self.device)
 
     def _tokens(self, tokens, shape=None) -> torch.Tensor:
-        x = torch.as_tensor(tokens, device=self.device)
-        if x.dtype != torch.int32:
-            x = x.to(torch.int32)
-        x = x.contiguous()
+        x = device_tokens(tokens, self.vocab, self.device, self.check_tokens)
         if shape is not None and tuple(x.shape) != tuple(shape):
             raise ValueError(f"tokens of shape {tuple(x.shape)}, expected {tuple(shape)}")
-        if x.numel() and (int(x.min()) < 0 or int(x.max()) >= self.vocab):
-            raise ValueError(f"token out of range [0, {self.vocab})")
         return x
 
     def _check_state(self, state: torch.Tensor, B: int) -> torch.Tensor:
@@ -188,20 +210,30 @@ class Yggdrasil:
 
     # ------------------------------------------------------------------------------------------------ consumers
     @torch.no_grad()
-    def score(self, tokens, state: Optional[torch.Tensor] = None, batch: int = 1024) -> np.ndarray:
-        """Bits of tokens[:, 1:] given the tokens before them, per row of tokens (B, L), as float64 (B,).
-        Rows start from state, or from zero (yggdrasil/inference.py:179-188). One fused launch per batch of rows: the
-        step and the float64 log-softmax of the reference's score mode (cpu/ygg.cpp:513-516), no logits written."""
+    def score(self, tokens, state: Optional[torch.Tensor] = None, batch: int = 1024, targets=None) -> np.ndarray:
+        """Bits of tokens[:, 1:] given the tokens before them, per row of tokens (B, L), as float64 (B,); with
+        targets (B, L), bits of targets[:, t] given tokens[:, :t + 1] (every token an input, as the reference scores
+        windows x against their next tokens y). Rows start from state, or from zero (yggdrasil/inference.py:179-188).
+        One fused launch per batch of rows: the step and the float64 log-softmax of the reference's score mode
+        (cpu/ygg.cpp:513-516), no logits written."""
         tokens = np.atleast_2d(np.asarray(tokens, np.int64))
+        if targets is not None:
+            targets = np.atleast_2d(np.asarray(targets, np.int64))
+            if targets.shape != tokens.shape:
+                raise ValueError(f"targets {targets.shape} for tokens {tokens.shape}")
         out = []
         for i in range(0, len(tokens), batch):
-            x = self._tokens(tokens[i:i + batch])
-            B, Lw = x.shape
+            rows = tokens[i:i + batch]
+            if targets is None:
+                xin, tgt = rows[:, :-1], rows[:, 1:]
+            else:
+                xin, tgt = rows, targets[i:i + batch]
+            B, T = xin.shape
             st = self.init_state(B) if state is None else self._check_state(state[i:i + B], B).clone()
             nll = torch.zeros(B, dtype=torch.float64, device=self.device)
-            if Lw > 1:
-                xin, tgt = x[:, :-1].contiguous(), x[:, 1:].contiguous()
-                check(_lib.lib().ygg_score(self._h, _ptr(xin), _ptr(tgt), B, Lw - 1, _ptr(st), _ptr(nll), _stream()))
+            if T > 0:
+                xd, yd = self._tokens(np.ascontiguousarray(xin)), self._tokens(np.ascontiguousarray(tgt))
+                check(_lib.lib().ygg_score(self._h, _ptr(xd), _ptr(yd), B, T, _ptr(st), _ptr(nll), _stream()))
             out.append((nll / LN2).cpu().numpy())
         return np.concatenate(out) if out else np.zeros(0)
 
