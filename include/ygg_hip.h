@@ -68,6 +68,13 @@ typedef struct {
                                   another YGG_KERNEL at load time). YGG_KERNEL=flow uses it for every call but
                                   ygg_generate */
     int32_t router_rounds;     /* rounds of the router plan (levels read per dependent step of the descent) */
+    int32_t solo_max_streams;  /* calls with B at most this use the kernel with all four wavefronts of a workgroup on
+                                  one stream (the router rows of its first 8 levels in registers, the rest in one
+                                  round): only with YGG_KERNEL=solo at load time, which uses it for every call but
+                                  ygg_score and digest runs (INT32_MAX); 0 otherwise, and for router plans whose first
+                                  two rounds take more than 8 levels or whose later ones more than 6, or
+                                  (L - 1) d_state > 512 */
+    int32_t reserved;          /* 0 (keeps the 64-bit fields below 8-byte aligned) */
     int64_t file_array_bytes;  /* bytes of the file's arrays (the reference's Model::bytes, cpu/ygg.cpp:158, 167) */
     int64_t device_bytes;      /* device memory held by the model */
     int64_t gather_bytes[8];   /* per layer: bytes of one expert's transition, layer-input and readout weights */

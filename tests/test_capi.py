@@ -51,8 +51,9 @@ def test_exports_every_declared_symbol(lib):
 def test_version_and_info_layout(lib):
     L = lib.lib()
     assert L.ygg_version() == lib.ABI_VERSION
-    # ygg_info: 16 int32 + 2 int64 + 8 int64
-    assert ctypes.sizeof(lib.YggInfo) == 20 * 4 + 8 * 10
+    # ygg_info: 22 int32 (the last reserved, for the alignment of what follows) + 2 int64 + 8 int64
+    assert ctypes.sizeof(lib.YggInfo) == 22 * 4 + 8 * 10
+    assert lib.YggInfo.file_array_bytes.offset == 22 * 4
 
 
 def test_bad_arguments(lib):

@@ -23,8 +23,10 @@ def _say(msg):
     print(msg, flush=True)
 
 
-def _model(cfg: int) -> Path:
-    w = synth.CONFIGS[cfg]
+def _model(cfg) -> Path:
+    """The model file of configuration cfg (an int), or of configuration 4 with its routed inputs stored factored at
+    rank 64 ("4f": bench.py --storage factored)."""
+    w = _workload(cfg)
     cache = Path(os.environ.get("YGG_BENCH_DIR", "/tmp/ygg_bench"))
     cache.mkdir(parents=True, exist_ok=True)
     p = cache / f"{w.name}_seed{w.model_seed}.bin"
@@ -57,11 +59,19 @@ def _gpu_sums(model, x: np.ndarray):
     return out
 
 
+def _workload(cfg):
+    import dataclasses
+    if cfg == "4f":
+        w = synth.CONFIGS[4]
+        return dataclasses.replace(w, name=w.name + "_factored", spec=dataclasses.replace(w.spec, input_rank=64))
+    return synth.CONFIGS[cfg]
+
+
 @pytest.mark.timeout(900)
-@pytest.mark.parametrize("cfg", [2, 3, 5, 4])
+@pytest.mark.parametrize("cfg", [2, 3, 5, 4, "4f"])
 def test_full_size_digest(cfg):
     from yggdrasil_amd.inference import Yggdrasil
-    w = synth.CONFIGS[cfg]
+    w = _workload(cfg)
     path = _model(cfg)
     x = w.make_tokens()
     B, T = x.shape
@@ -84,10 +94,11 @@ def test_full_size_digest(cfg):
 @pytest.mark.timeout(600)
 @pytest.mark.parametrize("cfg", [3, 4])
 def test_few_streams_full_model(cfg, monkeypatch):
-    """The few-stream kernels on the full configuration 3 and 4 models (D = 13 and 14: the deep descent ends in one
-    round of 63 nodes): 6 streams x 40 tokens through the kernel the library picks (layer-pipelined) and greedy
-    generation (the deep kernel), then through the deep kernel forced for every call (one launch, launches of 3
-    tokens, a step loop). Every leaf, state after every token, logit and generated token equals the oracle's."""
+    """The few-stream kernels on the full configuration 3 and 4 models (D = 13 and 14: the deep descent and the solo
+    kernel end in one round of 63 nodes): 6 streams x 40 tokens through the kernel the library picks
+    (layer-pipelined) and greedy generation (the deep kernel), then through the deep kernel forced for every call
+    (one launch, launches of 3 tokens, a step loop), then the solo kernel forced (one launch, a step loop, greedy
+    generation). Every leaf, state after every token, logit and generated token equals the oracle's."""
     import torch
     from yggdrasil_amd.inference import Yggdrasil
     w = synth.CONFIGS[cfg]
@@ -102,20 +113,22 @@ def test_few_streams_full_model(cfg, monkeypatch):
             assert np.array_equal(a, b), f"config {cfg} {what}: {k} differs at {np.argwhere(a != b)[:4].tolist()}"
 
     monkeypatch.delenv("YGG_DEEP", raising=False)
-    for k in ("auto", "deep"):
+    for k in ("auto", "deep", "solo"):
         if k == "auto":
             monkeypatch.delenv("YGG_KERNEL", raising=False)
         else:
             monkeypatch.setenv("YGG_KERNEL", k)
         model = Yggdrasil.load(path)
-        assert model.info.deep == 1 and model.info.kernel == 1 and model.info.deep_max_streams > 0
+        assert model.info.deep == 1 and model.info.kernel == 1
+        assert (model.info.deep_max_streams > 0) == (k != "solo")
+        assert (model.info.solo_max_streams > 0) == (k == "solo")
         _say(f"config {cfg}: 6 x 40, kernel {k}, pipe_max {model.info.pipe_max_streams}, "
-             f"deep_max {model.info.deep_max_streams}")
+             f"deep_max {model.info.deep_max_streams}, solo_max {model.info.solo_max_streams}")
         r = model.run(x, leaves=True, states=True)
         torch.cuda.synchronize()
         same({key: v.cpu().numpy() for key, v in r.items()}, f"{k} one launch")
-        if k == "auto":
-            # greedy generation of 12 tokens after a 4-token prompt: the oracle's argmax loop
+        if k in ("auto", "solo"):
+            # greedy generation of 12 tokens after a 4-token prompt (deep or solo kernel): the oracle's argmax loop
             out = model.generate(x[:, :4], 12, temperature=0)
             r0 = orc.run(x[:, :4])
             lg, st = r0["logits"][:, -1], r0["state"]
@@ -124,7 +137,14 @@ def test_few_streams_full_model(cfg, monkeypatch):
                 assert np.array_equal(out[:, 4 + i], tok), (cfg, i)
                 r1 = orc.run(tok[:, None], state=st)
                 lg, st = r1["logits"][:, 0], r1["state"]
-        else:
+        if k == "solo":
+            # one-token steps (the solo kernel) with the state carried
+            st = model.init_state(6)
+            for t in range(8):
+                lg, st = model.step(x[:, t], st)
+                assert np.array_equal(lg.cpu().numpy(), ref["logits"][:, t]), (cfg, t)
+                assert np.array_equal(st.cpu().numpy(), ref["states"][:, t]), (cfg, t)
+        elif k == "deep":
             parts, st = [], None
             for t0 in range(0, 39, 3):
                 rr = model.run(x[:, t0:t0 + 3], state=st, leaves=True, states=True)

@@ -19,7 +19,7 @@ SYMBOLS = ("ygg_load", "ygg_load_blob", "ygg_model_info", "ygg_free", "ygg_step"
            "ygg_float_free", "ygg_kernel_name", "ygg_last_error", "ygg_version")
 
 ERRORS = {1: "io", 2: "format", 3: "limits", 4: "nomem", 5: "arg", 6: "token", 7: "device"}
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 
 class FloatLayer(ctypes.Structure):
@@ -40,7 +40,7 @@ class YggInfo(ctypes.Structure):
     _fields_ = [(name, ctypes.c_int32) for name in (
         "n_layers", "d_state", "block_size", "vocab", "vocab_pad", "router_depth", "n_experts", "readout_rank",
         "layer_input_rank", "input_rank", "shift", "factored", "group", "device", "kernel",
-        "pipe_max_streams", "deep", "deep_max_streams", "flow_max_streams", "router_rounds")] + [
+        "pipe_max_streams", "deep", "deep_max_streams", "flow_max_streams", "router_rounds", "solo_max_streams", "reserved")] + [
         ("file_array_bytes", ctypes.c_int64), ("device_bytes", ctypes.c_int64),
         ("gather_bytes", ctypes.c_int64 * 8)]
 

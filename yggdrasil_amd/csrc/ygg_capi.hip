@@ -397,6 +397,9 @@ struct ygg_model {
     ygg::Kernel flow;                 // router rounds and updates pipelined over ticks: T > 1, B <= flow_max_streams[mode]
     int flow_max_streams[3] = {0, 0, 0};
     bool flow_all = false;            // YGG_KERNEL=flow: every call but generation
+    ygg::Kernel solo;                 // all wavefronts on one stream: one-token calls and generation, B <= solo_max_streams
+    int solo_max_streams = 0;
+    bool solo_all = false;            // YGG_KERNEL=solo: every call but score and digest calls
 };
 
 namespace {
@@ -441,11 +444,14 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
         return false;
     };
     const int R2f = L == 1 ? 16 : R2;
-    const int64_t rec_bound = (int64_t)n * (2 * fa.blk + R2 + R) + 128;     // gather record bytes, at most
+    const int64_t rec_bound = (int64_t)n * (2 * fa.blk + R2 + R) + 128 +   // gather record bytes, at most
+                              (factored ? (int64_t)fa.K * n + 2 * n + 4 : 0);
     const bool small_tables = (int64_t)E * V * n * 2 < ((int64_t)1 << 32) && (int64_t)E * rec_bound < ((int64_t)1 << 32);
-    if (kmode != "generic" && fa.blk == 16 && shape_ok(n, R, R2f) && !factored && L <= ygg::kMaxFastLayers &&
-        VP <= 256 && small_tables && transitions_split(fa, fl))
-        fast = ygg::find_fast_launcher(n, R, R2f, L, true, group);
+    // (factored routed inputs: fact_kernel, input ranks up to 64; the other specialised kernels take table storage)
+    if (kmode != "generic" && fa.blk == 16 && shape_ok(n, R, R2f) && L <= ygg::kMaxFastLayers && VP <= 256 &&
+        small_tables && (!factored || fa.K <= YGG_MAX_FACT_RANK) && transitions_split(fa, fl))
+        fast = factored ? ygg::find_fact_launcher(n, R, R2f, L, true, group)
+                        : ygg::find_fast_launcher(n, R, R2f, L, true, group);
     if (fast) launch = fast;
 
     RoundPlan rplan = round_plan(L > 1 ? fa.D : 0);
@@ -469,20 +475,29 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     // the deep descent: at most 4 rounds, the first of at least 2 levels, the rounds after the second at most 6
     // levels together (one lane per node)
     const char *denv = getenv("YGG_DEEP");
-    const bool deep = fast && L > 1 && !(denv && !strcmp(denv, "0")) && rplan.n >= 2 && rplan.n <= 4 &&
+    const bool deep = fast && !factored && L > 1 && !(denv && !strcmp(denv, "0")) && rplan.n >= 2 && rplan.n <= 4 &&
                       rplan.h[0] >= 2 && (rplan.n < 4 || rplan.h[2] + rplan.h[3] <= 6);
+    // the solo kernel: the first two rounds at most 8 levels together (its round A, from registers), the others at
+    // most 6 (one round with a lane per node); round A's rows of every routed layer in a lane's registers
+    const char *senv = getenv("YGG_SOLO");
+    const bool solo_plan = rplan.n >= 1 && rplan.n <= 4 && (rplan.n < 2 || rplan.h[0] + rplan.h[1] <= 8) &&
+                           (rplan.n < 4 || rplan.h[2] + rplan.h[3] <= 6);
+    ygg::Kernel solok;
+    if (fast && !factored && L > 1 && solo_plan && (L - 1) * n <= 512 && !(senv && !strcmp(senv, "0")) &&
+        kmode == "solo")
+        solok = ygg::find_solo_launcher(n, R, R2f, L, group);
     ygg::Kernel pipe, pipe_few, deepk, flowk;
-    if (fast && kmode != "fast" && kmode != "deep" && kmode != "flow") {
+    if (fast && !factored && kmode != "fast" && kmode != "deep" && kmode != "flow" && kmode != "solo") {
         pipe = ygg::find_pipe_launcher(n, R, R2f, L, true, group);
         pipe_few = ygg::find_pipe_launcher(n, R, R2f, L, false, group);
     }
     // the tick-pipelined kernel: plans of 3 or 4 rounds (YGG_FLOW=0: off)
     const char *fenv = getenv("YGG_FLOW");
-    if (fast && L > 1 && (kmode == "" || kmode == "flow") && !(fenv && !strcmp(fenv, "0")))
+    if (fast && !factored && L > 1 && (kmode == "" || kmode == "flow") && !(fenv && !strcmp(fenv, "0")))
         flowk = ygg::find_flow_launcher(n, R, R2f, L, rplan.n, group);
     // (the deep kernel exists where its LDS fits a workgroup)
     const ygg::Kernel deep_avail = deep ? ygg::find_deep_launcher(n, R, R2f, L, group) : ygg::Kernel();
-    if (kmode != "fast" && kmode != "pipe" && kmode != "flow") deepk = deep_avail;
+    if (kmode != "fast" && kmode != "pipe" && kmode != "flow" && kmode != "solo") deepk = deep_avail;
     const int64_t slots = plan_slots(rplan);
     // device arena plan: every array 256-byte aligned
     struct Piece { size_t off, bytes; };
@@ -629,15 +644,24 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     for (int md : {kModeRun, kModeScore})
         m->flow_max_streams[md] =
             flowk ? (m->flow_all ? INT32_MAX : ygg::flow_blocks_per_cu(n, R, R2f, L, rplan.n, group, md) * cus) : 0;
+    // the solo kernel only when forced (YGG_KERNEL=solo): measured slower than the per-stream kernel for one-token
+    // steps and than the deep kernel for generation on the benchmark shapes (round A's arithmetic and barrier on one
+    // wavefront per SIMD cost about what the memory round trips they remove cost)
+    m->solo = solok;
+    m->solo_all = solok && kmode == "solo";
+    m->solo_max_streams = m->solo_all ? INT32_MAX : 0;
     m->device = device;
     m->arena = arena;
     m->arena_bytes = total;
     m->run = launch;
     // the uncapped per-stream build while every stream of the call is resident with it
     if (fast) {
-        m->run_few = ygg::find_fast_launcher(n, R, R2f, L, false, group);
+        m->run_few = factored ? ygg::find_fact_launcher(n, R, R2f, L, false, group)
+                              : ygg::find_fast_launcher(n, R, R2f, L, false, group);
         for (int md = 0; md < 3; md++)
-            m->run_few_max_streams[md] = ygg::fast_blocks_per_cu(n, R, R2f, L, false, group, md) * 4 * cus;
+            m->run_few_max_streams[md] = (factored ? ygg::fact_blocks_per_cu(n, R, R2f, L, false, group, md)
+                                                   : ygg::fast_blocks_per_cu(n, R, R2f, L, false, group, md)) *
+                                         4 * cus;
     }
     uint8_t *A = (uint8_t *)arena;
     auto at = [&](const Piece &p) -> void * { return p.bytes ? A + p.off : nullptr; };
@@ -688,6 +712,7 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     I.deep_max_streams = m->deep_max_streams;
     I.flow_max_streams = m->flow_max_streams[kModeRun];
     I.router_rounds = L > 1 ? rplan.n : 0;
+    I.solo_max_streams = m->solo_max_streams;
     I.file_array_bytes = fa.bytes;
     I.device_bytes = (int64_t)total;
     for (int l = 0; l < L; l++) I.gather_bytes[l] = lp[l].gl.bytes;
@@ -700,13 +725,16 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
 constexpr int kFlowMinTokens = 32;
 
 // The kernel of a call of B streams and T tokens in mode (kModeRun, kModeGenerate: ygg_generate, kModeScore: a
-// digest or NLL). Generation: the deep kernel for >= 8 tokens and B <= deep_max_streams, else the per-stream kernel
+// digest or NLL). YGG_KERNEL=solo: the solo kernel (all wavefronts of a workgroup on one stream) for every call but
+// score calls. Generation: the deep kernel for >= 8 tokens and B <= deep_max_streams, else the per-stream kernel
 // (every token needs all layers of the one before it, so never a layer-pipelined one). Otherwise: the tick-pipelined
 // kernel for T >= kFlowMinTokens when its workgroups fit, the layer-pipelined kernel for T > 1 when its workgroups
 // fit, else the per-stream kernel. Of the two builds of a kernel, the uncapped one while all B streams are resident
 // with it. A kernel forced by YGG_KERNEL takes every call it can run.
 const ygg::Kernel &pick(const ygg_model *m, int B, int T, int mode) {
     const bool gen = mode == kModeGenerate;
+    if (m->solo && mode != kModeScore && (m->solo_all || (B <= m->solo_max_streams && (gen || T == 1))))
+        return m->solo;
     if (m->deep_all) return m->deep;
     if (gen && m->deep && B <= m->deep_max_streams && T >= 8) return m->deep;
     if (!gen && m->flow && (m->flow_all || (T >= kFlowMinTokens && B <= m->flow_max_streams[mode]))) return m->flow;
@@ -737,7 +765,7 @@ int set_error(int code, const char *msg) { return fail(code, "%s", msg); }
 
 extern "C" {
 
-int ygg_version(void) { return 8; }
+int ygg_version(void) { return 9; }
 
 const char *ygg_last_error(void) { return g_err.c_str(); }
 

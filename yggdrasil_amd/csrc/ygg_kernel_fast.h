@@ -56,15 +56,22 @@ template <int N_, int R_, int R2_> struct Shape : Fast<N_> {
     static constexpr int ZQ = R > 16 ? R : 16, ZL = R2 > 16 ? R2 : 16;    // LDS bytes of zq and zl
 };
 
-// the per-expert registers of one stream and layer
-template <class SH> struct Gather {
+// factored input storage (cpu/ygg.cpp:339-358): input ranks up to 64, this many dwords per coordinate
+constexpr int kFactK4 = YGG_MAX_FACT_RANK / 4;
+
+// the per-expert registers of one stream and layer. FACT: the model stores its routed inputs factored (the routed
+// layers' records hold U_r, c_r and su_r instead of a table)
+template <class SH, bool FACT = false> struct Gather {
     uint32_t aw[SH::AW], pw[SH::SPW], uw[SH::K4][SH::C];
     // the table row's C int16 entries of this lane as loaded: packed in pairs (C >= 2) or one sign-extended entry
-    // (C = 1); unpacked where the update reads them, so that nothing waits for the load in between
+    // (C = 1); unpacked where the update reads them, so that nothing waits for the load in between. FACT, routed: the
+    // factored bias c_r's entries, packed the same way
     int trw[(SH::C + 1) / 2];
     float mzr;             // group scales: the readout scale of this lane's readout row (m_z of the expert's row)
+    uint32_t fw[FACT ? kFactK4 : 1][SH::C];   // FACT: U_r, this lane's C dwords per 4 ranks (the U' layout)
+    float fs;                                  // FACT: su_r
 };
-template <class SH> __device__ __forceinline__ int table_entry(const Gather<SH> &G, int c) {
+template <class SH, bool FACT> __device__ __forceinline__ int table_entry(const Gather<SH, FACT> &G, int c) {
     if constexpr (SH::C == 1) return G.trw[0];
     else return (c & 1) ? (G.trw[c >> 1] >> 16) : (int)(int16_t)(G.trw[c >> 1] & 0xffff);
 }
@@ -493,8 +500,10 @@ __device__ __forceinline__ int descend_deep(const YggDevModel &m, const YggDevLa
 // the expert's whole gather record and table row, in one burst
 // MZ: the model has group scales (the expert's readout row scales, in every layer). UW = false: not U' (its user
 // has the layer-input term from elsewhere)
-template <class SH, bool MZ = false, bool UW = true>
-__device__ __forceinline__ void gather(Gather<SH> &G, const YggDevLayer &y, int r, int x, bool routed, int lane) {
+// FACT, routed: U_r's first K4 dwords per coordinate (K4 = input rank / 4), c_r and su_r instead of the table row
+template <class SH, bool MZ = false, bool UW = true, bool FACT = false>
+__device__ __forceinline__ void gather(Gather<SH, FACT> &G, const YggDevLayer &y, int r, int x, bool routed, int lane,
+                                       int K4 = 0) {
     using F = SH;
     // a layer's records and tables lie within 4 GiB (checked at load): 32-bit offsets
     const uint8_t *g = y.gath + (uint32_t)r * (uint32_t)y.gath_bytes;
@@ -515,13 +524,26 @@ __device__ __forceinline__ void gather(Gather<SH> &G, const YggDevLayer &y, int 
         }
         const int16_t *tr = y.table + ((uint32_t)r * (uint32_t)y.table_sr + (uint32_t)x * (uint32_t)y.table_sx) +
                             F::C * lane;
+        if (FACT && routed) tr = (const int16_t *)(g + y.off_FB) + F::C * lane;     // c_r in the record
         if constexpr (F::C == 1) {
             G.trw[0] = tr[0];
         } else {
 #pragma unroll
             for (int c = 0; c < F::C / 2; c++) G.trw[c] = (int)((const uint32_t *)tr)[c];
         }
+        if constexpr (FACT) {
+#pragma unroll
+            for (int k4 = 0; k4 < kFactK4; k4++) {
+                uint32_t tmp[F::C];
+#pragma unroll
+                for (int c = 0; c < F::C; c++) tmp[c] = 0u;
+                if (routed && k4 < K4) load_words<F::C, 4 * F::C>(tmp, g + y.off_F + ((k4 * F::NL + lane) * F::C) * 4);
+#pragma unroll
+                for (int c = 0; c < F::C; c++) G.fw[k4][c] = tmp[c];
+            }
+        }
     }
+    if constexpr (FACT) G.fs = routed ? *(const float *)(g + y.off_FS) : 0.0f;
     // (a model with group scales has the row scales in every layer; without, the readout scale is the layer's)
     if constexpr (MZ) G.mzr = y.mz[(uint32_t)r * SH::R + lane / SH::RL];
     else G.mzr = 0.0f;
@@ -621,10 +643,13 @@ __device__ __forceinline__ void uw_products(int (&d)[SH::C], const uint32_t (&uw
 // with A16 = 256 hi + lo, so A16 q = 256 (hi q) + (lo q) exactly, two v_dot4 chains on the raw int8 state.
 // MUL: per-coordinate layer-input scales at mul (group scales; LDS), else the layer's one scale. PRE: the products
 // U'_r zl of this lane's coordinates come computed, at dpre (LDS), instead of from G.uw and zls
-template <class SH, bool MUL = false, bool PRE = false>
-__device__ __forceinline__ void update(int (&qn)[SH::C], const Gather<SH> &G, const int8_t *qold,
+// FACT, routed: the input is rint(f32(U_r v[x]) f32(su_r mT_i)) + c_r (cpu/ygg.cpp:339-358) instead of the table row;
+// vx the token's code v[x] (K4 dwords, the same for every lane)
+template <class SH, bool MUL = false, bool PRE = false, bool FACT = false>
+__device__ __forceinline__ void update(int (&qn)[SH::C], const Gather<SH, FACT> &G, const int8_t *qold,
                                        const int8_t *zls, const YggDevLayer &y, bool routed, int shift, int lane,
-                                       const float *mul = nullptr, const int *dpre = nullptr) {
+                                       const float *mul = nullptr, const int *dpre = nullptr,
+                                       const uint32_t *vx = nullptr, int K4 = 0) {
     using F = SH;
     constexpr int BLK = F::BLK, C = F::C, RW = BLK / 4;     // dwords of one row's hi (and of its lo) bytes
     const int blk0 = (C * lane / BLK) * BLK;
@@ -639,7 +664,18 @@ __device__ __forceinline__ void update(int (&qn)[SH::C], const Gather<SH> &G, co
         a <<= 8;
 #pragma unroll
         for (int i = 0; i < RW; i++) a = dot4(G.aw[c * 2 * RW + RW + i], qv[i], a);
-        acc[c] = wadd((a + (1 << (shift - 1))) >> shift, table_entry(G, c));
+        int in = table_entry(G, c);
+        if constexpr (FACT) {
+            if (routed) {
+                int d = 0;
+#pragma unroll
+                for (int k4 = 0; k4 < kFactK4; k4++)
+                    if (k4 < K4) d = dot4(G.fw[k4][c], vx[k4], d);
+                const float fm = G.fs * y.mT[F::C * lane + c];
+                in = wadd(cvt_rne((float)d * fm), in);
+            }
+        }
+        acc[c] = wadd((a + (1 << (shift - 1))) >> shift, in);
     }
     if (routed) {
         int d[C];
@@ -740,11 +776,10 @@ __device__ __forceinline__ void store_logits(float *o, const float (&lg)[4], int
 // descend. CAP (not DEEP): at most 128 VGPRs, 4 wavefronts per SIMD (the most streams resident, some registers
 // spilled), else up to 256 (no spills; for calls whose streams all fit at the lower occupancy).
 // GROUP: the model has group scales (the tables of GroupTables and the experts' readout row scales)
-template <int N, int R, int R2, int L, int MODE, bool DEEP, bool CAP, bool GROUP>
-__global__ __launch_bounds__(64 * kFastWaves)
-__attribute__((amdgpu_waves_per_eu(DEEP ? 1 : (CAP ? 4 : 2))))
-void fast_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B, int T, int8_t *__restrict__ state,
-                 const YggIO io) {
+// FACT: the model stores its routed inputs factored (fact_kernel); only with DEEP = false
+template <int N, int R, int R2, int L, int MODE, bool DEEP, bool CAP, bool GROUP, bool FACT>
+__device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *__restrict__ tokens, int B, int T,
+                                          int8_t *__restrict__ state, const YggIO &io) {
     float *__restrict__ logits = io.logits;
     int32_t *__restrict__ leaves = io.leaves;
     int8_t *__restrict__ states = io.states;
@@ -767,6 +802,7 @@ void fast_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
     const int tid = threadIdx.x, wv = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int s = blockIdx.x * W + wv;
     const int V = m.V, VP = m.VP;
+    const int K4 = FACT ? m.K / 4 : 0;         // factored input rank / 4
     const bool live = wv < W && s < B;
     // The stream's first token and its state are read before the LDS tables are staged, so that their loads overlap
     // (a launch of one token would otherwise wait for them one after the other).
@@ -882,14 +918,17 @@ void fast_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
                                         rho, x, lane, tl, flush);
                 }
             }
-            Gather<SH> G;
-            gather<SH, GROUP>(G, y, r, x, l > 0, lane);
+            Gather<SH, FACT> G;
+            gather<SH, GROUP, true, FACT>(G, y, r, x, l > 0, lane, K4);
             if (l > 0) layer_input<SH>(zls, S.V[l - 1], S.mv[l - 1], qbw, rho, lane);
             wave_sync();
             int qn[F::C];
             const float *mul = nullptr;
             if constexpr (GROUP) mul = GT.mul[l > 0 ? l - 1 : 0];
-            if (lane < F::NL) update<SH, GROUP>(qn, G, qs + l * N, zls, y, l > 0, m.shift, lane, mul);
+            const uint32_t *vx = nullptr;
+            if constexpr (FACT) vx = (const uint32_t *)(y.vt + (size_t)x * m.K);
+            if (lane < F::NL)
+                update<SH, GROUP, false, FACT>(qn, G, qs + l * N, zls, y, l > 0, m.shift, lane, mul, nullptr, vx, K4);
             wave_sync();
             if (lane < F::NL) {
 #pragma unroll
@@ -924,6 +963,26 @@ void fast_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
     for (int i = lane; i < L * N; i += 64) st[i] = qs[i];
     if (SCORE && digest && lane == 0) digest[s] = dg;
     if (SCORE && nll && lane == 0) nll[s] += nacc;
+}
+
+
+template <int N, int R, int R2, int L, int MODE, bool DEEP, bool CAP, bool GROUP>
+__global__ __launch_bounds__(64 * kFastWaves)
+__attribute__((amdgpu_waves_per_eu(DEEP ? 1 : (CAP ? 4 : 2))))
+void fast_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B, int T, int8_t *__restrict__ state,
+                 const YggIO io) {
+    fast_body<N, R, R2, L, MODE, DEEP, CAP, GROUP, false>(m, tokens, B, T, state, io);
+}
+
+// fast_kernel for models whose routed layers store their input factored (cpu/ygg.cpp:339-358, input rank <= 64): a
+// routed expert's gather record holds U_r, c_r and su_r beside A16, U' and P; the token's code v[x] and the
+// coordinate scales mT are read from the layer's arrays
+template <int N, int R, int R2, int L, int MODE, bool CAP, bool GROUP>
+__global__ __launch_bounds__(64 * kFastWaves)
+__attribute__((amdgpu_waves_per_eu(CAP ? 4 : 2)))
+void fact_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B, int T, int8_t *__restrict__ state,
+                 const YggIO io) {
+    fast_body<N, R, R2, L, MODE, false, CAP, GROUP, true>(m, tokens, B, T, state, io);
 }
 
 // ----------------------------------------------------------------------------------------------- pipe_kernel

@@ -54,6 +54,9 @@ Kernel find_launcher(int n, int blk, int R);                            // run_k
 // fast_kernel, 4 streams per workgroup, 128-VGPR cap or none (ygg_kernels_fast.hip); its resident workgroups per CU
 Kernel find_fast_launcher(int n, int R, int R2, int L, bool cap, bool group);
 int fast_blocks_per_cu(int n, int R, int R2, int L, bool cap, bool group, int mode);
+// fact_kernel: fast_kernel for factored routed inputs (ygg_kernels_fact.hip), 2 to 5 layers
+Kernel find_fact_launcher(int n, int R, int R2, int L, bool cap, bool group);
+int fact_blocks_per_cu(int n, int R, int R2, int L, bool cap, bool group, int mode);
 // fast_kernel with the deep descent, one stream per workgroup; pipe_kernel, 128-VGPR cap or none
 // (ygg_kernels_deep.hip)
 Kernel find_deep_launcher(int n, int R, int R2, int L, bool group);
@@ -63,5 +66,8 @@ int pipe_blocks_per_cu(int n, int R, int R2, int L, bool cap, bool group, int mo
 // (ygg_kernels_flow.hip); the resident workgroups per CU of its build for a mode (kModeRun or kModeScore)
 Kernel find_flow_launcher(int n, int R, int R2, int L, int P, bool group);
 int flow_blocks_per_cu(int n, int R, int R2, int L, int P, bool group, int mode);
+// solo_kernel, one stream per workgroup with all four wavefronts on it (ygg_kernels_solo.hip): router plans of at
+// most 4 rounds whose first two take at most 8 levels and the others at most 6
+Kernel find_solo_launcher(int n, int R, int R2, int L, bool group);
 
 }  // namespace ygg

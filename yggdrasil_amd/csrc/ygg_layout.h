@@ -43,6 +43,7 @@
 
 #define YGG_MAX_LAYERS 8
 #define YGG_MAX_RANK 64
+#define YGG_MAX_FACT_RANK 64      // factored input ranks the specialised kernels take
 
 struct YggDevLayer {
     const uint8_t *gath;     // E gather records
