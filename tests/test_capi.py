@@ -51,7 +51,7 @@ def test_exports_every_declared_symbol(lib):
 def test_version_and_info_layout(lib):
     L = lib.lib()
     assert L.ygg_version() == lib.ABI_VERSION
-    # ygg_info: 22 int32 (the last reserved, for the alignment of what follows) + 2 int64 + 8 int64
+    # ygg_info: 22 int32 + 2 int64 + 8 int64
     assert ctypes.sizeof(lib.YggInfo) == 22 * 4 + 8 * 10
     assert lib.YggInfo.file_array_bytes.offset == 22 * 4
 
@@ -64,6 +64,7 @@ def test_bad_arguments(lib):
     assert L.ygg_load_blob(None, 10, 0, ctypes.byref(h)) == 5
     assert L.ygg_model_info(None, None) == 5
     assert L.ygg_run(None, None, 1, 1, None, None, None, None, None, None) == 5
+    assert L.ygg_run_grouped(None, None, 1, 1, None, None, None, None, None, None) == 5
     assert L.ygg_step(None, None, None, None, None, None, 1, None) == 5
     assert L.ygg_take_errors(None, None, None) == 5
     assert L.ygg_generate(None, None, 1, 1, None, 0.0, 0, 0, None, None, None) == 5

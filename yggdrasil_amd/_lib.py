@@ -14,12 +14,13 @@ import torch  # noqa: F401  (must precede the CDLL below, see the module docstri
 LIB_PATH = Path(__file__).resolve().parent / "libygg_hip.so"
 
 # every entry point of include/ygg_hip.h
-SYMBOLS = ("ygg_load", "ygg_load_blob", "ygg_model_info", "ygg_free", "ygg_step", "ygg_run", "ygg_score",
+SYMBOLS = ("ygg_load", "ygg_load_blob", "ygg_model_info", "ygg_free", "ygg_step", "ygg_run", "ygg_run_grouped",
+           "ygg_score",
            "ygg_generate", "ygg_take_errors", "ygg_float_load", "ygg_float_run", "ygg_float_take_errors",
            "ygg_float_free", "ygg_kernel_name", "ygg_last_error", "ygg_version")
 
 ERRORS = {1: "io", 2: "format", 3: "limits", 4: "nomem", 5: "arg", 6: "token", 7: "device"}
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 
 class FloatLayer(ctypes.Structure):
@@ -40,7 +41,7 @@ class YggInfo(ctypes.Structure):
     _fields_ = [(name, ctypes.c_int32) for name in (
         "n_layers", "d_state", "block_size", "vocab", "vocab_pad", "router_depth", "n_experts", "readout_rank",
         "layer_input_rank", "input_rank", "shift", "factored", "group", "device", "kernel",
-        "pipe_max_streams", "deep", "deep_max_streams", "flow_max_streams", "router_rounds", "solo_max_streams", "reserved")] + [
+        "pipe_max_streams", "deep", "deep_max_streams", "flow_max_streams", "router_rounds", "solo_max_streams", "grouped")] + [
         ("file_array_bytes", ctypes.c_int64), ("device_bytes", ctypes.c_int64),
         ("gather_bytes", ctypes.c_int64 * 8)]
 
@@ -72,6 +73,7 @@ def lib() -> ctypes.CDLL:
     L.ygg_free.restype = None
     L.ygg_step.argtypes = [vp, vp, vp, vp, vp, vp, i32, vp]
     L.ygg_run.argtypes = [vp, vp, i32, i32, vp, vp, vp, vp, vp, vp]
+    L.ygg_run_grouped.argtypes = [vp, vp, i32, i32, vp, vp, vp, vp, vp, vp]
     L.ygg_score.argtypes = [vp, vp, vp, i32, i32, vp, vp, vp]
     L.ygg_generate.argtypes = [vp, vp, i32, i32, vp, ctypes.c_float, i32, ctypes.c_uint64, vp, vp, vp]
     L.ygg_take_errors.argtypes = [vp, vp, ctypes.POINTER(ctypes.c_uint32)]

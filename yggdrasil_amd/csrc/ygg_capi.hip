@@ -400,6 +400,10 @@ struct ygg_model {
     ygg::Kernel solo;                 // all wavefronts on one stream: one-token calls and generation, B <= solo_max_streams
     int solo_max_streams = 0;
     bool solo_all = false;            // YGG_KERNEL=solo: every call but score and digest calls
+    bool grouped_ok = false;          // the leaf-grouped step takes the model (ygg_run_grouped)
+    void *grp_ws = nullptr;           // its workspace, grown to the largest call
+    size_t grp_ws_bytes = 0;
+    int grp_mfma_min = 0;             // tiles of at least this many streams on MFMA (0: none)
 };
 
 namespace {
@@ -649,6 +653,12 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     // wavefront per SIMD cost about what the memory round trips they remove cost)
     m->solo = solok;
     m->solo_all = solok && kmode == "solo";
+    // the leaf-grouped step: the benchmark shape with the specialised kernels' record layout, tensor scales, tables
+    m->grouped_ok = fast && !factored && !group && n == 128 && R == 8 && R2f == 16 && fa.blk == 16;
+    {
+        const char *gm = getenv("YGG_GROUP_MFMA_MIN");
+        m->grp_mfma_min = gm ? atoi(gm) : 8;
+    }
     m->solo_max_streams = m->solo_all ? INT32_MAX : 0;
     m->device = device;
     m->arena = arena;
@@ -713,6 +723,7 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     I.flow_max_streams = m->flow_max_streams[kModeRun];
     I.router_rounds = L > 1 ? rplan.n : 0;
     I.solo_max_streams = m->solo_max_streams;
+    I.grouped = m->grouped_ok ? 1 : 0;
     I.file_array_bytes = fa.bytes;
     I.device_bytes = (int64_t)total;
     for (int l = 0; l < L; l++) I.gather_bytes[l] = lp[l].gl.bytes;
@@ -765,7 +776,7 @@ int set_error(int code, const char *msg) { return fail(code, "%s", msg); }
 
 extern "C" {
 
-int ygg_version(void) { return 9; }
+int ygg_version(void) { return 10; }
 
 const char *ygg_last_error(void) { return g_err.c_str(); }
 
@@ -814,7 +825,10 @@ int ygg_model_info(const ygg_model *m, ygg_info *info) {
 void ygg_free(ygg_model *m) {
     if (!m) return;
     DeviceGuard g;
-    if (g.set(m->device) == hipSuccess) (void)hipFree(m->arena);
+    if (g.set(m->device) == hipSuccess) {
+        (void)hipFree(m->arena);
+        if (m->grp_ws) (void)hipFree(m->grp_ws);
+    }
     delete m;
 }
 
@@ -834,6 +848,38 @@ int ygg_run(const ygg_model *m, const int32_t *d_tokens, int B, int T, int8_t *d
     io.states = d_states;
     io.digest = (unsigned long long *)d_digest;
     HIP_TRY(k.fn(m->dev, d_tokens, B, T, d_state, io, (hipStream_t)stream));
+    return YGG_OK;
+}
+
+int ygg_run_grouped(ygg_model *m, const int32_t *d_tokens, int B, int T, int8_t *d_state, float *d_logits,
+                    int32_t *d_leaves, int8_t *d_states, uint64_t *d_digest, void *stream) {
+    if (!m) return fail(YGG_ERR_ARG, "model is NULL");
+    if (B < 0 || T < 0) return fail(YGG_ERR_ARG, "negative B (%d) or T (%d)", B, T);
+    if (!m->grouped_ok)
+        return fail(YGG_ERR_LIMITS, "the grouped step takes d_state 128, readout rank 8, layer-input rank 16, block 16, "
+                                    "table storage and tensor scales");
+    if (B == 0 || T == 0) return YGG_OK;
+    if (!d_state || !d_tokens) return fail(YGG_ERR_ARG, "tokens or state is NULL");
+    DeviceGuard g;
+    HIP_TRY(g.set(m->device));
+    const int emax = std::max(m->dev.V, m->dev.L > 1 ? m->dev.E : 0);
+    const size_t need = ygg::grouped_ws_bytes(B, emax, m->dev.L);
+    if (need > m->grp_ws_bytes) {
+        // (stream-ordered use of the old workspace ends before it is freed)
+        HIP_TRY(hipStreamSynchronize((hipStream_t)stream));
+        if (m->grp_ws) (void)hipFree(m->grp_ws);
+        m->grp_ws = nullptr;
+        m->grp_ws_bytes = 0;
+        HIP_TRY(hipMalloc(&m->grp_ws, need));
+        m->grp_ws_bytes = need;
+    }
+    YggIO io{};
+    io.logits = d_logits;
+    io.leaves = d_leaves;
+    io.states = d_states;
+    io.digest = (unsigned long long *)d_digest;
+    HIP_TRY(ygg::launch_grouped(m->dev, d_tokens, B, T, d_state, io, m->grp_ws, emax, m->grp_mfma_min,
+                                (hipStream_t)stream));
     return YGG_OK;
 }
 

@@ -69,5 +69,11 @@ int flow_blocks_per_cu(int n, int R, int R2, int L, int P, bool group, int mode)
 // solo_kernel, one stream per workgroup with all four wavefronts on it (ygg_kernels_solo.hip): router plans of at
 // most 4 rounds whose first two take at most 8 levels and the others at most 6
 Kernel find_solo_launcher(int n, int R, int R2, int L, bool group);
+// the leaf-grouped step (ygg_kernels_group.hip; n 128, readout rank 8, layer-input rank 16, table storage, tensor
+// scales): every (token, layer) of the call as route, plan and update launches on the stream, in a workspace of
+// grouped_ws_bytes(B, emax, L) bytes at ws (emax: the most experts of a layer, V or 2^D)
+hipError_t launch_grouped(const YggDevModel &m, const int32_t *tokens, int B, int T, int8_t *state, const YggIO &io,
+                          void *ws, int emax, int mfma_min, hipStream_t stream);
+size_t grouped_ws_bytes(int B, int emax, int L);
 
 }  // namespace ygg

@@ -174,7 +174,7 @@ class Yggdrasil:
         return logits.clone(), h.clone()
 
     def run(self, tokens, state: Optional[torch.Tensor] = None, logits: bool = True, leaves: bool = False,
-            states: bool = False, digest=False) -> dict:
+            states: bool = False, digest=False, _entry: str = "ygg_run") -> dict:
         """T tokens per stream in one launch: tokens (B, T) from state (default zero; not modified) ->
         dict(state=(B, layers, n) after the last token, logits=(B, T, classes), leaves=(B, T, layers) int32,
         states=(B, T, layers, n) int8, digest=(B,) int64 bit pattern of the uint64 digest)."""
@@ -195,12 +195,18 @@ class Yggdrasil:
                             device=dev)
         else:
             dg = None
-        check(_lib.lib().ygg_run(self._h, _ptr(x), B, T, _ptr(st), _ptr(lg), _ptr(lv), _ptr(sv), _ptr(dg),
-                                 _stream()))
+        check(getattr(_lib.lib(), _entry)(self._h, _ptr(x), B, T, _ptr(st), _ptr(lg), _ptr(lv), _ptr(sv), _ptr(dg),
+                                          _stream()))
         for k, v in (("logits", lg), ("leaves", lv), ("states", sv), ("digest", dg)):
             if v is not None:
                 out[k] = v
         return out
+
+    def run_grouped(self, tokens, state: Optional[torch.Tensor] = None, logits: bool = True, leaves: bool = False,
+                    states: bool = False, digest=False) -> dict:
+        """run() computed leaf-grouped (ygg_run_grouped): the streams that take the same expert at a (token, layer) are
+        updated together, on int8 MFMA for large groups. Same arguments and results as run()."""
+        return self.run(tokens, state, logits, leaves, states, digest, _entry="ygg_run_grouped")
 
     def take_errors(self) -> int:
         """Wait for the current stream; the error bits kernels set since the last call (bit 0: bad token)."""
