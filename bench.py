@@ -290,6 +290,9 @@ def main():
     ap.add_argument("--cpu-procs", type=int, default=CPU_SHARE)
     ap.add_argument("--cpu-streams", type=int, default=256, help="streams per CPU baseline process")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--entry", default="run", choices=["run", "grouped"],
+                    help="the timed C-ABI call: ygg_run (per-stream kernels) or ygg_run_grouped (leaf-grouped "
+                         "phases, MFMA tiles from YGG_GROUP_MFMA_MIN streams)")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(f"bench.py runs on one GPU only: the streams are independent, so N GPUs would each run this same "
@@ -321,10 +324,14 @@ def main():
     stream = torch.cuda.current_stream()
     sp = ctypes.c_void_p(stream.cuda_stream)
 
+    entry = L.ygg_run_grouped if a.entry == "grouped" else L.ygg_run
+    if a.entry == "grouped" and not info.grouped:
+        raise SystemExit("ygg_run_grouped does not take this model")
+
     def launch(with_leaves=False):
         st.zero_()
-        _lib.check(L.ygg_run(model._h, p(x), B, T, p(st), p(logits), p(leaves) if with_leaves else None, None,
-                             None, sp))
+        _lib.check(entry(model._h, p(x), B, T, p(st), p(logits), p(leaves) if with_leaves else None, None,
+                         None, sp))
 
     # the first warmup launch also records the leaves, for the compulsory-byte count
     for i in range(max(1, a.warmup)):
@@ -349,7 +356,7 @@ def main():
     for k0, k1 in ks:
         st.zero_()
         k0.record(stream)
-        _lib.check(L.ygg_run(model._h, p(x), B, T, p(st), p(logits), None, None, None, sp))
+        _lib.check(entry(model._h, p(x), B, T, p(st), p(logits), None, None, None, sp))
         k1.record(stream)
     e1.record(stream)
     torch.cuda.synchronize()
@@ -361,7 +368,9 @@ def main():
         f"tokens/s, compulsory {achieved:.0f} GB/s ({achieved / PEAK_HBM_GBS:.3f} of 8 TB/s), per-stream "
         f"{alg['per_stream'] / (kernel_ms / 1e3) / 1e9:.0f} GB/s")
 
-    kernel = model.kernel_name(B, T)
+    kernel = model.kernel_name(B, T) if a.entry == "run" else \
+        f"ygg_run_grouped: grp_route, grp_plan, grp_update per (token, layer), MFMA tiles from " \
+        f"{os.environ.get('YGG_GROUP_MFMA_MIN', '8')} streams"
     # HBM bytes per launch measured by rocprofv3 (FETCH_SIZE, WRITE_SIZE, copy-calibrated) for this workload and kernel
     traffic = None
     tf = ROOT / "profiles" / f"traffic_{w.name}.json"
@@ -374,7 +383,7 @@ def main():
             traffic = None
 
     batch1 = None
-    if a.batch1_tokens > 0:
+    if a.batch1_tokens > 0 and a.entry == "run":
         batch1 = run_batch1(model, w, a.batch1_tokens, L, _lib)
         log(f"batch-1: {batch1}")
 
@@ -395,7 +404,8 @@ def main():
                                f"D={info.router_depth} R={info.readout_rank} R2={info.layer_input_rank} "
                                f"(seed {w.model_seed}, {info.file_array_bytes / 1e9:.2f} GB YGG1)",
                    "streams": B, "tokens_per_stream": T, "model_file_bytes": int(info.file_array_bytes),
-                   "step": "one ygg_run launch: every token of every stream, logits written per token",
+                   "step": f"one {'ygg_run launch' if a.entry == 'run' else 'ygg_run_grouped call'}: every token "
+                           f"of every stream, logits written per token",
                    "parallelism": "1 GPU (streams independent)"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic,

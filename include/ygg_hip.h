@@ -75,7 +75,8 @@ typedef struct {
                                   two rounds take more than 8 levels or whose later ones more than 6, or
                                   (L - 1) d_state > 512 */
     int32_t grouped;           /* 1: ygg_run_grouped takes the model (d_state 128, readout rank 8, layer-input rank 16,
-                                  block 16, table storage, tensor scales); 0: it reports YGG_ERR_LIMITS */
+                                  block 16, table storage, tensor scales, router depth <= 14); 0: it reports
+                                  YGG_ERR_LIMITS */
     int64_t file_array_bytes;  /* bytes of the file's arrays (the reference's Model::bytes, cpu/ygg.cpp:158, 167) */
     int64_t device_bytes;      /* device memory held by the model */
     int64_t gather_bytes[8];   /* per layer: bytes of one expert's transition, layer-input and readout weights */
@@ -115,7 +116,7 @@ int ygg_run(const ygg_model *m, const int32_t *d_tokens, int B, int T, int8_t *d
    streams that take the same expert at that phase, reads the expert's record once per group and contracts groups of
    at least YGG_GROUP_MFMA_MIN streams (default 8, read at load) on int8 MFMA. Same arguments, results and error
    behaviour as ygg_run (digest included). Models of d_state 128, readout rank 8, layer-input rank 16, block 16, table
-   storage and tensor scales only (else YGG_ERR_LIMITS). The first call, and any call with more streams than an earlier
+   storage, tensor scales and router depth at most 14 only (else YGG_ERR_LIMITS). The first call, and any call with more streams than an earlier
    one, allocates its workspace with hipMalloc (and waits for the stream): under graph capture, make a call of at
    least that many streams first. Calls on one model must not overlap (they share the workspace). */
 int ygg_run_grouped(ygg_model *m, const int32_t *d_tokens, int B, int T, int8_t *d_state, float *d_logits,

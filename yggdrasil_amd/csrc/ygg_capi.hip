@@ -654,7 +654,8 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     m->solo = solok;
     m->solo_all = solok && kmode == "solo";
     // the leaf-grouped step: the benchmark shape with the specialised kernels' record layout, tensor scales, tables
-    m->grouped_ok = fast && !factored && !group && n == 128 && R == 8 && R2f == 16 && fa.blk == 16;
+    m->grouped_ok = fast && !factored && !group && n == 128 && R == 8 && R2f == 16 && fa.blk == 16 &&
+                    (L == 1 || fa.D <= 14);
     {
         const char *gm = getenv("YGG_GROUP_MFMA_MIN");
         m->grp_mfma_min = gm ? atoi(gm) : 8;
@@ -862,8 +863,7 @@ int ygg_run_grouped(ygg_model *m, const int32_t *d_tokens, int B, int T, int8_t 
     if (!d_state || !d_tokens) return fail(YGG_ERR_ARG, "tokens or state is NULL");
     DeviceGuard g;
     HIP_TRY(g.set(m->device));
-    const int emax = std::max(m->dev.V, m->dev.L > 1 ? m->dev.E : 0);
-    const size_t need = ygg::grouped_ws_bytes(B, emax, m->dev.L);
+    const size_t need = ygg::grouped_ws_bytes(B, m->dev.L);
     if (need > m->grp_ws_bytes) {
         // (stream-ordered use of the old workspace ends before it is freed)
         HIP_TRY(hipStreamSynchronize((hipStream_t)stream));
@@ -878,7 +878,7 @@ int ygg_run_grouped(ygg_model *m, const int32_t *d_tokens, int B, int T, int8_t 
     io.leaves = d_leaves;
     io.states = d_states;
     io.digest = (unsigned long long *)d_digest;
-    HIP_TRY(ygg::launch_grouped(m->dev, d_tokens, B, T, d_state, io, m->grp_ws, emax, m->grp_mfma_min,
+    HIP_TRY(ygg::launch_grouped(m->dev, d_tokens, B, T, d_state, io, m->grp_ws, m->grp_mfma_min,
                                 (hipStream_t)stream));
     return YGG_OK;
 }

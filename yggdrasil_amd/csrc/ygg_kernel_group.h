@@ -5,10 +5,10 @@
 // A call runs every (token, layer) of B streams as a phase of three launches on the caller's stream (so that the
 // whole call can be captured in one hipGraph):
 //   grp_route   one wavefront per stream: the layer's expert (the router descent of fast_kernel on the state below,
-//               which the phase before wrote) and the layer input zl; a histogram of streams per expert (atomics) that
-//               also gives each stream its index in its expert's group; the leaves output
-//   grp_plan    one workgroup: offsets of the groups (a scan of the histogram), the streams in expert order, the tile
-//               list (tiles of at most 16 streams of one expert), the histogram cleared for the next phase
+//               which the phase before wrote) and the layer input zl; the leaves output
+//   grp_plan    one workgroup: a counting sort of the streams by expert in LDS (a histogram whose LDS atomics give
+//               each stream its index in its group, a scan for the groups' offsets, a scatter), and the tile list
+//               (tiles of at most 16 streams of one expert)
 //   grp_update  one wavefront per tile: the update, the readout (zq kept per stream and layer) and the digest of each
 //               stream of the tile; at the last layer the logits of its streams (every layer's unembedding term in
 //               layer order, cpu/ygg.cpp:457)
@@ -27,11 +27,11 @@ typedef int v4i32 __attribute__((ext_vector_type(4)));
 constexpr int kGrpTile = 16;        // streams per tile (the MFMA's 16 rows)
 constexpr int kGrpSlots = 8;        // zq bytes per stream and layer (readout rank 8)
 
-// The workspace of a grouped call (device memory): B streams, experts up to emax per layer, L layers.
+// The workspace of a grouped call (device memory): B streams, L layers.
+constexpr int kGrpMaxExperts = 16384;      // experts (and tokens) per layer the plan's LDS histogram holds
 struct GroupWS {
     int32_t *leaf;                  // [B] expert of the phase, -1: the stream has stopped
     int32_t *pos;                   // [B] index in its expert's group
-    int32_t *cnt;                   // [emax] streams per expert; zero between phases
     int32_t *stop;                  // [B] first token not processed (T until a bad token)
     int32_t *sorted;                // [B] stream ids in expert order
     int4 *tiles;                    // [2 B + 1] (expert, first index into sorted, streams, 0)
@@ -40,13 +40,13 @@ struct GroupWS {
     int8_t *zq;                     // [B][L][8] readouts of the current token
 };
 
-// bytes of a workspace for B streams, emax experts, L layers (each piece 256-byte aligned)
-inline size_t group_ws_bytes(int B, int emax, int L) {
+// bytes of a workspace for B streams, L layers (each piece 256-byte aligned)
+inline size_t group_ws_bytes(int B, int L) {
     auto al = [](size_t b) { return (b + 255) / 256 * 256; };
-    return al(4 * (size_t)B) * 4 + al(4 * (size_t)emax) + al(16 * (size_t)(2 * B + 1)) + al(4) +
-           al(16 * (size_t)B) + al((size_t)B * L * kGrpSlots);
+    return al(4 * (size_t)B) * 4 + al(16 * (size_t)(2 * B + 1)) + al(4) + al(16 * (size_t)B) +
+           al((size_t)B * L * kGrpSlots);
 }
-inline GroupWS group_ws_carve(void *base, int B, int emax, int L) {
+inline GroupWS group_ws_carve(void *base, int B, int L) {
     auto al = [](size_t b) { return (b + 255) / 256 * 256; };
     uint8_t *p = (uint8_t *)base;
     GroupWS w;
@@ -54,7 +54,6 @@ inline GroupWS group_ws_carve(void *base, int B, int emax, int L) {
     w.pos = (int32_t *)p; p += al(4 * (size_t)B);
     w.stop = (int32_t *)p; p += al(4 * (size_t)B);
     w.sorted = (int32_t *)p; p += al(4 * (size_t)B);
-    w.cnt = (int32_t *)p; p += al(4 * (size_t)emax);
     w.tiles = (int4 *)p; p += al(16 * (size_t)(2 * B + 1));
     w.ntiles = (int32_t *)p; p += al(4);
     w.zl = (int8_t *)p; p += al(16 * (size_t)B);
@@ -64,10 +63,9 @@ inline GroupWS group_ws_carve(void *base, int B, int emax, int L) {
 
 // ------------------------------------------------------------------------------------------------- init, route, plan
 
-// a call's start: the histogram cleared, every stream running
-__global__ __launch_bounds__(256) void grp_init(int B, int emax, int T, GroupWS ws) {
+// a call's start: every stream running
+__global__ __launch_bounds__(256) void grp_init(int B, int T, GroupWS ws) {
     const int i = blockIdx.x * 256 + threadIdx.x;
-    if (i < emax) ws.cnt[i] = 0;
     if (i < B) ws.stop[i] = T;
 }
 
@@ -135,49 +133,82 @@ __global__ __launch_bounds__(256) void grp_route(const YggDevModel m, const int3
     }
     if (lane == 0) {
         ws.leaf[s] = r;
-        ws.pos[s] = atomicAdd(&ws.cnt[r], 1);
         if (leaves) leaves[((size_t)s * T + t) * m.L + l] = r;
     }
 }
 
-// One workgroup of 1024 threads: group offsets by a scan of the histogram (each thread a run of ceil(E / 1024)
-// experts), the tile list, the streams in expert order, the histogram cleared.
+// One workgroup of 1024 threads, E <= kGrpMaxExperts experts: the streams' positions in their groups (LDS atomics
+// on the histogram; the order of a group's streams is immaterial, every stream's arithmetic is its own), the groups'
+// offsets (thread k takes the experts k + 1024 j, their stream and tile counts scanned over the workgroup; the order
+// of the groups is immaterial too), the tile list, the streams in expert order.
 __global__ __launch_bounds__(1024) void grp_plan(int B, int E, GroupWS ws) {
-    __shared__ int s_str[1024], s_til[1024];
-    const int tid = threadIdx.x;
-    const int per = (E + 1023) / 1024, e0 = tid * per, e1 = e0 + per < E ? e0 + per : E;
-    int nstr = 0, ntil = 0;
-    for (int e = e0; e < e1; e++) {
-        const int c = ws.cnt[e];
-        nstr += c;
-        ntil += (c + kGrpTile - 1) / kGrpTile;
-    }
-    s_str[tid] = nstr;
-    s_til[tid] = ntil;
+    __shared__ int hist[kGrpMaxExperts];
+    __shared__ int wsum[16], wtil[16];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    for (int e = tid; e < E; e += 1024) hist[e] = 0;
     __syncthreads();
-    // inclusive scans (Hillis-Steele over the 1024 partial sums)
-    for (int o = 1; o < 1024; o <<= 1) {
-        const int a = tid >= o ? s_str[tid - o] : 0, b = tid >= o ? s_til[tid - o] : 0;
-        __syncthreads();
-        s_str[tid] += a;
-        s_til[tid] += b;
-        __syncthreads();
+    constexpr int PL = 8;       // streams per thread and pass, their loads issued together
+    for (int s0 = tid; s0 < B; s0 += 1024 * PL) {
+        int rr[PL];
+#pragma unroll
+        for (int k = 0; k < PL; k++) rr[k] = s0 + 1024 * k < B ? ws.leaf[s0 + 1024 * k] : -1;
+#pragma unroll
+        for (int k = 0; k < PL; k++)
+            if (rr[k] >= 0) ws.pos[s0 + 1024 * k] = atomicAdd(&hist[rr[k]], 1);
     }
-    int off = s_str[tid] - nstr, toff = s_til[tid] - ntil;
-    for (int e = e0; e < e1; e++) {
-        const int c = ws.cnt[e];
-        for (int k = 0; k < c; k += kGrpTile) ws.tiles[toff++] = make_int4(e, off + k, c - k < kGrpTile ? c - k : kGrpTile, 0);
-        ws.cnt[e] = off;          // (the group's offset, until the scatter has used it)
+    __syncthreads();
+    int ns = 0, nt = 0;
+    for (int e = tid; e < E; e += 1024) {
+        const int c = hist[e];
+        ns += c;
+        nt += (c + kGrpTile - 1) / kGrpTile;
+    }
+    // inclusive scans over the wavefront, then over the 16 wavefront totals
+    int is = ns, it = nt;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int us = __shfl_up(is, o), ut = __shfl_up(it, o);
+        if (lane >= o) {
+            is += us;
+            it += ut;
+        }
+    }
+    if (lane == 63) {
+        wsum[wv] = is;
+        wtil[wv] = it;
+    }
+    __syncthreads();
+    int bs = 0, bt = 0, tt = 0;
+#pragma unroll
+    for (int w = 0; w < 16; w++) {
+        if (w < wv) {
+            bs += wsum[w];
+            bt += wtil[w];
+        }
+        tt += wtil[w];
+    }
+    int off = bs + is - ns, toff = bt + it - nt;
+    for (int e = tid; e < E; e += 1024) {
+        const int c = hist[e];
+        for (int k = 0; k < c; k += kGrpTile)
+            ws.tiles[toff++] = make_int4(e, off + k, c - k < kGrpTile ? c - k : kGrpTile, 0);
+        hist[e] = off;          // (the group's offset, for the scatter)
         off += c;
     }
-    if (tid == 1023) *ws.ntiles = s_til[1023];
+    if (tid == 0) *ws.ntiles = tt;
     __syncthreads();
-    for (int s = tid; s < B; s += 1024) {
-        const int r = ws.leaf[s];
-        if (r >= 0) ws.sorted[ws.cnt[r] + ws.pos[s]] = s;
+    for (int s0 = tid; s0 < B; s0 += 1024 * PL) {
+        int rr[PL], pp[PL];
+#pragma unroll
+        for (int k = 0; k < PL; k++) {
+            const bool in = s0 + 1024 * k < B;
+            rr[k] = in ? ws.leaf[s0 + 1024 * k] : -1;
+            pp[k] = in ? ws.pos[s0 + 1024 * k] : 0;
+        }
+#pragma unroll
+        for (int k = 0; k < PL; k++)
+            if (rr[k] >= 0) ws.sorted[hist[rr[k]] + pp[k]] = s0 + 1024 * k;
     }
-    __syncthreads();
-    for (int e = tid; e < E; e += 1024) ws.cnt[e] = 0;
 }
 
 // ------------------------------------------------------------------------------------------------- update

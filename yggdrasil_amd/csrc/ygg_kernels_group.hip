@@ -7,12 +7,13 @@
 namespace ygg {
 
 hipError_t launch_grouped(const YggDevModel &m, const int32_t *tokens, int B, int T, int8_t *state, const YggIO &io,
-                          void *ws_mem, int emax, int mfma_min, hipStream_t stream) {
+                          void *ws_mem, int mfma_min, hipStream_t stream) {
     if (B <= 0 || T <= 0) return hipSuccess;
-    const GroupWS ws = group_ws_carve(ws_mem, B, emax, m.L);
-    const int n0 = B > emax ? B : emax;
-    hipLaunchKernelGGL(grp_init, dim3((n0 + 255) / 256), dim3(256), 0, stream, B, emax, T, ws);
+    if (m.V > kGrpMaxExperts || (m.L > 1 && m.E > kGrpMaxExperts)) return hipErrorInvalidValue;
+    const GroupWS ws = group_ws_carve(ws_mem, B, m.L);
+    hipLaunchKernelGGL(grp_init, dim3((B + 255) / 256), dim3(256), 0, stream, B, T, ws);
     // update workgroups: about one wavefront per tile of the worst case (every stream alone at its expert)
+    const int emax = m.L > 1 && m.E > m.V ? m.E : m.V;
     const int tiles_max = B / kGrpTile + (B < emax ? B : emax) + 1;
     int gu = (tiles_max + 3) / 4;
     if (gu > 4096) gu = 4096;
@@ -27,6 +28,6 @@ hipError_t launch_grouped(const YggDevModel &m, const int32_t *tokens, int B, in
     return hipGetLastError();
 }
 
-size_t grouped_ws_bytes(int B, int emax, int L) { return group_ws_bytes(B, emax, L); }
+size_t grouped_ws_bytes(int B, int L) { return group_ws_bytes(B, L); }
 
 }  // namespace ygg

@@ -70,10 +70,10 @@ int flow_blocks_per_cu(int n, int R, int R2, int L, int P, bool group, int mode)
 // most 4 rounds whose first two take at most 8 levels and the others at most 6
 Kernel find_solo_launcher(int n, int R, int R2, int L, bool group);
 // the leaf-grouped step (ygg_kernels_group.hip; n 128, readout rank 8, layer-input rank 16, table storage, tensor
-// scales): every (token, layer) of the call as route, plan and update launches on the stream, in a workspace of
-// grouped_ws_bytes(B, emax, L) bytes at ws (emax: the most experts of a layer, V or 2^D)
+// scales, at most 16384 experts a layer): every (token, layer) of the call as route, plan and update launches on
+// the stream, in a workspace of grouped_ws_bytes(B, L) bytes at ws
 hipError_t launch_grouped(const YggDevModel &m, const int32_t *tokens, int B, int T, int8_t *state, const YggIO &io,
-                          void *ws, int emax, int mfma_min, hipStream_t stream);
-size_t grouped_ws_bytes(int B, int emax, int L);
+                          void *ws, int mfma_min, hipStream_t stream);
+size_t grouped_ws_bytes(int B, int L);
 
 }  // namespace ygg
