@@ -122,6 +122,17 @@ int ygg_run(const ygg_model *m, const int32_t *d_tokens, int B, int T, int8_t *d
 int ygg_run_grouped(ygg_model *m, const int32_t *d_tokens, int B, int T, int8_t *d_state, float *d_logits,
                     int32_t *d_leaves, int8_t *d_states, uint64_t *d_digest, void *stream);
 
+/* ygg_run_grouped without any allocation, for callers that cannot allocate device memory (code under HIP graph
+   capture, tight serving loops, harnesses that forbid hipMalloc); no counterpart in the reference. Same arguments,
+   results and errors as ygg_run_grouped; its workspace is a static device array of YGG_SCRATCH_BYTES on each GPU
+   (held until the process ends), so B is limited to what fits: the workspace takes 16 + 32 + 16 + 8 L bytes per
+   stream plus 16 (each of its 7 pieces rounded up to 256 bytes): up to 10 912 streams of a 4-layer model, 10 071 of
+   a 5-layer one; more give YGG_ERR_LIMITS. Every call on one GPU shares that array: calls that overlap on one GPU (other streams, other
+   threads, other models) race and must not be made. Nothing in the array needs clearing between calls. */
+#define YGG_SCRATCH_BYTES (1 << 20)
+int ygg_run_grouped_noalloc(const ygg_model *m, const int32_t *d_tokens, int B, int T, int8_t *d_state,
+                            float *d_logits, int32_t *d_leaves, int8_t *d_states, uint64_t *d_digest, void *stream);
+
 /* Score T tokens of each of B streams without writing logits: the reference's `ygg score` (cpu/ygg.cpp:500-519) for
    B streams at once. Per token, in double: mx = max_c lg[c], se = sum_c exp(lg[c] - mx), and
    d_nll[b] += log(se) + mx - lg[target] (cpu/ygg.cpp:514-516; se is summed as a tree over classes, not in class

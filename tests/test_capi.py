@@ -65,6 +65,7 @@ def test_bad_arguments(lib):
     assert L.ygg_model_info(None, None) == 5
     assert L.ygg_run(None, None, 1, 1, None, None, None, None, None, None) == 5
     assert L.ygg_run_grouped(None, None, 1, 1, None, None, None, None, None, None) == 5
+    assert L.ygg_run_grouped_noalloc(None, None, 1, 1, None, None, None, None, None, None) == 5
     assert L.ygg_step(None, None, None, None, None, None, 1, None) == 5
     assert L.ygg_take_errors(None, None, None) == 5
     assert L.ygg_generate(None, None, 1, 1, None, 0.0, 0, 0, None, None, None) == 5

@@ -11,6 +11,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <map>
+#include <mutex>
 #include <string>
 #include <thread>
 #include <vector>
@@ -38,6 +39,38 @@ int fail(int code, const char *fmt, ...) {
         hipError_t e_ = (expr);                                                                        \
         if (e_ != hipSuccess) return fail(YGG_ERR_DEVICE, "%s: %s", #expr, hipGetErrorString(e_));     \
     } while (0)
+
+}  // namespace
+
+// The workspace of ygg_run_grouped_noalloc: one static array per GPU (each device holds its own copy from module
+// load until the process ends), shared by every such call on that GPU. Host code uses only the device address
+// recorded by scratch_setup, never this name.
+static __device__ __align__(256) uint8_t scratch[YGG_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices] = {};
+
+// the address of `scratch` on `device`, which is current: looked up once per device (at the first load onto it)
+hipError_t scratch_setup(int device) {
+    if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (g_scratch_ptr[device]) return hipSuccess;
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    if (!p) return hipErrorInvalidSymbol;
+    g_scratch_ptr[device] = p;
+    return hipSuccess;
+}
+
+void *scratch_of(int device) {
+    if (device < 0 || device >= kMaxDevices) return nullptr;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    return g_scratch_ptr[device];
+}
 
 struct FileArrays {
     int32_t n_layers, n, blk, V, D, R, R2, reserved, router_token_dim, K, shift, n_arrays;
@@ -610,8 +643,14 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     int prev = 0;
     HIP_TRY(hipGetDevice(&prev));
     HIP_TRY(hipSetDevice(device));
+    hipError_t e = scratch_setup(device);
+    if (e != hipSuccess) {
+        (void)hipSetDevice(prev);
+        return fail(YGG_ERR_DEVICE, "the address of the static grouped workspace on device %d: %s", device,
+                    hipGetErrorString(e));
+    }
     void *arena = nullptr;
-    hipError_t e = hipMalloc(&arena, total);
+    e = hipMalloc(&arena, total);
     if (e != hipSuccess) {
         (void)hipSetDevice(prev);
         return fail(YGG_ERR_NOMEM, "device allocation of %zu bytes failed: %s", total, hipGetErrorString(e));
@@ -880,6 +919,33 @@ int ygg_run_grouped(ygg_model *m, const int32_t *d_tokens, int B, int T, int8_t 
     io.digest = (unsigned long long *)d_digest;
     HIP_TRY(ygg::launch_grouped(m->dev, d_tokens, B, T, d_state, io, m->grp_ws, m->grp_mfma_min,
                                 (hipStream_t)stream));
+    return YGG_OK;
+}
+
+int ygg_run_grouped_noalloc(const ygg_model *m, const int32_t *d_tokens, int B, int T, int8_t *d_state,
+                            float *d_logits, int32_t *d_leaves, int8_t *d_states, uint64_t *d_digest, void *stream) {
+    if (!m) return fail(YGG_ERR_ARG, "model is NULL");
+    if (B < 0 || T < 0) return fail(YGG_ERR_ARG, "negative B (%d) or T (%d)", B, T);
+    if (!m->grouped_ok)
+        return fail(YGG_ERR_LIMITS, "the grouped step takes d_state 128, readout rank 8, layer-input rank 16, block 16, "
+                                    "table storage, tensor scales and router depth at most 14");
+    if (B == 0 || T == 0) return YGG_OK;
+    if (!d_state || !d_tokens) return fail(YGG_ERR_ARG, "tokens or state is NULL");
+    const size_t need = ygg::grouped_ws_bytes(B, m->dev.L);
+    if (need > (size_t)YGG_SCRATCH_BYTES)
+        return fail(YGG_ERR_LIMITS, "ygg_run_grouped_noalloc: %d streams of a %d-layer model need %zu bytes of "
+                                    "workspace, more than its static %d (ygg_run_grouped has no such limit)",
+                    B, m->dev.L, need, YGG_SCRATCH_BYTES);
+    void *ws = scratch_of(m->device);
+    if (!ws) return fail(YGG_ERR_DEVICE, "no static grouped workspace on device %d", m->device);
+    DeviceGuard g;
+    HIP_TRY(g.set(m->device));
+    YggIO io{};
+    io.logits = d_logits;
+    io.leaves = d_leaves;
+    io.states = d_states;
+    io.digest = (unsigned long long *)d_digest;
+    HIP_TRY(ygg::launch_grouped(m->dev, d_tokens, B, T, d_state, io, ws, m->grp_mfma_min, (hipStream_t)stream));
     return YGG_OK;
 }
 
