@@ -118,7 +118,8 @@ CPU_SHARE = 16
 # so for any AVX-512 VNNI host rather than the build host's -march=native.
 REF_MARCH = "-march=x86-64-v4 -mavx512vnni"
 SOFTMAX_NOTE = ("the reference's time mode computes an f32 softmax of every token's logits (cpu/ygg.cpp:61-72, "
-                "552), included in its ns/token; the GPU value writes the logits and computes no softmax")
+                "552), included in its ns/token; the GPU value writes the logits and computes no softmax; the same "
+                "softmax on the GPU (ygg_softmax) is timed apart in the line's softmax object")
 
 
 def cpu_baseline(path: Path, tokens: np.ndarray, procs: int, streams_per_proc: int) -> dict:
@@ -382,6 +383,23 @@ def main():
         except (OSError, ValueError):
             traffic = None
 
+    # the f32 softmax of every logit row (what the reference's time mode adds per token), timed apart from the step
+    sm = None
+    if a.entry == "run":
+        pr = torch.empty_like(logits)
+        s0, s1 = ev(), ev()
+        _lib.check(L.ygg_softmax(p(logits), B * T, info.vocab, p(pr), None, sp))
+        s0.record(stream)
+        _lib.check(L.ygg_softmax(p(logits), B * T, info.vocab, p(pr), None, sp))
+        s1.record(stream)
+        torch.cuda.synchronize()
+        sm_ms = s0.elapsed_time(s1)
+        sm = {"ms": round(sm_ms, 4), "rows": B * T,
+              "GBps": round(2 * 4 * B * T * info.vocab / (sm_ms / 1e3) / 1e9, 1),
+              "step_plus_softmax_tokens_per_s": round(B * T / ((kernel_ms + sm_ms) / 1e3), 1)}
+        log(f"softmax of {B * T} rows: {sm}")
+        del pr
+
     batch1 = None
     if a.batch1_tokens > 0 and a.entry == "run":
         batch1 = run_batch1(model, w, a.batch1_tokens, L, _lib)
@@ -415,6 +433,7 @@ def main():
                      "per_stream_GBps": round(alg["per_stream"] / (kernel_ms / 1e3) / 1e9, 1),
                      "kernel": kernel, "kernel_ms": round(kernel_ms, 4)},
         "cpu_baseline": cpu,
+        "softmax": sm,
         "batch1": batch1,
     }
     print(json.dumps(out), flush=True)
@@ -444,6 +463,19 @@ def run_batch1(model, w, n_tok: int, L, _lib) -> dict:
     torch.cuda.synchronize()
     run_us = e0.elapsed_time(e1) * 1e3 / n_tok
     ref_logits = lg.clone()
+    # the reference's time mode also takes the f32 softmax of every token's logits (cpu/ygg.cpp:545-553): the same
+    # persistent launch followed by ygg_softmax over its n_tok rows
+    pr = torch.empty_like(lg)
+    ls = torch.empty(n_tok, dtype=torch.float32, device=dev)
+    st.zero_()
+    torch.cuda.synchronize()
+    e0.record(stream)
+    _lib.check(L.ygg_run(model._h, ptr(x1), 1, n_tok, ptr(st), ptr(lg), None, None, None, sp))
+    _lib.check(L.ygg_softmax(ptr(lg), n_tok, V, ptr(pr), ptr(ls), sp))
+    e1.record(stream)
+    torch.cuda.synchronize()
+    time_mode_us = e0.elapsed_time(e1) * 1e3 / n_tok
+    del pr, ls
     # (b) graphs of per-token steps
     G = 512
     graphs = []
@@ -480,6 +512,7 @@ def run_batch1(model, w, n_tok: int, L, _lib) -> dict:
     torch.cuda.synchronize()
     gen_us = e0.elapsed_time(e1) * 1e3 / n_tok
     return {"tokens": n_tok, "us_per_token_persistent_launch": round(run_us, 3),
+            "us_per_token_time_mode": round(time_mode_us, 3),
             "us_per_token_graph_step": round(graph_us, 3), "graph_steps_per_graph": G,
             "graph_logits_equal_persistent": same, "us_per_token_generate_greedy": round(gen_us, 3),
             "kernels": {"persistent_launch": model.kernel_name(1, n_tok), "graph_step": model.kernel_name(1, 1),

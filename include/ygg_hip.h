@@ -133,6 +133,12 @@ int ygg_run_grouped(ygg_model *m, const int32_t *d_tokens, int B, int T, int8_t 
 int ygg_run_grouped_noalloc(const ygg_model *m, const int32_t *d_tokens, int B, int T, int8_t *d_state,
                             float *d_logits, int32_t *d_leaves, int8_t *d_states, uint64_t *d_digest, void *stream);
 
+/* The f32 softmax of the reference's time mode, softmax() at cpu/ygg.cpp:59-72 (which `ygg time` applies to every
+   token's logits, cpu/ygg.cpp:545-553): for each of `rows` rows of V (1..256) logits at d_logits, the probabilities
+   into d_probs (bit-identical to the reference's; may be d_logits itself) and, unless d_lse is NULL, the row's
+   log-sum-exp (the value softmax() returns; the device's logf) into d_lse. On the caller's current device and stream. */
+int ygg_softmax(const float *d_logits, int64_t rows, int V, float *d_probs, float *d_lse, void *stream);
+
 /* Score T tokens of each of B streams without writing logits: the reference's `ygg score` (cpu/ygg.cpp:500-519) for
    B streams at once. Per token, in double: mx = max_c lg[c], se = sum_c exp(lg[c] - mx), and
    d_nll[b] += log(se) + mx - lg[target] (cpu/ygg.cpp:514-516; se is summed as a tree over classes, not in class

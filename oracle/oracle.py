@@ -21,6 +21,7 @@ LIB = HERE / "libygg_oracle.so"
 REF_DIR = HERE / "_ref"
 REF_YGG = REF_DIR / "ygg"
 REF_DUMP = REF_DIR / "ygg_dump"
+REF_SOFTMAX = REF_DIR / "ygg_softmax"
 DIGEST_INIT = 0xCBF29CE484222325
 DIGEST_MUL = 0x100000001B3
 DIGEST_LEAF = 0xD6E8FEB86659FD93
@@ -43,6 +44,7 @@ def lib():
                              ctypes.c_int]
         L.yo_run_sums.argtypes = [vp, vp, ctypes.c_int, ctypes.c_int, vp, vp, vp, ctypes.c_int, ctypes.c_char_p,
                                   ctypes.c_int]
+        L.yo_softmax.argtypes = [vp, ctypes.c_long, ctypes.c_int, vp, vp]
         _lib = L
     return _lib
 
@@ -125,6 +127,19 @@ class Oracle:
         return dg, ls, st
 
 
+def softmax(logits: np.ndarray):
+    """The f32 softmax of the reference's `time` mode (cpu/ygg.cpp:44-72) over the last axis of logits: (probs of the
+    same shape, log-sum-exp of each row)."""
+    lg = np.ascontiguousarray(logits, np.float32)
+    V = lg.shape[-1]
+    rows = lg.size // V if V else 0
+    pr = np.empty_like(lg)
+    ls = np.empty(lg.shape[:-1], np.float32)
+    if rows:
+        lib().yo_softmax(_ptr(lg), rows, V, _ptr(pr), _ptr(ls))
+    return pr, ls
+
+
 def logit_bits_sum(logits: np.ndarray) -> np.ndarray:
     """Per stream, the sum of the f32 bit patterns (as uint32) of logits (B, T, V), as uint64."""
     b = np.ascontiguousarray(logits, np.float32).view(np.uint32).astype(np.uint64)
@@ -204,6 +219,23 @@ def ref_dump(model_path, tokens: np.ndarray):
         sv = np.fromfile(sf, np.int8)
     L = lv.size // (B * T)
     return dict(logits=lg.reshape(B, T, -1), leaves=lv.reshape(B, T, L), states=sv.reshape(B, T, L, -1))
+
+
+def have_ref_softmax() -> bool:
+    return REF_SOFTMAX.exists()
+
+
+def ref_softmax(logits: np.ndarray):
+    """The reference's own softmax() (cpu/ygg.cpp:59-72) through oracle/_ref/ygg_softmax: (probs, lse) per row."""
+    lg = np.ascontiguousarray(logits, np.float32)
+    V = lg.shape[-1]
+    rows = lg.size // V
+    with tempfile.TemporaryDirectory() as tmp:
+        lf, pf, sf = (os.path.join(tmp, f) for f in ("lg.f32", "p.f32", "s.f32"))
+        lg.tofile(lf)
+        subprocess.run([str(REF_SOFTMAX), str(rows), str(V), lf, pf, sf], check=True, stdout=subprocess.DEVNULL,
+                       stderr=subprocess.PIPE)
+        return np.fromfile(pf, np.float32).reshape(lg.shape), np.fromfile(sf, np.float32).reshape(lg.shape[:-1])
 
 
 def ref_logits(model_path, tokens: np.ndarray) -> np.ndarray:

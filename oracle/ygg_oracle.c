@@ -407,3 +407,50 @@ int yo_run_sums(const yo_model *m, const int32_t *tokens, int B, int T, int8_t *
 }
 
 uint64_t yo_digest_init(void) { return YO_DIGEST_INIT; }
+
+/* ------------------------------------------------------------------------------------------- f32 softmax
+ * The per-token softmax of the reference's `time` mode, softmax() and vexp() at cpu/ygg.cpp:44-72, as scalar C:
+ *   mx = max_i lg[i];  e_i = exp2(clamp(lg[i] - mx, -87, 88))  (vexp below);
+ *   tot = the 16 lane sums s_j = sum over k of e[16 k + j] (k ascending), joined as ((s_j + s_(8+j)), then + the
+ *         element 4 apart, then 2 apart, then 1 apart) -- the 16-lane accumulator and the halving reduction of the
+ *         reference's vector code (checked bit for bit against the reference build in tests/test_oracle.py);
+ *   probs_i = e_i * (1 / tot);  lse = mx + logf(tot).
+ * vexp(x): t = x * f32(log2 e), n = t rounded to nearest even, f = t - n, p = the reference's degree-6 polynomial for
+ * 2^f in Horner form with fused multiply-adds (cpu/ygg.cpp:48-55), result p * 2^n. */
+static float vexp1(float x) {
+    x = fminf(fmaxf(x, -87.f), 88.f);
+    const float t = x * 1.4426950408889634f;
+    const float n = rintf(t);
+    const float f = t - n;
+    float p = 1.5353362e-4f;
+    p = fmaf(p, f, 1.3398874e-3f);
+    p = fmaf(p, f, 9.6181291e-3f);
+    p = fmaf(p, f, 5.5504109e-2f);
+    p = fmaf(p, f, 2.4022651e-1f);
+    p = fmaf(p, f, 6.9314718e-1f);
+    p = fmaf(p, f, 1.0f);
+    return ldexpf(p, (int)n);
+}
+
+void yo_softmax(const float *logits, long rows, int V, float *probs, float *lse) {
+    for (long r = 0; r < rows; r++) {
+        const float *lg = logits + (size_t)r * V;
+        float *pr = probs + (size_t)r * V;
+        float mx = -INFINITY;
+        for (int i = 0; i < V; i++) mx = lg[i] > mx ? lg[i] : mx;
+        float s[16];
+        for (int j = 0; j < 16; j++) s[j] = 0.0f;
+        for (int i = 0; i < V; i++) {
+            const float e = vexp1(lg[i] - mx);
+            pr[i] = e;
+            s[i & 15] = s[i & 15] + e;
+        }
+        float h[8], q[4];
+        for (int j = 0; j < 8; j++) h[j] = s[j] + s[8 + j];
+        for (int j = 0; j < 4; j++) q[j] = h[j] + h[4 + j];
+        const float tot = (q[0] + q[2]) + (q[1] + q[3]);
+        const float inv = 1.0f / tot;
+        for (int i = 0; i < V; i++) pr[i] = pr[i] * inv;
+        lse[r] = mx + logf(tot);
+    }
+}

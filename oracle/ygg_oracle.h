@@ -33,6 +33,9 @@ int yo_run(const yo_model *m, const int32_t *tokens, int B, int T, int8_t *state
 int yo_run_sums(const yo_model *m, const int32_t *tokens, int B, int T, int8_t *state, uint64_t *digest,
                 uint64_t *lgsum, int threads, char *err, int errlen);
 uint64_t yo_digest_init(void);
+/* The f32 softmax of the reference's `time` mode (cpu/ygg.cpp:44-72) over rows of V logits: probabilities into
+   probs (rows, V) and the log-sum-exp of each row into lse (rows). */
+void yo_softmax(const float *logits, long rows, int V, float *probs, float *lse);
 
 #ifdef __cplusplus
 }

@@ -342,3 +342,75 @@ def test_run_sums_equal_run(tmp_path):
     np.testing.assert_array_equal(ls, O.logit_bits_sum(full["logits"]))
     np.testing.assert_array_equal(st, full["state"])
     assert (ls > 0).all()
+
+
+# ------------------------------------------------------------------------------------------- f32 softmax
+SOFTMAX_GOLDEN = Path(__file__).resolve().parent / "golden" / "softmax_golden.npz"
+
+
+@pytest.mark.parametrize("V", [5, 17, 27, 256])
+def test_softmax_golden(V):
+    """The oracle's softmax equals, bit for bit, what the reference's own softmax() (cpu/ygg.cpp:59-72, built here)
+    returned for the committed rows (tests/golden/make_softmax_golden.py): probabilities and log-sum-exp."""
+    g = np.load(SOFTMAX_GOLDEN)
+    p, s = O.softmax(g[f"logits_{V}"])
+    np.testing.assert_array_equal(p.view(np.uint32), g[f"probs_{V}"].view(np.uint32))
+    np.testing.assert_array_equal(s.view(np.uint32), g[f"lse_{V}"].view(np.uint32))
+
+
+@pytest.mark.skipif(not O.have_ref_softmax(), reason="reference softmax driver not built (make -C oracle ref)")
+@pytest.mark.parametrize("V", [1, 5, 16, 17, 27, 200, 256])
+def test_softmax_live_reference(V):
+    """Fresh rows at spreads 0.01 to 500 against the reference build, bit for bit."""
+    rng = np.random.default_rng(V)
+    lg = np.concatenate([(rng.standard_normal((64, V)) * s).astype(np.float32) for s in (0.01, 1.0, 20.0, 500.0)])
+    p, s = O.softmax(lg)
+    rp, rs = O.ref_softmax(lg)
+    np.testing.assert_array_equal(p.view(np.uint32), rp.view(np.uint32))
+    np.testing.assert_array_equal(s.view(np.uint32), rs.view(np.uint32))
+
+
+def test_softmax_closed_forms():
+    """Equal logits: every term is exp(0) = 1 exactly, so tot = V and every probability is f32(1 / V), lse = mx +
+    log(V). One class 1000 above the rest: the others' terms are exp(-87) (the clamp), so the sum rounds to 1, that
+    class's probability is 1 and lse its logit. Integer logits shifted by an integer give the same probabilities (the
+    differences lg - mx are the same numbers) and lse shifted by it."""
+    for V in (1, 5, 27, 256):
+        lg = np.full((3, V), 2.5, np.float32)
+        lg[1] = -7.0
+        lg[2] = 0.0
+        p, s = O.softmax(lg)
+        assert np.all(p == np.float32(1.0) / np.float32(V))
+        np.testing.assert_allclose(s, lg[:, 0] + np.log(V), rtol=1e-6, atol=1e-6)
+    lg = np.full((2, 256), -1000.0, np.float32)
+    lg[0, 3] = 0.0
+    lg[1, 255] = 12.0
+    p, s = O.softmax(lg)
+    assert p[0, 3] == 1.0 and p[1, 255] == 1.0
+    assert np.all(p[0, :3] == p[0, 4]) and 0 < p[0, 0] < 1e-37
+    np.testing.assert_array_equal(s, [0.0, 12.0])
+    rng = np.random.default_rng(5)
+    lg = rng.integers(-40, 40, (16, 256)).astype(np.float32)
+    p0, s0 = O.softmax(lg)
+    p1, s1 = O.softmax(lg + np.float32(1000.0))
+    np.testing.assert_array_equal(p0, p1)
+    np.testing.assert_allclose(s1 - s0, 1000.0, rtol=0, atol=1e-3)
+
+
+def test_softmax_sum_order_is_pinned():
+    """The golden rows tell a left-to-right sum apart from the reference's 16-lane accumulation and halving join:
+    summing each row's probabilities (terms of the golden rows' magnitudes) both ways in f32 gives different totals
+    on some rows, so a restatement with the wrong order would fail test_softmax_golden."""
+    g = np.load(SOFTMAX_GOLDEN)
+    differ = 0
+    for terms in g["probs_256"]:
+        seq = np.float32(0.0)
+        for v in terms:
+            seq = np.float32(seq + v)
+        lanes = [np.float32(0.0)] * 16
+        for i, v in enumerate(terms):
+            lanes[i % 16] = np.float32(lanes[i % 16] + v)
+        h = [np.float32(lanes[j] + lanes[8 + j]) for j in range(8)]
+        q = [np.float32(h[j] + h[4 + j]) for j in range(4)]
+        differ += int(seq != np.float32(np.float32(q[0] + q[2]) + np.float32(q[1] + q[3])))
+    assert differ > 0

@@ -15,7 +15,7 @@ LIB_PATH = Path(__file__).resolve().parent / "libygg_hip.so"
 
 # every entry point of include/ygg_hip.h
 SYMBOLS = ("ygg_load", "ygg_load_blob", "ygg_model_info", "ygg_free", "ygg_step", "ygg_run", "ygg_run_grouped",
-           "ygg_run_grouped_noalloc", "ygg_score",
+           "ygg_run_grouped_noalloc", "ygg_softmax", "ygg_score",
            "ygg_generate", "ygg_take_errors", "ygg_float_load", "ygg_float_run", "ygg_float_take_errors",
            "ygg_float_free", "ygg_kernel_name", "ygg_last_error", "ygg_version")
 
@@ -75,6 +75,7 @@ def lib() -> ctypes.CDLL:
     L.ygg_run.argtypes = [vp, vp, i32, i32, vp, vp, vp, vp, vp, vp]
     L.ygg_run_grouped.argtypes = [vp, vp, i32, i32, vp, vp, vp, vp, vp, vp]
     L.ygg_run_grouped_noalloc.argtypes = [vp, vp, i32, i32, vp, vp, vp, vp, vp, vp]
+    L.ygg_softmax.argtypes = [vp, ctypes.c_int64, i32, vp, vp, vp]
     L.ygg_score.argtypes = [vp, vp, vp, i32, i32, vp, vp, vp]
     L.ygg_generate.argtypes = [vp, vp, i32, i32, vp, ctypes.c_float, i32, ctypes.c_uint64, vp, vp, vp]
     L.ygg_take_errors.argtypes = [vp, vp, ctypes.POINTER(ctypes.c_uint32)]

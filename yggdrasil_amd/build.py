@@ -31,7 +31,8 @@ HIPCC_FLAGS = ["--offload-arch=" + ARCH, "-O3", "-std=c++17", "-ffp-contract=off
                "-mcode-object-version=5", "-Wall", "-Wno-unused-result",
                "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 SOURCES = ["ygg_kernels.hip", "ygg_kernels_fast.hip", "ygg_kernels_fact.hip", "ygg_kernels_deep.hip",
-           "ygg_kernels_flow.hip", "ygg_kernels_solo.hip", "ygg_kernels_group.hip", "ygg_capi.hip", "ygg_float.hip"]
+           "ygg_kernels_flow.hip", "ygg_kernels_solo.hip", "ygg_kernels_group.hip", "ygg_softmax.hip", "ygg_capi.hip",
+           "ygg_float.hip"]
 
 
 def hipcc() -> str:

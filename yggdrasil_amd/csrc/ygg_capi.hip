@@ -949,6 +949,15 @@ int ygg_run_grouped_noalloc(const ygg_model *m, const int32_t *d_tokens, int B, 
     return YGG_OK;
 }
 
+int ygg_softmax(const float *d_logits, int64_t rows, int V, float *d_probs, float *d_lse, void *stream) {
+    if (rows < 0) return fail(YGG_ERR_ARG, "negative rows (%lld)", (long long)rows);
+    if (V < 1 || V > 256) return fail(YGG_ERR_ARG, "V = %d outside [1, 256]", V);
+    if (rows == 0) return YGG_OK;
+    if (!d_logits || !d_probs) return fail(YGG_ERR_ARG, "logits or probs is NULL");
+    HIP_TRY(ygg::launch_softmax(d_logits, rows, V, d_probs, d_lse, (hipStream_t)stream));
+    return YGG_OK;
+}
+
 int ygg_score(const ygg_model *m, const int32_t *d_tokens, const int32_t *d_targets, int B, int T, int8_t *d_state,
               double *d_nll, void *stream) {
     if (!m) return fail(YGG_ERR_ARG, "model is NULL");

@@ -75,5 +75,7 @@ Kernel find_solo_launcher(int n, int R, int R2, int L, bool group);
 hipError_t launch_grouped(const YggDevModel &m, const int32_t *tokens, int B, int T, int8_t *state, const YggIO &io,
                           void *ws, int mfma_min, hipStream_t stream);
 size_t grouped_ws_bytes(int B, int L);
+// the f32 softmax of the reference's time mode over rows of V <= 256 logits (ygg_softmax.hip)
+hipError_t launch_softmax(const float *logits, int64_t rows, int V, float *probs, float *lse, hipStream_t stream);
 
 }  // namespace ygg

@@ -61,8 +61,32 @@ def device_tokens(tokens, vocab: int, device, check_device: bool = False) -> tor
     return host.to(device, non_blocking=True)
 
 
+def softmax(logits: torch.Tensor, out: Optional[torch.Tensor] = None, lse: bool = True):
+    """The f32 softmax the reference's time mode applies to every token's logits (cpu/ygg.cpp:59-72, 545-553), on
+    the GPU (ygg_softmax): logits (..., V) f32 on a ROCm device, V <= 256 -> (probabilities of the same shape, equal to
+    the reference's to the bit, in out if given (it may be logits itself); the log-sum-exp of each row, (...) f32, or
+    None when lse is False). Stream-ordered on the current stream; nothing waits."""
+    if not (isinstance(logits, torch.Tensor) and logits.device.type == "cuda" and logits.dtype == torch.float32):
+        raise ValueError("logits must be a float32 tensor on a ROCm device")
+    if logits.dim() < 1:
+        raise ValueError("logits need a class axis")
+    V = logits.shape[-1]
+    if not 1 <= V <= 256:
+        raise ValueError(f"V = {V} outside [1, 256]")
+    x = logits.contiguous()
+    p = torch.empty_like(x) if out is None else out
+    if p.shape != x.shape or p.dtype != torch.float32 or not p.is_contiguous() or p.device != x.device:
+        raise ValueError("out must be a contiguous float32 tensor shaped like logits, on the same device")
+    ls = torch.empty(x.shape[:-1], dtype=torch.float32, device=x.device) if lse else None
+    with torch.cuda.device(x.device):
+        check(_lib.lib().ygg_softmax(_ptr(x), x.numel() // V if V else 0, V, _ptr(p), _ptr(ls), _stream()))
+    return p, ls
+
+
 class Yggdrasil:
     """An int8 model on one GPU (the ``hip`` backend)."""
+
+    softmax = staticmethod(softmax)
 
     def __init__(self, path, device=None, graph: bool = False, check_tokens: bool = False):
         if not torch.cuda.is_available():
