@@ -191,9 +191,12 @@ def _counter_sums(d: str) -> dict:
     return out
 
 
-def traffic_summary(fetch_dir, write_dir, copy_fetch_dir, copy_write_dir, copy_bytes, workload, algorithmic):
+def traffic_summary(fetch_dir, write_dir, copy_fetch_dir, copy_write_dir, copy_bytes, workload, algorithmic,
+                    rdreq_dir=None, kernel=None):
     """HBM bytes of the last step-kernel dispatch from two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE; KiB per
-    dispatch), each scaled by bytes moved / counter reading of a plain device copy of copy_bytes."""
+    dispatch), each scaled by bytes moved / counter reading of a plain device copy of copy_bytes. rdreq_dir: a third
+    run of TCC_EA0_RDREQ_sum and TCC_EA0_RDREQ_DRAM_sum (128-byte read requests leaving L2, and those addressed to
+    the memory controller, behind which the MALL sits)."""
     f, w = _counter_sums(fetch_dir), _counter_sums(write_dir)
     cf, cw = _counter_sums(copy_fetch_dir), _counter_sums(copy_write_dir)
     copies_f = [v for (_, n), v in cf.items() if "copyBuffer" in n]
@@ -202,8 +205,9 @@ def traffic_summary(fetch_dir, write_dir, copy_fetch_dir, copy_write_dir, copy_b
         raise SystemExit("no copyBuffer dispatch in the calibration runs")
     ff = copy_bytes / (1024 * float(np.mean(copies_f)))
     wf = copy_bytes / (1024 * float(np.mean(copies_w)))
-    kf = max(k for k in f if k[1].startswith("ygg::"))
-    kw = max(k for k in w if k[1].startswith("ygg::"))
+    pick = (lambda n: n == kernel) if kernel else (lambda n: n.startswith("ygg::"))
+    kf = max(k for k in f if pick(k[1]))
+    kw = max(k for k in w if pick(k[1]))
     assert kf[1] == kw[1], (kf, kw)
     fetched, written = f[kf] * 1024 * ff, w[kw] * 1024 * wf
     doc = {"workload": workload, "kernel": kf[1], "fetch_size_kib": f[kf], "write_size_kib": w[kw],
@@ -215,6 +219,23 @@ def traffic_summary(fetch_dir, write_dir, copy_fetch_dir, copy_write_dir, copy_b
     if algorithmic:
         doc["algorithmic_bytes_per_launch"] = int(algorithmic)
         doc["traffic_over_algorithmic"] = round((fetched + written) / algorithmic, 3)
+    if rdreq_dir:
+        import csv
+        by = {}
+        for fcsv in sorted(Path(rdreq_dir).rglob("*counter_collection.csv")):
+            for r in csv.DictReader(open(fcsv)):
+                name = r["Kernel_Name"].split("(")[0].strip()
+                name = name[5:] if name.startswith("void ") else name
+                if name == kf[1]:
+                    k = (int(r["Dispatch_Id"]), r["Counter_Name"])
+                    by[k] = by.get(k, 0.0) + float(r["Counter_Value"])
+        last = max(d for d, _ in by)
+        rq, dr = by.get((last, "TCC_EA0_RDREQ_sum"), 0.0), by.get((last, "TCC_EA0_RDREQ_DRAM_sum"), 0.0)
+        doc["read_requests_128B"] = int(rq)
+        doc["read_requests_to_memory_controller_128B"] = int(dr)
+        doc["mall_split"] = ("none measurable: every L2 read request is addressed to the memory controller, which "
+                             "serves MALL hits and HBM reads alike; traffic counts both") if rq and dr == rq else \
+            f"{dr / rq:.4f} of the read requests go to the memory controller" if rq else None
     return doc
 
 
@@ -263,12 +284,13 @@ def main():
         return
     if len(sys.argv) > 1 and sys.argv[1] == "--traffic":
         # python bench.py --traffic FETCH_DIR WRITE_DIR COPY_FETCH_DIR COPY_WRITE_DIR COPY_BYTES BENCH_JSON OUT_JSON
+        #                           [RDREQ_DIR]
         fd, wd, cfd, cwd, cb, bj, out = sys.argv[2:9]
+        rdq = sys.argv[9] if len(sys.argv) > 9 else None
         b = json.loads(Path(bj).read_text().strip().splitlines()[-1])
         wl = b["config"]["workload"].split(" (")[0]
-        doc = traffic_summary(fd, wd, cfd, cwd, int(cb), wl, b["roofline"]["algorithmic_bytes_per_launch"])
-        if doc["kernel"] != b["roofline"]["kernel"]:
-            raise SystemExit(f"profiled kernel {doc['kernel']} is not the bench's {b['roofline']['kernel']}")
+        doc = traffic_summary(fd, wd, cfd, cwd, int(cb), wl, b["roofline"]["algorithmic_bytes_per_launch"], rdq,
+                              b["roofline"]["kernel"])
         Path(out).write_text(json.dumps(doc, indent=1) + "\n")
         print(json.dumps(doc))
         return
@@ -373,15 +395,19 @@ def main():
         f"ygg_run_grouped: grp_route, grp_plan, grp_update per (token, layer), MFMA tiles from " \
         f"{os.environ.get('YGG_GROUP_MFMA_MIN', '8')} streams"
     # HBM bytes per launch measured by rocprofv3 (FETCH_SIZE, WRITE_SIZE, copy-calibrated) for this workload and kernel
-    traffic = None
+    traffic, traffic_detail = None, None
     tf = ROOT / "profiles" / f"traffic_{w.name}.json"
     if tf.exists() and B == w.streams and T == w.steps:
         try:
             doc = json.loads(tf.read_text())
             if doc.get("kernel") == kernel:
                 traffic = doc.get("hbm_bytes_per_launch")
+                traffic_detail = {k: doc[k] for k in ("fetched_bytes", "written_bytes", "traffic_over_algorithmic",
+                                                      "read_requests_128B", "read_requests_to_memory_controller_128B",
+                                                      "mall_split") if k in doc}
+                traffic_detail["source"] = f"profiles/{tf.name}"
         except (OSError, ValueError):
-            traffic = None
+            traffic, traffic_detail = None, None
 
     # the f32 softmax of every logit row (what the reference's time mode adds per token), timed apart from the step
     sm = None
@@ -426,7 +452,7 @@ def main():
                            f"of every stream, logits written per token",
                    "parallelism": "1 GPU (streams independent)"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic,
+                     "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic, "traffic_detail": traffic_detail,
                      "algorithmic_bytes_per_launch": alg["compulsory"],
                      "compulsory_bytes_per_token": round(alg["per_token_compulsory"], 1),
                      "per_stream_bytes_per_token": round(alg["per_token_per_stream"], 1),
