@@ -467,8 +467,10 @@ def main():
 
 
 def run_batch1(model, w, n_tok: int, L, _lib) -> dict:
-    """One stream: (a) one persistent ygg_run launch over n_tok tokens; (b) the per-token ygg_step loop captured in
-    hipGraphs of 512 steps each (state in place), replayed back to back. Both write the logits of every token."""
+    """One stream of n_tok known tokens: (a) one persistent ygg_run launch; (a') the same followed by ygg_softmax over
+    its rows (the reference's time mode: known tokens, state carried, an f32 softmax per token), eagerly and captured
+    in one hipGraph; (b) the per-token ygg_step loop captured in hipGraphs of 512 steps each (state in place, a launch
+    per token, as a caller whose every token depends on the last would run); (c) greedy generation on the device."""
     import torch
     dev = model.device
     x1 = torch.as_tensor(w.make_tokens(1, n_tok)[0], device=dev).contiguous()
@@ -501,7 +503,24 @@ def run_batch1(model, w, n_tok: int, L, _lib) -> dict:
     e1.record(stream)
     torch.cuda.synchronize()
     time_mode_us = e0.elapsed_time(e1) * 1e3 / n_tok
-    del pr, ls
+    # the same run captured in one hipGraph (the launch and the softmax as its two nodes) and replayed: the batch-1
+    # latency run of the whole token file, as `ygg time` runs it on the host
+    g1 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g1):
+        cs = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        _lib.check(L.ygg_run(model._h, ptr(x1), 1, n_tok, ptr(st), ptr(lg), None, None, None, cs))
+        _lib.check(L.ygg_softmax(ptr(lg), n_tok, V, ptr(pr), ptr(ls), cs))
+    st.zero_()
+    g1.replay()
+    st.zero_()
+    torch.cuda.synchronize()
+    e0.record(stream)
+    g1.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    graph_run_us = e0.elapsed_time(e1) * 1e3 / n_tok
+    graph_run_same = bool(torch.equal(lg, ref_logits))
+    del g1, pr, ls
     # (b) graphs of per-token steps
     G = 512
     graphs = []
@@ -539,6 +558,7 @@ def run_batch1(model, w, n_tok: int, L, _lib) -> dict:
     gen_us = e0.elapsed_time(e1) * 1e3 / n_tok
     return {"tokens": n_tok, "us_per_token_persistent_launch": round(run_us, 3),
             "us_per_token_time_mode": round(time_mode_us, 3),
+            "us_per_token_graph_run": round(graph_run_us, 3), "graph_run_logits_equal_persistent": graph_run_same,
             "us_per_token_graph_step": round(graph_us, 3), "graph_steps_per_graph": G,
             "graph_logits_equal_persistent": same, "us_per_token_generate_greedy": round(gen_us, 3),
             "kernels": {"persistent_launch": model.kernel_name(1, n_tok), "graph_step": model.kernel_name(1, 1),
