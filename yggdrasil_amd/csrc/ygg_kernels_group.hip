@@ -10,6 +10,9 @@ hipError_t launch_grouped(const YggDevModel &m, const int32_t *tokens, int B, in
                           void *ws_mem, int mfma_min, hipStream_t stream) {
     if (B <= 0 || T <= 0) return hipSuccess;
     if (m.V > kGrpMaxExperts || (m.L > 1 && m.E > kGrpMaxExperts)) return hipErrorInvalidValue;
+    // (the MFMA tile stages a whole record in LDS)
+    for (int l = 0; l < m.L; l++)
+        if (m.layers[l].gath_bytes > kGrpRec) return hipErrorInvalidValue;
     const GroupWS ws = group_ws_carve(ws_mem, B, m.L);
     hipLaunchKernelGGL(grp_init, dim3((B + 255) / 256), dim3(256), 0, stream, B, T, ws);
     // update workgroups: about one wavefront per tile of the worst case (every stream alone at its expert)
