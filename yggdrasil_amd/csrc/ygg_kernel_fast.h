@@ -1286,8 +1286,8 @@ __device__ __forceinline__ void flow_update(FlowShared<SH, L, P, GROUP, SCORE> &
                                             unsigned long long &dg, double &nacc, int lane) {
     using F = SH;
     using FS = FlowShared<SH, L, P, GROUP, SCORE>;
-    constexpr int N = SH::N, QM = FS::QR - 1, LG = kFlowLogits<L, P>;
-    const int V = m.V, VP = m.VP;
+    constexpr int QM = FS::QR - 1, LG = kFlowLogits<L, P>;
+    const int VP = m.VP;
     t = ok ? t : 0;
     int8_t *qnew = sh.qring[l][(t + 1) & QM];
     int qn[F::C];
