@@ -279,8 +279,10 @@ def gather_probe(gbytes: float = 3.63, rec_bytes: int = 7168, steps: int = 256) 
 
 def main():
     if len(sys.argv) > 1 and sys.argv[1] == "--probe":
-        # python bench.py --probe: the gather probe only (no model)
-        print(json.dumps({"gather_probe": gather_probe()}), flush=True)
+        # python bench.py --probe [GB]: the gather probe only (no model), over a buffer of GB (default the
+        # configuration-4 model's size)
+        gb = float(sys.argv[2]) if len(sys.argv) > 2 else 3.63
+        print(json.dumps({"gather_probe": gather_probe(gb)}), flush=True)
         return
     if len(sys.argv) > 1 and sys.argv[1] == "--traffic":
         # python bench.py --traffic FETCH_DIR WRITE_DIR COPY_FETCH_DIR COPY_WRITE_DIR COPY_BYTES BENCH_JSON OUT_JSON
