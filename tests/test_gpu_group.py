@@ -137,16 +137,46 @@ def test_grouped_edges(model_dir):
     model.close()
 
 
-def test_grouped_rejects_other_shapes(model_dir):
-    """A model outside the grouped step's shape (d_state 64) reports YGG_ERR_LIMITS and runs nothing."""
+@pytest.mark.parametrize("spec", [synth.ModelSpec(64, 16, 6, 27, 2), synth.ModelSpec(128, 16, 6, 27, 3, group=True),
+                                  synth.ModelSpec(128, 16, 6, 27, 3, input_rank=16),
+                                  synth.ModelSpec(128, 16, 15, 5, 2)],
+                         ids=["d64", "group_scales", "factored", "depth15"])
+def test_grouped_rejects_other_shapes(model_dir, spec):
+    """Models outside the grouped step's shape (d_state 64, group scales, factored inputs, router depth 15) report
+    YGG_ERR_LIMITS from both grouped entry points and run nothing."""
+    import ctypes
+    import torch
     from yggdrasil_amd import _lib
-    path = model_dir / "grp_d64.bin"
-    synth.write_model(synth.ModelSpec(64, 16, 6, 27, 2), 1, path)
+    path = model_dir / f"grp_reject_{spec.d_state}_{int(spec.group)}_{spec.input_rank}_{spec.router_depth}.bin"
+    synth.write_model(spec, 1, path)
     model = _load(path)
     assert model.info.grouped == 0
     with pytest.raises(_lib.YggError) as e:
         model.run_grouped(np.zeros((2, 3), np.int32))
     assert _lib.ERRORS[e.value.code] == "limits"
+    x = torch.zeros(2, 3, dtype=torch.int32, device=model.device)
+    st = model.init_state(2)
+    rc = _lib.lib().ygg_run_grouped_noalloc(model._h, ctypes.c_void_p(x.data_ptr()), 2, 3,
+                                             ctypes.c_void_p(st.data_ptr()), None, None, None, None, None)
+    assert _lib.ERRORS[rc] == "limits"
+    model.close()
+
+
+def test_grouped_many_streams(model_dir):
+    """20 000 streams (the plan's streams-per-thread passes run three times; the workspace grows past an earlier
+    call's) against the per-stream kernel on the same inputs: leaves, final state and digest equal."""
+    import torch
+    path = _model(model_dir, 3, 27, 3, "gauss")
+    model = _load(path)
+    small = model.run_grouped(np.ascontiguousarray(synth.uniform_tokens(27, 100, 2, 1), np.int32))
+    x = torch.as_tensor(synth.uniform_tokens(27, 20000, 3, 2), device=model.device)
+    a = model.run(x, logits=False, leaves=True, digest=True)
+    b = model.run_grouped(x, logits=False, leaves=True, digest=True)
+    torch.cuda.synchronize()
+    del small
+    for k in ("leaves", "state", "digest"):
+        assert torch.equal(a[k], b[k]), k
+    assert model.take_errors() == 0
     model.close()
 
 
