@@ -72,6 +72,8 @@ def test_kernel_case(hip, model_dir, ci, kernel_env):
     common = specialised(spec)
     if common:
         _expect_kernel(model, kernel_env)
+    elif fast_only(spec):
+        _expect_fast_only(model, kernel_env, spec)
     else:
         assert model.info.kernel == 0 and model.info.pipe_max_streams == 0 and model.info.deep_max_streams == 0
     got = _gpu_run(model, x)
@@ -99,6 +101,34 @@ def specialised(spec) -> bool:
     r2 = 16 if spec.n_layers == 1 else spec.layer_input_rank
     return (spec.d_state, spec.readout_rank, r2) in SHAPES and spec.block_size == 16 and spec.input_rank <= 64 and \
         (not spec.group or spec.d_state != 96) and spec.n_layers <= 5
+
+
+# the per-stream kernel's other shapes (state width, readout rank, layer-input rank, block; csrc/ygg_launch.h
+# YGG_FAST_EXTRA): the kernel-test shapes outside SHAPES or at block 8, table storage, 2 to 5 layers
+FAST_ONLY = {(128, 16, 32, 8), (64, 8, 0, 8), (256, 16, 48, 8), (128, 16, 4, 16), (256, 8, 20, 16), (64, 8, 0, 16),
+             (64, 32, 20, 16)}
+
+
+def fast_only(spec) -> bool:
+    """Whether a model runs on the per-stream kernel alone (a shape of FAST_ONLY; fast8_kernel at block 8)."""
+    return (not specialised(spec) and 2 <= spec.n_layers <= 5 and spec.input_rank == 0 and
+            (spec.d_state, spec.readout_rank, spec.layer_input_rank, spec.block_size) in FAST_ONLY and
+            not (spec.group and spec.d_state == 96))
+
+
+def _expect_fast_only(model, kernel_env, spec):
+    """A fast-only shape: every call on the per-stream kernel (any YGG_KERNEL but generic, which forces the general
+    one); no other family is built for it."""
+    info = model.info
+    assert info.kernel == (0 if kernel_env == "generic" else 1), info.kernel
+    assert info.pipe_max_streams == info.deep_max_streams == info.flow_max_streams == info.solo_max_streams == 0
+    assert info.grouped == 0
+    want = "ygg::run_kernel<" if kernel_env == "generic" else \
+        ("ygg::fast8_kernel<" if spec.block_size == 8 else "ygg::fast_kernel<")
+    for B, T in ((8, 64), (8, 1), (4096, 64)):
+        assert model.kernel_name(B, T).startswith(want), model.kernel_name(B, T)
+    assert model.kernel_name(8, 64, score=True).startswith(want)
+    assert model.kernel_name(8, 64, generate=True).startswith(want)
 
 
 def default_plan(D: int) -> list:

@@ -30,9 +30,9 @@ ARCH = "gfx950"
 HIPCC_FLAGS = ["--offload-arch=" + ARCH, "-O3", "-std=c++17", "-ffp-contract=off", "-fPIC",
                "-mcode-object-version=5", "-Wall", "-Wno-unused-result",
                "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
-SOURCES = ["ygg_kernels.hip", "ygg_kernels_fast.hip", "ygg_kernels_fact.hip", "ygg_kernels_deep.hip",
-           "ygg_kernels_flow.hip", "ygg_kernels_solo.hip", "ygg_kernels_group.hip", "ygg_softmax.hip", "ygg_capi.hip",
-           "ygg_float.hip"]
+SOURCES = ["ygg_kernels.hip", "ygg_kernels_fast.hip", "ygg_kernels_fast_x.hip", "ygg_kernels_fact.hip",
+           "ygg_kernels_deep.hip", "ygg_kernels_flow.hip", "ygg_kernels_solo.hip", "ygg_kernels_group.hip",
+           "ygg_softmax.hip", "ygg_capi.hip", "ygg_float.hip"]
 
 
 def hipcc() -> str:

@@ -480,16 +480,29 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
 #undef YGG_S
         return false;
     };
+    auto extra_ok = [](int nn, int rr, int r2, int b) {
+#define YGG_X(N_, R_, R2_, B_) \
+    if (nn == N_ && rr == R_ && r2 == R2_ && b == B_) return true;
+        YGG_FAST_EXTRA(YGG_X)
+#undef YGG_X
+        return false;
+    };
     const int R2f = L == 1 ? 16 : R2;
+    // std_shape: every specialised kernel family has builds; extra: the per-stream kernel only (YGG_FAST_EXTRA)
+    const bool std_shape = fa.blk == 16 && shape_ok(n, R, R2f);
+    const bool extra_shape = !std_shape && L > 1 && !factored && extra_ok(n, R, R2, fa.blk);
     const int64_t rec_bound = (int64_t)n * (2 * fa.blk + R2 + R) + 128 +   // gather record bytes, at most
                               (factored ? (int64_t)fa.K * n + 2 * n + 4 : 0);
     const bool small_tables = (int64_t)E * V * n * 2 < ((int64_t)1 << 32) && (int64_t)E * rec_bound < ((int64_t)1 << 32);
     // (factored routed inputs: fact_kernel, input ranks up to 64; the other specialised kernels take table storage)
-    if (kmode != "generic" && fa.blk == 16 && shape_ok(n, R, R2f) && L <= ygg::kMaxFastLayers && VP <= 256 &&
+    if (kmode != "generic" && (std_shape || extra_shape) && L <= ygg::kMaxFastLayers && VP <= 256 &&
         small_tables && (!factored || fa.K <= YGG_MAX_FACT_RANK) && transitions_split(fa, fl))
-        fast = factored ? ygg::find_fact_launcher(n, R, R2f, L, true, group)
-                        : ygg::find_fast_launcher(n, R, R2f, L, true, group);
+        fast = extra_shape ? ygg::find_fast_extra_launcher(n, R, R2, fa.blk, L, group)
+               : factored  ? ygg::find_fact_launcher(n, R, R2f, L, true, group)
+                           : ygg::find_fast_launcher(n, R, R2f, L, true, group);
     if (fast) launch = fast;
+    // the other specialised families (deep descent, layer and tick pipelines, solo, grouped) at YGG_SHAPES only
+    const bool family = fast && std_shape;
 
     RoundPlan rplan = round_plan(L > 1 ? fa.D : 0);
     // YGG_ROUNDS=h0,h1,...: an explicit plan for the specialised kernels (every round 1..4 levels, sum D)
@@ -512,7 +525,7 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     // the deep descent: at most 4 rounds, the first of at least 2 levels, the rounds after the second at most 6
     // levels together (one lane per node)
     const char *denv = getenv("YGG_DEEP");
-    const bool deep = fast && !factored && L > 1 && !(denv && !strcmp(denv, "0")) && rplan.n >= 2 && rplan.n <= 4 &&
+    const bool deep = family && !factored && L > 1 && !(denv && !strcmp(denv, "0")) && rplan.n >= 2 && rplan.n <= 4 &&
                       rplan.h[0] >= 2 && (rplan.n < 4 || rplan.h[2] + rplan.h[3] <= 6);
     // the solo kernel: the first two rounds at most 8 levels together (its round A, from registers), the others at
     // most 6 (one round with a lane per node); round A's rows of every routed layer in a lane's registers
@@ -520,17 +533,17 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     const bool solo_plan = rplan.n >= 1 && rplan.n <= 4 && (rplan.n < 2 || rplan.h[0] + rplan.h[1] <= 8) &&
                            (rplan.n < 4 || rplan.h[2] + rplan.h[3] <= 6);
     ygg::Kernel solok;
-    if (fast && !factored && L > 1 && solo_plan && (L - 1) * n <= 512 && !(senv && !strcmp(senv, "0")) &&
+    if (family && !factored && L > 1 && solo_plan && (L - 1) * n <= 512 && !(senv && !strcmp(senv, "0")) &&
         kmode == "solo")
         solok = ygg::find_solo_launcher(n, R, R2f, L, group);
     ygg::Kernel pipe, pipe_few, deepk, flowk;
-    if (fast && !factored && kmode != "fast" && kmode != "deep" && kmode != "flow" && kmode != "solo") {
+    if (family && !factored && kmode != "fast" && kmode != "deep" && kmode != "flow" && kmode != "solo") {
         pipe = ygg::find_pipe_launcher(n, R, R2f, L, true, group);
         pipe_few = ygg::find_pipe_launcher(n, R, R2f, L, false, group);
     }
     // the tick-pipelined kernel: plans of 3 or 4 rounds (YGG_FLOW=0: off)
     const char *fenv = getenv("YGG_FLOW");
-    if (fast && !factored && L > 1 && (kmode == "" || kmode == "flow") && !(fenv && !strcmp(fenv, "0")))
+    if (family && !factored && L > 1 && (kmode == "" || kmode == "flow") && !(fenv && !strcmp(fenv, "0")))
         flowk = ygg::find_flow_launcher(n, R, R2f, L, rplan.n, group);
     // (the deep kernel exists where its LDS fits a workgroup)
     const ygg::Kernel deep_avail = deep ? ygg::find_deep_launcher(n, R, R2f, L, group) : ygg::Kernel();
@@ -693,7 +706,7 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     m->solo = solok;
     m->solo_all = solok && kmode == "solo";
     // the leaf-grouped step: the benchmark shape with the specialised kernels' record layout, tensor scales, tables
-    m->grouped_ok = fast && !factored && !group && n == 128 && R == 8 && R2f == 16 && fa.blk == 16 &&
+    m->grouped_ok = family && !factored && !group && n == 128 && R == 8 && R2f == 16 && fa.blk == 16 &&
                     (L == 1 || fa.D <= 14);
     {
         const char *gm = getenv("YGG_GROUP_MFMA_MIN");
@@ -705,7 +718,7 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     m->arena_bytes = total;
     m->run = launch;
     // the uncapped per-stream build while every stream of the call is resident with it
-    if (fast) {
+    if (family) {
         m->run_few = factored ? ygg::find_fact_launcher(n, R, R2f, L, false, group)
                               : ygg::find_fast_launcher(n, R, R2f, L, false, group);
         for (int md = 0; md < 3; md++)

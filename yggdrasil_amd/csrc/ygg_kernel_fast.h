@@ -44,16 +44,20 @@ template <int N> struct Fast {
     static constexpr float kInvN = 1.0f / (float)N;
 };
 
-// a specialised shape: state width N, readout rank R, layer-input rank R2 (a multiple of 16)
-template <int N_, int R_, int R2_> struct Shape : Fast<N_> {
-    static constexpr int N = N_, R = R_, R2 = R2_;
+// a specialised shape: state width N, readout rank R, layer-input rank R2 (a multiple of 4, 0: no layer input),
+// transition block BLK (16 or 8)
+template <int N_, int R_, int R2_, int BLK_ = 16> struct Shape : Fast<N_> {
+    static constexpr int N = N_, R = R_, R2 = R2_, BLK = BLK_;
+    static constexpr int AW = Fast<N_>::C * BLK / 2, NA = AW / 4;   // A hi/lo dwords and 16-byte chunks per lane
     static constexpr int RL = ReadoutLanes<N, R>::RL, SP = ReadoutLanes<N, R>::SP, GP = ReadoutLanes<N, R>::GP;
     static constexpr int SPW = SP / 4;
     static constexpr int SPA = SP % 16 == 0 ? 16 : (SP % 8 == 0 ? 8 : 4);
     static constexpr int K4 = R2 / 4;      // U' dwords per coordinate
-    static constexpr int RG = R2 / 16;     // passes of 16 V' rows
+    static constexpr int K4A = K4 > 0 ? K4 : 1;                     // (array extent)
+    static constexpr int RG = (R2 + 15) / 16;      // passes of 16 V' rows (V' is held zero-padded to 16 RG rows)
+    static constexpr int R2P = 16 * RG, R2A = R2P > 0 ? R2P : 1;   // V' rows and m_v entries held; array extent
     static constexpr int QC = R / 4;       // 16-byte chunks of a lane's 4 unembedding classes
-    static constexpr int ZQ = R > 16 ? R : 16, ZL = R2 > 16 ? R2 : 16;    // LDS bytes of zq and zl
+    static constexpr int ZQ = R > 16 ? R : 16, ZL = R2P > 16 ? R2P : 16;    // LDS bytes of zq and zl
 };
 
 // factored input storage (cpu/ygg.cpp:339-358): input ranks up to 64, this many dwords per coordinate
@@ -62,7 +66,7 @@ constexpr int kFactK4 = YGG_MAX_FACT_RANK / 4;
 // the per-expert registers of one stream and layer. FACT: the model stores its routed inputs factored (the routed
 // layers' records hold U_r, c_r and su_r instead of a table)
 template <class SH, bool FACT = false> struct Gather {
-    uint32_t aw[SH::AW], pw[SH::SPW], uw[SH::K4][SH::C];
+    uint32_t aw[SH::AW], pw[SH::SPW], uw[SH::K4A][SH::C];
     // the table row's C int16 entries of this lane as loaded: packed in pairs (C >= 2) or one sign-extended entry
     // (C = 1); unpacked where the update reads them, so that nothing waits for the load in between. FACT, routed: the
     // factored bias c_r's entries, packed the same way
@@ -107,8 +111,8 @@ template <class SH, int L, bool WITHV = true> struct SharedTables {
     static constexpr int LR = L > 1 ? L - 1 : 1;
     int8_t Q[L][256 * SH::R];
     int8_t W[LR][15 * kLdsRow<SH::N>];
-    int8_t V[WITHV ? LR : 1][WITHV ? SH::R2 * kLdsRow<SH::N> : 16];
-    float mv[LR][SH::R2];
+    int8_t V[WITHV ? LR : 1][WITHV ? SH::R2A * kLdsRow<SH::N> : 16];
+    float mv[LR][SH::R2A];
 };
 
 template <class SH, int L> constexpr int kTablesBytes = (int)sizeof(SharedTables<SH, L>);
@@ -174,7 +178,7 @@ __device__ __forceinline__ void load_group_tables(GroupTables<SH, L> &G, const Y
 template <class SH, int L, int NT, bool WITHV = true>
 __device__ __forceinline__ void load_tables(SharedTables<SH, L, WITHV> &S, const YggDevModel &m, int tid) {
     // 16-byte chunks: RC per row in memory, SC per row in LDS
-    constexpr int N = SH::N, R2 = SH::R2, QC = SH::QC;
+    constexpr int N = SH::N, R2 = SH::R2P, QC = SH::QC;      // (V' and m_v as held: R2 rounded up to 16)
     constexpr int RC = N / 16, SC = kLdsRow<N> / 16, LR = L > 1 ? L - 1 : 1;
     constexpr int QK = (16 * SH::R + NT - 1) / NT;     // Q chunks (at most 16 R: VP <= 256) per thread and layer
     constexpr int VR = 15 + (WITHV ? R2 : 0);          // first-round rows and V' rows of a routed layer
@@ -206,7 +210,7 @@ __device__ __forceinline__ void load_tables(SharedTables<SH, L, WITHV> &S, const
     }
 #pragma unroll
     for (int l = 1; l < L; l++)
-        if (tid / R2 == l - 1) mvv = m.layers[l].mv[tid % R2];
+        if (R2 > 0 && tid / (R2 > 0 ? R2 : 1) == l - 1) mvv = m.layers[l].mv[tid % (R2 > 0 ? R2 : 1)];
 #pragma unroll
     for (int l = 0; l < L; l++)
 #pragma unroll
@@ -224,7 +228,7 @@ __device__ __forceinline__ void load_tables(SharedTables<SH, L, WITHV> &S, const
             else if (WITHV && c < VR * RC)
                 ((uint4 *)S.V[l - 1])[((c - 15 * RC) / RC) * SC + (c - 15 * RC) % RC] = rv[l - 1][k];
         }
-    if (L > 1 && tid < R2 * (L - 1)) S.mv[tid / R2][tid % R2] = mvv;
+    if (L > 1 && R2 > 0 && tid < R2 * (L - 1)) S.mv[tid / (R2 > 0 ? R2 : 1)][tid % (R2 > 0 ? R2 : 1)] = mvv;
 }
 
 // Touch every 64-byte line of the kernel argument (the model description, read by scalar loads) at entry: the
@@ -585,14 +589,15 @@ __device__ __forceinline__ void layer_input(int8_t *zls, const int8_t *V0, const
 
 // layer_input with V' in registers: vr[p] the quad share of row 16 p + qj (loaded once by load_vrows)
 template <class SH>
-__device__ __forceinline__ void load_vrows(uint32_t (&vr)[SH::RG][Fast<SH::N>::QW], const YggDevLayer &y, int lane) {
+__device__ __forceinline__ void load_vrows(uint32_t (&vr)[SH::RG > 0 ? SH::RG : 1][Fast<SH::N>::QW], const YggDevLayer &y,
+                                          int lane) {
     constexpr int N = SH::N;
     const int qk = lane & 3, qj = lane >> 2;
 #pragma unroll
     for (int p = 0; p < SH::RG; p++) quad_share<N>(vr[p], y.vl + (size_t)(16 * p + qj) * N, qk);
 }
 template <class SH>
-__device__ __forceinline__ void layer_input_regs(int8_t *zls, const uint32_t (&vr)[SH::RG][Fast<SH::N>::QW],
+__device__ __forceinline__ void layer_input_regs(int8_t *zls, const uint32_t (&vr)[SH::RG > 0 ? SH::RG : 1][Fast<SH::N>::QW],
                                                  const float *mv0, const uint32_t (&qbw)[Fast<SH::N>::QW], float rho,
                                                  int lane) {
     using F = Fast<SH::N>;
@@ -614,7 +619,7 @@ __device__ __forceinline__ void layer_input_regs(int8_t *zls, const uint32_t (&v
 
 // this lane's share of expert r's U' (the layout the gather record holds) and its products with zl
 template <class SH>
-__device__ __forceinline__ void load_uw(uint32_t (&uw)[SH::K4][SH::C], const YggDevLayer &y, int r, int lane) {
+__device__ __forceinline__ void load_uw(uint32_t (&uw)[SH::K4A][SH::C], const YggDevLayer &y, int r, int lane) {
     using F = SH;
     const uint8_t *g = y.gath + (uint32_t)r * (uint32_t)y.gath_bytes + y.off_U;
     const int ln = lane < F::NL ? lane : F::NL - 1;
@@ -627,7 +632,7 @@ __device__ __forceinline__ void load_uw(uint32_t (&uw)[SH::K4][SH::C], const Ygg
     }
 }
 template <class SH>
-__device__ __forceinline__ void uw_products(int (&d)[SH::C], const uint32_t (&uw)[SH::K4][SH::C], const int8_t *zls) {
+__device__ __forceinline__ void uw_products(int (&d)[SH::C], const uint32_t (&uw)[SH::K4A][SH::C], const int8_t *zls) {
 #pragma unroll
     for (int c = 0; c < SH::C; c++) d[c] = 0;
 #pragma unroll
@@ -677,7 +682,7 @@ __device__ __forceinline__ void update(int (&qn)[SH::C], const Gather<SH, FACT> 
         }
         acc[c] = wadd((a + (1 << (shift - 1))) >> shift, in);
     }
-    if (routed) {
+    if (F::R2 > 0 && routed) {        // (no layer input at rank 0, cpu/ygg.cpp:360)
         int d[C];
         if constexpr (PRE) {
 #pragma unroll
@@ -777,7 +782,7 @@ __device__ __forceinline__ void store_logits(float *o, const float (&lg)[4], int
 // spilled), else up to 256 (no spills; for calls whose streams all fit at the lower occupancy).
 // GROUP: the model has group scales (the tables of GroupTables and the experts' readout row scales)
 // FACT: the model stores its routed inputs factored (fact_kernel); only with DEEP = false
-template <int N, int R, int R2, int L, int MODE, bool DEEP, bool CAP, bool GROUP, bool FACT>
+template <int N, int R, int R2, int L, int MODE, bool DEEP, bool CAP, bool GROUP, bool FACT, int BLK = 16>
 __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *__restrict__ tokens, int B, int T,
                                           int8_t *__restrict__ state, const YggIO &io) {
     float *__restrict__ logits = io.logits;
@@ -786,7 +791,7 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
     unsigned long long *__restrict__ digest = io.digest;
     const int32_t *__restrict__ targets = io.targets;
     double *__restrict__ nll = io.nll;
-    using SH = Shape<N, R, R2>;
+    using SH = Shape<N, R, R2, BLK>;
     using F = SH;
     constexpr int W = DEEP ? 1 : kFastWaves, LR = L > 1 ? L - 1 : 1;
     constexpr bool GEN = MODE == kModeGenerate, SCORE = MODE == kModeScore;
@@ -972,6 +977,16 @@ __attribute__((amdgpu_waves_per_eu(DEEP ? 1 : (CAP ? 4 : 2))))
 void fast_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B, int T, int8_t *__restrict__ state,
                  const YggIO io) {
     fast_body<N, R, R2, L, MODE, DEEP, CAP, GROUP, false>(m, tokens, B, T, state, io);
+}
+
+// fast_kernel for transition blocks of 8 (fast-only shapes: the router, layer input and readout are the same; a
+// lane's A16 rows hold 8 hi and 8 lo bytes each)
+template <int N, int R, int R2, int L, int MODE, bool CAP, bool GROUP>
+__global__ __launch_bounds__(64 * kFastWaves)
+__attribute__((amdgpu_waves_per_eu(CAP ? 4 : 2)))
+void fast8_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B, int T, int8_t *__restrict__ state,
+                  const YggIO io) {
+    fast_body<N, R, R2, L, MODE, false, CAP, GROUP, false, 8>(m, tokens, B, T, state, io);
 }
 
 // fast_kernel for models whose routed layers store their input factored (cpu/ygg.cpp:339-358, input rank <= 64): a
