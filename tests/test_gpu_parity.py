@@ -104,16 +104,18 @@ def specialised(spec) -> bool:
 
 
 # the per-stream kernel's other shapes (state width, readout rank, layer-input rank, block; csrc/ygg_launch.h
-# YGG_FAST_EXTRA): the kernel-test shapes outside SHAPES or at block 8, table storage, 2 to 5 layers
+# YGG_FAST_EXTRA, YGG_FACT_EXTRA): the kernel-test shapes outside SHAPES or at block 8, 2 to 5 layers
 FAST_ONLY = {(128, 16, 32, 8), (64, 8, 0, 8), (256, 16, 48, 8), (128, 16, 4, 16), (256, 8, 20, 16), (64, 8, 0, 16),
              (64, 32, 20, 16)}
+FACT_ONLY = {(128, 16, 16, 16), (64, 8, 0, 8)}
 
 
 def fast_only(spec) -> bool:
-    """Whether a model runs on the per-stream kernel alone (a shape of FAST_ONLY; fast8_kernel at block 8)."""
-    return (not specialised(spec) and 2 <= spec.n_layers <= 5 and spec.input_rank == 0 and
-            (spec.d_state, spec.readout_rank, spec.layer_input_rank, spec.block_size) in FAST_ONLY and
-            not (spec.group and spec.d_state == 96))
+    """Whether a model runs on the per-stream kernel alone (a shape of FAST_ONLY, or of FACT_ONLY with factored
+    inputs of rank <= 64; the block-8 builds at block 8)."""
+    shape = (spec.d_state, spec.readout_rank, spec.layer_input_rank, spec.block_size)
+    return (not specialised(spec) and 2 <= spec.n_layers <= 5 and not (spec.group and spec.d_state == 96) and
+            (shape in FACT_ONLY and 0 < spec.input_rank <= 64 if spec.input_rank else shape in FAST_ONLY))
 
 
 def _expect_fast_only(model, kernel_env, spec):
@@ -123,8 +125,9 @@ def _expect_fast_only(model, kernel_env, spec):
     assert info.kernel == (0 if kernel_env == "generic" else 1), info.kernel
     assert info.pipe_max_streams == info.deep_max_streams == info.flow_max_streams == info.solo_max_streams == 0
     assert info.grouped == 0
+    family = "fact" if spec.input_rank else "fast"
     want = "ygg::run_kernel<" if kernel_env == "generic" else \
-        ("ygg::fast8_kernel<" if spec.block_size == 8 else "ygg::fast_kernel<")
+        (f"ygg::{family}8_kernel<" if spec.block_size == 8 else f"ygg::{family}_kernel<")
     for B, T in ((8, 64), (8, 1), (4096, 64)):
         assert model.kernel_name(B, T).startswith(want), model.kernel_name(B, T)
     assert model.kernel_name(8, 64, score=True).startswith(want)

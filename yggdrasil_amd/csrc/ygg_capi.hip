@@ -490,14 +490,22 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     const int R2f = L == 1 ? 16 : R2;
     // std_shape: every specialised kernel family has builds; extra: the per-stream kernel only (YGG_FAST_EXTRA)
     const bool std_shape = fa.blk == 16 && shape_ok(n, R, R2f);
-    const bool extra_shape = !std_shape && L > 1 && !factored && extra_ok(n, R, R2, fa.blk);
+    auto fact_extra_ok = [](int nn, int rr, int r2, int b) {
+#define YGG_X(N_, R_, R2_, B_) \
+    if (nn == N_ && rr == R_ && r2 == R2_ && b == B_) return true;
+        YGG_FACT_EXTRA(YGG_X)
+#undef YGG_X
+        return false;
+    };
+    const bool extra_shape = !std_shape && L > 1 &&
+                             (factored ? fact_extra_ok(n, R, R2, fa.blk) : extra_ok(n, R, R2, fa.blk));
     const int64_t rec_bound = (int64_t)n * (2 * fa.blk + R2 + R) + 128 +   // gather record bytes, at most
                               (factored ? (int64_t)fa.K * n + 2 * n + 4 : 0);
     const bool small_tables = (int64_t)E * V * n * 2 < ((int64_t)1 << 32) && (int64_t)E * rec_bound < ((int64_t)1 << 32);
     // (factored routed inputs: fact_kernel, input ranks up to 64; the other specialised kernels take table storage)
     if (kmode != "generic" && (std_shape || extra_shape) && L <= ygg::kMaxFastLayers && VP <= 256 &&
         small_tables && (!factored || fa.K <= YGG_MAX_FACT_RANK) && transitions_split(fa, fl))
-        fast = extra_shape ? ygg::find_fast_extra_launcher(n, R, R2, fa.blk, L, group)
+        fast = extra_shape ? ygg::find_fast_extra_launcher(n, R, R2, fa.blk, L, group, factored)
                : factored  ? ygg::find_fact_launcher(n, R, R2f, L, true, group)
                            : ygg::find_fast_launcher(n, R, R2f, L, true, group);
     if (fast) launch = fast;

@@ -999,6 +999,14 @@ void fact_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
                  const YggIO io) {
     fast_body<N, R, R2, L, MODE, false, CAP, GROUP, true>(m, tokens, B, T, state, io);
 }
+// fact_kernel at transition blocks of 8
+template <int N, int R, int R2, int L, int MODE, bool CAP, bool GROUP>
+__global__ __launch_bounds__(64 * kFastWaves)
+__attribute__((amdgpu_waves_per_eu(CAP ? 4 : 2)))
+void fact8_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B, int T, int8_t *__restrict__ state,
+                  const YggIO io) {
+    fast_body<N, R, R2, L, MODE, false, CAP, GROUP, true, 8>(m, tokens, B, T, state, io);
+}
 
 // ----------------------------------------------------------------------------------------------- pipe_kernel
 

@@ -53,15 +53,18 @@ constexpr int kMaxFastLayers = 5;
 // the per-stream kernel has builds for them (ygg_kernels_fast_x.hip).
 #define YGG_FAST_EXTRA(X) X(128, 16, 32, 8) X(64, 8, 0, 8) X(256, 16, 48, 8) X(128, 16, 4, 16) X(256, 8, 20, 16) \
     X(64, 8, 0, 16) X(64, 32, 20, 16)
+// the same for factored routed inputs (fact_kernel, fact8_kernel)
+#define YGG_FACT_EXTRA(X) X(128, 16, 16, 16) X(64, 8, 0, 8)
 
 Kernel find_launcher(int n, int blk, int R);                            // run_kernel (ygg_kernels.hip)
 // group: the model has group scales (builds for n of 64, 128 and 256 only)
 // fast_kernel, 4 streams per workgroup, 128-VGPR cap or none (ygg_kernels_fast.hip); its resident workgroups per CU
 Kernel find_fast_launcher(int n, int R, int R2, int L, bool cap, bool group);
 int fast_blocks_per_cu(int n, int R, int R2, int L, bool cap, bool group, int mode);
-// the fast-only shapes' per-stream kernel (uncapped; fast8_kernel at block 8) and its resident workgroups per CU
-Kernel find_fast_extra_launcher(int n, int R, int R2, int blk, int L, bool group);
-int fast_extra_blocks_per_cu(int n, int R, int R2, int blk, int L, bool group, int mode);
+// the fast-only shapes' per-stream kernel (uncapped; fast8_kernel at block 8; fact_kernel / fact8_kernel for factored
+// inputs) and its resident workgroups per CU
+Kernel find_fast_extra_launcher(int n, int R, int R2, int blk, int L, bool group, bool factored);
+int fast_extra_blocks_per_cu(int n, int R, int R2, int blk, int L, bool group, bool factored, int mode);
 // fact_kernel: fast_kernel for factored routed inputs (ygg_kernels_fact.hip), 2 to 5 layers
 Kernel find_fact_launcher(int n, int R, int R2, int L, bool cap, bool group);
 int fact_blocks_per_cu(int n, int R, int R2, int L, bool cap, bool group, int mode);
