@@ -1188,16 +1188,22 @@ void pipe_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
 // Tokens come through the scalar cache (their wait counter is not the vector loads').
 constexpr int kFlowStates = 8;     // state ring slots per layer (> the rounds)
 template <int L, int P> constexpr int kFlowLogits = (L - 1) * (P + 2) + 1;   // tokens in flight between layers
-template <int L> constexpr int kFlowWaves = 2 * L - 1;
 constexpr int kFlowToken0 = 2;     // tick of the token layer's update of token 0 (its records issued two ticks ahead)
 
 // BIG: the largest shape, whose 32 KiB record does not fit twice in the update wave's registers: its descent wave
 // keeps V' in registers (not LDS) and computes the U'z products itself, handing them over in dring, so the update
 // wave's records hold A16, P and the table row only
 template <class SH> constexpr bool kFlowBig = SH::N * SH::R2 >= 256 * 64;
+// SPLIT (all but BIG; at 5 layers the run builds): two descent wavefronts per routed layer, one for the tokens of each
+// parity. A token's rounds run a tick apart, so in every tick each of the two takes every other round (the rounds of
+// its tokens) and hands each round's loads to its own next round: half the descent work a wave and tick, no data
+// crosses between them. (5-layer score builds: 13 wavefronts would put 4 on a SIMD, a cap of 128 VGPRs, and spill.)
+template <class SH, int L, int MODE> constexpr bool kFlowSplit = !kFlowBig<SH> && (L <= 4 || MODE == kModeRun);
+// wavefronts: the token layer's, then per routed layer the descent wave (SPLIT: two) and the update wave
+template <class SH, int L, int MODE> constexpr int kFlowWaves = kFlowSplit<SH, L, MODE> ? 3 * L - 2 : 2 * L - 1;
 // VREG: V' in the descent wave's registers (BIG, up to 4 layers: 7 wavefronts leave 256 VGPRs a wave; at 5 layers,
 // 9 wavefronts leave 168, and V' stays in LDS)
-template <class SH, int L> constexpr bool kFlowVreg = kFlowBig<SH> && kFlowWaves<L> <= 8;
+template <class SH, int L> constexpr bool kFlowVreg = kFlowBig<SH> && 2 * L - 1 <= 8;
 // ZQR (BIG at 5 layers, where LDS is short): each layer leaves its zq row of token t in a ring and the last layer's
 // update wave adds every layer's unembedding term, in layer order, instead of the layers adding theirs to a ring of
 // logit rows
@@ -1205,7 +1211,8 @@ template <class SH, int L> constexpr bool kFlowVreg = kFlowBig<SH> && kFlowWaves
 // loop holds the double-precision exp and log constants, which in an update wave's loop spill beside the record.
 template <class SH, int L, int MODE>
 constexpr bool kFlowNllWave = MODE == kModeScore && kFlowBig<SH> && !kFlowVreg<SH, L>;
-template <class SH, int L, int MODE> constexpr int kFlowThreads = 64 * (kFlowWaves<L> + (kFlowNllWave<SH, L, MODE> ? 1 : 0));
+template <class SH, int L, int MODE>
+constexpr int kFlowThreads = 64 * (kFlowWaves<SH, L, MODE> + (kFlowNllWave<SH, L, MODE> ? 1 : 0));
 
 // SC (score builds): with V' in LDS the finished logits of token t wait in lgs[t & 1] for the NLL wave
 template <class SH, int L, int P, bool GROUP, bool SC> struct FlowShared {
@@ -1388,6 +1395,26 @@ __device__ __forceinline__ void flow_nll(FlowShared<SH, L, P, GROUP, true> &sh, 
     else if (lane == 0) atomicOr(m.err, 2u);
 }
 
+// Wave w's role, 3 l + k: layer l's update wave (k = 0; the token layer's for l = 0) or a descent wave (k = 1; SPLIT:
+// k = 1 and 2, of token parity 0 and 1). Wave w of a workgroup runs on SIMD w % 4, and the tables spread the work over
+// the four: a layer's two descent waves, whose heavier set of rounds alternates tick by tick, share a SIMD where they
+// can, and no two descent waves of the unsplit form do.
+template <int L, bool SPLIT> __device__ __forceinline__ int flow_role(int w) {
+    if constexpr (SPLIT) {
+        constexpr int r2[4] = {0, 3, 4, 5};
+        constexpr int r3[7] = {0, 4, 7, 6, 3, 5, 8};
+        constexpr int r4[10] = {0, 3, 6, 9, 4, 7, 10, 11, 5, 8};
+        constexpr int r5[13] = {0, 6, 9, 12, 3, 7, 10, 13, 4, 8, 11, 14, 5};
+        return L == 2 ? r2[w] : L == 3 ? r3[w] : L == 4 ? r4[w] : r5[w];
+    } else {
+        constexpr int r4[7] = {0, 4, 3, 7, 10, 6, 9};
+        constexpr int r5[9] = {0, 4, 7, 10, 3, 6, 9, 13, 12};
+        if constexpr (L == 4) return r4[w];
+        if constexpr (L == 5) return r5[w];
+        return w == 0 ? 0 : 3 * ((w + 1) >> 1) + (w & 1);
+    }
+}
+
 // MODE: kModeRun (logits, leaves, states) or kModeScore (also the digest and the NLL)
 template <int N, int R, int R2, int L, int P, int MODE, bool GROUP>
 __global__ __launch_bounds__((kFlowThreads<Shape<N, R, R2>, L, MODE>)) __attribute__((amdgpu_waves_per_eu(1)))
@@ -1401,12 +1428,22 @@ void flow_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
     constexpr int QM = FS::QR - 1, NT = kFlowThreads<SH, L, MODE>;
     __shared__ __attribute__((aligned(16))) FS sh;
 
-    // wave 0: the token layer; waves 2 l - 1 and 2 l: routed layer l's descent and update waves; NLLW: wave 2 L - 1
-    // the NLL (set up as no layer's: descent set, layer 0)
+    // wave 0: the token layer; the routed layers' descent waves (SPLIT: two, for the tokens of parity dpar 0 and 1)
+    // and update waves placed by flow_role; NLLW: wave 2 L - 1 the NLL (set up as no layer's: descent set, layer 0)
+    constexpr bool SPLIT = kFlowSplit<SH, L, MODE>;
     const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const bool nllw = NLLW && w == 2 * L - 1;
-    const int l = nllw ? 0 : (w + 1) >> 1;
-    const bool descent = (w & 1) != 0;
+    int l, dpar = 0;
+    bool descent;
+    if (nllw) {
+        l = 0;
+        descent = true;
+    } else {
+        const int c = flow_role<L, SPLIT>(w);
+        l = c / 3;
+        descent = c % 3 != 0;
+        dpar = c % 3 == 2;
+    }
     const int qk = lane & 3, qj = lane >> 2;
     const int s = blockIdx.x;
     const int V = m.V, VP = m.VP;
@@ -1544,7 +1581,9 @@ void flow_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
 #pragma unroll
             for (int i = 0; i < F::QW; i++) wv[j][i] = 0u;
         }
-        for (int k = 0; k < ticks; k++) {
+        // one tick: A < 0 every round, else (SPLIT) the rounds j with j % 2 == A (the rest are the other wave's)
+        auto dtick = [&](int k, auto A_) {
+            constexpr int A = decltype(A_)::value;
             const int stop = __builtin_amdgcn_readfirstlane(sh.stop_t);
             const int t0 = k - o_prev;                            // the token whose first-round thresholds load now
             const int xr = token_at(t0);
@@ -1553,6 +1592,7 @@ void flow_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
             float lrho = 0.0f;
 #pragma unroll
             for (int j = P - 1; j >= 0; j--) {
+                if (A >= 0 && (j & 1) != A) continue;          // (SPLIT: the other wave's round this tick)
                 const int t = k - o_prev - 1 - j;
                 uint32_t qbw[F::QW];
                 int ix, x;
@@ -1589,8 +1629,8 @@ void flow_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
                     lrho = rho;
                 }
             }
-            // ---- the leaf reached and its layer input, for the update wave
-            if (lt >= 0 && lt < T && lt < stop) {
+            // ---- the leaf reached and its layer input, for the update wave (SPLIT: by the wave that ran the last round)
+            if ((A < 0 || ((P - 1) & 1) == A) && lt >= 0 && lt < T && lt < stop) {
                 if (lane == 0) {
                     sh.leafx[l][lt & 1][0] = lr;
                     sh.leafx[l][lt & 1][1] = lx;
@@ -1614,11 +1654,31 @@ void flow_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
                 }
                 load_uw<SH>(uwp, y, lr, lane);
             }
-            // ---- the first round's thresholds of token t0, for next tick
-            const int x0 = (xr < 0 || xr >= V) ? 0 : xr;
-            th[0] = y.thr[(size_t)x0 * y.thr_stride + (qj < nn0 ? qj : nn0 - 1)];
-            xs[0] = x0;
+            // ---- the first round's thresholds of token t0, for next tick (SPLIT: by the wave whose round 0 it is)
+            if (A < 0 || A == 1) {
+                const int x0 = (xr < 0 || xr >= V) ? 0 : xr;
+                th[0] = y.thr[(size_t)x0 * y.thr_stride + (qj < nn0 ? qj : nn0 - 1)];
+                xs[0] = x0;
+            }
             flow_barrier();
+        };
+        if constexpr (SPLIT) {
+            // round j of token t runs in tick o_prev + 1 + t + j, so this wave's rounds in tick k are those with
+            // j = k + o_prev + 1 + dpar (mod 2): in even ticks those of parity a0
+            const int a0 = (o_prev + 1 + dpar) & 1;
+            if (a0 == 0) {
+                for (int k = 0; k < ticks; k += 2) {
+                    dtick(k, std::integral_constant<int, 0>());
+                    dtick(k + 1, std::integral_constant<int, 1>());
+                }
+            } else {
+                for (int k = 0; k < ticks; k += 2) {
+                    dtick(k, std::integral_constant<int, 1>());
+                    dtick(k + 1, std::integral_constant<int, 0>());
+                }
+            }
+        } else {
+            for (int k = 0; k < ticks; k++) dtick(k, std::integral_constant<int, -1>());
         }
     }
     __syncthreads();
