@@ -1198,9 +1198,14 @@ template <class SH> constexpr bool kFlowBig = SH::N * SH::R2 >= 256 * 64;
 // parity. A token's rounds run a tick apart, so in every tick each of the two takes every other round (the rounds of
 // its tokens) and hands each round's loads to its own next round: half the descent work a wave and tick, no data
 // crosses between them. (5-layer score builds: 13 wavefronts would put 4 on a SIMD, a cap of 128 VGPRs, and spill.)
-template <class SH, int L, int MODE> constexpr bool kFlowSplit = !kFlowBig<SH> && (L <= 4 || MODE == kModeRun);
-// wavefronts: the token layer's, then per routed layer the descent wave (SPLIT: two) and the update wave
-template <class SH, int L, int MODE> constexpr int kFlowWaves = kFlowSplit<SH, L, MODE> ? 3 * L - 2 : 2 * L - 1;
+// SPLIT builds also finish the logits on a wavefront of their own (LOGW): each layer's update wave leaves its readout
+// row zq of token t in a ring, and a tick after the last layer's update the logits wave adds the bias and every
+// layer's unembedding term, in layer order, stores the row and, scoring, adds the NLL and the digest.
+template <class SH, int L, bool SC> constexpr bool kFlowSplitSC = !kFlowBig<SH> && (L <= 4 || !SC);
+template <class SH, int L, int MODE> constexpr bool kFlowSplit = kFlowSplitSC<SH, L, MODE == kModeScore>;
+// wavefronts: the token layer's, then per routed layer the descent wave (SPLIT: two) and the update wave (SPLIT: and
+// the logits wave last)
+template <class SH, int L, int MODE> constexpr int kFlowWaves = kFlowSplit<SH, L, MODE> ? 3 * L - 1 : 2 * L - 1;
 // VREG: V' in the descent wave's registers (BIG, up to 4 layers: 7 wavefronts leave 256 VGPRs a wave; at 5 layers,
 // 9 wavefronts leave 168, and V' stays in LDS)
 template <class SH, int L> constexpr bool kFlowVreg = kFlowBig<SH> && 2 * L - 1 <= 8;
@@ -1217,16 +1222,18 @@ constexpr int kFlowThreads = 64 * (kFlowWaves<SH, L, MODE> + (kFlowNllWave<SH, L
 // SC (score builds): with V' in LDS the finished logits of token t wait in lgs[t & 1] for the NLL wave
 template <class SH, int L, int P, bool GROUP, bool SC> struct FlowShared {
     static constexpr bool BIG = kFlowBig<SH>, VREG = kFlowVreg<SH, L>, ZQR = BIG && !VREG;
+    static constexpr bool LOGW = kFlowSplitSC<SH, L, SC>, ZQRING = ZQR || LOGW;
     static constexpr int QR = (BIG && P < 4) ? 4 : kFlowStates;           // state ring slots (> P)
-    static constexpr int LG = kFlowLogits<L, P>;
-    static constexpr int LGS = ZQR ? (SC ? 2 : 1) : LG;                   // logits slots
+    // tokens in flight between the token layer's update and the last reader of their ring slots (LOGW: one tick more)
+    static constexpr int LG = kFlowLogits<L, P> + (LOGW ? 1 : 0);
+    static constexpr int LGS = ZQR ? (SC ? 2 : 1) : LOGW ? 1 : LG;        // logits slots
     alignas(16) SharedTables<SH, L, !VREG> S;
     alignas(16) GroupTablesOf<SH, L, GROUP> GT;
     alignas(16) int8_t qring[L][QR][SH::N];
     alignas(16) int dring[BIG ? L : 1][2][BIG ? SH::N : 4];               // U'z of token t: [l][t & 1]
     alignas(16) float lgs[LGS][256];
-    alignas(16) int8_t zqr[ZQR ? L : 1][ZQR ? LG : 1][SH::ZQ];             // ZQR: zq of layer l, token t
-    alignas(16) unsigned long long dterm[kFlowLogits<L, P>][L];
+    alignas(16) int8_t zqr[ZQRING ? L : 1][ZQRING ? LG : 1][SH::ZQ];       // ZQR, LOGW: zq of layer l, token t
+    alignas(16) unsigned long long dterm[LG][L];
     alignas(16) int8_t zlw[L][4][SH::ZL];                 // layer input of token t: [l][t & 3]
     alignas(16) int8_t zqw[L][SH::ZQ];
     int leafx[L][2][2];                                   // leaf and token of token t: [l][t & 1]
@@ -1271,7 +1278,7 @@ template <class SH, int L, int P, bool SCORE, bool GROUP>
 __device__ __forceinline__ void flow_outputs(FlowShared<SH, L, P, GROUP, SCORE> &sh, const YggDevModel &m,
                                              const int (&qn)[SH::C], const int8_t *qnew, int l, int t, int r, int s,
                                              int T, const YggIO &io, int lane) {
-    constexpr int N = SH::N, LG = kFlowLogits<L, P>;
+    constexpr int N = SH::N, LG = FlowShared<SH, L, P, GROUP, SCORE>::LG;
     if (io.leaves && lane == 0) io.leaves[((size_t)s * T + t) * L + l] = r;
     if (io.states) {
         int8_t *so = io.states + (((size_t)s * T + t) * L + l) * N;
@@ -1290,7 +1297,7 @@ __device__ __forceinline__ void flow_finish(FlowShared<SH, L, P, GROUP, SCORE> &
                                             const float (&lg)[4], int t, int s, int T, const YggIO &io,
                                             unsigned long long &dg, double &nacc, int lane) {
     using FS = FlowShared<SH, L, P, GROUP, SCORE>;
-    constexpr int LG = kFlowLogits<L, P>;
+    constexpr int LG = FS::LG;
     const int V = m.V;
     if (SCORE && FS::ZQR && io.nll) *(float4 *)(sh.lgs[t & 1] + 4 * lane) = make_float4(lg[0], lg[1], lg[2], lg[3]);
     wave_sync();
@@ -1316,7 +1323,7 @@ __device__ __forceinline__ void flow_update(FlowShared<SH, L, P, GROUP, SCORE> &
                                             unsigned long long &dg, double &nacc, int lane) {
     using F = SH;
     using FS = FlowShared<SH, L, P, GROUP, SCORE>;
-    constexpr int QM = FS::QR - 1, LG = kFlowLogits<L, P>;
+    constexpr int QM = FS::QR - 1, LG = FS::LG;
     const int VP = m.VP;
     t = ok ? t : 0;
     int8_t *qnew = sh.qring[l][(t + 1) & QM];
@@ -1334,8 +1341,13 @@ __device__ __forceinline__ void flow_update(FlowShared<SH, L, P, GROUP, SCORE> &
     }
     wave_sync();
     // (a token outside the stream reads out into the wave's own row, not the ring slot of a token in flight)
-    int8_t *zq = (FS::ZQR && ok) ? sh.zqr[FS::ZQR ? l : 0][FS::ZQR ? t % LG : 0] : sh.zqw[l];
+    int8_t *zq = (FS::ZQRING && ok) ? sh.zqr[FS::ZQRING ? l : 0][FS::ZQRING ? t % LG : 0] : sh.zqw[l];
     readout<SH>(zq, G.pw, qnew, GROUP ? G.mzr : y.readout_scale, lane);
+    if constexpr (FS::LOGW) {
+        // the logits wave adds the unembedding term after the barrier
+        if (ok) flow_outputs<SH, L, P, SCORE, GROUP>(sh, m, qn, qnew, l, t, r, s, T, io, lane);
+        return;
+    }
     wave_sync();
     if (!ok) return;
     if constexpr (FS::ZQR) {
@@ -1395,6 +1407,31 @@ __device__ __forceinline__ void flow_nll(FlowShared<SH, L, P, GROUP, true> &sh, 
     else if (lane == 0) atomicOr(m.err, 2u);
 }
 
+// the logits of token t, a tick after the last layer's update (the logits wave): the bias, then every layer's
+// unembedding term of the zq rows the layers left, in layer order (the reference's order of additions)
+template <class SH, int L, int P, bool SCORE, bool GROUP>
+__device__ __forceinline__ void flow_logits(FlowShared<SH, L, P, GROUP, SCORE> &sh, const YggDevModel &m,
+                                            const float (&bias)[4], int t, int s, int T, const YggIO &io,
+                                            unsigned long long &dg, double &nacc, int lane) {
+    using FS = FlowShared<SH, L, P, GROUP, SCORE>;
+    float lg[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) lg[u] = bias[u];
+#pragma unroll
+    for (int j = 0; j < L; j++) {
+        float term[4];
+        const float *sq = nullptr;
+        if constexpr (GROUP) sq = sh.GT.sq[j];
+        unembed_terms<SH::R, GROUP>(term, sh.zqr[FS::ZQRING ? j : 0][FS::ZQRING ? t % FS::LG : 0], sh.S.Q[j],
+                                    m.layers[j].unembed_scale, lane, sq);
+#pragma unroll
+        for (int u = 0; u < 4; u++) lg[u] = lg[u] + term[u];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; u++) lg[u] = 4 * lane + u < m.VP ? lg[u] : 0.0f;
+    flow_finish<SH, L, P, SCORE, GROUP>(sh, m, lg, t, s, T, io, dg, nacc, lane);
+}
+
 // Wave w's role, 3 l + k: layer l's update wave (k = 0; the token layer's for l = 0) or a descent wave (k = 1; SPLIT:
 // k = 1 and 2, of token parity 0 and 1). Wave w of a workgroup runs on SIMD w % 4, and the tables spread the work over
 // the four: a layer's two descent waves, whose heavier set of rounds alternates tick by tick, share a SIMD where they
@@ -1429,13 +1466,16 @@ void flow_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
     __shared__ __attribute__((aligned(16))) FS sh;
 
     // wave 0: the token layer; the routed layers' descent waves (SPLIT: two, for the tokens of parity dpar 0 and 1)
-    // and update waves placed by flow_role; NLLW: wave 2 L - 1 the NLL (set up as no layer's: descent set, layer 0)
-    constexpr bool SPLIT = kFlowSplit<SH, L, MODE>;
+    // and update waves placed by flow_role; NLLW: wave 2 L - 1 the NLL; LOGW (the SPLIT builds): wave 3 L - 2 the
+    // logits (both set up as no layer's: descent set, layer 0)
+    constexpr bool SPLIT = kFlowSplit<SH, L, MODE>, LOGW = FS::LOGW;
+    static_assert(LOGW == SPLIT, "the split builds finish the logits on the logits wave");
     const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const bool nllw = NLLW && w == 2 * L - 1;
+    const bool logw = LOGW && w == 3 * L - 2;
     int l, dpar = 0;
     bool descent;
-    if (nllw) {
+    if (nllw || logw) {
         l = 0;
         descent = true;
     } else {
@@ -1465,14 +1505,16 @@ void flow_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
     for (int u = 0; u < 4; u++) bias[u] = 4 * lane + u < VP ? m.output_bias[4 * lane + u] : 0.0f;
     __syncthreads();
 
-    // (even: some waves run 2 a loop; NLLW: one tick more, for the NLL of the last token)
-    const int ticks = (kFlowToken0 + (L - 1) * (P + 2) + T + 1 + (NLLW ? 1 : 0)) & ~1;
+    // (even: some waves run 2 a loop; NLLW, LOGW: one tick more, for the NLL or the logits of the last token)
+    const int ticks = (kFlowToken0 + (L - 1) * (P + 2) + T + 1 + ((NLLW || LOGW) ? 1 : 0)) & ~1;
     const int o_prev = kFlowToken0 + (l - 1) * (P + 2);                   // the layer below's update of token 0
     const int32_t *tok = tokens + (size_t)s * T;
     // the token at an index clamped into the stream (stages on tokens outside the stream or the vocabulary still run,
     // on token 0, and store nothing)
     auto token_at = [&](int t) { return scalar_load(tok + (t < 0 ? 0 : (t < T ? t : T - 1))); };
-    unsigned long long dg = (SCORE && io.digest && l == L - 1 && !descent) ? io.digest[s] : 0ull;
+    // the wave that finishes the tokens: the logits wave, else the last layer's update wave
+    const bool fin = LOGW ? logw : (l == L - 1 && !descent);
+    unsigned long long dg = (SCORE && io.digest && fin) ? io.digest[s] : 0ull;
     double nacc = 0.0;
     // everything loaded so far has arrived: no value from before the ticks is waited for inside them
     __builtin_amdgcn_s_waitcnt(0);
@@ -1485,6 +1527,17 @@ void flow_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
                 const int stop = __builtin_amdgcn_readfirstlane(sh.stop_t);
                 const int tn = k - 1 - kFlowToken0 - (L - 1) * (P + 2);
                 if (io.nll && tn >= 0 && tn < T && tn < stop) flow_nll<SH, L, P, GROUP>(sh, m, tn, s, T, io, nacc, lane);
+                flow_barrier();
+            }
+        }
+    } else if (T > 0 && logw) {
+        // ---- the logits wave: at tick k the logits of the token the last layer updated at tick k - 1 (tokens from
+        // the stop on were not updated: the stop only moves to a token the last layer has not reached)
+        if constexpr (LOGW) {
+            for (int k = 0; k < ticks; k++) {
+                const int stop = __builtin_amdgcn_readfirstlane(sh.stop_t);
+                const int tn = k - 1 - kFlowToken0 - (L - 1) * (P + 2);
+                if (tn >= 0 && tn < T && tn < stop) flow_logits<SH, L, P, SCORE, GROUP>(sh, m, bias, tn, s, T, io, dg, nacc, lane);
                 flow_barrier();
             }
         }
@@ -1627,20 +1680,21 @@ void flow_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
                     lx = x;
                     lr = ix - m.E;
                     lrho = rho;
+                    // ---- the leaf reached and its layer input, for the update wave: before the earlier rounds, whose
+                    // inputs were loaded later last tick and are still arriving
+                    if (lt >= 0 && lt < T && lt < stop) {
+                        if (lane == 0) {
+                            sh.leafx[l][lt & 1][0] = lr;
+                            sh.leafx[l][lt & 1][1] = lx;
+                        }
+                        uint32_t qb[F::QW];
+                        quad_share<N>(qb, sh.qring[l - 1][(lt + 1) & QM], qk);
+                        if constexpr (VREG)
+                            layer_input_regs<SH>(sh.zlw[l][lt & 3], vr, sh.S.mv[l - 1], qb, lrho, lane);
+                        else
+                            layer_input<SH>(sh.zlw[l][lt & 3], sh.S.V[l - 1], sh.S.mv[l - 1], qb, lrho, lane);
+                    }
                 }
-            }
-            // ---- the leaf reached and its layer input, for the update wave (SPLIT: by the wave that ran the last round)
-            if ((A < 0 || ((P - 1) & 1) == A) && lt >= 0 && lt < T && lt < stop) {
-                if (lane == 0) {
-                    sh.leafx[l][lt & 1][0] = lr;
-                    sh.leafx[l][lt & 1][1] = lx;
-                }
-                uint32_t qbw[F::QW];
-                quad_share<N>(qbw, sh.qring[l - 1][(lt + 1) & QM], qk);
-                if constexpr (VREG)
-                    layer_input_regs<SH>(sh.zlw[l][lt & 3], vr, sh.S.mv[l - 1], qbw, lrho, lane);
-                else
-                    layer_input<SH>(sh.zlw[l][lt & 3], sh.S.V[l - 1], sh.S.mv[l - 1], qbw, lrho, lane);
             }
             if constexpr (BIG) {
                 // ---- the U'z products of the leaf before (its U' arrived during this tick), for the update wave's
@@ -1685,10 +1739,9 @@ void flow_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
     if (!descent) {
         const int te = T < sh.stop_t ? T : sh.stop_t;                // tokens processed
         for (int i = lane; i < N; i += 64) st[i] = sh.qring[l][te & QM][i];
-        if (SCORE && io.digest && l == L - 1 && lane == 0) io.digest[s] = dg;
-        if (SCORE && !NLLW && io.nll && l == L - 1 && lane == 0) io.nll[s] += nacc;
     }
-    if (nllw && io.nll && lane == 0) io.nll[s] += nacc;
+    if (SCORE && io.digest && fin && lane == 0) io.digest[s] = dg;
+    if (SCORE && io.nll && (NLLW ? nllw : fin) && lane == 0) io.nll[s] += nacc;
 }
 
 }  // namespace ygg
