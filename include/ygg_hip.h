@@ -61,11 +61,12 @@ typedef struct {
     int32_t deep_max_streams;  /* ygg_generate calls of at least 8 tokens with B at most this (the CUs) use the
                                   one-stream-per-workgroup kernel with the deep descent; 0: never. YGG_KERNEL=deep
                                   uses it for every call */
-    int32_t flow_max_streams;  /* ygg_run/ygg_score calls of at least 32 tokens with B at most this use the
-                                  tick-pipelined kernel (one workgroup per stream, a wavefront per layer, router
-                                  rounds and updates overlapped across tokens): its resident workgroups per CU times
-                                  the CUs; 0: never (plans other than 3 or 4 rounds, the largest shape, YGG_FLOW=0 or
-                                  another YGG_KERNEL at load time). YGG_KERNEL=flow uses it for every call but
+    int32_t flow_max_streams;  /* ygg_run calls of at least 32 tokens with B at most this use the tick-pipelined
+                                  kernel (one workgroup per stream, router rounds and updates of consecutive tokens
+                                  overlapped): 8 streams per CU, or for the largest shape twice its resident
+                                  workgroups, or its resident workgroups if more (score calls: the same rule for
+                                  the score build); 0: never (plans other than 3 or 4 rounds, YGG_FLOW=0 or another
+                                  YGG_KERNEL at load time). YGG_KERNEL=flow uses it for every call but
                                   ygg_generate */
     int32_t router_rounds;     /* rounds of the router plan (levels read per dependent step of the descent) */
     int32_t solo_max_streams;  /* calls with B at most this use the kernel with all four wavefronts of a workgroup on

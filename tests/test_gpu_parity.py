@@ -504,17 +504,20 @@ def test_default_dispatch(hip, model_dir, monkeypatch):
     # mode 0: run, 1: generate, 2: score or a run with a digest; D = 10: a plan of 3 rounds
     fast = "ygg::fast_kernel<128, 8, 16, 4, {}, false, {}, false>"
     flow = "ygg::flow_kernel<128, 8, 16, 4, 3, {}, false>"
-    assert info.router_rounds == 3 and 0 < info.flow_max_streams < info.pipe_max_streams
+    # the tick-pipelined kernel up to 8 streams per CU (the CUs: deep_max_streams) for calls of >= 32 tokens, and
+    # above that the per-stream kernel, not the layer-pipelined one
+    assert info.router_rounds == 3 and info.flow_max_streams >= 8 * info.deep_max_streams > 0
     assert model.kernel_name(1, 64) == flow.format(0)
     assert model.kernel_name(1, 64, score=True) == flow.format(2)
     assert model.kernel_name(info.flow_max_streams, 32) == flow.format(0)
+    assert model.kernel_name(info.flow_max_streams, 32, score=True) == flow.format(2)
     assert model.kernel_name(1, 31) == "ygg::pipe_kernel<128, 8, 16, 4, 0, false, false>"
-    assert model.kernel_name(info.flow_max_streams + 1, 64) == "ygg::pipe_kernel<128, 8, 16, 4, 0, true, false>" or \
-        model.kernel_name(info.flow_max_streams + 1, 64) == "ygg::pipe_kernel<128, 8, 16, 4, 0, false, false>"
+    assert model.kernel_name(info.flow_max_streams + 1, 64) in (fast.format(0, "false"), fast.format(0, "true"))
     assert info.solo_max_streams == 0 and info.deep_max_streams > 0     # the solo kernel only when forced
     assert model.kernel_name(1, 1) == fast.format(0, "false")
     assert model.kernel_name(1, 1, score=True) == fast.format(2, "false")
-    assert model.kernel_name(info.pipe_max_streams + 1, 64) == fast.format(0, "false")
+    assert model.kernel_name(max(info.pipe_max_streams, info.flow_max_streams) + 1, 64) == fast.format(0, "false")
+    assert model.kernel_name(info.pipe_max_streams + 1, 16) == fast.format(0, "false")
     assert model.kernel_name(16384, 64) == fast.format(0, "true")
     assert model.kernel_name(16384, 64, score=True) == fast.format(2, "true")
     assert model.kernel_name(1, 100, generate=True) == "ygg::fast_kernel<128, 8, 16, 4, 1, true, false, false>"

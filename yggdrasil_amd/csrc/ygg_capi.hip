@@ -701,13 +701,19 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     m->deep = deepk;
     m->deep_all = deepk && kmode == "deep";
     m->deep_max_streams = deepk ? (m->deep_all ? INT32_MAX : cus) : 0;
-    // flow_kernel for T > 1 while every stream's workgroup is resident (or always with YGG_KERNEL=flow)
+    // flow_kernel for T >= kFlowMinTokens up to flow_max_streams (or always with YGG_KERNEL=flow): measured at 512
+    // tokens against the per-stream kernel, the builds with the split descent win up to 8 streams per CU on every
+    // benchmark and reference model whether the workgroups are all resident or not (configuration 4's model at 1024
+    // streams: 2.30 against 4.54 ms; at 16 per CU the two tie or the per-stream kernel wins), the unsplit build of the
+    // largest shape up to two rounds of resident workgroups (per mode: the 5-layer score builds are unsplit, and the
+    // largest shape's has one wavefront more; generation never runs on it)
     m->flow = flowk;
     m->flow_all = flowk && kmode == "flow";
-    // (per mode: the score build of the largest shape has one wavefront more; generation never runs on it)
-    for (int md : {kModeRun, kModeScore})
-        m->flow_max_streams[md] =
-            flowk ? (m->flow_all ? INT32_MAX : ygg::flow_blocks_per_cu(n, R, R2f, L, rplan.n, group, md) * cus) : 0;
+    for (int md : {kModeRun, kModeScore}) {
+        const int resident = flowk ? ygg::flow_blocks_per_cu(n, R, R2f, L, rplan.n, group, md) * cus : 0;
+        const int reach = ygg::flow_split_build(n, R, R2f, L, md) ? 8 * cus : 2 * resident;
+        m->flow_max_streams[md] = flowk ? (m->flow_all ? INT32_MAX : std::max(resident, reach)) : 0;
+    }
     // the solo kernel only when forced (YGG_KERNEL=solo): measured slower than the per-stream kernel for one-token
     // steps and than the deep kernel for generation on the benchmark shapes (round A's arithmetic and barrier on one
     // wavefront per SIMD cost about what the memory round trips they remove cost)
@@ -800,9 +806,10 @@ constexpr int kFlowMinTokens = 32;
 // digest or NLL). YGG_KERNEL=solo: the solo kernel (all wavefronts of a workgroup on one stream) for every call but
 // score calls. Generation: the deep kernel for >= 8 tokens and B <= deep_max_streams, else the per-stream kernel
 // (every token needs all layers of the one before it, so never a layer-pipelined one). Otherwise: the tick-pipelined
-// kernel for T >= kFlowMinTokens when its workgroups fit, the layer-pipelined kernel for T > 1 when its workgroups
-// fit, else the per-stream kernel. Of the two builds of a kernel, the uncapped one while all B streams are resident
-// with it. A kernel forced by YGG_KERNEL takes every call it can run.
+// kernel for T >= kFlowMinTokens and B <= flow_max_streams, the layer-pipelined kernel for T > 1 when its
+// workgroups fit (for T >= kFlowMinTokens only where there is no tick-pipelined build: more streams than that one
+// takes run best on the per-stream kernel), else the per-stream kernel. Of the two builds of a kernel, the uncapped
+// one while all B streams are resident with it. A kernel forced by YGG_KERNEL takes every call it can run.
 const ygg::Kernel &pick(const ygg_model *m, int B, int T, int mode) {
     const bool gen = mode == kModeGenerate;
     if (m->solo && mode != kModeScore && (m->solo_all || (B <= m->solo_max_streams && (gen || T == 1))))
@@ -810,7 +817,7 @@ const ygg::Kernel &pick(const ygg_model *m, int B, int T, int mode) {
     if (m->deep_all) return m->deep;
     if (gen && m->deep && B <= m->deep_max_streams && T >= 8) return m->deep;
     if (!gen && m->flow && (m->flow_all || (T >= kFlowMinTokens && B <= m->flow_max_streams[mode]))) return m->flow;
-    if (!gen && m->pipe && (m->pipe_all || (T > 1 && B <= m->pipe_max_streams)))
+    if (!gen && m->pipe && (m->pipe_all || (T > 1 && B <= m->pipe_max_streams && !(m->flow && T >= kFlowMinTokens))))
         return (m->pipe_few && B <= m->pipe_few_max_streams[mode]) ? m->pipe_few : m->pipe;
     return (m->run_few && B <= m->run_few_max_streams[mode]) ? m->run_few : m->run;
 }

@@ -90,6 +90,15 @@ Kernel find_flow_launcher(int n, int R, int R2, int L, int P, bool group) {
     return Kernel();
 }
 
+// whether the build of this shape, layer count and mode splits the descent (kFlowSplit)
+bool flow_split_build(int n, int R, int R2, int L, int mode) {
+#define YGG_W(N_, R_, R2_) \
+    if (n == N_ && R == R_ && R2 == R2_) return !kFlowBig<Shape<N_, R_, R2_>> && (L <= 4 || mode != kModeScore);
+    YGG_SHAPES(YGG_W)
+#undef YGG_W
+    return false;
+}
+
 int flow_blocks_per_cu(int n, int R, int R2, int L, int P, bool group, int mode) {
 #define YGG_W(N_, R_, R2_) \
     if (n == N_ && R == R_ && R2 == R2_) \

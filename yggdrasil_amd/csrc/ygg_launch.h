@@ -77,6 +77,7 @@ int pipe_blocks_per_cu(int n, int R, int R2, int L, bool cap, bool group, int mo
 // (ygg_kernels_flow.hip); the resident workgroups per CU of its build for a mode (kModeRun or kModeScore)
 Kernel find_flow_launcher(int n, int R, int R2, int L, int P, bool group);
 int flow_blocks_per_cu(int n, int R, int R2, int L, int P, bool group, int mode);
+bool flow_split_build(int n, int R, int R2, int L, int mode);
 // solo_kernel, one stream per workgroup with all four wavefronts on it (ygg_kernels_solo.hip): router plans of at
 // most 4 rounds whose first two take at most 8 levels and the others at most 6
 Kernel find_solo_launcher(int n, int R, int R2, int L, bool group);
