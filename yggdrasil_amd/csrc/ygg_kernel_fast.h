@@ -1433,15 +1433,16 @@ __device__ __forceinline__ void flow_logits(FlowShared<SH, L, P, GROUP, SCORE> &
 }
 
 // Wave w's role, 3 l + k: layer l's update wave (k = 0; the token layer's for l = 0) or a descent wave (k = 1; SPLIT:
-// k = 1 and 2, of token parity 0 and 1). Wave w of a workgroup runs on SIMD w % 4, and the tables spread the work over
-// the four: a layer's two descent waves, whose heavier set of rounds alternates tick by tick, share a SIMD where they
-// can, and no two descent waves of the unsplit form do.
+// k = 1 and 2, of token parity 0 and 1); SPLIT: 2 the logits wave. Wave w of a workgroup runs on SIMD w % 4, and the
+// tables spread the work over the four: a layer's two descent waves, whose heavier set of rounds alternates tick by
+// tick, share a SIMD where they can, and no two descent waves of the unsplit form do.
+constexpr int kFlowLogitsRole = 2;
 template <int L, bool SPLIT> __device__ __forceinline__ int flow_role(int w) {
     if constexpr (SPLIT) {
-        constexpr int r2[4] = {0, 3, 4, 5};
-        constexpr int r3[7] = {0, 4, 7, 6, 3, 5, 8};
-        constexpr int r4[10] = {0, 3, 6, 9, 4, 7, 10, 11, 5, 8};
-        constexpr int r5[13] = {0, 6, 9, 12, 3, 7, 10, 13, 4, 8, 11, 14, 5};
+        constexpr int r2[5] = {0, 3, 4, 5, 2};
+        constexpr int r3[8] = {0, 4, 7, 6, 3, 5, 8, 2};
+        constexpr int r4[11] = {0, 3, 6, 9, 4, 7, 10, 11, 5, 8, 2};
+        constexpr int r5[14] = {0, 6, 9, 12, 3, 7, 10, 13, 4, 8, 11, 14, 5, 2};
         return L == 2 ? r2[w] : L == 3 ? r3[w] : L == 4 ? r4[w] : r5[w];
     } else {
         constexpr int r4[7] = {0, 4, 3, 7, 10, 6, 9};
@@ -1466,20 +1467,20 @@ void flow_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
     __shared__ __attribute__((aligned(16))) FS sh;
 
     // wave 0: the token layer; the routed layers' descent waves (SPLIT: two, for the tokens of parity dpar 0 and 1)
-    // and update waves placed by flow_role; NLLW: wave 2 L - 1 the NLL; LOGW (the SPLIT builds): wave 3 L - 2 the
-    // logits (both set up as no layer's: descent set, layer 0)
+    // and update waves placed by flow_role; NLLW: wave 2 L - 1 the NLL; LOGW (the SPLIT builds): the logits wave
+    // placed by flow_role (both set up as no layer's: descent set, layer 0)
     constexpr bool SPLIT = kFlowSplit<SH, L, MODE>, LOGW = FS::LOGW;
     static_assert(LOGW == SPLIT, "the split builds finish the logits on the logits wave");
     const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const bool nllw = NLLW && w == 2 * L - 1;
-    const bool logw = LOGW && w == 3 * L - 2;
+    const int c = nllw ? 0 : flow_role<L, SPLIT>(w);
+    const bool logw = LOGW && c == kFlowLogitsRole;
     int l, dpar = 0;
     bool descent;
     if (nllw || logw) {
         l = 0;
         descent = true;
     } else {
-        const int c = flow_role<L, SPLIT>(w);
         l = c / 3;
         descent = c % 3 != 0;
         dpar = c % 3 == 2;
