@@ -490,6 +490,56 @@ def test_deep_descent_plans(hip, model_dir, c12, monkeypatch, which, plan):
         model.close()
 
 
+@pytest.mark.parametrize("which,plan", [
+    ("c4small", None), ("c4small", "4,4,2"), ("c4small", "2,4,2,2"), ("c4small", "4,2,3,1"), ("c4small", "4,4,1,1"),
+    ("c4small", "1,3,3,3"), ("c12", None), ("c12", "2,2,3,3"), ("group", None), ("ref_small", None),
+    ("ref_medium", None), ("c3", None)])
+def test_one_token_build(hip, model_dir, c12, c3, monkeypatch, which, plan):
+    """Calls of one token (ygg_step, and ygg_run with T = 1) of up to 4 streams per CU take the one-token build (the
+    deep descent with its second round read from global memory) wherever the deep descent takes the plan and the
+    shape is not the largest: 12 streams stepped 6 tokens with the state carried, leaves, states and logits equal
+    the oracle's."""
+    import torch
+    if which in ("c4small", "group"):
+        path = model_dir / ("c4small_gauss.bin" if which == "c4small" else "c4small_group.bin")
+        if not path.exists():
+            synth.write_model(synth.ModelSpec(128, 16, 10, 256, 4, router="gauss", group=which == "group"), 11, path)
+    elif which.startswith("ref_"):
+        # (the reference's small and medium trained shapes: n, readout rank, layer-input rank)
+        n, R, R2 = {"ref_small": (64, 8, 16), "ref_medium": (128, 16, 32)}[which]
+        path = model_dir / f"one_{which}.bin"
+        if not path.exists():
+            synth.write_model(synth.ModelSpec(n, 16, 10, 256, 3, readout_rank=R, layer_input_rank=R2, router="gauss"),
+                              12, path)
+    else:
+        path = c12 if which == "c12" else c3
+    monkeypatch.delenv("YGG_KERNEL", raising=False)
+    monkeypatch.delenv("YGG_DEEP", raising=False)
+    if plan:
+        monkeypatch.setenv("YGG_ROUNDS", plan)
+    model = hip.load(path)
+    info = model.info
+    name = model.kernel_name(12, 1)
+    built = deep_plan([int(h) for h in plan.split(",")] if plan else default_plan(info.router_depth))
+    _say(f"one-token build {which} plan {plan}: {name}")
+    assert (", 3, false, false, " in name) == built, name
+    assert ", 3, false, false, " not in model.kernel_name(12, 2)
+    x = synth.zipf_bytes(12, 6, 7) % info.vocab
+    ref = Oracle(path).run(x, states=True)
+    parts, st = [], None
+    for t in range(x.shape[1]):
+        parts.append(_gpu_run(model, x[:, t:t + 1], state=st))
+        st = torch.as_tensor(parts[-1]["state"], device=model.device)
+    got = {key: np.concatenate([q[key] for q in parts], 1) for key in ("leaves", "states", "logits")}
+    _compare(got, ref)
+    st = torch.zeros_like(st)
+    for t in range(x.shape[1]):
+        lg, st = model.step(x[:, t], st)
+        np.testing.assert_array_equal(lg.cpu().numpy(), ref["logits"][:, t])
+        np.testing.assert_array_equal(st.cpu().numpy(), ref["states"][:, t])
+    model.close()
+
+
 def test_default_dispatch(hip, model_dir, monkeypatch):
     """The kernel the library picks per call (ygg_kernel_name), and parity of the layer-pipelined kernel's capped
     build, which only calls with more streams than the uncapped build keeps resident reach (the per-stream kernel's
@@ -514,7 +564,9 @@ def test_default_dispatch(hip, model_dir, monkeypatch):
     assert model.kernel_name(1, 31) == "ygg::pipe_kernel<128, 8, 16, 4, 0, false, false>"
     assert model.kernel_name(info.flow_max_streams + 1, 64) in (fast.format(0, "false"), fast.format(0, "true"))
     assert info.solo_max_streams == 0 and info.deep_max_streams > 0     # the solo kernel only when forced
-    assert model.kernel_name(1, 1) == fast.format(0, "false")
+    # one-token run calls of up to 4 streams per CU: the one-token build (the deep descent, no staged second round)
+    assert model.kernel_name(1, 1) == "ygg::fast_kernel<128, 8, 16, 4, 3, false, false, false>"
+    assert model.kernel_name(4 * info.deep_max_streams + 1, 1) == fast.format(0, "false")
     assert model.kernel_name(1, 1, score=True) == fast.format(2, "false")
     assert model.kernel_name(max(info.pipe_max_streams, info.flow_max_streams) + 1, 64) == fast.format(0, "false")
     assert model.kernel_name(info.pipe_max_streams + 1, 16) == fast.format(0, "false")

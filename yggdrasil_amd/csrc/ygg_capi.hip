@@ -425,6 +425,8 @@ struct ygg_model {
     int pipe_max_streams = 0, pipe_few_max_streams[3] = {0, 0, 0};
     bool pipe_all = false;            // YGG_KERNEL=pipe: every call
     ygg::Kernel deep;                 // deep descent: generate with B <= deep_max_streams
+    ygg::Kernel one;                  // the deep descent, second round from global memory: run calls of one token
+    int one_max_streams = 0;          // ... with B at most this (one workgroup of 4 streams per CU)
     int deep_max_streams = 0;
     bool deep_all = false;            // YGG_KERNEL=deep: every call
     ygg::Kernel flow;                 // router rounds and updates pipelined over ticks: T > 1, B <= flow_max_streams[mode]
@@ -700,6 +702,11 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     // per workgroup of fast_kernel win); YGG_KERNEL=deep takes it for every call
     m->deep = deepk;
     m->deep_all = deepk && kmode == "deep";
+    // one-token run calls (ygg_step): the deep descent without staging its second round (three dependent global
+    // loads per routed layer instead of four) where the deep descent is on and no kernel is forced
+    // (its tail round's registers leave 2-3 waves per SIMD: for the latency of few streams, one workgroup per CU)
+    if (deep && kmode == "") m->one = ygg::find_one_launcher(n, R, R2f, L, group);
+    m->one_max_streams = m->one ? 4 * cus : 0;       // (fast_kernel: 4 streams per workgroup)
     m->deep_max_streams = deepk ? (m->deep_all ? INT32_MAX : cus) : 0;
     // flow_kernel for T >= kFlowMinTokens up to flow_max_streams (or always with YGG_KERNEL=flow): measured at 512
     // tokens against the per-stream kernel, the builds with the split descent win up to 8 streams per CU on every
@@ -804,8 +811,10 @@ constexpr int kFlowMinTokens = 32;
 
 // The kernel of a call of B streams and T tokens in mode (kModeRun, kModeGenerate: ygg_generate, kModeScore: a
 // digest or NLL). YGG_KERNEL=solo: the solo kernel (all wavefronts of a workgroup on one stream) for every call but
-// score calls. Generation: the deep kernel for >= 8 tokens and B <= deep_max_streams, else the per-stream kernel
-// (every token needs all layers of the one before it, so never a layer-pipelined one). Otherwise: the tick-pipelined
+// score calls. Run calls of one token and up to 4 streams per CU: the one-token build (the deep descent, its second
+// round from global memory). Generation: the deep kernel for >= 8 tokens and B <= deep_max_streams, else the
+// per-stream kernel (every token needs all layers of the one before it, so never a layer-pipelined one). Otherwise:
+// the tick-pipelined
 // kernel for T >= kFlowMinTokens and B <= flow_max_streams, the layer-pipelined kernel for T > 1 when its
 // workgroups fit (for T >= kFlowMinTokens only where there is no tick-pipelined build: more streams than that one
 // takes run best on the per-stream kernel), else the per-stream kernel. Of the two builds of a kernel, the uncapped
@@ -815,6 +824,7 @@ const ygg::Kernel &pick(const ygg_model *m, int B, int T, int mode) {
     if (m->solo && mode != kModeScore && (m->solo_all || (B <= m->solo_max_streams && (gen || T == 1))))
         return m->solo;
     if (m->deep_all) return m->deep;
+    if (m->one && mode == kModeRun && T == 1 && B <= m->one_max_streams) return m->one;
     if (gen && m->deep && B <= m->deep_max_streams && T >= 8) return m->deep;
     if (!gen && m->flow && (m->flow_all || (T >= kFlowMinTokens && B <= m->flow_max_streams[mode]))) return m->flow;
     if (!gen && m->pipe && (m->pipe_all || (T > 1 && B <= m->pipe_max_streams && !(m->flow && T >= kFlowMinTokens))))

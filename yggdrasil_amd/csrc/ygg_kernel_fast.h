@@ -425,10 +425,11 @@ __device__ __forceinline__ Tail make_tail(const YggDevModel &m, int lane) {
     return t;
 }
 
-// The deep descent -> leaf index. W0/th0 as in descend; W1 the layer's LDS second-round rows and th2 this lane's four
-// second-round thresholds (slots 2^h0 + 4 lane .. + 3 of the token's row); qb the state below (LDS) for the tail's
-// whole-row dots. hook() runs once, while the tail round's loads are in flight (or after the descent).
-template <int N, class Hook = NoHook>
+// The deep descent -> leaf index. W0/th0 as in descend; W1 the layer's LDS second-round rows (R1G: the layer's rows of
+// the second round in global memory, from slot 2^h0) and th2 this lane's four second-round thresholds (slots
+// 2^h0 + 4 lane .. + 3 of the token's row); qb the state below (LDS) for the tail's whole-row dots. hook() runs once,
+// while the tail round's loads are in flight (or after the descent).
+template <int N, class Hook = NoHook, bool R1G = false>
 __device__ __forceinline__ int descend_deep(const YggDevModel &m, const YggDevLayer &y, const int8_t *W0, float th0,
                                             const int8_t *W1, const float4 &th2, const uint32_t (&qbw)[Fast<N>::QW],
                                             const int8_t *qb, float rho, int x, int lane, const Tail &tl,
@@ -454,7 +455,10 @@ __device__ __forceinline__ int descend_deep(const YggDevModel &m, const YggDevLa
         const int h = m.round_h[1], nn = (1 << h) - 1;
         const int sl = ((ix - (1 << h0)) << h) + qj;          // slot within the second round's slots
         uint32_t wv[F::QW];
-        if (qj < nn) quad_share_r2<N>(wv, W1 + sl * N, qk, sl);
+        if (qj < nn) {
+            if constexpr (R1G) quad_share<N>(wv, W1 + (size_t)sl * N, qk);
+            else quad_share_r2<N>(wv, W1 + sl * N, qk, sl);
+        }
         // slot sl's threshold is component sl & 3 of lane sl >> 2's th2 (sl < 256)
         const int src = (sl >> 2) & 63;
         const float a = __shfl(th2.x, src), b = __shfl(th2.y, src), c = __shfl(th2.z, src), d = __shfl(th2.w, src);
@@ -776,7 +780,8 @@ __device__ __forceinline__ void store_logits(float *o, const float (&lg)[4], int
 
 // MODE: kModeRun (logits, leaves, states), kModeScore (also the digest and the NLL: their constants and lane terms
 // take registers the other modes keep for streams) or kModeGenerate (sample the next input from the logits of every
-// token, io.gen, instead of reading it from tokens). DEEP: one
+// token, io.gen, instead of reading it from tokens); kModeOne: kModeRun with the deep descent for calls of one token
+// (4 streams per workgroup, the second round's rows from global memory: nothing staged beyond the usual tables). DEEP: one
 // stream per workgroup with the deep descent (generation for few streams), else 4 streams per workgroup with
 // descend. CAP (not DEEP): at most 128 VGPRs, 4 wavefronts per SIMD (the most streams resident, some registers
 // spilled), else up to 256 (no spills; for calls whose streams all fit at the lower occupancy).
@@ -795,6 +800,7 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
     using F = SH;
     constexpr int W = DEEP ? 1 : kFastWaves, LR = L > 1 ? L - 1 : 1;
     constexpr bool GEN = MODE == kModeGenerate, SCORE = MODE == kModeScore;
+    constexpr bool DD = DEEP || MODE == kModeOne;         // the deep descent (DEEP: its second round from LDS)
     __shared__ __attribute__((aligned(16))) SharedTables<SH, L> S;
     __shared__ __attribute__((aligned(16))) GroupTablesOf<SH, L, GROUP> GT;
     __shared__ __attribute__((aligned(16))) int8_t W1s[DEEP ? LR : 1][DEEP ? kR2Slots<N> * N : 16];
@@ -826,7 +832,7 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
     if (!live) return;
 
     Tail tl{};
-    if constexpr (DEEP) tl = make_tail(m, lane);
+    if constexpr (DD) tl = make_tail(m, lane);
     const int n2 = m.n_rounds > 1 ? 1 << (m.round_h[0] + m.round_h[1]) : 0;   // second-round slots
     int8_t *qs = qsw[wv];
     int8_t *zls = zlw[wv];
@@ -860,7 +866,7 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
 #pragma unroll
         for (int l = 1; l < L; l++) {
             float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            if (DEEP && 4 * lane < n2)
+            if (DD && 4 * lane < n2)
                 v = *(const float4 *)(m.layers[l].thr + (size_t)x * m.layers[l].thr_stride + (1 << m.round_h[0]) +
                                       4 * lane);
             th2x[l - 1] = v.x; th2y[l - 1] = v.y; th2z[l - 1] = v.z; th2w[l - 1] = v.w;
@@ -907,7 +913,7 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
                 rho = below_and_rho<N>(qbw, qs + (l - 1) * N, y.rms_eps, lane);
                 if constexpr (GROUP)
                     if (y.r2b) rho = group_rho<N>(qbw, GT.r2[l - 1], y.rms_eps);
-                if constexpr (!DEEP) {
+                if constexpr (!DD) {
                     r = descend<N>(m, y, S.W[l - 1], th, qbw, rho, x, lane, flush);
                 } else {
                     float4 t2 = make_float4(th2x[0], th2y[0], th2z[0], th2w[0]);
@@ -919,8 +925,13 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
                         t2.z = b ? th2z[i] : t2.z;
                         t2.w = b ? th2w[i] : t2.w;
                     }
-                    r = descend_deep<N>(m, y, S.W[l - 1], th, W1s[DEEP ? l - 1 : 0], t2, qbw, qs + (l - 1) * N,
-                                        rho, x, lane, tl, flush);
+                    if constexpr (DEEP)
+                        r = descend_deep<N>(m, y, S.W[l - 1], th, W1s[DEEP ? l - 1 : 0], t2, qbw, qs + (l - 1) * N,
+                                            rho, x, lane, tl, flush);
+                    else
+                        r = descend_deep<N, decltype(flush), true>(m, y, S.W[l - 1], th,
+                                                                   y.w + ((size_t)1 << m.round_h[0]) * N, t2, qbw,
+                                                                   qs + (l - 1) * N, rho, x, lane, tl, flush);
                 }
             }
             Gather<SH, FACT> G;

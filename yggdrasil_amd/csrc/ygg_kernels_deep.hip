@@ -86,6 +86,34 @@ template <int N, int R, int R2, int L, bool GROUP> Kernel deep_k() {
         return Kernel();
 }
 
+// fast_kernel's one-token build (kModeOne: the deep descent with the second round from global memory, 4 streams per
+// workgroup); not for the largest shape, whose tail-round registers beside its record would spill
+template <int N, int R, int R2, int L, bool GROUP>
+hipError_t launch_one(const YggDevModel &m, const int32_t *tokens, int B, int T, int8_t *state, const YggIO &io,
+                      hipStream_t stream) {
+    if (io_mode(io) != kModeRun || T != 1) return hipErrorInvalidValue;     // (the dispatch gives it no other call)
+    const dim3 grid((B + kFastWaves - 1) / kFastWaves), block(64 * kFastWaves);
+    hipLaunchKernelGGL((fast_kernel<N, R, R2, L, kModeOne, false, false, GROUP>), grid, block, 0, stream, m, tokens, B,
+                       T, state, io);
+    return hipGetLastError();
+}
+
+template <int N, int R, int R2, int L, bool GROUP> Kernel one_k() {
+    if constexpr (L >= 2 && kHasCap<N, R, R2> && (!GROUP || kGroupOk<N>))
+        return make_kernel(launch_one<N, R, R2, L, GROUP>, "ygg::fast_kernel<%d, %d, %d, %d, 3, false, false, %s>", N,
+                           R, R2, L, GROUP ? "true" : "false");
+    else
+        return Kernel();
+}
+
+template <int N, int R, int R2, bool GROUP> Kernel one_for(int L) {
+    if (L == 2) return one_k<N, R, R2, 2, GROUP>();
+    if (L == 3) return one_k<N, R, R2, 3, GROUP>();
+    if (L == 4) return one_k<N, R, R2, 4, GROUP>();
+    if (L == 5) return one_k<N, R, R2, 5, GROUP>();
+    return Kernel();
+}
+
 template <int N, int R, int R2, bool CAP, bool GROUP> Kernel pipe_for(int L) {
     if (L == 1) {
         if constexpr (R == 8) return pipe_k<N, R, R2, 1, CAP, GROUP>();
@@ -140,6 +168,15 @@ int pipe_blocks_per_cu(int n, int R, int R2, int L, bool cap, bool group, int mo
     YGG_SHAPES(YGG_P)
 #undef YGG_P
     return 0;
+}
+
+// fast_kernel's one-token build (2 <= L <= 5, all shapes but the largest)
+Kernel find_one_launcher(int n, int R, int R2, int L, bool group) {
+#define YGG_D(N_, R_, R2_) \
+    if (n == N_ && R == R_ && R2 == R2_) return group ? one_for<N_, R_, R2_, true>(L) : one_for<N_, R_, R2_, false>(L);
+    YGG_SHAPES(YGG_D)
+#undef YGG_D
+    return Kernel();
 }
 
 // fast_kernel with the deep descent (2 <= L <= 5, where its LDS fits)

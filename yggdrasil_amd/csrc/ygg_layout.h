@@ -98,6 +98,9 @@ struct YggIO {
 constexpr int kModeRun = 0;         // logits, leaves, states after every token
 constexpr int kModeGenerate = 1;    // io.gen: each token sampled from the step before
 constexpr int kModeScore = 2;       // io.digest or io.nll
+// a build of the per-stream kernel, not a mode argument: kModeRun for calls of one token with the deep descent, its
+// second round's rows read from global memory instead of staged in LDS
+constexpr int kModeOne = 3;
 inline int io_mode(const YggIO &io) {
     return io.gen ? kModeGenerate : ((io.digest || io.nll) ? kModeScore : kModeRun);
 }
