@@ -540,6 +540,33 @@ def test_one_token_build(hip, model_dir, c12, c3, monkeypatch, which, plan):
     model.close()
 
 
+def test_flow_beyond_resident(hip, model_dir, monkeypatch):
+    """The default dispatch runs calls of >= 32 tokens of up to 8 streams per CU on the tick-pipelined kernel even
+    where its workgroups are not all resident (4 layers: one per CU, so 8 rounds of workgroups): leaves, states and
+    logits of every stream, and the scoring build's NLL and digest, equal the oracle's."""
+    monkeypatch.delenv("YGG_KERNEL", raising=False)
+    monkeypatch.delenv("YGG_DEEP", raising=False)
+    from oracle import oracle as O
+    path = model_dir / "c4small_gauss.bin"
+    if not path.exists():
+        synth.write_model(synth.ModelSpec(128, 16, 10, 256, 4, router="gauss"), 11, path)
+    model = hip.load(path)
+    info = model.info
+    B = info.flow_max_streams
+    T = 33
+    name = model.kernel_name(B, T)
+    _say(f"flow beyond resident: {B} streams x {T} tokens, {name}")
+    assert name == "ygg::flow_kernel<128, 8, 16, 4, 3, 0, false>" and B >= 8 * info.deep_max_streams
+    assert model.kernel_name(B, T, score=True) == "ygg::flow_kernel<128, 8, 16, 4, 3, 2, false>"
+    x = synth.zipf_bytes(B, T + 1, 8)
+    ref = Oracle(path).run(x[:, :-1], states=True, digest=True)
+    _compare(_gpu_run(model, x[:, :-1]), ref)
+    np.testing.assert_allclose(model.score(x, batch=B), O.nll_bits(ref["logits"], x[:, 1:]), rtol=1e-12, atol=1e-9)
+    dg = model.run(x[:, :-1], logits=False, digest=True)["digest"].cpu().numpy().view(np.uint64)
+    np.testing.assert_array_equal(dg, ref["digest"])
+    model.close()
+
+
 def test_default_dispatch(hip, model_dir, monkeypatch):
     """The kernel the library picks per call (ygg_kernel_name), and parity of the layer-pipelined kernel's capped
     build, which only calls with more streams than the uncapped build keeps resident reach (the per-stream kernel's
