@@ -1214,9 +1214,15 @@ template <class SH> constexpr bool kFlowBig = SH::N * SH::R2 >= 256 * 64;
 // layer's unembedding term, in layer order, stores the row and, scoring, adds the NLL and the digest.
 template <class SH, int L, bool SC> constexpr bool kFlowSplitSC = !kFlowBig<SH> && (L <= 4 || !SC);
 template <class SH, int L, int MODE> constexpr bool kFlowSplit = kFlowSplitSC<SH, L, MODE == kModeScore>;
+// LIW (SPLIT builds of 2 layers): the layer inputs on a wavefront of their own (the layer-input wave). The descent
+// wave that ran a token's last round leaves its rho in LDS, and a tick later that wave forms the token's layer input
+// from the state below (still in its ring), a tick before the update reads it. (Measured at batch 1: configuration 1
+// 2.29 -> 1.96 ms; with more layers the extra wavefront lowered residency or crowded a SIMD, and lost.)
+template <class SH, int L, int MODE> constexpr bool kFlowLiw = kFlowSplit<SH, L, MODE> && L == 2;
 // wavefronts: the token layer's, then per routed layer the descent wave (SPLIT: two) and the update wave (SPLIT: and
-// the logits wave last)
-template <class SH, int L, int MODE> constexpr int kFlowWaves = kFlowSplit<SH, L, MODE> ? 3 * L - 1 : 2 * L - 1;
+// the logits wave; LIW: and the layer-input wave)
+template <class SH, int L, int MODE>
+constexpr int kFlowWaves = kFlowSplit<SH, L, MODE> ? 3 * L - 1 + (kFlowLiw<SH, L, MODE> ? 1 : 0) : 2 * L - 1;
 // VREG: V' in the descent wave's registers (BIG, up to 4 layers: 7 wavefronts leave 256 VGPRs a wave; at 5 layers,
 // 9 wavefronts leave 168, and V' stays in LDS)
 template <class SH, int L> constexpr bool kFlowVreg = kFlowBig<SH> && 2 * L - 1 <= 8;
@@ -1246,6 +1252,7 @@ template <class SH, int L, int P, bool GROUP, bool SC> struct FlowShared {
     alignas(16) int8_t zqr[ZQRING ? L : 1][ZQRING ? LG : 1][SH::ZQ];       // ZQR, LOGW: zq of layer l, token t
     alignas(16) unsigned long long dterm[LG][L];
     alignas(16) int8_t zlw[L][4][SH::ZL];                 // layer input of token t: [l][t & 3]
+    float rhol[L][4];                                     // LIW: rho of token t's state below, for the layer input
     alignas(16) int8_t zqw[L][SH::ZQ];
     int leafx[L][2][2];                                   // leaf and token of token t: [l][t & 1]
     int stop_t;
@@ -1444,13 +1451,13 @@ __device__ __forceinline__ void flow_logits(FlowShared<SH, L, P, GROUP, SCORE> &
 }
 
 // Wave w's role, 3 l + k: layer l's update wave (k = 0; the token layer's for l = 0) or a descent wave (k = 1; SPLIT:
-// k = 1 and 2, of token parity 0 and 1); SPLIT: 2 the logits wave. Wave w of a workgroup runs on SIMD w % 4, and the
+// k = 1 and 2, of token parity 0 and 1); SPLIT: 2 the logits wave; LIW: 1 the layer-input wave. Wave w of a workgroup runs on SIMD w % 4, and the
 // tables spread the work over the four: a layer's two descent waves, whose heavier set of rounds alternates tick by
 // tick, share a SIMD where they can, and no two descent waves of the unsplit form do.
-constexpr int kFlowLogitsRole = 2;
+constexpr int kFlowLogitsRole = 2, kFlowLayerInputRole = 1;
 template <int L, bool SPLIT> __device__ __forceinline__ int flow_role(int w) {
     if constexpr (SPLIT) {
-        constexpr int r2[5] = {0, 3, 4, 5, 2};
+        constexpr int r2[6] = {0, 3, 4, 5, 2, 1};
         constexpr int r3[8] = {0, 4, 7, 6, 3, 5, 8, 2};
         constexpr int r4[11] = {0, 3, 6, 9, 4, 7, 10, 11, 5, 8, 2};
         constexpr int r5[14] = {0, 6, 9, 12, 3, 7, 10, 13, 4, 8, 11, 14, 5, 2};
@@ -1485,10 +1492,11 @@ void flow_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
     const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const bool nllw = NLLW && w == 2 * L - 1;
     const int c = nllw ? 0 : flow_role<L, SPLIT>(w);
-    const bool logw = LOGW && c == kFlowLogitsRole;
+    constexpr bool LIW = kFlowLiw<SH, L, MODE>;
+    const bool logw = LOGW && c == kFlowLogitsRole, liw = LIW && c == kFlowLayerInputRole;
     int l, dpar = 0;
     bool descent;
-    if (nllw || logw) {
+    if (nllw || logw || liw) {
         l = 0;
         descent = true;
     } else {
@@ -1539,6 +1547,25 @@ void flow_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
                 const int stop = __builtin_amdgcn_readfirstlane(sh.stop_t);
                 const int tn = k - 1 - kFlowToken0 - (L - 1) * (P + 2);
                 if (io.nll && tn >= 0 && tn < T && tn < stop) flow_nll<SH, L, P, GROUP>(sh, m, tn, s, T, io, nacc, lane);
+                flow_barrier();
+            }
+        }
+    } else if (T > 0 && liw) {
+        // ---- the layer-input wave: at tick k the layer inputs of the tokens whose last router round ran at tick
+        // k - 1, one per routed layer (their updates read them next tick; the state below is kept 8 tokens)
+        if constexpr (LIW) {
+            for (int k = 0; k < ticks; k++) {
+                const int stop = __builtin_amdgcn_readfirstlane(sh.stop_t);
+#pragma unroll 1
+                for (int li = 1; li < L; li++) {
+                    const int t = k - kFlowToken0 - (li - 1) * (P + 2) - P - 1;
+                    if (t >= 0 && t < T && t < stop) {
+                        uint32_t qb[F::QW];
+                        quad_share<N>(qb, sh.qring[li - 1][(t + 1) & QM], qk);
+                        layer_input<SH>(sh.zlw[li][t & 3], sh.S.V[li - 1], sh.S.mv[li - 1], qb, sh.rhol[li][t & 3],
+                                        lane);
+                    }
+                }
                 flow_barrier();
             }
         }
@@ -1693,12 +1720,16 @@ void flow_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
                     lr = ix - m.E;
                     lrho = rho;
                     // ---- the leaf reached and its layer input, for the update wave: before the earlier rounds, whose
-                    // inputs were loaded later last tick and are still arriving
+                    // inputs were loaded later last tick and are still arriving (LIW: the rho, for the layer-input
+                    // wave next tick)
                     if (lt >= 0 && lt < T && lt < stop) {
                         if (lane == 0) {
                             sh.leafx[l][lt & 1][0] = lr;
                             sh.leafx[l][lt & 1][1] = lx;
+                            if constexpr (LIW) sh.rhol[l][lt & 3] = lrho;
                         }
+                    }
+                    if (!LIW && lt >= 0 && lt < T && lt < stop) {
                         uint32_t qb[F::QW];
                         quad_share<N>(qb, sh.qring[l - 1][(lt + 1) & QM], qk);
                         if constexpr (VREG)
