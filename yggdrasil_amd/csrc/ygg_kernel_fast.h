@@ -509,13 +509,14 @@ __device__ __forceinline__ int descend_deep(const YggDevModel &m, const YggDevLa
 // MZ: the model has group scales (the expert's readout row scales, in every layer). UW = false: not U' (its user
 // has the layer-input term from elsewhere)
 // FACT, routed: U_r's first K4 dwords per coordinate (K4 = input rank / 4), c_r and su_r instead of the table row
-template <class SH, bool MZ = false, bool UW = true, bool FACT = false>
+// PART: 0 all of it, 1 what the update reads (A16, U', the table row), 2 what the readout reads (P, the row scale)
+template <class SH, bool MZ = false, bool UW = true, bool FACT = false, int PART = 0>
 __device__ __forceinline__ void gather(Gather<SH, FACT> &G, const YggDevLayer &y, int r, int x, bool routed, int lane,
                                        int K4 = 0) {
     using F = SH;
     // a layer's records and tables lie within 4 GiB (checked at load): 32-bit offsets
     const uint8_t *g = y.gath + (uint32_t)r * (uint32_t)y.gath_bytes;
-    if (lane < F::NL) {
+    if (PART != 2 && lane < F::NL) {
 #pragma unroll
         for (int c = 0; c < F::NA; c++) {
             const uint4 v = *(const uint4 *)(g + (c * F::NL + lane) * 16);
@@ -552,6 +553,7 @@ __device__ __forceinline__ void gather(Gather<SH, FACT> &G, const YggDevLayer &y
         }
     }
     if constexpr (FACT) G.fs = routed ? *(const float *)(g + y.off_FS) : 0.0f;
+    if constexpr (PART == 1) return;
     // (a model with group scales has the row scales in every layer; without, the readout scale is the layer's)
     if constexpr (MZ) G.mzr = y.mz[(uint32_t)r * SH::R + lane / SH::RL];
     else G.mzr = 0.0f;
@@ -1334,11 +1336,13 @@ __device__ __forceinline__ void flow_finish(FlowShared<SH, L, P, GROUP, SCORE> &
 // the update of token t by layer l (its record G arrived during the last ticks), its readout into the logits of token
 // t, and the outputs; the last layer completes the token. It computes whether ok or not (the record is then read in
 // every tick, so no path leaves its loads pending) and stores only for a token of the stream (ok).
-template <class SH, int L, int P, bool SCORE, bool GROUP>
+// mid() runs once the update has read the record's A16, U' and table row (the single-buffer builds load the next
+// record's there while the readout still reads P)
+template <class SH, int L, int P, bool SCORE, bool GROUP, class Mid = NoHook>
 __device__ __forceinline__ void flow_update(FlowShared<SH, L, P, GROUP, SCORE> &sh, const YggDevModel &m,
                                             const YggDevLayer &y, const Gather<SH> &G, const float (&bias)[4],
                                             int l, int t, bool ok, int r, int s, int T, const YggIO &io,
-                                            unsigned long long &dg, double &nacc, int lane) {
+                                            unsigned long long &dg, double &nacc, int lane, Mid mid = Mid()) {
     using F = SH;
     using FS = FlowShared<SH, L, P, GROUP, SCORE>;
     constexpr int QM = FS::QR - 1, LG = FS::LG;
@@ -1357,6 +1361,7 @@ __device__ __forceinline__ void flow_update(FlowShared<SH, L, P, GROUP, SCORE> &
             for (int c = 0; c < F::C; c++) qnew[F::C * lane + c] = (int8_t)qn[c];
         }
     }
+    mid();
     wave_sync();
     // (a token outside the stream reads out into the wave's own row, not the ring slot of a token in flight)
     int8_t *zq = (FS::ZQRING && ok) ? sh.zqr[FS::ZQRING ? l : 0][FS::ZQRING ? t % LG : 0] : sh.zqw[l];
@@ -1493,6 +1498,11 @@ void flow_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
     const bool nllw = NLLW && w == 2 * L - 1;
     const int c = nllw ? 0 : flow_role<L, SPLIT>(w);
     constexpr bool LIW = kFlowLiw<SH, L, MODE>;
+    // SB1 (the split builds of 4 layers or more with records of n = 128): one record buffer per update wave, reloaded
+    // part by part as the update and the readout finish with it. About 25 fewer VGPRs: two resident workgroups per CU
+    // instead of one (measured at 512-2048 streams: 5-16% faster). Where residency does not rise (fewer layers,
+    // smaller records) the shorter load window cost up to 16%.
+    constexpr bool SB1 = SPLIT && L >= 4 && N >= 128;
     const bool logw = LOGW && c == kFlowLogitsRole, liw = LIW && c == kFlowLayerInputRole;
     int l, dpar = 0;
     bool descent;
@@ -1582,9 +1592,31 @@ void flow_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
         }
     } else if (T > 0 && l == 0) {
         // ---- the token layer: the record of token k at tick k into buffer k & 1, its update at tick k + 2 (before
-        // that tick's record refills the buffer)
+        // that tick's record refills the buffer). SB1 (the split builds): one buffer, the record of token k - 1
+        // loaded at tick k as the update of token k - 2 finishes with each part of the one before
         Gather<SH> G0, G1;
         int gx0 = 0, gx1 = 0;
+        if constexpr (SB1) {
+            for (int k = 0; k < ticks; k++) {
+                const int stop = __builtin_amdgcn_readfirstlane(sh.stop_t);
+                const int xn = token_at(k - 1);
+                const int t = k - kFlowToken0;
+                bool ok = t >= 0 && t < T && t < stop;
+                if (ok && (gx0 < 0 || gx0 >= V)) {
+                    if (lane == 0) {
+                        atomicOr(m.err, 1u);
+                        sh.stop_t = t;
+                    }
+                    ok = false;
+                }
+                const int xg = (xn < 0 || xn >= V) ? 0 : xn;
+                flow_update<SH, L, P, SCORE, GROUP>(sh, m, y, G0, bias, 0, t, ok, gx0, s, T, io, dg, nacc, lane,
+                                                    [&]() { gather<SH, GROUP, true, false, 1>(G0, y, xg, xg, false, lane); });
+                gather<SH, GROUP, true, false, 2>(G0, y, xg, xg, false, lane);
+                gx0 = xn;
+                flow_barrier();
+            }
+        }
         auto tick = [&](int k, Gather<SH> &G, int &gx) {
             const int stop = __builtin_amdgcn_readfirstlane(sh.stop_t);
             const int xn = token_at(k);
@@ -1603,9 +1635,11 @@ void flow_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
             gather<SH, GROUP>(G, y, xg, xg, false, lane);
             flow_barrier();
         };
-        for (int k = 0; k < ticks; k += 2) {
-            tick(k, G0, gx0);
-            tick(k + 1, G1, gx1);
+        if constexpr (!SB1) {
+            for (int k = 0; k < ticks; k += 2) {
+                tick(k, G0, gx0);
+                tick(k + 1, G1, gx1);
+            }
         }
     } else if (T > 0 && !descent) {
         // ---- a routed layer's update wave: at tick k the record of token k - o_prev - P - 1 (its leaf left by the
@@ -1613,6 +1647,23 @@ void flow_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
         const int o_g = o_prev + P + 1;
         Gather<SH> G0, G1;
         int gr0 = 0, gr1 = 0;
+        if constexpr (SB1) {
+            // (one buffer: the update of token k - o_g - 1 from the record loaded last tick, and as it finishes with
+            // each part of it, that part of the record of token k - o_g)
+            for (int k = 0; k < ticks; k++) {
+                const int stop = __builtin_amdgcn_readfirstlane(sh.stop_t);
+                const int tg = k - o_g;
+                const int *lx = sh.leafx[l][tg & 1];
+                const int r = __builtin_amdgcn_readfirstlane(lx[0]), x = __builtin_amdgcn_readfirstlane(lx[1]);
+                const int t = tg - 1;
+                flow_update<SH, L, P, SCORE, GROUP>(sh, m, y, G0, bias, l, t, t >= 0 && t < T && t < stop, gr0, s, T,
+                                                    io, dg, nacc, lane,
+                                                    [&]() { gather<SH, GROUP, !BIG, false, 1>(G0, y, r, x, true, lane); });
+                gather<SH, GROUP, !BIG, false, 2>(G0, y, r, x, true, lane);
+                gr0 = r;
+                flow_barrier();
+            }
+        }
         auto tick = [&](int k, Gather<SH> &Gg, int &grg, const Gather<SH> &Gu, int gru) {
             const int stop = __builtin_amdgcn_readfirstlane(sh.stop_t);
             const int tg = k - o_g;
@@ -1625,9 +1676,11 @@ void flow_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
                                                 dg, nacc, lane);
             flow_barrier();
         };
-        for (int k = 0; k < ticks; k += 2) {
-            tick(k, G0, gr0, G1, gr1);
-            tick(k + 1, G1, gr1, G0, gr0);
+        if constexpr (!SB1) {
+            for (int k = 0; k < ticks; k += 2) {
+                tick(k, G0, gr0, G1, gr1);
+                tick(k + 1, G1, gr1, G0, gr0);
+            }
         }
     } else if (T > 0) {
         // ---- a descent wave: its router plan (round j: rh[j] levels from slot rb[j], subtrees at depth rd[j])
