@@ -1231,10 +1231,11 @@ template <class SH, int L> constexpr bool kFlowVreg = kFlowBig<SH> && 2 * L - 1 
 // ZQR (BIG at 5 layers, where LDS is short): each layer leaves its zq row of token t in a ring and the last layer's
 // update wave adds every layer's unembedding term, in layer order, instead of the layers adding theirs to a ring of
 // logit rows
-// Score builds of the form with V' in LDS run the NLL on a wavefront of their own (after the layers' waves): its tick
-// loop holds the double-precision exp and log constants, which in an update wave's loop spill beside the record.
+// Score builds of the form with V' in LDS and the SPLIT score builds run the NLL on a wavefront of their own (after
+// the other waves): its tick loop holds the double-precision exp and log constants, which in an update wave's loop
+// spill beside the record, and its log-sum-exp would otherwise lengthen the tick of the wave finishing the logits.
 template <class SH, int L, int MODE>
-constexpr bool kFlowNllWave = MODE == kModeScore && kFlowBig<SH> && !kFlowVreg<SH, L>;
+constexpr bool kFlowNllWave = MODE == kModeScore && ((kFlowBig<SH> && !kFlowVreg<SH, L>) || kFlowSplit<SH, L, MODE>);
 template <class SH, int L, int MODE>
 constexpr int kFlowThreads = 64 * (kFlowWaves<SH, L, MODE> + (kFlowNllWave<SH, L, MODE> ? 1 : 0));
 
@@ -1245,7 +1246,7 @@ template <class SH, int L, int P, bool GROUP, bool SC> struct FlowShared {
     static constexpr int QR = (BIG && P < 4) ? 4 : kFlowStates;           // state ring slots (> P)
     // tokens in flight between the token layer's update and the last reader of their ring slots (LOGW: one tick more)
     static constexpr int LG = kFlowLogits<L, P> + (LOGW ? 1 : 0);
-    static constexpr int LGS = ZQR ? (SC ? 2 : 1) : LOGW ? 1 : LG;        // logits slots
+    static constexpr int LGS = (ZQR || LOGW) ? (SC ? 2 : 1) : LG;         // logits slots
     alignas(16) SharedTables<SH, L, !VREG> S;
     alignas(16) GroupTablesOf<SH, L, GROUP> GT;
     alignas(16) int8_t qring[L][QR][SH::N];
@@ -1319,10 +1320,12 @@ __device__ __forceinline__ void flow_finish(FlowShared<SH, L, P, GROUP, SCORE> &
     using FS = FlowShared<SH, L, P, GROUP, SCORE>;
     constexpr int LG = FS::LG;
     const int V = m.V;
-    if (SCORE && FS::ZQR && io.nll) *(float4 *)(sh.lgs[t & 1] + 4 * lane) = make_float4(lg[0], lg[1], lg[2], lg[3]);
+    // (ZQR, LOGW: the NLL wave takes the NLL from the logits row left in lgs)
+    constexpr bool ROW = FS::ZQR || FS::LOGW;
+    if (SCORE && ROW && io.nll) *(float4 *)(sh.lgs[t & 1] + 4 * lane) = make_float4(lg[0], lg[1], lg[2], lg[3]);
     wave_sync();
     if (io.logits) store_logits(io.logits + ((size_t)s * T + t) * V, lg, V, lane);
-    if (SCORE && !FS::ZQR && io.nll) {
+    if (SCORE && !ROW && io.nll) {
         const int yv = scalar_load(io.targets + (size_t)s * T + t);
         if (yv >= 0 && yv < V) nacc += token_nll(lg, V, yv, lane);
         else if (lane == 0) atomicOr(m.err, 2u);
@@ -1490,12 +1493,12 @@ void flow_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
     __shared__ __attribute__((aligned(16))) FS sh;
 
     // wave 0: the token layer; the routed layers' descent waves (SPLIT: two, for the tokens of parity dpar 0 and 1)
-    // and update waves placed by flow_role; NLLW: wave 2 L - 1 the NLL; LOGW (the SPLIT builds): the logits wave
+    // and update waves placed by flow_role; NLLW: the last wave the NLL; LOGW (the SPLIT builds): the logits wave
     // placed by flow_role (both set up as no layer's: descent set, layer 0)
     constexpr bool SPLIT = kFlowSplit<SH, L, MODE>, LOGW = FS::LOGW;
     static_assert(LOGW == SPLIT, "the split builds finish the logits on the logits wave");
     const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
-    const bool nllw = NLLW && w == 2 * L - 1;
+    const bool nllw = NLLW && w == kFlowWaves<SH, L, MODE>;
     const int c = nllw ? 0 : flow_role<L, SPLIT>(w);
     constexpr bool LIW = kFlowLiw<SH, L, MODE>;
     // SB1 (the split builds of 4 layers or more with records of n = 128): one record buffer per update wave, reloaded
@@ -1535,8 +1538,8 @@ void flow_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
     for (int u = 0; u < 4; u++) bias[u] = 4 * lane + u < VP ? m.output_bias[4 * lane + u] : 0.0f;
     __syncthreads();
 
-    // (even: some waves run 2 a loop; NLLW, LOGW: one tick more, for the NLL or the logits of the last token)
-    const int ticks = (kFlowToken0 + (L - 1) * (P + 2) + T + 1 + ((NLLW || LOGW) ? 1 : 0)) & ~1;
+    // (even: some waves run 2 a loop; NLLW, LOGW: one tick more each, for the NLL and the logits of the last token)
+    const int ticks = (kFlowToken0 + (L - 1) * (P + 2) + T + 1 + (NLLW ? 1 : 0) + (LOGW ? 1 : 0)) & ~1;
     const int o_prev = kFlowToken0 + (l - 1) * (P + 2);                   // the layer below's update of token 0
     const int32_t *tok = tokens + (size_t)s * T;
     // the token at an index clamped into the stream (stages on tokens outside the stream or the vocabulary still run,
@@ -1550,12 +1553,13 @@ void flow_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
     __builtin_amdgcn_s_waitcnt(0);
 
     if (T > 0 && nllw) {
-        // ---- the NLL wave: at tick k the NLL of the token the last layer completed at tick k - 1 (tokens from the
-        // stop on were not completed: the stop only moves to a token the last layer has not reached)
+        // ---- the NLL wave: at tick k the NLL of the token whose logits were finished at tick k - 1, by the last
+        // layer or (LOGW) the logits wave a tick after it (tokens from the stop on were not completed: the stop only
+        // moves to a token the last layer has not reached)
         if constexpr (NLLW) {
             for (int k = 0; k < ticks; k++) {
                 const int stop = __builtin_amdgcn_readfirstlane(sh.stop_t);
-                const int tn = k - 1 - kFlowToken0 - (L - 1) * (P + 2);
+                const int tn = k - 1 - kFlowToken0 - (L - 1) * (P + 2) - (LOGW ? 1 : 0);
                 if (io.nll && tn >= 0 && tn < T && tn < stop) flow_nll<SH, L, P, GROUP>(sh, m, tn, s, T, io, nacc, lane);
                 flow_barrier();
             }
