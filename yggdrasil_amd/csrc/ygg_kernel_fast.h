@@ -1175,7 +1175,7 @@ void pipe_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
 
 
 // ----------------------------------------------------------------------------------------------- flow_kernel
-// Scoring with the tokens known, one stream per workgroup, one wavefront per layer, as a software pipeline over ticks.
+// Scoring with the tokens known, one stream per workgroup, as a software pipeline over ticks.
 // Of layer l's work on token t only the update is on the layer's own recurrence (q_l(t) needs q_l(t - 1)): the router
 // rounds and the gather need just the layer below at the same token. So a routed layer runs as stages, one per router
 // round and one for the update, a tick apart: a round's row and threshold loads are issued in one tick and consumed in
@@ -1183,17 +1183,18 @@ void pipe_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
 // the global loads of every stage stay in flight across them. A tick then costs the stages' arithmetic, not their
 // chain of memory round trips (pipe_kernel does each layer's whole chain in one tick).
 //
-// Waves: the token layer has one; a routed layer two, a descent wave (its router rounds, the layer input) and an update
-// wave (the record, the update, the readout), which share a SIMD's issue slots with other layers' waves and so overlap
-// each other's LDS and arithmetic latencies.
+// Waves: the token layer has one; a routed layer a descent wave (its router rounds, the layer input; SPLIT: two, one
+// per token parity) and an update wave (the record, the update, the readout); SPLIT builds add the logits wave (and
+// at 2 layers the layer-input wave, in score builds the NLL wave). They share the SIMDs' issue slots, placed by a
+// table, and so overlap each other's LDS and arithmetic latencies.
 //
 // Schedule (P router rounds, o_l the tick of layer l's update of token 0): the token layer gathers token t at tick t
-// (two record buffers) and updates it at tick o_0 + t = 2 + t; routed layer l's descent wave runs round j of token t at
-// tick o_(l-1) + 1 + t + j (round 0 from the LDS rows, its thresholds loaded a tick before) and leaves the leaf and the
-// layer input in LDS after round P - 1; its update wave issues the token's record the tick after and updates it the
-// tick after that (two record buffers: a record has a whole tick to arrive), o_l = o_(l-1) + P + 2. States live in a
-// ring per layer (slot (t + 1) mod QR after token t, slot 0 the state before token 0); logits add up layer by layer,
-// in order, in a ring over the tokens in flight.
+// (two record buffers; SB1: one, refilled a tick later) and updates it at tick o_0 + t = 2 + t; routed layer l's
+// descent runs round j of token t at tick o_(l-1) + 1 + t + j (round 0 from the LDS rows, its thresholds loaded a tick
+// before) and leaves the leaf and the layer input in LDS after round P - 1; its update wave issues the token's record
+// the tick after and updates it the tick after that, o_l = o_(l-1) + P + 2. States live in a ring per layer (slot
+// (t + 1) mod QR after token t, slot 0 the state before token 0); logits add up layer by layer, in order (in a ring of
+// logit rows over the tokens in flight, or the logits wave from the layers' readout rows).
 //
 // Every stage runs in every tick, on a clamped token and valid tree nodes while the pipeline fills and drains, and
 // only its stores are conditional: the registers carried from tick to tick are then written once per tick in
