@@ -721,6 +721,35 @@ def test_score_bad_target_nll_wave(hip, model_dir, monkeypatch):
 
 
 @pytest.mark.parametrize("group", [False, True], ids=["tensor", "group"])
+def test_medium_shape_capped_builds(hip, model_dir, monkeypatch, group):
+    """The reference's medium shape on its capped per-stream builds (run and score), which only calls with more streams
+    than the uncapped builds keep resident reach: leaves, states after every token and logits of a run, and the fused
+    score, equal the oracle's."""
+    import torch
+    from oracle import oracle as O
+    monkeypatch.delenv("YGG_KERNEL", raising=False)
+    spec = dataclasses.replace(REFERENCE_SHAPES["medium"], group=group)
+    path = model_dir / f"refshape_medium{'_group' if group else ''}.bin"
+    if not path.exists():
+        synth.write_model(spec, 13, path)
+    model = hip.load(path)
+    g = "true" if group else "false"
+    capped = f"ygg::fast_kernel<128, 16, 32, 5, 0, false, true, {g}>"
+    lo = _smallest_batch(model, 1, capped, 16384)
+    B = lo + 3
+    assert B > model.info.pipe_max_streams and model.kernel_name(B, 4) == capped
+    assert model.kernel_name(B, 4, score=True) == f"ygg::fast_kernel<128, 16, 32, 5, 2, false, true, {g}>"
+    _say(f"medium shape, {'group' if group else 'tensor'}: capped per-stream builds at {B} streams")
+    x = synth.uniform_tokens(spec.vocab, B, 5, 7)
+    ref = Oracle(path).run(x[:, :4], states=True)
+    _compare(_gpu_run(model, x[:, :4]), ref)
+    bits = model.score(x, batch=B)
+    np.testing.assert_allclose(bits, O.nll_bits(ref["logits"], x[:, 1:]), rtol=1e-12, atol=1e-9)
+    torch.cuda.synchronize()
+    model.close()
+
+
+@pytest.mark.parametrize("group", [False, True], ids=["tensor", "group"])
 @pytest.mark.parametrize("name", list(REFERENCE_SHAPES))
 def test_reference_model_shapes(hip, model_dir, kernel_env, name, group):
     """The reference's trained model shapes on every kernel, with tensor or group scales (the export's "auto" picks
