@@ -70,6 +70,7 @@ class Oracle:
         if rc:
             raise OracleError(rc, err.value.decode())
         self._h = h
+        self._free = L.yo_free      # (kept on the instance: at interpreter exit the module's globals may be gone)
         info = np.zeros(12, np.int32)
         L.yo_info(h, _ptr(info))
         (self.n_layers, self.n, self.block, self.vocab, self.depth, self.readout_rank, self.layer_input_rank,
@@ -78,7 +79,7 @@ class Oracle:
 
     def close(self):
         if getattr(self, "_h", None):
-            lib().yo_free(self._h)
+            self._free(self._h)
             self._h = None
 
     __del__ = close

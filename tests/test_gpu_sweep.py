@@ -1,0 +1,82 @@
+"""GPU parity over a seeded random sweep: models of the specialised shapes with random layer counts, router depths,
+vocabularies, router kinds and tensor or group scales, run at random batch sizes (up to 2100 streams, across the
+dispatch's thresholds) and token counts with each kernel forced in turn or picked by the library. Per case: leaves,
+states after every token and logits of a run equal the oracle's, the fused score equals the reference formula on the
+oracle's logits, and greedy generation equals the oracle's argmax loop. Each case prints its parameters first."""
+import os
+import random
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from oracle.oracle import Oracle
+from yggdrasil_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+# (state width, readout rank, layer-input rank): the specialised shapes
+SHAPES = [(64, 8, 16), (96, 8, 16), (128, 8, 16), (128, 16, 32), (256, 32, 64)]
+KERNELS = ["", "fast", "pipe", "flow", "deep", "generic"]      # "": the library's own pick
+
+
+def _cases(seed: int, count: int):
+    rnd = random.Random(seed)
+    for c in range(count):
+        n, R, R2 = rnd.choice(SHAPES)
+        L = rnd.randint(2, 5)
+        D = rnd.randint(9, 10 if n == 256 else (12 if R == 16 else 14))
+        V = rnd.choice([5, 27, 256])
+        group = n != 96 and rnd.random() < 0.3
+        router = rnd.choice(["uniform", "gauss", "skew"])
+        u = rnd.random()
+        B = rnd.randint(1, 40) if u < 0.7 else (rnd.randint(41, 600) if u < 0.9 else rnd.randint(1000, 2100))
+        T = rnd.choice([1, 2, 3, 7, 31, 32, 33, 64]) if B <= 600 else rnd.choice([1, 2, 32, 33])
+        yield c, synth.ModelSpec(n, 16, D, V, L, R, R2, group=group, router=router), B, T, rnd.choice(KERNELS), \
+            rnd.randint(0, 10 ** 6)
+
+
+def _greedy_oracle(path, first: int, n: int) -> list:
+    o = Oracle(path)
+    st, tok, seq = None, first, []
+    for _ in range(n):
+        r = o.run(np.array([[tok]], np.int32), state=st)
+        st = r["state"]
+        tok = int(np.argmax(r["logits"][0, 0]))     # the first maximal class, as the device's greedy sampler
+        seq.append(tok)
+    return seq
+
+
+@pytest.mark.parametrize("seed", [11, 12])
+def test_random_sweep(model_dir, monkeypatch, seed):
+    import torch
+    from yggdrasil_amd.inference import Yggdrasil
+    failures = []
+    for c, spec, B, T, kernel, mseed in _cases(seed, 40):
+        if kernel:
+            monkeypatch.setenv("YGG_KERNEL", kernel)
+        else:
+            monkeypatch.delenv("YGG_KERNEL", raising=False)
+        monkeypatch.delenv("YGG_DEEP", raising=False)
+        tag = f"seed {seed} case {c}: {spec} B={B} T={T} kernel={kernel or 'auto'}"
+        print(tag, flush=True)
+        path = model_dir / f"sweep{seed}_{c}.bin"
+        synth.write_model(spec, mseed, path)
+        x = synth.uniform_tokens(spec.vocab, B, T + 1, mseed + 1)
+        ref = Oracle(path).run(x[:, :T], states=True)
+        model = Yggdrasil.load(path)
+        r = model.run(x[:, :T], leaves=True, states=True)
+        torch.cuda.synchronize()
+        for key in ("leaves", "states", "logits"):
+            if not np.array_equal(r[key].cpu().numpy(), ref[key]):
+                failures.append(f"{tag}: {key} on {model.kernel_name(B, T)}")
+        bits = model.score(x, batch=B)
+        if not np.allclose(bits, O.nll_bits(ref["logits"], x[:, 1:]), rtol=1e-12, atol=1e-9):
+            failures.append(f"{tag}: score on {model.kernel_name(B, T, score=True)}")
+        if T >= 2:
+            got = list(model.generate(x[:1, :1], T, temperature=0.0)[0, 1:])
+            if got != _greedy_oracle(path, int(x[0, 0]), T):
+                failures.append(f"{tag}: generation on {model.kernel_name(1, T, generate=True)}")
+        model.close()
+        path.unlink()
+    assert not failures, failures
