@@ -410,11 +410,13 @@ struct Tail {
     bool on;
 };
 
-__device__ __forceinline__ Tail make_tail(const YggDevModel &m, int lane) {
+// (r0 = 1, the one-token build's folded tail: the second and third rounds of a three-round plan)
+__device__ __forceinline__ Tail make_tail(const YggDevModel &m, int lane, int r0 = 2) {
     Tail t{0, 0, false};
-    if (m.n_rounds < 3) return t;
-    const int h0 = m.round_h[0], h1 = m.round_h[1], h2 = m.round_h[2], h3 = m.n_rounds > 3 ? m.round_h[3] : 0;
-    const int base2 = (1 << h0) + (1 << (h0 + h1)), base3 = base2 + (1 << (h0 + h1 + h2));
+    if (m.n_rounds < r0 + 1) return t;
+    const int h0 = m.round_h[0], hb = r0 == 2 ? m.round_h[1] : 0;       // the levels before the tail: h0 + hb
+    const int h2 = m.round_h[r0], h3 = m.n_rounds > r0 + 1 ? m.round_h[r0 + 1] : 0;
+    const int base2 = (1 << h0) + (r0 == 2 ? 1 << (h0 + hb) : 0), base3 = base2 + (1 << (h0 + hb + h2));
     const int nn2 = (1 << h2) - 1, nn3 = (1 << h3) - 1;
     if (lane < nn2) {
         t = Tail{base2 + lane, h2, true};
@@ -423,6 +425,13 @@ __device__ __forceinline__ Tail make_tail(const YggDevModel &m, int lane) {
         t = Tail{base3 + (c << h3) + (q - c * nn3), h2 + h3, true};
     }
     return t;
+}
+
+// The one-token build (R1G) folds the second round into the tail as well when the plan has three rounds whose last
+// two take at most 6 levels (the reference's trained shapes: D = 10, rounds 4, 3, 3): one dependent global round per
+// routed layer instead of two.
+__device__ __forceinline__ bool tail_fold(const YggDevModel &m) {
+    return m.n_rounds == 3 && m.round_h[1] + m.round_h[2] <= 6;
 }
 
 // The deep descent -> leaf index. W0/th0 as in descend; W1 the layer's LDS second-round rows (R1G: the layer's rows of
@@ -451,36 +460,40 @@ __device__ __forceinline__ int descend_deep(const YggDevModel &m, const YggDevLa
         const int loc = walk_round(lane_mask(right && qk == 0 && qj < nn1), h0);
         ix = (1 << h0) + (loc - nn1);
     }
-    {
-        const int h = m.round_h[1], nn = (1 << h) - 1;
-        const int sl = ((ix - (1 << h0)) << h) + qj;          // slot within the second round's slots
-        uint32_t wv[F::QW];
-        if (qj < nn) {
-            if constexpr (R1G) quad_share<N>(wv, W1 + (size_t)sl * N, qk);
-            else quad_share_r2<N>(wv, W1 + sl * N, qk, sl);
-        }
-        // slot sl's threshold is component sl & 3 of lane sl >> 2's th2 (sl < 256)
-        const int src = (sl >> 2) & 63;
-        const float a = __shfl(th2.x, src), b = __shfl(th2.y, src), c = __shfl(th2.z, src), d = __shfl(th2.w, src);
-        const int k = sl & 3;
-        const float th = k == 0 ? a : (k == 1 ? b : (k == 2 ? c : d));
-        int dot = 0;
-        if (qj < nn) {
+    const bool fold = R1G && tail_fold(m);
+    if (!fold) {
+        {
+            const int h = m.round_h[1], nn = (1 << h) - 1;
+            const int sl = ((ix - (1 << h0)) << h) + qj;          // slot within the second round's slots
+            uint32_t wv[F::QW];
+            if (qj < nn) {
+                if constexpr (R1G) quad_share<N>(wv, W1 + (size_t)sl * N, qk);
+                else quad_share_r2<N>(wv, W1 + sl * N, qk, sl);
+            }
+            // slot sl's threshold is component sl & 3 of lane sl >> 2's th2 (sl < 256)
+            const int src = (sl >> 2) & 63;
+            const float a = __shfl(th2.x, src), b = __shfl(th2.y, src), c = __shfl(th2.z, src), d = __shfl(th2.w, src);
+            const int k = sl & 3;
+            const float th = k == 0 ? a : (k == 1 ? b : (k == 2 ? c : d));
+            int dot = 0;
+            if (qj < nn) {
 #pragma unroll
-            for (int i = 0; i < F::QW; i++) dot = dot4(wv[i], qbw[i], dot);
+                for (int i = 0; i < F::QW; i++) dot = dot4(wv[i], qbw[i], dot);
+            }
+            dot = sum4(dot);
+            const bool right = (float)dot * rho > th;
+            const int loc = walk_round(lane_mask(right && qk == 0 && qj < nn), h);
+            ix = (ix << h) + (loc - nn);
         }
-        dot = sum4(dot);
-        const bool right = (float)dot * rho > th;
-        const int loc = walk_round(lane_mask(right && qk == 0 && qj < nn), h);
-        ix = (ix << h) + (loc - nn);
-    }
-    if (m.n_rounds == 2) {
-        hook();
-        return ix - m.E;
+        if (m.n_rounds == 2) {
+            hook();
+            return ix - m.E;
+        }
     }
     {
+        const int r0 = fold ? 1 : 2, d0 = fold ? h0 : h0 + m.round_h[1];   // the tail's first round, levels before it
         const float *thr = y.thr + (size_t)x * y.thr_stride;
-        const int slot = tl.ta + ((ix - (1 << (h0 + m.round_h[1]))) << tl.tsh);
+        const int slot = tl.ta + ((ix - (1 << d0)) << tl.tsh);
         uint32_t rw[N / 4];
         float th = 0.0f;
         if (tl.on) {
@@ -494,11 +507,11 @@ __device__ __forceinline__ int descend_deep(const YggDevModel &m, const YggDevLa
 #pragma unroll
         for (int i = 0; i < N / 4; i++) dot = dot4(rw[i], qf[i], dot);
         const unsigned long long mask = lane_mask(tl.on && (float)dot * rho > th);
-        const int h2 = m.round_h[2], nn2 = (1 << h2) - 1;
+        const int h2 = m.round_h[r0], nn2 = (1 << h2) - 1;
         const int c = walk_bits(mask, h2) - nn2;
         ix = (ix << h2) + c;
-        if (m.n_rounds == 4) {
-            const int h3 = m.round_h[3], nn3 = (1 << h3) - 1;
+        if (m.n_rounds == r0 + 2) {
+            const int h3 = m.round_h[r0 + 1], nn3 = (1 << h3) - 1;
             ix = (ix << h3) + (walk_bits(mask >> (nn2 + c * nn3), h3) - nn3);
         }
     }
@@ -834,7 +847,7 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
     if (!live) return;
 
     Tail tl{};
-    if constexpr (DD) tl = make_tail(m, lane);
+    if constexpr (DD) tl = make_tail(m, lane, (!DEEP && tail_fold(m)) ? 1 : 2);
     const int n2 = m.n_rounds > 1 ? 1 << (m.round_h[0] + m.round_h[1]) : 0;   // second-round slots
     int8_t *qs = qsw[wv];
     int8_t *zls = zlw[wv];
