@@ -493,20 +493,20 @@ def test_deep_descent_plans(hip, model_dir, c12, monkeypatch, which, plan):
 @pytest.mark.parametrize("which,plan", [
     ("c4small", None), ("c4small", "4,4,2"), ("c4small", "2,4,2,2"), ("c4small", "4,2,3,1"), ("c4small", "4,4,1,1"),
     ("c4small", "1,3,3,3"), ("c12", None), ("c12", "2,2,3,3"), ("group", None), ("ref_small", None),
-    ("ref_medium", None), ("c3", None)])
+    ("ref_medium", None), ("ref_large", None), ("c3", None)])
 def test_one_token_build(hip, model_dir, c12, c3, monkeypatch, which, plan):
     """Calls of one token (ygg_step, and ygg_run with T = 1) of up to 4 streams per CU take the one-token build (the
-    deep descent with its second round read from global memory) wherever the deep descent takes the plan and the
-    shape is not the largest: 12 streams stepped 6 tokens with the state carried, leaves, states and logits equal
-    the oracle's."""
+    deep descent with its second round read from global memory, or folded into the tail for three-round plans)
+    wherever the deep descent takes the plan: 12 streams stepped 6 tokens with the state carried, leaves, states and
+    logits equal the oracle's."""
     import torch
     if which in ("c4small", "group"):
         path = model_dir / ("c4small_gauss.bin" if which == "c4small" else "c4small_group.bin")
         if not path.exists():
             synth.write_model(synth.ModelSpec(128, 16, 10, 256, 4, router="gauss", group=which == "group"), 11, path)
     elif which.startswith("ref_"):
-        # (the reference's small and medium trained shapes: n, readout rank, layer-input rank)
-        n, R, R2 = {"ref_small": (64, 8, 16), "ref_medium": (128, 16, 32)}[which]
+        # (the reference's trained shapes: n, readout rank, layer-input rank)
+        n, R, R2 = {"ref_small": (64, 8, 16), "ref_medium": (128, 16, 32), "ref_large": (256, 32, 64)}[which]
         path = model_dir / f"one_{which}.bin"
         if not path.exists():
             synth.write_model(synth.ModelSpec(n, 16, 10, 256, 3, readout_rank=R, layer_input_rank=R2, router="gauss"),

@@ -86,8 +86,8 @@ template <int N, int R, int R2, int L, bool GROUP> Kernel deep_k() {
         return Kernel();
 }
 
-// fast_kernel's one-token build (kModeOne: the deep descent with the second round from global memory, 4 streams per
-// workgroup); not for the largest shape, whose tail-round registers beside its record would spill
+// fast_kernel's one-token build (kModeOne: the deep descent with the second round from global memory or folded into
+// the tail, 4 streams per workgroup; at the largest shape 324 VGPRs, one wavefront per SIMD as its run build)
 template <int N, int R, int R2, int L, bool GROUP>
 hipError_t launch_one(const YggDevModel &m, const int32_t *tokens, int B, int T, int8_t *state, const YggIO &io,
                       hipStream_t stream) {
@@ -99,7 +99,7 @@ hipError_t launch_one(const YggDevModel &m, const int32_t *tokens, int B, int T,
 }
 
 template <int N, int R, int R2, int L, bool GROUP> Kernel one_k() {
-    if constexpr (L >= 2 && kHasCap<N, R, R2> && (!GROUP || kGroupOk<N>))
+    if constexpr (L >= 2 && (!GROUP || kGroupOk<N>))
         return make_kernel(launch_one<N, R, R2, L, GROUP>, "ygg::fast_kernel<%d, %d, %d, %d, 3, false, false, %s>", N,
                            R, R2, L, GROUP ? "true" : "false");
     else
