@@ -120,6 +120,55 @@ def test_generate_sampled_replays_through_oracle(gmodel, kernel_env, temperature
     model.close()
 
 
+@pytest.mark.parametrize("which", ["medium", "large", "c4shape_5layers"])
+def test_generate_without_deep_build(model_dir, monkeypatch, which):
+    """Models whose deep build does not fit a workgroup's LDS (the reference's medium and large shapes at 5 layers,
+    configuration 4's shape at 5 layers) generate few streams on the generate build with the one-token build's
+    descent: its second round folded into the tail (three-round plans of at most 6 levels after the first: D = 10),
+    else read from global memory (D = 12: rounds 4, 4, 4). Greedy tokens and the logits they come from equal the
+    oracle's argmax loop; sampled tokens' logits replay through the oracle and each token is the sampler's."""
+    import torch
+    from yggdrasil_amd.inference import Yggdrasil
+    monkeypatch.delenv("YGG_KERNEL", raising=False)
+    monkeypatch.delenv("YGG_DEEP", raising=False)
+    spec = {"medium": synth.ModelSpec(128, 16, 10, 27, 5, 16, 32, router="gauss"),
+            "large": synth.ModelSpec(256, 16, 10, 27, 5, 32, 64, router="gauss"),
+            "c4shape_5layers": synth.ModelSpec(128, 16, 12, 256, 5, router="gauss")}[which]
+    path = model_dir / f"gen_one_{which}.bin"
+    if not path.exists():
+        synth.write_model(spec, 19, path)
+    model = Yggdrasil.load(path)
+    assert model.info.deep_max_streams == 0
+    name = model.kernel_name(6, 40, generate=True)
+    _say(f"generation without a deep build, {which}: {name}")
+    assert name.startswith(f"ygg::fast_kernel<{spec.d_state}, ") and ", 4, false, false, " in name, name
+    assert ", 4, false, false, " not in model.kernel_name(1 << 20, 40, generate=True)
+    assert ", 4, false, false, " not in model.kernel_name(6, 7, generate=True)
+    prompt = synth.zipf_bytes(6, 9, 21) % spec.vocab
+    n = 40
+    out, lg = model.generate(prompt, n, temperature=0, return_logits=True)
+    torch.cuda.synchronize()
+    orc = O.Oracle(path)
+    want, want_lg = _oracle_greedy(orc, prompt, n)
+    np.testing.assert_array_equal(out[:, 9:], want)
+    np.testing.assert_array_equal(lg.cpu().numpy(), want_lg)
+    temperature, top_k, seed = 0.8, 5, 3
+    out, lg = model.generate(prompt, n, temperature=temperature, top_k=top_k, seed=seed, return_logits=True)
+    torch.cuda.synchronize()
+    lg = lg.cpu().numpy()
+    np.testing.assert_array_equal(lg, orc.run(out[:, :-1].astype(np.int32))["logits"][:, 8:])
+    close = 0
+    for b in range(out.shape[0]):
+        for t in range(n):
+            c, margin = O.sample(lg[b, t], temperature, top_k, O.sample_uniform(seed, b, t))
+            if margin > 1e-4:
+                assert out[b, 9 + t] == c, (b, t, out[b, 9 + t], c, margin)
+            else:
+                close += 1
+    assert close < 4, close
+    model.close()
+
+
 def test_generate_distribution(gmodel, monkeypatch):
     """16384 streams from one prompt, one draw each: frequencies follow softmax(logits / T) over the top_k."""
     import torch

@@ -427,6 +427,8 @@ struct ygg_model {
     ygg::Kernel deep;                 // deep descent: generate with B <= deep_max_streams
     ygg::Kernel one;                  // the deep descent, second round from global memory: run calls of one token
     int one_max_streams = 0;          // ... with B at most this (one workgroup of 4 streams per CU)
+    ygg::Kernel gen_one;              // the same descent for generation where there is no deep kernel
+    int gen_one_max_streams = 0;
     int deep_max_streams = 0;
     bool deep_all = false;            // YGG_KERNEL=deep: every call
     ygg::Kernel flow;                 // router rounds and updates pipelined over ticks: T > 1, B <= flow_max_streams[mode]
@@ -707,6 +709,10 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     // (its tail round's registers leave 2-3 waves per SIMD: for the latency of few streams, one workgroup per CU)
     if (deep && kmode == "") m->one = ygg::find_one_launcher(n, R, R2f, L, group);
     m->one_max_streams = m->one ? 4 * cus : 0;       // (fast_kernel: 4 streams per workgroup)
+    // generation of few streams where no deep kernel fits (its second-round rows beside the tables exceed a
+    // workgroup's LDS): the one-token build's descent in a generate build
+    if (deep && kmode == "" && !deep_avail) m->gen_one = ygg::find_gen_one_launcher(n, R, R2f, L, group);
+    m->gen_one_max_streams = m->gen_one ? cus : 0;
     m->deep_max_streams = deepk ? (m->deep_all ? INT32_MAX : cus) : 0;
     // flow_kernel for T >= kFlowMinTokens up to flow_max_streams (or always with YGG_KERNEL=flow): measured at 512
     // tokens against the per-stream kernel, the builds with the split descent win up to 8 streams per CU on every
@@ -812,8 +818,9 @@ constexpr int kFlowMinTokens = 32;
 // The kernel of a call of B streams and T tokens in mode (kModeRun, kModeGenerate: ygg_generate, kModeScore: a
 // digest or NLL). YGG_KERNEL=solo: the solo kernel (all wavefronts of a workgroup on one stream) for every call but
 // score calls. Run calls of one token and up to 4 streams per CU: the one-token build (the deep descent, its second
-// round from global memory). Generation: the deep kernel for >= 8 tokens and B <= deep_max_streams, else the
-// per-stream kernel (every token needs all layers of the one before it, so never a layer-pipelined one). Otherwise:
+// round from global memory). Generation: the deep kernel for >= 8 tokens and B <= deep_max_streams (where there is
+// none, the generate build with the one-token build's descent for B up to the CUs), else the per-stream kernel (every
+// token needs all layers of the one before it, so never a layer-pipelined one). Otherwise:
 // the tick-pipelined
 // kernel for T >= kFlowMinTokens and B <= flow_max_streams, the layer-pipelined kernel for T > 1 when its
 // workgroups fit (for T >= kFlowMinTokens only where there is no tick-pipelined build: more streams than that one
@@ -826,6 +833,7 @@ const ygg::Kernel &pick(const ygg_model *m, int B, int T, int mode) {
     if (m->deep_all) return m->deep;
     if (m->one && mode == kModeRun && T == 1 && B <= m->one_max_streams) return m->one;
     if (gen && m->deep && B <= m->deep_max_streams && T >= 8) return m->deep;
+    if (gen && m->gen_one && B <= m->gen_one_max_streams && T >= 8) return m->gen_one;
     if (!gen && m->flow && (m->flow_all || (T >= kFlowMinTokens && B <= m->flow_max_streams[mode]))) return m->flow;
     if (!gen && m->pipe && (m->pipe_all || (T > 1 && B <= m->pipe_max_streams && !(m->flow && T >= kFlowMinTokens))))
         return (m->pipe_few && B <= m->pipe_few_max_streams[mode]) ? m->pipe_few : m->pipe;

@@ -106,6 +106,35 @@ template <int N, int R, int R2, int L, bool GROUP> Kernel one_k() {
         return Kernel();
 }
 
+// generation with the one-token build's descent (kModeGenOne), for models with no deep build: the second round
+// from global memory or folded into the tail instead of staged in LDS
+template <int N, int R, int R2, int L, bool GROUP>
+hipError_t launch_gen_one(const YggDevModel &m, const int32_t *tokens, int B, int T, int8_t *state, const YggIO &io,
+                          hipStream_t stream) {
+    if (io_mode(io) != kModeGenerate) return hipErrorInvalidValue;     // (the dispatch gives it no other call)
+    // one stream per workgroup of 4 wavefronts (all stage the LDS tables, one runs the stream)
+    const dim3 grid(B), block(64 * kFastWaves);
+    hipLaunchKernelGGL((fast_kernel<N, R, R2, L, kModeGenOne, false, false, GROUP>), grid, block, 0, stream, m,
+                       tokens, B, T, state, io);
+    return hipGetLastError();
+}
+
+template <int N, int R, int R2, int L, bool GROUP> Kernel gen_one_k() {
+    if constexpr (L >= 2 && (!GROUP || kGroupOk<N>) && !kDeepFits<N, R, R2, L, GROUP>)
+        return make_kernel(launch_gen_one<N, R, R2, L, GROUP>, "ygg::fast_kernel<%d, %d, %d, %d, 4, false, false, %s>",
+                           N, R, R2, L, GROUP ? "true" : "false");
+    else
+        return Kernel();
+}
+
+template <int N, int R, int R2, bool GROUP> Kernel gen_one_for(int L) {
+    if (L == 2) return gen_one_k<N, R, R2, 2, GROUP>();
+    if (L == 3) return gen_one_k<N, R, R2, 3, GROUP>();
+    if (L == 4) return gen_one_k<N, R, R2, 4, GROUP>();
+    if (L == 5) return gen_one_k<N, R, R2, 5, GROUP>();
+    return Kernel();
+}
+
 template <int N, int R, int R2, bool GROUP> Kernel one_for(int L) {
     if (L == 2) return one_k<N, R, R2, 2, GROUP>();
     if (L == 3) return one_k<N, R, R2, 3, GROUP>();
@@ -170,10 +199,20 @@ int pipe_blocks_per_cu(int n, int R, int R2, int L, bool cap, bool group, int mo
     return 0;
 }
 
-// fast_kernel's one-token build (2 <= L <= 5, all shapes but the largest)
+// fast_kernel's one-token build (2 <= L <= 5)
 Kernel find_one_launcher(int n, int R, int R2, int L, bool group) {
 #define YGG_D(N_, R_, R2_) \
     if (n == N_ && R == R_ && R2 == R2_) return group ? one_for<N_, R_, R2_, true>(L) : one_for<N_, R_, R2_, false>(L);
+    YGG_SHAPES(YGG_D)
+#undef YGG_D
+    return Kernel();
+}
+
+// fast_kernel's generation build with the one-token build's descent (2 <= L <= 5, where the deep build does not fit)
+Kernel find_gen_one_launcher(int n, int R, int R2, int L, bool group) {
+#define YGG_D(N_, R_, R2_) \
+    if (n == N_ && R == R_ && R2 == R2_) \
+        return group ? gen_one_for<N_, R_, R2_, true>(L) : gen_one_for<N_, R_, R2_, false>(L);
     YGG_SHAPES(YGG_D)
 #undef YGG_D
     return Kernel();
