@@ -705,10 +705,12 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     m->deep = deepk;
     m->deep_all = deepk && kmode == "deep";
     // one-token run calls (ygg_step): the deep descent without staging its second round (three dependent global
-    // loads per routed layer instead of four) where the deep descent is on and no kernel is forced
-    // (its tail round's registers leave 2-3 waves per SIMD: for the latency of few streams, one workgroup per CU)
+    // loads per routed layer instead of four) where the deep descent is on and no kernel is forced, one stream per
+    // workgroup up to the CU count of streams (configuration 4: 10.4-11.5 us per step at 4 to 256 streams, against
+    // 13.6-14.3 with 4 streams per workgroup, whose tail rounds share a CU's memory path; above, the per-stream run
+    // build: 13.2 us at 256 streams, 15.1 at 1024)
     if (deep && kmode == "") m->one = ygg::find_one_launcher(n, R, R2f, L, group);
-    m->one_max_streams = m->one ? 4 * cus : 0;       // (fast_kernel: 4 streams per workgroup)
+    m->one_max_streams = m->one ? cus : 0;
     // generation of few streams where no deep kernel fits (its second-round rows beside the tables exceed a
     // workgroup's LDS): the one-token build's descent in a generate build
     if (deep && kmode == "" && !deep_avail) m->gen_one = ygg::find_gen_one_launcher(n, R, R2f, L, group);
@@ -817,8 +819,8 @@ constexpr int kFlowMinTokens = 32;
 
 // The kernel of a call of B streams and T tokens in mode (kModeRun, kModeGenerate: ygg_generate, kModeScore: a
 // digest or NLL). YGG_KERNEL=solo: the solo kernel (all wavefronts of a workgroup on one stream) for every call but
-// score calls. Run calls of one token and up to 4 streams per CU: the one-token build (the deep descent, its second
-// round from global memory). Generation: the deep kernel for >= 8 tokens and B <= deep_max_streams (where there is
+// score calls. Run calls of one token and up to the CU count of streams: the one-token build (the deep descent, its
+// second round from global memory). Generation: the deep kernel for >= 8 tokens and B <= deep_max_streams (where there is
 // none, the generate build with the one-token build's descent for B up to the CUs), else the per-stream kernel (every
 // token needs all layers of the one before it, so never a layer-pipelined one). Otherwise:
 // the tick-pipelined

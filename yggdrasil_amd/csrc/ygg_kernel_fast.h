@@ -796,8 +796,8 @@ __device__ __forceinline__ void store_logits(float *o, const float (&lg)[4], int
 // MODE: kModeRun (logits, leaves, states), kModeScore (also the digest and the NLL: their constants and lane terms
 // take registers the other modes keep for streams) or kModeGenerate (sample the next input from the logits of every
 // token, io.gen, instead of reading it from tokens); kModeOne: kModeRun with the deep descent for calls of one token
-// (4 streams per workgroup, the second round's rows from global memory: nothing staged beyond the usual tables);
-// kModeGenOne: kModeGenerate with kModeOne's descent and one stream per workgroup, for models with no DEEP build. DEEP: one
+// (one stream per workgroup, the second round's rows from global memory: nothing staged beyond the usual tables);
+// kModeGenOne: kModeGenerate with kModeOne's descent, for models with no DEEP build. DEEP: one
 // stream per workgroup with the deep descent (generation for few streams), else 4 streams per workgroup with
 // descend. CAP (not DEEP): at most 128 VGPRs, 4 wavefronts per SIMD (the most streams resident, some registers
 // spilled), else up to 256 (no spills; for calls whose streams all fit at the lower occupancy).
@@ -814,9 +814,9 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
     double *__restrict__ nll = io.nll;
     using SH = Shape<N, R, R2, BLK>;
     using F = SH;
-    // one stream per workgroup for the generation builds of few streams (DEEP, kModeGenOne): a stream's loads then
+    // one stream per workgroup for the builds of few streams (DEEP, kModeOne, kModeGenOne): a stream's loads then
     // have a CU's memory path to themselves
-    constexpr int W = (DEEP || MODE == kModeGenOne) ? 1 : kFastWaves, LR = L > 1 ? L - 1 : 1;
+    constexpr int W = (DEEP || MODE == kModeOne || MODE == kModeGenOne) ? 1 : kFastWaves, LR = L > 1 ? L - 1 : 1;
     constexpr bool GEN = MODE == kModeGenerate || MODE == kModeGenOne, SCORE = MODE == kModeScore;
     constexpr bool DD = DEEP || MODE == kModeOne || MODE == kModeGenOne;   // the deep descent (DEEP: second round in LDS)
     __shared__ __attribute__((aligned(16))) SharedTables<SH, L> S;
@@ -836,7 +836,8 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
     // The stream's first token and its state are read before the LDS tables are staged, so that their loads overlap
     // (a launch of one token would otherwise wait for them one after the other).
     const int32_t *tok = tokens + (size_t)s * (GEN ? 1 : T);
-    if constexpr (W > 1) touch_args<L>(m);     // (measured: the DEEP kernel generated 15% slower with it)
+    // (measured: the generation kernels run slower with it, 15% with DEEP; one-token launches faster)
+    if constexpr (!DEEP && MODE != kModeGenOne) touch_args<L>(m);
     int x_next = (live && T > 0) ? __builtin_amdgcn_readfirstlane(tok[0]) : 0;
     int8_t *st = state + (size_t)s * L * N;
     constexpr int SB = (L * N + 63) / 64;     // state bytes per lane

@@ -87,12 +87,13 @@ template <int N, int R, int R2, int L, bool GROUP> Kernel deep_k() {
 }
 
 // fast_kernel's one-token build (kModeOne: the deep descent with the second round from global memory or folded into
-// the tail, 4 streams per workgroup; at the largest shape 324 VGPRs, one wavefront per SIMD as its run build)
+// the tail, one stream per workgroup; at the largest shape 324 VGPRs, one wavefront per SIMD as its run build)
 template <int N, int R, int R2, int L, bool GROUP>
 hipError_t launch_one(const YggDevModel &m, const int32_t *tokens, int B, int T, int8_t *state, const YggIO &io,
                       hipStream_t stream) {
     if (io_mode(io) != kModeRun || T != 1) return hipErrorInvalidValue;     // (the dispatch gives it no other call)
-    const dim3 grid((B + kFastWaves - 1) / kFastWaves), block(64 * kFastWaves);
+    // one stream per workgroup of 4 wavefronts (all stage the LDS tables, one runs the stream)
+    const dim3 grid(B), block(64 * kFastWaves);
     hipLaunchKernelGGL((fast_kernel<N, R, R2, L, kModeOne, false, false, GROUP>), grid, block, 0, stream, m, tokens, B,
                        T, state, io);
     return hipGetLastError();
