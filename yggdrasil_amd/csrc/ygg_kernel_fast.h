@@ -183,10 +183,11 @@ __device__ __forceinline__ void load_tables(SharedTables<SH, L, WITHV> &S, const
     constexpr int QK = (16 * SH::R + NT - 1) / NT;     // Q chunks (at most 16 R: VP <= 256) per thread and layer
     constexpr int VR = 15 + (WITHV ? R2 : 0);          // first-round rows and V' rows of a routed layer
     constexpr int RK = (VR * RC + NT - 1) / NT;        // their chunks per thread
-    static_assert(L == 1 || NT >= R2 * (L - 1), "one thread per m_v entry");
+    constexpr int R2D = R2 > 0 ? R2 : 1, MVN = L > 1 ? R2 * (L - 1) : 0;   // m_v entries: MVK per thread
+    constexpr int MVK = MVN > 0 ? (MVN + NT - 1) / NT : 1;
     const int qch = m.VP * SH::R / 16, rows = (1 << m.round_h[0]) - 1;
     uint4 qv[L][QK], rv[LR][RK];
-    float mvv = 0.0f;
+    float mvv[MVK];
 #pragma unroll
     for (int l = 0; l < L; l++)
 #pragma unroll
@@ -209,8 +210,13 @@ __device__ __forceinline__ void load_tables(SharedTables<SH, L, WITHV> &S, const
         }
     }
 #pragma unroll
-    for (int l = 1; l < L; l++)
-        if (R2 > 0 && tid / (R2 > 0 ? R2 : 1) == l - 1) mvv = m.layers[l].mv[tid % (R2 > 0 ? R2 : 1)];
+    for (int k = 0; k < MVK; k++) {
+        const int c = tid + k * NT;
+        mvv[k] = 0.0f;
+#pragma unroll
+        for (int l = 1; l < L; l++)
+            if (c < MVN && c / R2D == l - 1) mvv[k] = m.layers[l].mv[c % R2D];
+    }
 #pragma unroll
     for (int l = 0; l < L; l++)
 #pragma unroll
@@ -228,7 +234,9 @@ __device__ __forceinline__ void load_tables(SharedTables<SH, L, WITHV> &S, const
             else if (WITHV && c < VR * RC)
                 ((uint4 *)S.V[l - 1])[((c - 15 * RC) / RC) * SC + (c - 15 * RC) % RC] = rv[l - 1][k];
         }
-    if (L > 1 && R2 > 0 && tid < R2 * (L - 1)) S.mv[tid / (R2 > 0 ? R2 : 1)][tid % (R2 > 0 ? R2 : 1)] = mvv;
+#pragma unroll
+    for (int k = 0; k < MVK; k++)
+        if (tid + k * NT < MVN) S.mv[(tid + k * NT) / R2D][(tid + k * NT) % R2D] = mvv[k];
 }
 
 // Touch every 64-byte line of the kernel argument (the model description, read by scalar loads) at entry: the
@@ -827,7 +835,7 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
     __shared__ __attribute__((aligned(16))) int8_t zqw[W][SH::ZQ];
 
     // the wavefront index, stream, tokens and leaves are uniform over a wavefront: kept in scalar registers. With one
-    // stream per workgroup (W = 1) all 4 wavefronts stage the LDS tables and wavefronts 1-3 then leave.
+    // stream per workgroup (W = 1) wavefronts 1-3 stage the LDS tables and then leave.
     const int tid = threadIdx.x, wv = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int s = blockIdx.x * W + wv;
     const int V = m.V, VP = m.VP;
@@ -844,10 +852,23 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
     int sb[SB];
 #pragma unroll
     for (int k = 0; k < SB; k++) sb[k] = (live && lane + 64 * k < L * N) ? st[lane + 64 * k] : 0;
-    load_tables<SH, L, 64 * kFastWaves>(S, m, tid);
-    if constexpr (GROUP) load_group_tables<SH, L, 64 * kFastWaves>(GT, m, tid);
-    if constexpr (DEEP) load_round2<N, L, 64 * kFastWaves>(W1s, m, tid);
-    __syncthreads();
+    if constexpr (W == 1) {
+        // one stream per workgroup: wavefronts 1-3 stage the LDS tables while the stream's wavefront starts its first
+        // token (its own load, then the token layer's record); that one waits for them at a workgroup barrier just
+        // before it first reads them, ahead of the first token's first update. Every wavefront meets one barrier (or
+        // ends: a wavefront that has ended no longer holds a barrier)
+        if (wv > 0) {
+            load_tables<SH, L, 64 * (kFastWaves - 1)>(S, m, tid - 64);
+            if constexpr (GROUP) load_group_tables<SH, L, 64 * (kFastWaves - 1)>(GT, m, tid - 64);
+            if constexpr (DEEP) load_round2<N, L, 64 * (kFastWaves - 1)>(W1s, m, tid - 64);
+            __syncthreads();
+            return;
+        }
+    } else {
+        load_tables<SH, L, 64 * kFastWaves>(S, m, tid);
+        if constexpr (GROUP) load_group_tables<SH, L, 64 * kFastWaves>(GT, m, tid);
+        __syncthreads();
+    }
     if (!live) return;
 
     Tail tl{};
@@ -955,6 +976,8 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
             }
             Gather<SH, FACT> G;
             gather<SH, GROUP, true, FACT>(G, y, r, x, l > 0, lane, K4);
+            if constexpr (W == 1)
+                if (t == 0 && l == 0) __syncthreads();      // the LDS tables staged (see above)
             if (l > 0) layer_input<SH>(zls, S.V[l - 1], S.mv[l - 1], qbw, rho, lane);
             wave_sync();
             int qn[F::C];

@@ -21,7 +21,7 @@ constexpr bool kDeepFits = kTablesBytes<Shape<N, R, R2>, L> + sizeof(GroupTables
 template <int N, int R, int R2, int L, bool GROUP>
 hipError_t launch_deep(const YggDevModel &m, const int32_t *tokens, int B, int T, int8_t *state, const YggIO &io,
                        hipStream_t stream) {
-    // one stream per workgroup of 4 wavefronts (all stage the LDS tables, one runs the stream)
+    // one stream per workgroup of 4 wavefronts (three stage the LDS tables, one runs the stream)
     const dim3 grid(B), block(64 * kFastWaves);
     switch (io_mode(io)) {
     case kModeGenerate:
@@ -92,7 +92,7 @@ template <int N, int R, int R2, int L, bool GROUP>
 hipError_t launch_one(const YggDevModel &m, const int32_t *tokens, int B, int T, int8_t *state, const YggIO &io,
                       hipStream_t stream) {
     if (io_mode(io) != kModeRun || T != 1) return hipErrorInvalidValue;     // (the dispatch gives it no other call)
-    // one stream per workgroup of 4 wavefronts (all stage the LDS tables, one runs the stream)
+    // one stream per workgroup of 4 wavefronts (three stage the LDS tables, one runs the stream)
     const dim3 grid(B), block(64 * kFastWaves);
     hipLaunchKernelGGL((fast_kernel<N, R, R2, L, kModeOne, false, false, GROUP>), grid, block, 0, stream, m, tokens, B,
                        T, state, io);
@@ -113,7 +113,7 @@ template <int N, int R, int R2, int L, bool GROUP>
 hipError_t launch_gen_one(const YggDevModel &m, const int32_t *tokens, int B, int T, int8_t *state, const YggIO &io,
                           hipStream_t stream) {
     if (io_mode(io) != kModeGenerate) return hipErrorInvalidValue;     // (the dispatch gives it no other call)
-    // one stream per workgroup of 4 wavefronts (all stage the LDS tables, one runs the stream)
+    // one stream per workgroup of 4 wavefronts (three stage the LDS tables, one runs the stream)
     const dim3 grid(B), block(64 * kFastWaves);
     hipLaunchKernelGGL((fast_kernel<N, R, R2, L, kModeGenOne, false, false, GROUP>), grid, block, 0, stream, m,
                        tokens, B, T, state, io);
