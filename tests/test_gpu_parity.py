@@ -495,7 +495,7 @@ def test_deep_descent_plans(hip, model_dir, c12, monkeypatch, which, plan):
     ("c4small", "1,3,3,3"), ("c12", None), ("c12", "2,2,3,3"), ("group", None), ("ref_small", None),
     ("ref_medium", None), ("ref_large", None), ("c3", None)])
 def test_one_token_build(hip, model_dir, c12, c3, monkeypatch, which, plan):
-    """Calls of one token (ygg_step, and ygg_run with T = 1) of up to the CU count of streams take the one-token build
+    """Calls of one token (ygg_step, and ygg_run with T = 1) whose streams are all resident take the one-token build
     (the deep descent with its second round read from global memory, or folded into the tail for three-round plans;
     one stream per workgroup) wherever the deep descent takes the plan: 12 streams stepped 6 tokens with the state
     carried, leaves, states and logits equal the oracle's."""
@@ -591,11 +591,12 @@ def test_default_dispatch(hip, model_dir, monkeypatch):
     assert model.kernel_name(1, 31) == "ygg::pipe_kernel<128, 8, 16, 4, 0, false, false>"
     assert model.kernel_name(info.flow_max_streams + 1, 64) in (fast.format(0, "false"), fast.format(0, "true"))
     assert info.solo_max_streams == 0 and info.deep_max_streams > 0     # the solo kernel only when forced
-    # one-token run calls of up to the CU count of streams: the one-token build (the deep descent, no staged second
-    # round, one stream per workgroup)
-    assert model.kernel_name(1, 1) == "ygg::fast_kernel<128, 8, 16, 4, 3, false, false, false>"
-    assert model.kernel_name(info.deep_max_streams, 1) == "ygg::fast_kernel<128, 8, 16, 4, 3, false, false, false>"
-    assert model.kernel_name(info.deep_max_streams + 1, 1) == fast.format(0, "false")
+    # one-token run calls whose streams are all resident on the one-token build (the deep descent, no staged second
+    # round, one stream per workgroup): that build; more streams: the per-stream run build
+    one = "ygg::fast_kernel<128, 8, 16, 4, 3, false, false, false>"
+    assert model.kernel_name(1, 1) == one and model.kernel_name(info.deep_max_streams, 1) == one
+    lo = _smallest_batch(model, 1, fast.format(0, "false"), 8 * info.deep_max_streams)
+    assert (lo - 1) % info.deep_max_streams == 0 and model.kernel_name(lo - 1, 1) == one
     assert model.kernel_name(1, 1, score=True) == fast.format(2, "false")
     assert model.kernel_name(max(info.pipe_max_streams, info.flow_max_streams) + 1, 64) == fast.format(0, "false")
     assert model.kernel_name(info.pipe_max_streams + 1, 16) == fast.format(0, "false")

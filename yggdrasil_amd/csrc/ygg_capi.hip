@@ -426,7 +426,7 @@ struct ygg_model {
     bool pipe_all = false;            // YGG_KERNEL=pipe: every call
     ygg::Kernel deep;                 // deep descent: generate with B <= deep_max_streams
     ygg::Kernel one;                  // the deep descent, second round from global memory: run calls of one token
-    int one_max_streams = 0;          // ... with B at most this (one workgroup of 4 streams per CU)
+    int one_max_streams = 0;          // ... with B at most this (its workgroups, one stream each, all resident)
     ygg::Kernel gen_one;              // the same descent for generation where there is no deep kernel
     int gen_one_max_streams = 0;
     int deep_max_streams = 0;
@@ -706,11 +706,11 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     m->deep_all = deepk && kmode == "deep";
     // one-token run calls (ygg_step): the deep descent without staging its second round (three dependent global
     // loads per routed layer instead of four) where the deep descent is on and no kernel is forced, one stream per
-    // workgroup up to the CU count of streams (configuration 4: 10.4-11.5 us per step at 4 to 256 streams, against
-    // 13.6-14.3 with 4 streams per workgroup, whose tail rounds share a CU's memory path; above, the per-stream run
-    // build: 13.2 us at 256 streams, 15.1 at 1024)
+    // workgroup while the workgroups are all resident (configuration 4: 10.4-13.7 us per step at 4 to 768 streams,
+    // against 13.6-14.3 with 4 streams per workgroup, whose tail rounds share a CU's memory path, and 13.3-14.4 on
+    // the per-stream run build from 320 streams; past residency, at 1024, the run build: 15.0 against 17.8)
     if (deep && kmode == "") m->one = ygg::find_one_launcher(n, R, R2f, L, group);
-    m->one_max_streams = m->one ? cus : 0;
+    m->one_max_streams = m->one ? ygg::one_blocks_per_cu(n, R, R2f, L, group) * cus : 0;
     // generation of few streams where no deep kernel fits (its second-round rows beside the tables exceed a
     // workgroup's LDS): the one-token build's descent in a generate build
     if (deep && kmode == "" && !deep_avail) m->gen_one = ygg::find_gen_one_launcher(n, R, R2f, L, group);
@@ -819,8 +819,8 @@ constexpr int kFlowMinTokens = 32;
 
 // The kernel of a call of B streams and T tokens in mode (kModeRun, kModeGenerate: ygg_generate, kModeScore: a
 // digest or NLL). YGG_KERNEL=solo: the solo kernel (all wavefronts of a workgroup on one stream) for every call but
-// score calls. Run calls of one token and up to the CU count of streams: the one-token build (the deep descent, its
-// second round from global memory). Generation: the deep kernel for >= 8 tokens and B <= deep_max_streams (where there is
+// score calls. Run calls of one token with all their streams resident on the one-token build (one stream per
+// workgroup): that build (the deep descent, its second round from global memory). Generation: the deep kernel for >= 8 tokens and B <= deep_max_streams (where there is
 // none, the generate build with the one-token build's descent for B up to the CUs), else the per-stream kernel (every
 // token needs all layers of the one before it, so never a layer-pipelined one). Otherwise:
 // the tick-pipelined

@@ -136,6 +136,26 @@ template <int N, int R, int R2, bool GROUP> Kernel gen_one_for(int L) {
     return Kernel();
 }
 
+// the one-token build's resident workgroups (one stream each) per CU on the current device
+template <int N, int R, int R2, int L, bool GROUP> int one_blocks() {
+    if constexpr (L >= 2 && (!GROUP || kGroupOk<N>)) {
+        int nb = 0;
+        const void *f = reinterpret_cast<const void *>(&fast_kernel<N, R, R2, L, kModeOne, false, false, GROUP>);
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, f, 64 * kFastWaves, 0) != hipSuccess) return 0;
+        return nb;
+    } else {
+        return 0;
+    }
+}
+
+template <int N, int R, int R2, bool GROUP> int one_occ(int L) {
+    if (L == 2) return one_blocks<N, R, R2, 2, GROUP>();
+    if (L == 3) return one_blocks<N, R, R2, 3, GROUP>();
+    if (L == 4) return one_blocks<N, R, R2, 4, GROUP>();
+    if (L == 5) return one_blocks<N, R, R2, 5, GROUP>();
+    return 0;
+}
+
 template <int N, int R, int R2, bool GROUP> Kernel one_for(int L) {
     if (L == 2) return one_k<N, R, R2, 2, GROUP>();
     if (L == 3) return one_k<N, R, R2, 3, GROUP>();
@@ -207,6 +227,14 @@ Kernel find_one_launcher(int n, int R, int R2, int L, bool group) {
     YGG_SHAPES(YGG_D)
 #undef YGG_D
     return Kernel();
+}
+
+int one_blocks_per_cu(int n, int R, int R2, int L, bool group) {
+#define YGG_D(N_, R_, R2_) \
+    if (n == N_ && R == R_ && R2 == R2_) return group ? one_occ<N_, R_, R2_, true>(L) : one_occ<N_, R_, R2_, false>(L);
+    YGG_SHAPES(YGG_D)
+#undef YGG_D
+    return 0;
 }
 
 // fast_kernel's generation build with the one-token build's descent (2 <= L <= 5, where the deep build does not fit)
