@@ -136,11 +136,12 @@ template <int N, int R, int R2, bool GROUP> Kernel gen_one_for(int L) {
     return Kernel();
 }
 
-// the one-token build's resident workgroups (one stream each) per CU on the current device
-template <int N, int R, int R2, int L, bool GROUP> int one_blocks() {
-    if constexpr (L >= 2 && (!GROUP || kGroupOk<N>)) {
+// the one-token build's (BUILD = kModeOne) or the generation build's (kModeGenOne) resident workgroups (one stream
+// each) per CU on the current device
+template <int N, int R, int R2, int L, bool GROUP, int BUILD> int one_blocks() {
+    if constexpr (L >= 2 && (!GROUP || kGroupOk<N>) && (BUILD == kModeOne || !kDeepFits<N, R, R2, L, GROUP>)) {
         int nb = 0;
-        const void *f = reinterpret_cast<const void *>(&fast_kernel<N, R, R2, L, kModeOne, false, false, GROUP>);
+        const void *f = reinterpret_cast<const void *>(&fast_kernel<N, R, R2, L, BUILD, false, false, GROUP>);
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, f, 64 * kFastWaves, 0) != hipSuccess) return 0;
         return nb;
     } else {
@@ -148,11 +149,11 @@ template <int N, int R, int R2, int L, bool GROUP> int one_blocks() {
     }
 }
 
-template <int N, int R, int R2, bool GROUP> int one_occ(int L) {
-    if (L == 2) return one_blocks<N, R, R2, 2, GROUP>();
-    if (L == 3) return one_blocks<N, R, R2, 3, GROUP>();
-    if (L == 4) return one_blocks<N, R, R2, 4, GROUP>();
-    if (L == 5) return one_blocks<N, R, R2, 5, GROUP>();
+template <int N, int R, int R2, bool GROUP, int BUILD> int one_occ(int L) {
+    if (L == 2) return one_blocks<N, R, R2, 2, GROUP, BUILD>();
+    if (L == 3) return one_blocks<N, R, R2, 3, GROUP, BUILD>();
+    if (L == 4) return one_blocks<N, R, R2, 4, GROUP, BUILD>();
+    if (L == 5) return one_blocks<N, R, R2, 5, GROUP, BUILD>();
     return 0;
 }
 
@@ -229,9 +230,12 @@ Kernel find_one_launcher(int n, int R, int R2, int L, bool group) {
     return Kernel();
 }
 
-int one_blocks_per_cu(int n, int R, int R2, int L, bool group) {
+int one_blocks_per_cu(int n, int R, int R2, int L, bool group, bool gen) {
 #define YGG_D(N_, R_, R2_) \
-    if (n == N_ && R == R_ && R2 == R2_) return group ? one_occ<N_, R_, R2_, true>(L) : one_occ<N_, R_, R2_, false>(L);
+    if (n == N_ && R == R_ && R2 == R2_) { \
+        if (gen) return group ? one_occ<N_, R_, R2_, true, kModeGenOne>(L) : one_occ<N_, R_, R2_, false, kModeGenOne>(L); \
+        return group ? one_occ<N_, R_, R2_, true, kModeOne>(L) : one_occ<N_, R_, R2_, false, kModeOne>(L); \
+    }
     YGG_SHAPES(YGG_D)
 #undef YGG_D
     return 0;

@@ -72,7 +72,8 @@ int fact_blocks_per_cu(int n, int R, int R2, int L, bool cap, bool group, int mo
 // (ygg_kernels_deep.hip)
 Kernel find_deep_launcher(int n, int R, int R2, int L, bool group);
 Kernel find_one_launcher(int n, int R, int R2, int L, bool group);
-int one_blocks_per_cu(int n, int R, int R2, int L, bool group);
+// resident workgroups per CU of the one-token build, or (gen) of the generation build with its descent
+int one_blocks_per_cu(int n, int R, int R2, int L, bool group, bool gen);
 Kernel find_gen_one_launcher(int n, int R, int R2, int L, bool group);
 Kernel find_pipe_launcher(int n, int R, int R2, int L, bool cap, bool group);
 int pipe_blocks_per_cu(int n, int R, int R2, int L, bool cap, bool group, int mode);
