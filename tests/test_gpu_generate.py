@@ -169,6 +169,28 @@ def test_generate_without_deep_build(model_dir, monkeypatch, which):
     model.close()
 
 
+def test_generate_beyond_deep_streams(gmodel, monkeypatch):
+    """More streams than the deep kernel takes (one workgroup per CU) generate on the generation build with the
+    one-token build's descent, one stream per workgroup: greedy tokens and the logits they come from equal the
+    oracle's argmax loop."""
+    import torch
+    from yggdrasil_amd.inference import Yggdrasil
+    monkeypatch.delenv("YGG_KERNEL", raising=False)
+    monkeypatch.delenv("YGG_DEEP", raising=False)
+    model = Yggdrasil.load(gmodel)
+    B, n = model.info.deep_max_streams + 3, 24
+    name = model.kernel_name(B, n, generate=True)
+    _say(f"generation of {B} streams: {name}")
+    assert name == "ygg::fast_kernel<128, 8, 16, 4, 4, false, false, false>", name
+    prompt = synth.zipf_bytes(B, 3, 8)
+    out, lg = model.generate(prompt, n, temperature=0, return_logits=True)
+    torch.cuda.synchronize()
+    want, want_lg = _oracle_greedy(O.Oracle(gmodel), prompt, n)
+    np.testing.assert_array_equal(out[:, 3:], want)
+    np.testing.assert_array_equal(lg.cpu().numpy(), want_lg)
+    model.close()
+
+
 def test_generate_distribution(gmodel, monkeypatch):
     """16384 streams from one prompt, one draw each: frequencies follow softmax(logits / T) over the top_k."""
     import torch

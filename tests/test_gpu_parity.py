@@ -604,7 +604,12 @@ def test_default_dispatch(hip, model_dir, monkeypatch):
     assert model.kernel_name(16384, 64, score=True) == fast.format(2, "true")
     assert model.kernel_name(1, 100, generate=True) == "ygg::fast_kernel<128, 8, 16, 4, 1, true, false, false>"
     assert model.kernel_name(1, 4, generate=True) == fast.format(1, "false")
-    assert model.kernel_name(info.deep_max_streams + 1, 100, generate=True) == fast.format(1, "false")
+    # more streams than the deep kernel takes: the generation build with the one-token build's descent while its
+    # one-stream workgroups are all resident, then the per-stream generate build
+    gen_one = "ygg::fast_kernel<128, 8, 16, 4, 4, false, false, false>"
+    assert model.kernel_name(info.deep_max_streams + 1, 100, generate=True) == gen_one
+    lo = _smallest_batch(model, 100, fast.format(1, "false"), 8 * info.deep_max_streams, generate=True)
+    assert lo > info.deep_max_streams + 1 and model.kernel_name(lo - 1, 100, generate=True) == gen_one
     assert model.kernel_name(16384, 100, generate=True) == fast.format(1, "true")
     from yggdrasil_amd import _lib
     assert _lib.lib().ygg_kernel_name(model._h, 1, 1, 3, ctypes.create_string_buffer(128), 128) == 5   # bad mode
@@ -616,13 +621,14 @@ def test_default_dispatch(hip, model_dir, monkeypatch):
     model.close()
 
 
-def _smallest_batch(model, T, name, hi, score=False):
+def _smallest_batch(model, T, name, hi, score=False, generate=False):
     """The smallest stream count (<= hi, which runs on the kernel named) whose calls of T tokens run on it."""
     lo = 1
-    assert model.kernel_name(hi, T, score=score) == name, model.kernel_name(hi, T, score=score)
+    assert model.kernel_name(hi, T, score=score, generate=generate) == name, \
+        model.kernel_name(hi, T, score=score, generate=generate)
     while lo < hi:
         mid = (lo + hi) // 2
-        if model.kernel_name(mid, T, score=score) == name:
+        if model.kernel_name(mid, T, score=score, generate=generate) == name:
             hi = mid
         else:
             lo = mid + 1

@@ -427,7 +427,7 @@ struct ygg_model {
     ygg::Kernel deep;                 // deep descent: generate with B <= deep_max_streams
     ygg::Kernel one;                  // the deep descent, second round from global memory: run calls of one token
     int one_max_streams = 0;          // ... with B at most this (its workgroups, one stream each, all resident)
-    ygg::Kernel gen_one;              // the same descent for generation where there is no deep kernel
+    ygg::Kernel gen_one;              // the same descent for generation past the deep kernel (or without one)
     int gen_one_max_streams = 0;
     int deep_max_streams = 0;
     bool deep_all = false;            // YGG_KERNEL=deep: every call
@@ -711,10 +711,11 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     // the per-stream run build from 320 streams; past residency, at 1024, the run build: 15.0 against 17.8)
     if (deep && kmode == "") m->one = ygg::find_one_launcher(n, R, R2f, L, group);
     m->one_max_streams = m->one ? ygg::one_blocks_per_cu(n, R, R2f, L, group, false) * cus : 0;
-    // generation of few streams where no deep kernel fits (its second-round rows beside the tables exceed a
-    // workgroup's LDS): the one-token build's descent in a generate build, one stream per workgroup, while its
-    // workgroups are all resident
-    if (deep && kmode == "" && !deep_avail) m->gen_one = ygg::find_gen_one_launcher(n, R, R2f, L, group);
+    // generation of more streams than the deep kernel takes (one workgroup per CU), or where no deep kernel fits
+    // (its second-round rows beside the tables exceed a workgroup's LDS): the one-token build's descent in a generate
+    // build, one stream per workgroup, while its workgroups are all resident (configuration 4 at 257 / 384 / 512
+    // streams: 7.4 / 8.0 / 8.0 us per token step against 9.0 / 8.8 / 8.8 on the per-stream generate build)
+    if (deep && kmode == "") m->gen_one = ygg::find_gen_one_launcher(n, R, R2f, L, group);
     m->gen_one_max_streams = m->gen_one ? ygg::one_blocks_per_cu(n, R, R2f, L, group, true) * cus : 0;
     m->deep_max_streams = deepk ? (m->deep_all ? INT32_MAX : cus) : 0;
     // flow_kernel for T >= kFlowMinTokens up to flow_max_streams (or always with YGG_KERNEL=flow): measured at 512
@@ -822,8 +823,8 @@ constexpr int kFlowMinTokens = 32;
 // digest or NLL). YGG_KERNEL=solo: the solo kernel (all wavefronts of a workgroup on one stream) for every call but
 // score calls. Run calls of one token with all their streams resident on the one-token build (one stream per
 // workgroup): that build (the deep descent, its second round from global memory). Generation: the deep kernel for
-// >= 8 tokens and B <= deep_max_streams (where there is none, the generate build with the one-token build's descent
-// while its workgroups are all resident), else the per-stream kernel (every token needs all layers of the one before
+// >= 8 tokens and B <= deep_max_streams, then the generate build with the one-token build's descent while its
+// workgroups are all resident, else the per-stream kernel (every token needs all layers of the one before
 // it, so never a layer-pipelined one). Otherwise: the tick-pipelined kernel for T >= kFlowMinTokens and B <= flow_max_streams, the layer-pipelined kernel for T > 1 when its
 // workgroups fit (for T >= kFlowMinTokens only where there is no tick-pipelined build: more streams than that one
 // takes run best on the per-stream kernel), else the per-stream kernel. Of the two builds of a kernel, the uncapped

@@ -107,8 +107,8 @@ template <int N, int R, int R2, int L, bool GROUP> Kernel one_k() {
         return Kernel();
 }
 
-// generation with the one-token build's descent (kModeGenOne), for models with no deep build: the second round
-// from global memory or folded into the tail instead of staged in LDS
+// generation with the one-token build's descent (kModeGenOne), for more streams than the deep build takes and for
+// models with no deep build: the second round from global memory or folded into the tail instead of staged in LDS
 template <int N, int R, int R2, int L, bool GROUP>
 hipError_t launch_gen_one(const YggDevModel &m, const int32_t *tokens, int B, int T, int8_t *state, const YggIO &io,
                           hipStream_t stream) {
@@ -121,7 +121,7 @@ hipError_t launch_gen_one(const YggDevModel &m, const int32_t *tokens, int B, in
 }
 
 template <int N, int R, int R2, int L, bool GROUP> Kernel gen_one_k() {
-    if constexpr (L >= 2 && (!GROUP || kGroupOk<N>) && !kDeepFits<N, R, R2, L, GROUP>)
+    if constexpr (L >= 2 && (!GROUP || kGroupOk<N>))
         return make_kernel(launch_gen_one<N, R, R2, L, GROUP>, "ygg::fast_kernel<%d, %d, %d, %d, 4, false, false, %s>",
                            N, R, R2, L, GROUP ? "true" : "false");
     else
@@ -139,7 +139,7 @@ template <int N, int R, int R2, bool GROUP> Kernel gen_one_for(int L) {
 // the one-token build's (BUILD = kModeOne) or the generation build's (kModeGenOne) resident workgroups (one stream
 // each) per CU on the current device
 template <int N, int R, int R2, int L, bool GROUP, int BUILD> int one_blocks() {
-    if constexpr (L >= 2 && (!GROUP || kGroupOk<N>) && (BUILD == kModeOne || !kDeepFits<N, R, R2, L, GROUP>)) {
+    if constexpr (L >= 2 && (!GROUP || kGroupOk<N>)) {
         int nb = 0;
         const void *f = reinterpret_cast<const void *>(&fast_kernel<N, R, R2, L, BUILD, false, false, GROUP>);
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, f, 64 * kFastWaves, 0) != hipSuccess) return 0;
@@ -241,7 +241,7 @@ int one_blocks_per_cu(int n, int R, int R2, int L, bool group, bool gen) {
     return 0;
 }
 
-// fast_kernel's generation build with the one-token build's descent (2 <= L <= 5, where the deep build does not fit)
+// fast_kernel's generation build with the one-token build's descent (2 <= L <= 5)
 Kernel find_gen_one_launcher(int n, int R, int R2, int L, bool group) {
 #define YGG_D(N_, R_, R2_) \
     if (n == N_ && R == R_ && R2 == R2_) \

@@ -101,8 +101,9 @@ constexpr int kModeScore = 2;       // io.digest or io.nll
 // a build of the per-stream kernel, not a mode argument: kModeRun for calls of one token with the deep descent, its
 // second round's rows read from global memory instead of staged in LDS
 constexpr int kModeOne = 3;
-// a build of the per-stream kernel, not a mode argument: kModeGenerate with the same descent as kModeOne, for few
-// streams of models with no deep build (their second-round rows do not fit LDS beside the tables)
+// a build of the per-stream kernel, not a mode argument: kModeGenerate with the same descent as kModeOne, one stream
+// per workgroup, for more streams than the deep build takes, or for models with no deep build (their second-round rows
+// do not fit LDS beside the tables)
 constexpr int kModeGenOne = 4;
 inline int io_mode(const YggIO &io) {
     return io.gen ? kModeGenerate : ((io.digest || io.nll) ? kModeScore : kModeRun);
