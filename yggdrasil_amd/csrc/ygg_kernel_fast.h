@@ -855,8 +855,8 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
     if constexpr (W == 1) {
         // one stream per workgroup: wavefronts 1-3 stage the LDS tables while the stream's wavefront starts its first
         // token (its own load, then the token layer's record); that one waits for them at a workgroup barrier just
-        // before it first reads them, ahead of the first token's first update. Every wavefront meets one barrier (or
-        // ends: a wavefront that has ended no longer holds a barrier)
+        // before it first reads them, ahead of the first token's first update. Every wavefront meets exactly one
+        // barrier, whatever the number of tokens
         if (wv > 0) {
             load_tables<SH, L, 64 * (kFastWaves - 1)>(S, m, tid - 64);
             if constexpr (GROUP) load_group_tables<SH, L, 64 * (kFastWaves - 1)>(GT, m, tid - 64);
@@ -887,6 +887,7 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
     wave_sync();
     unsigned long long dg = (SCORE && digest) ? digest[s] : 0ull;
     double nacc = 0.0;
+    bool staged = W > 1;      // W = 1: the stream's wavefront has met the barrier that waits for the LDS tables
 
     for (int t = 0; t < T; t++) {
         const int x = x_next;
@@ -977,7 +978,10 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
             Gather<SH, FACT> G;
             gather<SH, GROUP, true, FACT>(G, y, r, x, l > 0, lane, K4);
             if constexpr (W == 1)
-                if (t == 0 && l == 0) __syncthreads();      // the LDS tables staged (see above)
+                if (!staged) {      // the LDS tables staged (see above)
+                    __syncthreads();
+                    staged = true;
+                }
             if (l > 0) layer_input<SH>(zls, S.V[l - 1], S.mv[l - 1], qbw, rho, lane);
             wave_sync();
             int qn[F::C];
@@ -1017,6 +1021,9 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
             for (int i = lane; i < L * N; i += 64) so[i] = qs[i];
         }
     }
+    // (a call that ended before its first update, T = 0 or a first token out of range, still meets the barrier)
+    if constexpr (W == 1)
+        if (!staged) __syncthreads();
     wave_sync();
     for (int i = lane; i < L * N; i += 64) st[i] = qs[i];
     if (SCORE && digest && lane == 0) digest[s] = dg;
