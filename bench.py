@@ -239,51 +239,7 @@ def traffic_summary(fetch_dir, write_dir, copy_fetch_dir, copy_write_dir, copy_b
     return doc
 
 
-def gather_probe(gbytes: float = 3.63, rec_bytes: int = 7168, steps: int = 256) -> dict:
-    """What the memory system delivers for the step's access pattern without its arithmetic (libygg_probe.so):
-    wavefronts each gathering one rec_bytes record at a pseudo-random index of a gbytes buffer per step, the next
-    index depending on the bytes just read (one gather in flight per chain, as a stream of the step has), for a few
-    wavefront and chain counts; and the same with the indices known ahead. GB/s of bytes read, HIP events."""
-    import torch
-    L = ctypes.CDLL(str(ROOT / "yggdrasil_amd" / "libygg_probe.so"))
-    L.ygg_probe_gather.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_int, ctypes.c_int, ctypes.c_int,
-                                   ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
-    nbytes = int(gbytes * 1e9) // rec_bytes * rec_bytes
-    buf = torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(3)
-    stream = torch.cuda.current_stream()
-    sp = ctypes.c_void_p(stream.cuda_stream)
-    rows = []
-    for waves, chains, dep in ((4096, 1, 1), (8192, 1, 1), (4096, 2, 1), (4096, 4, 1), (16384, 1, 1), (4096, 1, 0)):
-        out = torch.empty(waves * 64, dtype=torch.int32, device="cuda")
-        args = (ctypes.c_void_p(buf.data_ptr()), ctypes.c_uint64(nbytes), rec_bytes, waves, chains, steps, dep,
-                ctypes.c_void_p(out.data_ptr()), sp)
-        rc = L.ygg_probe_gather(*args)
-        if rc:
-            raise RuntimeError(f"ygg_probe_gather: hip error {rc}")
-        best = None
-        for _ in range(3):
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record(stream)
-            L.ygg_probe_gather(*args)
-            e1.record(stream)
-            torch.cuda.synchronize()
-            ms = e0.elapsed_time(e1)
-            best = ms if best is None else min(best, ms)
-        gbs = waves * chains * steps * rec_bytes / (best / 1e3) / 1e9
-        rows.append({"waves": waves, "chains": chains, "dependent": bool(dep), "ms": round(best, 4),
-                     "GBps": round(gbs, 1)})
-        log(f"gather probe: {rows[-1]}")
-    del buf
-    return {"buffer_bytes": nbytes, "record_bytes": rec_bytes, "steps": steps, "runs": rows}
-
-
 def main():
-    if len(sys.argv) > 1 and sys.argv[1] == "--probe":
-        # python bench.py --probe [GB]: the gather probe only (no model), over a buffer of GB (default the
-        # configuration-4 model's size)
-        gb = float(sys.argv[2]) if len(sys.argv) > 2 else 3.63
-        print(json.dumps({"gather_probe": gather_probe(gb)}), flush=True)
-        return
     if len(sys.argv) > 1 and sys.argv[1] == "--traffic":
         # python bench.py --traffic FETCH_DIR WRITE_DIR COPY_FETCH_DIR COPY_WRITE_DIR COPY_BYTES BENCH_JSON OUT_JSON
         #                           [RDREQ_DIR]
@@ -574,17 +530,21 @@ def run_batch1(model, w, n_tok: int, L, _lib) -> dict:
                               ptr(out), None, sp))
     st.zero_()
     torch.cuda.synchronize()
+    model.spec_stats(reset=True)
     e0.record(stream)
     _lib.check(L.ygg_generate(model._h, ptr(x1), 1, n_tok, ptr(st), ctypes.c_float(0.0), 0, ctypes.c_uint64(0),
                               ptr(out), None, sp))
     e1.record(stream)
     torch.cuda.synchronize()
     gen_us = e0.elapsed_time(e1) * 1e3 / n_tok
+    # the generation's steps taken from the speculating helpers' slots (all zero without that build)
+    spec = model.spec_stats()
     return {"tokens": n_tok, "us_per_token_persistent_launch": round(run_us, 3),
             "us_per_token_time_mode": round(time_mode_us, 3),
             "us_per_token_graph_run": round(graph_run_us, 3), "graph_run_logits_equal_persistent": graph_run_same,
             "us_per_token_graph_step": round(graph_us, 3), "graph_steps_per_graph": G,
             "graph_logits_equal_persistent": same, "us_per_token_generate_greedy": round(gen_us, 3),
+            "generate_spec": spec,
             "kernels": {"persistent_launch": model.kernel_name(1, n_tok), "graph_step": model.kernel_name(1, 1),
                         "generate": model.kernel_name(1, n_tok, generate=True)}}
 

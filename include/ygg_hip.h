@@ -69,12 +69,9 @@ typedef struct {
                                   YGG_KERNEL at load time). YGG_KERNEL=flow uses it for every call but
                                   ygg_generate */
     int32_t router_rounds;     /* rounds of the router plan (levels read per dependent step of the descent) */
-    int32_t solo_max_streams;  /* calls with B at most this use the kernel with all four wavefronts of a workgroup on
-                                  one stream (the router rows of its first 8 levels in registers, the rest in one
-                                  round): only with YGG_KERNEL=solo at load time, which uses it for every call but
-                                  ygg_score and digest runs (INT32_MAX); 0 otherwise, and for router plans whose first
-                                  two rounds take more than 8 levels or whose later ones more than 6, or
-                                  (L - 1) d_state > 512 */
+    int32_t spec_max_streams;  /* 1: ygg_generate calls of one stream (B = 1) and at least 8 tokens run with helper
+                                  workgroups that compute the next token's first layers for every candidate token
+                                  (d_state <= 128, the deep descent's plans; YGG_SPEC=0 at load time: off); 0: never */
     int32_t grouped;           /* 1: ygg_run_grouped takes the model (d_state 128, readout rank 8, layer-input rank 16,
                                   block 16, table storage, tensor scales, router depth <= 14); 0: it reports
                                   YGG_ERR_LIMITS */
@@ -127,7 +124,7 @@ int ygg_run_grouped(ygg_model *m, const int32_t *d_tokens, int B, int T, int8_t 
    capture, tight serving loops, harnesses that forbid hipMalloc); no counterpart in the reference. Same arguments,
    results and errors as ygg_run_grouped; its workspace is a static device array of YGG_SCRATCH_BYTES on each GPU
    (held until the process ends), so B is limited to what fits: the workspace takes 16 + 32 + 16 + 8 L bytes per
-   stream plus 16 (each of its 7 pieces rounded up to 256 bytes): up to 10 912 streams of a 4-layer model, 10 071 of
+   stream plus 16 (each of its 8 pieces rounded up to 256 bytes): up to 10 912 streams of a 4-layer model, 10 071 of
    a 5-layer one; more give YGG_ERR_LIMITS. Every call on one GPU shares that array: calls that overlap on one GPU (other streams, other
    threads, other models) race and must not be made. Nothing in the array needs clearing between calls. */
 #define YGG_SCRATCH_BYTES (1 << 20)
@@ -156,9 +153,21 @@ int ygg_score(const ygg_model *m, const int32_t *d_tokens, const int32_t *d_targ
    exp((lg[c] - max) / temperature), by inverse CDF over classes in order with a 24-bit uniform that depends only on
    (seed, b, t). d_first (B) int32; d_state (B, L, n) int8 in and out (left after consuming x_0 .. x_{n-1});
    d_out (B, n) int32; d_logits (B, n, vocab) f32 or NULL. A first token outside [0, vocab) sets bit 0 of the error
-   word and leaves that stream's d_out unwritten. */
+   word and leaves that stream's d_out unwritten.
+   One stream (B = 1) and n >= 8 on a model with info.spec_max_streams = 1: the launch also runs helper workgroups
+   that compute step t + 1's first layers for every candidate token while step t finishes, in the model's
+   speculation area; results are the same bit for bit. Calls of this kind that overlap on one model (other
+   streams, other threads) share that area: each one's results stay correct, but they take each other's slots and
+   run slower. */
 int ygg_generate(const ygg_model *m, const int32_t *d_first, int B, int n, int8_t *d_state, float temperature,
                  int top_k, uint64_t seed, int32_t *d_out, float *d_logits, void *stream);
+
+/* Counters of the speculating generation since the last reset (no counterpart in the reference; for tests and
+   benchmarks): out[0] steps whose first layers came from a helper, out[1] steps the stream computed itself (after
+   the first of each call), out[2] helper wavefronts that served a step, out[3] helper wavefronts that started (one
+   per candidate token they cover), out[4] helper wavefronts that stopped waiting (no publication for 200 us). Synchronous: call after the generating stream has finished. reset != 0
+   sets them to zero. All zero for a model without the speculating build. */
+int ygg_spec_stats(const ygg_model *m, uint64_t out[5], int reset);
 
 /* Wait for `stream`, then return and clear the model's error word: bit 0 set when a kernel met a token outside
    [0, vocab), bit 1 when ygg_score met a target outside it, since the last call. */

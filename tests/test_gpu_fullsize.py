@@ -37,12 +37,13 @@ def _model(cfg) -> Path:
     return p
 
 
-def _gpu_sums(model, x: np.ndarray):
-    """One launch over all of x; per-stream digest and logit bit sums."""
+def _gpu_sums(model, x: np.ndarray, digest: bool = True):
+    """One launch over all of x; per-stream digest (None without: the plain run build, the one bench.py times), logit
+    bit sums and final states."""
     import torch
     B, T = x.shape
     xt = torch.as_tensor(x, device=model.device).contiguous()
-    r = model.run(xt, digest=True)
+    r = model.run(xt, digest=digest)
     torch.cuda.synchronize()
     assert model.take_errors() == 0
     lg = r["logits"]
@@ -52,7 +53,7 @@ def _gpu_sums(model, x: np.ndarray):
         bits = lg[b0:b0 + step].view(torch.int32).to(torch.int64) & 0xFFFFFFFF
         sums[b0:b0 + step] = bits.sum(dim=(1, 2))
     torch.cuda.synchronize()
-    out = (r["digest"].cpu().numpy().view(np.uint64), sums.cpu().numpy().astype(np.uint64),
+    out = (r["digest"].cpu().numpy().view(np.uint64) if digest else None, sums.cpu().numpy().astype(np.uint64),
            r["state"].cpu().numpy())
     del r, lg
     torch.cuda.empty_cache()
@@ -67,16 +68,32 @@ def _workload(cfg):
     return synth.CONFIGS[cfg]
 
 
+# The build bench.py times for each configuration's full launch (ygg_run, no digest), as bench.py's roofline.kernel
+# names it; the run with a digest takes the score build of the same kernel.
+TIMED = {2: "ygg::flow_kernel<64, 8, 16, 2, 3, 0, false>", 3: "ygg::flow_kernel<96, 8, 16, 3, 4, 0, false>",
+         4: "ygg::fast_kernel<128, 8, 16, 4, 0, false, false, false>",
+         5: "ygg::fast_kernel<128, 8, 16, 4, 0, false, true, false>"}
+
+
 @pytest.mark.timeout(900)
 @pytest.mark.parametrize("cfg", [2, 3, 5, 4, "4f"])
 def test_full_size_digest(cfg):
+    """Two launches over the full workload: the plain run build (the one bench.py times: logits and final states
+    against the oracle's per-stream logit bit sums and states) and the score build (with the digest of every leaf
+    and state as well)."""
     from yggdrasil_amd.inference import Yggdrasil
     w = _workload(cfg)
     path = _model(cfg)
     x = w.make_tokens()
     B, T = x.shape
     model = Yggdrasil.load(path)
-    _say(f"config {cfg}: {B} x {T}, kernel {model.kernel_name(B, T)}")
+    timed = model.kernel_name(B, T)
+    _say(f"config {cfg}: {B} x {T}, timed kernel {timed}, digest kernel {model.kernel_name(B, T, score=True)}")
+    if cfg in TIMED:
+        assert timed == TIMED[cfg], timed
+    t0 = time.time()
+    _, ls0, st0 = _gpu_sums(model, x, digest=False)
+    _say(f"config {cfg}: timed build done in {time.time() - t0:.1f}s")
     t0 = time.time()
     dg, ls, st = _gpu_sums(model, x)
     model.close()
@@ -84,6 +101,9 @@ def test_full_size_digest(cfg):
     t0 = time.time()
     rdg, rls, rst = O.Oracle(path).run_sums(x)
     _say(f"config {cfg}: oracle done in {time.time() - t0:.1f}s")
+    np.testing.assert_array_equal(st0, rst)
+    bad = np.nonzero(ls0 != rls)[0]
+    assert bad.size == 0, f"timed build: logit sums differ on {bad.size} of {B} streams, first {bad[:8].tolist()}"
     np.testing.assert_array_equal(st, rst)
     bad = np.nonzero(dg != rdg)[0]
     assert bad.size == 0, f"digest differs on {bad.size} of {B} streams, first {bad[:8].tolist()}"
@@ -94,11 +114,10 @@ def test_full_size_digest(cfg):
 @pytest.mark.timeout(600)
 @pytest.mark.parametrize("cfg", [3, 4])
 def test_few_streams_full_model(cfg, monkeypatch):
-    """The few-stream kernels on the full configuration 3 and 4 models (D = 13 and 14: the deep descent and the solo
-    kernel end in one round of 63 nodes): 6 streams x 40 tokens through the kernel the library picks
-    (layer-pipelined) and greedy generation (the deep kernel), then through the deep kernel forced for every call
-    (one launch, launches of 3 tokens, a step loop), then the solo kernel forced (one launch, a step loop, greedy
-    generation). Every leaf, state after every token, logit and generated token equals the oracle's."""
+    """The few-stream kernels on the full configuration 3 and 4 models (D = 13 and 14: the deep descent ends in one
+    round of 63 nodes): 6 streams x 40 tokens through the kernel the library picks (layer-pipelined) and greedy
+    generation (the deep kernel), then through the deep kernel forced for every call (one launch, launches of 3
+    tokens, a step loop). Every leaf, state after every token, logit and generated token equals the oracle's."""
     import torch
     from yggdrasil_amd.inference import Yggdrasil
     w = synth.CONFIGS[cfg]
@@ -113,22 +132,21 @@ def test_few_streams_full_model(cfg, monkeypatch):
             assert np.array_equal(a, b), f"config {cfg} {what}: {k} differs at {np.argwhere(a != b)[:4].tolist()}"
 
     monkeypatch.delenv("YGG_DEEP", raising=False)
-    for k in ("auto", "deep", "solo"):
+    for k in ("auto", "deep"):
         if k == "auto":
             monkeypatch.delenv("YGG_KERNEL", raising=False)
         else:
             monkeypatch.setenv("YGG_KERNEL", k)
         model = Yggdrasil.load(path)
         assert model.info.deep == 1 and model.info.kernel == 1
-        assert (model.info.deep_max_streams > 0) == (k != "solo")
-        assert (model.info.solo_max_streams > 0) == (k == "solo")
+        assert model.info.deep_max_streams > 0
         _say(f"config {cfg}: 6 x 40, kernel {k}, pipe_max {model.info.pipe_max_streams}, "
-             f"deep_max {model.info.deep_max_streams}, solo_max {model.info.solo_max_streams}")
+             f"deep_max {model.info.deep_max_streams}")
         r = model.run(x, leaves=True, states=True)
         torch.cuda.synchronize()
         same({key: v.cpu().numpy() for key, v in r.items()}, f"{k} one launch")
-        if k in ("auto", "solo"):
-            # greedy generation of 12 tokens after a 4-token prompt (deep or solo kernel): the oracle's argmax loop
+        if k == "auto":
+            # greedy generation of 12 tokens after a 4-token prompt (the deep kernel): the oracle's argmax loop
             out = model.generate(x[:, :4], 12, temperature=0)
             r0 = orc.run(x[:, :4])
             lg, st = r0["logits"][:, -1], r0["state"]
@@ -137,14 +155,7 @@ def test_few_streams_full_model(cfg, monkeypatch):
                 assert np.array_equal(out[:, 4 + i], tok), (cfg, i)
                 r1 = orc.run(tok[:, None], state=st)
                 lg, st = r1["logits"][:, 0], r1["state"]
-        if k == "solo":
-            # one-token steps (the solo kernel) with the state carried
-            st = model.init_state(6)
-            for t in range(8):
-                lg, st = model.step(x[:, t], st)
-                assert np.array_equal(lg.cpu().numpy(), ref["logits"][:, t]), (cfg, t)
-                assert np.array_equal(st.cpu().numpy(), ref["states"][:, t]), (cfg, t)
-        elif k == "deep":
+        if k == "deep":
             parts, st = [], None
             for t0 in range(0, 39, 3):
                 rr = model.run(x[:, t0:t0 + 3], state=st, leaves=True, states=True)

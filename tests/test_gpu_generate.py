@@ -20,11 +20,10 @@ def _say(msg):
     print(msg, flush=True)
 
 
-@pytest.fixture(params=["fast", "deep", "solo", "generic"])
+@pytest.fixture(params=["fast", "deep", "generic"])
 def kernel_env(request, monkeypatch):
     """Generation runs on the per-stream kernels only (the layer-pipelined one overlaps tokens): force each (deep: one
-    stream per workgroup with the deep router descent, which the library picks for few streams; solo: one stream per
-    workgroup with all four wavefronts on it)."""
+    stream per workgroup with the deep router descent, which the library picks for few streams)."""
     monkeypatch.setenv("YGG_KERNEL", request.param)
     monkeypatch.delenv("YGG_DEEP", raising=False)
     return request.param
@@ -44,8 +43,7 @@ def _load(path, kernel_env):
     m = Yggdrasil.load(path)
     assert m.info.kernel == (0 if kernel_env == "generic" else 1), m.info.kernel
     assert (m.info.deep_max_streams > 0) == (kernel_env in ("deep", "auto")), m.info.deep_max_streams
-    assert (m.info.solo_max_streams > 0) == (kernel_env == "solo"), m.info.solo_max_streams
-    want = {"solo": "ygg::solo_kernel<", "auto": "ygg::fast_kernel<", "deep": "ygg::fast_kernel<",
+    want = {"auto": "ygg::fast_kernel<", "deep": "ygg::fast_kernel<",
             "fast": "ygg::fast_kernel<", "generic": "ygg::run_kernel<"}[kernel_env]
     assert m.kernel_name(8, 32, generate=True).startswith(want), m.kernel_name(8, 32, generate=True)
     return m

@@ -227,7 +227,8 @@ def test_grouped_graph_replay(model_dir):
 @pytest.mark.timeout(600)
 def test_grouped_full_size_c5():
     """The full configuration-5 workload (8192 streams x 512 tokens, skewed router) in one grouped call: per-stream
-    digest, logit bit sums and final state equal the per-stream kernel's (ygg_run) on the same inputs."""
+    digest, logit bit sums and final state equal the C oracle's and the per-stream kernel's (ygg_run) on the same
+    inputs."""
     import os
     import time
     import torch
@@ -266,4 +267,10 @@ def test_grouped_full_size_c5():
     for name, u, v in zip(("logit sums", "digest", "state"), a, b):
         bad = np.argwhere(u != v)
         assert bad.size == 0, f"{name} differs at {bad[:4].tolist()}"
+    t0 = time.time()
+    rdg, rls, rst = Oracle(path).run_sums(x)
+    _say(f"c5 oracle done in {time.time() - t0:.1f}s")
+    for name, u, v in zip(("logit sums", "digest", "state"), b, (rls, rdg, rst)):
+        bad = np.argwhere(u.astype(np.uint64) != v.astype(np.uint64)) if name != "state" else np.argwhere(u != v)
+        assert bad.size == 0, f"grouped {name} differs from the oracle at {bad[:4].tolist()}"
     model.close()

@@ -40,14 +40,12 @@ def _compare(got, ref, keys=("leaves", "states", "logits")):
                                  f"gpu {a[tuple(bad[0])]} oracle {b[tuple(bad[0])]}")
 
 
-@pytest.fixture(params=["flow", "pipe", "fast", "deep", "solo", "generic"])
+@pytest.fixture(params=["flow", "pipe", "fast", "deep", "generic"])
 def kernel_env(request, monkeypatch):
     """Load models with one kernel forced for every call (YGG_KERNEL): the tick-pipelined one (flow: models of 2 or
     more layers, else the per-stream one), the layer-pipelined one, the specialised per-stream one (4 streams per
     workgroup), its one-stream-per-workgroup form with the deep router descent (deep: models whose router plan allows
-    it, else the per-stream one), the one with all four wavefronts of a workgroup on one stream (solo: models whose
-    plan and shape it takes, for every call but score and digest calls, else the per-stream one), or the general one;
-    all but the last apply only to the specialised shapes."""
+    it, else the per-stream one), or the general one; all but the last apply only to the specialised shapes."""
     monkeypatch.setenv("YGG_KERNEL", request.param)
     monkeypatch.delenv("YGG_DEEP", raising=False)
     return request.param
@@ -123,7 +121,7 @@ def _expect_fast_only(model, kernel_env, spec):
     one); no other family is built for it."""
     info = model.info
     assert info.kernel == (0 if kernel_env == "generic" else 1), info.kernel
-    assert info.pipe_max_streams == info.deep_max_streams == info.flow_max_streams == info.solo_max_streams == 0
+    assert info.pipe_max_streams == info.deep_max_streams == info.flow_max_streams == 0
     assert info.grouped == 0
     family = "fact" if spec.input_rank else "fast"
     want = "ygg::run_kernel<" if kernel_env == "generic" else \
@@ -154,14 +152,6 @@ def flow_built(info) -> bool:
     return info.n_layers > 1 and info.router_rounds in (3, 4)
 
 
-def solo_built(info) -> bool:
-    """Models with solo_kernel builds: 2 to 5 layers, (L - 1) d_state <= 512, a router plan whose first two rounds
-    take at most 8 levels and whose third and fourth at most 6."""
-    plan = default_plan(info.router_depth)
-    return info.n_layers > 1 and (info.n_layers - 1) * info.d_state <= 512 and len(plan) <= 4 and \
-        sum(plan[:2]) <= 8 and sum(plan[2:]) <= 6
-
-
 def _expect_kernel(model, kernel_env):
     """The forced kernel is the one in use (the shapes passed here are all common-shape models). A model with factored
     routed inputs runs every call on fact_kernel (the specialised per-stream kernel for that storage)."""
@@ -169,7 +159,6 @@ def _expect_kernel(model, kernel_env):
     assert info.kernel == (0 if kernel_env == "generic" else 1), info.kernel
     if info.factored and kernel_env != "generic":
         assert info.pipe_max_streams == info.deep_max_streams == info.flow_max_streams == 0
-        assert info.solo_max_streams == 0
         for B, T in ((8, 64), (8, 1), (4096, 64)):
             assert model.kernel_name(B, T).startswith("ygg::fact_kernel<"), model.kernel_name(B, T)
         assert model.kernel_name(8, 64, score=True).startswith("ygg::fact_kernel<")
@@ -185,17 +174,12 @@ def _expect_kernel(model, kernel_env):
     deep = bool(info.deep)
     assert (info.deep_max_streams > 0) == (kernel_env == "deep" and deep), info.deep_max_streams
     assert (info.flow_max_streams > 0) == (kernel_env == "flow" and flow_built(info)), info.flow_max_streams
-    assert (info.solo_max_streams > 0) == (kernel_env == "solo" and solo_built(info)), info.solo_max_streams
     name = model.kernel_name(8, 64)
     want = {"generic": "ygg::run_kernel<", "pipe": "ygg::pipe_kernel<", "fast": "ygg::fast_kernel<",
-            "deep": "ygg::fast_kernel<", "flow": "ygg::flow_kernel<", "solo": "ygg::solo_kernel<"}[kernel_env]
-    if (kernel_env == "flow" and not flow_built(info)) or (kernel_env == "solo" and not solo_built(info)):
+            "deep": "ygg::fast_kernel<", "flow": "ygg::flow_kernel<"}[kernel_env]
+    if kernel_env == "flow" and not flow_built(info):
         want = "ygg::fast_kernel<"
     assert name.startswith(want), name
-    if want == "ygg::solo_kernel<":
-        assert name.endswith(", 0, true>" if info.group else ", 0, false>"), name
-        assert model.kernel_name(8, 64, score=True).startswith("ygg::fast_kernel<")
-        return
     if want == "ygg::flow_kernel<":
         assert name.endswith(", true>" if info.group else ", false>"), name
         return
@@ -590,7 +574,7 @@ def test_default_dispatch(hip, model_dir, monkeypatch):
     assert model.kernel_name(info.flow_max_streams, 32, score=True) == flow.format(2)
     assert model.kernel_name(1, 31) == "ygg::pipe_kernel<128, 8, 16, 4, 0, false, false>"
     assert model.kernel_name(info.flow_max_streams + 1, 64) in (fast.format(0, "false"), fast.format(0, "true"))
-    assert info.solo_max_streams == 0 and info.deep_max_streams > 0     # the solo kernel only when forced
+    assert info.deep_max_streams > 0
     # one-token run calls whose streams are all resident on the one-token build (the deep descent, no staged second
     # round, one stream per workgroup): that build; more streams: the per-stream run build
     one = "ygg::fast_kernel<128, 8, 16, 4, 3, false, false, false>"
@@ -788,76 +772,4 @@ def test_reference_model_shapes(hip, model_dir, kernel_env, name, group):
     dg = model.run(x, logits=False, digest=True)["digest"].cpu().numpy().view(np.uint64)
     np.testing.assert_array_equal(dg, Oracle(path).run(x, logits=False, leaves=False, digest=True)["digest"])
     torch.cuda.synchronize()
-    model.close()
-
-
-@pytest.mark.parametrize("D,n,group", [(3, 128, False), (8, 128, False), (10, 64, True), (12, 128, False),
-                                       (13, 96, False), (14, 128, False), (14, 128, True), (16, 64, False)])
-def test_solo_plans(hip, model_dir, monkeypatch, D, n, group):
-    """The solo kernel (all wavefronts of a workgroup on one stream, forced with YGG_KERNEL=solo) over router plans of 1
-    to 4 rounds (D = 3: one round; 8: two, no last round; 10, 13: a second round of 3 levels; 12: a last round of 4
-    levels; 14: the configuration-4 plan 4, 4, 3, 3; 16: a plan it does not take, so the library keeps the
-    per-stream kernel): one-token
-    steps with the state carried, replayed from a graph, and greedy generation, every leaf, state and logit equal to
-    the oracle's. A small vocabulary keeps the depth-14 tables small."""
-    import torch
-    from yggdrasil_amd import _lib
-    monkeypatch.setenv("YGG_KERNEL", "solo")
-    L = 2 if D == 16 else (3 if group and D == 14 else 4)
-    spec = synth.ModelSpec(n, 16, D, 5, L, router="gauss", group=group)
-    path = model_dir / f"solo_{D}_{n}_{int(group)}.bin"
-    if not path.exists():
-        synth.write_model(spec, 13, path)
-    B, T = 5, 24
-    x = synth.uniform_tokens(5, B, T, 3)
-    ref = Oracle(path).run(x, states=True)
-    model = hip.load(path)
-    built = solo_built(model.info)
-    assert built == (D != 16), (D, model.info.router_rounds)
-    assert model.kernel_name(B, 1).startswith("ygg::solo_kernel<" if built else "ygg::fast_kernel<")
-    _say(f"solo D={D} n={n} group={group}: {model.kernel_name(B, 1)}")
-    # one-token launches, state carried in place, leaves and logits per step
-    L_ = _lib.lib()
-    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-    p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
-    xt = torch.as_tensor(x, device=model.device).t().contiguous()      # (T, B): one contiguous row per step
-    st = model.init_state(B)
-    lg = torch.empty(T, B, model.vocab, device=model.device)
-    lv = torch.empty(T, B, L, dtype=torch.int32, device=model.device)
-    sv = torch.empty(T, B, L, n, dtype=torch.int8, device=model.device)
-    for t in range(T):
-        _lib.check(L_.ygg_run(model._h, p(xt[t]), B, 1, p(st), p(lg[t]), p(lv[t]), p(sv[t]), None, s))
-    torch.cuda.synchronize()
-    got = {"logits": lg.transpose(0, 1).cpu().numpy(), "leaves": lv.transpose(0, 1).cpu().numpy(),
-           "states": sv.transpose(0, 1).cpu().numpy()}
-    _compare(got, ref)
-    np.testing.assert_array_equal(st.cpu().numpy(), ref["state"])
-    # the same steps captured in a graph and replayed twice, eager work and a sync between the replays
-    st.zero_()
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
-        cs = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-        for t in range(T):
-            _lib.check(L_.ygg_step(model._h, p(xt[t]), p(st), p(st), p(lg[t]), None, B, cs))
-    for _ in range(2):
-        st.zero_()
-        lg.zero_()
-        g.replay()
-        _ = torch.randn(1000, device=model.device).sum()
-        torch.cuda.synchronize()
-        np.testing.assert_array_equal(lg.transpose(0, 1).cpu().numpy(), ref["logits"])
-        np.testing.assert_array_equal(st.cpu().numpy(), ref["state"])
-    # greedy generation from a 3-token prompt
-    prompt = x[:, :3]
-    out, glg = model.generate(prompt, 16, temperature=0, return_logits=True)
-    torch.cuda.synchronize()
-    orc = Oracle(path)
-    r = orc.run(prompt)
-    lgt, state = r["logits"][:, -1], r["state"]
-    for i in range(16):
-        np.testing.assert_array_equal(glg[:, i].cpu().numpy(), lgt, err_msg=f"generated step {i}")
-        tok = lgt.argmax(-1).astype(np.int32)
-        np.testing.assert_array_equal(out[:, 3 + i], tok)
-        r = orc.run(tok[:, None], state=state)
-        lgt, state = r["logits"][:, 0], r["state"]
     model.close()

@@ -17,10 +17,10 @@ LIB_PATH = Path(__file__).resolve().parent / "libygg_hip.so"
 SYMBOLS = ("ygg_load", "ygg_load_blob", "ygg_model_info", "ygg_free", "ygg_step", "ygg_run", "ygg_run_grouped",
            "ygg_run_grouped_noalloc", "ygg_softmax", "ygg_score",
            "ygg_generate", "ygg_take_errors", "ygg_float_load", "ygg_float_run", "ygg_float_take_errors",
-           "ygg_float_free", "ygg_kernel_name", "ygg_last_error", "ygg_version")
+           "ygg_float_free", "ygg_kernel_name", "ygg_spec_stats", "ygg_last_error", "ygg_version")
 
 ERRORS = {1: "io", 2: "format", 3: "limits", 4: "nomem", 5: "arg", 6: "token", 7: "device"}
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 
 class FloatLayer(ctypes.Structure):
@@ -41,7 +41,7 @@ class YggInfo(ctypes.Structure):
     _fields_ = [(name, ctypes.c_int32) for name in (
         "n_layers", "d_state", "block_size", "vocab", "vocab_pad", "router_depth", "n_experts", "readout_rank",
         "layer_input_rank", "input_rank", "shift", "factored", "group", "device", "kernel",
-        "pipe_max_streams", "deep", "deep_max_streams", "flow_max_streams", "router_rounds", "solo_max_streams", "grouped")] + [
+        "pipe_max_streams", "deep", "deep_max_streams", "flow_max_streams", "router_rounds", "spec_max_streams", "grouped")] + [
         ("file_array_bytes", ctypes.c_int64), ("device_bytes", ctypes.c_int64),
         ("gather_bytes", ctypes.c_int64 * 8)]
 
@@ -80,6 +80,7 @@ def lib() -> ctypes.CDLL:
     L.ygg_generate.argtypes = [vp, vp, i32, i32, vp, ctypes.c_float, i32, ctypes.c_uint64, vp, vp, vp]
     L.ygg_take_errors.argtypes = [vp, vp, ctypes.POINTER(ctypes.c_uint32)]
     L.ygg_kernel_name.argtypes = [vp, i32, i32, i32, ctypes.c_char_p, ctypes.c_size_t]
+    L.ygg_spec_stats.argtypes = [vp, ctypes.POINTER(ctypes.c_uint64), i32]
     L.ygg_float_load.argtypes = [ctypes.POINTER(FloatDesc), i32, i32, ctypes.POINTER(vp)]
     L.ygg_float_run.argtypes = [vp, vp, i32, i32, vp, vp, vp, vp, vp]
     L.ygg_float_take_errors.argtypes = [vp, vp, ctypes.POINTER(ctypes.c_uint32)]

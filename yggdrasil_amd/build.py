@@ -19,7 +19,6 @@ PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 CSRC = PKG / "csrc"
 LIB = PKG / "libygg_hip.so"
-PROBE_LIB = PKG / "libygg_probe.so"          # measurement probe for bench.py --probe (not part of the C-ABI)
 BUILD = PKG / "_build"
 ORACLE = ROOT / "oracle"
 REFERENCE_CPU = Path("/root/reference/cpu")
@@ -31,7 +30,7 @@ HIPCC_FLAGS = ["--offload-arch=" + ARCH, "-O3", "-std=c++17", "-ffp-contract=off
                "-mcode-object-version=5", "-Wall", "-Wno-unused-result",
                "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 SOURCES = ["ygg_kernels.hip", "ygg_kernels_fast.hip", "ygg_kernels_fast_x.hip", "ygg_kernels_fact.hip",
-           "ygg_kernels_deep.hip", "ygg_kernels_flow.hip", "ygg_kernels_solo.hip", "ygg_kernels_group.hip",
+           "ygg_kernels_deep.hip", "ygg_kernels_flow.hip", "ygg_kernels_group.hip",
            "ygg_softmax.hip", "ygg_capi.hip", "ygg_float.hip"]
 
 
@@ -50,8 +49,7 @@ def _run(cmd, cwd=None):
 
 
 def build_library(verbose: bool = False) -> Path:
-    """Compile every HIP source for gfx950 and link libygg_hip.so, and the measurement probe libygg_probe.so (always
-    rebuilds)."""
+    """Compile every HIP source for gfx950 and link libygg_hip.so (always rebuilds)."""
     BUILD.mkdir(exist_ok=True)
     cc = hipcc()
     objs = []
@@ -65,9 +63,6 @@ def build_library(verbose: bool = False) -> Path:
     tmp = LIB.with_suffix(".so.tmp")
     _run([cc, "--offload-arch=" + ARCH, "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)])
     os.replace(tmp, LIB)
-    tmp = PROBE_LIB.with_suffix(".so.tmp")
-    _run([cc, *HIPCC_FLAGS, "-shared", "-o", str(tmp), str(CSRC / "ygg_probe.hip")])
-    os.replace(tmp, PROBE_LIB)
     if verbose:
         print(f"built {LIB}")
     return LIB

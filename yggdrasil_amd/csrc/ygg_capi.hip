@@ -409,7 +409,26 @@ void relayout_expert(const FileArrays &fa, const FileLayer &fy, const GatherLayo
 }
 
 
+// every unit of a speculation area to zero (a stale tag)
+__global__ void spec_clear_kernel(uint64_t *a, size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) a[i] = 0;
+}
+
 }  // namespace
+
+struct DeviceGuard {
+    int prev = -1;
+    hipError_t set(int dev) {
+        hipError_t e = hipGetDevice(&prev);
+        if (e != hipSuccess) return e;
+        return prev == dev ? hipSuccess : hipSetDevice(dev);
+    }
+    ~DeviceGuard() {
+        int cur = -1;
+        if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+    }
+};
 
 struct ygg_model {
     YggDevModel dev;
@@ -434,9 +453,11 @@ struct ygg_model {
     ygg::Kernel flow;                 // router rounds and updates pipelined over ticks: T > 1, B <= flow_max_streams[mode]
     int flow_max_streams[3] = {0, 0, 0};
     bool flow_all = false;            // YGG_KERNEL=flow: every call but generation
-    ygg::Kernel solo;                 // all wavefronts on one stream: one-token calls and generation, B <= solo_max_streams
-    int solo_max_streams = 0;
-    bool solo_all = false;            // YGG_KERNEL=solo: every call but score and digest calls
+    ygg::Kernel spec;                 // generation of one stream with speculating helpers (B = 1, T >= 8)
+    uint64_t *spec_area = nullptr;    // its speculation area (spec_area_units(V) tagged units)
+    mutable uint32_t spec_next = 1;   // the next call's first epoch (epoch 0 never occurs: a cleared unit is stale)
+    mutable std::mutex spec_mu;
+    int spec_helpers = 0;             // helper workgroups of a call: enough for every candidate token, at most 63
     bool grouped_ok = false;          // the leaf-grouped step takes the model (ygg_run_grouped)
     void *grp_ws = nullptr;           // its workspace, grown to the largest call
     size_t grp_ws_bytes = 0;
@@ -513,7 +534,7 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
                : factored  ? ygg::find_fact_launcher(n, R, R2f, L, true, group)
                            : ygg::find_fast_launcher(n, R, R2f, L, true, group);
     if (fast) launch = fast;
-    // the other specialised families (deep descent, layer and tick pipelines, solo, grouped) at YGG_SHAPES only
+    // the other specialised families (deep descent, layer and tick pipelines, grouped) at YGG_SHAPES only
     const bool family = fast && std_shape;
 
     RoundPlan rplan = round_plan(L > 1 ? fa.D : 0);
@@ -539,17 +560,8 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     const char *denv = getenv("YGG_DEEP");
     const bool deep = family && !factored && L > 1 && !(denv && !strcmp(denv, "0")) && rplan.n >= 2 && rplan.n <= 4 &&
                       rplan.h[0] >= 2 && (rplan.n < 4 || rplan.h[2] + rplan.h[3] <= 6);
-    // the solo kernel: the first two rounds at most 8 levels together (its round A, from registers), the others at
-    // most 6 (one round with a lane per node); round A's rows of every routed layer in a lane's registers
-    const char *senv = getenv("YGG_SOLO");
-    const bool solo_plan = rplan.n >= 1 && rplan.n <= 4 && (rplan.n < 2 || rplan.h[0] + rplan.h[1] <= 8) &&
-                           (rplan.n < 4 || rplan.h[2] + rplan.h[3] <= 6);
-    ygg::Kernel solok;
-    if (family && !factored && L > 1 && solo_plan && (L - 1) * n <= 512 && !(senv && !strcmp(senv, "0")) &&
-        kmode == "solo")
-        solok = ygg::find_solo_launcher(n, R, R2f, L, group);
     ygg::Kernel pipe, pipe_few, deepk, flowk;
-    if (family && !factored && kmode != "fast" && kmode != "deep" && kmode != "flow" && kmode != "solo") {
+    if (family && !factored && kmode != "fast" && kmode != "deep" && kmode != "flow") {
         pipe = ygg::find_pipe_launcher(n, R, R2f, L, true, group);
         pipe_few = ygg::find_pipe_launcher(n, R, R2f, L, false, group);
     }
@@ -559,7 +571,7 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
         flowk = ygg::find_flow_launcher(n, R, R2f, L, rplan.n, group);
     // (the deep kernel exists where its LDS fits a workgroup)
     const ygg::Kernel deep_avail = deep ? ygg::find_deep_launcher(n, R, R2f, L, group) : ygg::Kernel();
-    if (kmode != "fast" && kmode != "pipe" && kmode != "flow" && kmode != "solo") deepk = deep_avail;
+    if (kmode != "fast" && kmode != "pipe" && kmode != "flow") deepk = deep_avail;
     const int64_t slots = plan_slots(rplan);
     // device arena plan: every array 256-byte aligned
     struct Piece { size_t off, bytes; };
@@ -717,6 +729,10 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     // streams: 7.4 / 8.0 / 8.0 us per token step against 9.0 / 8.8 / 8.8 on the per-stream generate build)
     if (deep && kmode == "") m->gen_one = ygg::find_gen_one_launcher(n, R, R2f, L, group);
     m->gen_one_max_streams = m->gen_one ? ygg::one_blocks_per_cu(n, R, R2f, L, group, true) * cus : 0;
+    // generation of one stream with helper workgroups that compute the next step's first layers for every candidate
+    // token (YGG_SPEC=0: off): its speculation area is allocated and cleared here
+    const char *spenv = getenv("YGG_SPEC");
+    if (deep && kmode == "" && !(spenv && !strcmp(spenv, "0"))) m->spec = ygg::find_spec_launcher(n, R, R2f, L, group);
     m->deep_max_streams = deepk ? (m->deep_all ? INT32_MAX : cus) : 0;
     // flow_kernel for T >= kFlowMinTokens up to flow_max_streams (or always with YGG_KERNEL=flow): measured at 512
     // tokens against the per-stream kernel, the builds with the split descent win up to 8 streams per CU on every
@@ -731,11 +747,6 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
         const int reach = ygg::flow_split_build(n, R, R2f, L, md) ? 8 * cus : 2 * resident;
         m->flow_max_streams[md] = flowk ? (m->flow_all ? INT32_MAX : std::max(resident, reach)) : 0;
     }
-    // the solo kernel only when forced (YGG_KERNEL=solo): measured slower than the per-stream kernel for one-token
-    // steps and than the deep kernel for generation on the benchmark shapes (round A's arithmetic and barrier on one
-    // wavefront per SIMD cost about what the memory round trips they remove cost)
-    m->solo = solok;
-    m->solo_all = solok && kmode == "solo";
     // the leaf-grouped step: the benchmark shape with the specialised kernels' record layout, tensor scales, tables
     m->grouped_ok = family && !factored && !group && n == 128 && R == 8 && R2f == 16 && fa.blk == 16 &&
                     (L == 1 || fa.D <= 14);
@@ -743,10 +754,29 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
         const char *gm = getenv("YGG_GROUP_MFMA_MIN");
         m->grp_mfma_min = gm ? atoi(gm) : 8;
     }
-    m->solo_max_streams = m->solo_all ? INT32_MAX : 0;
     m->device = device;
     m->arena = arena;
     m->arena_bytes = total;
+    if (m->spec) {
+        // (without it, generation runs without helpers)
+        DeviceGuard sg;
+        void *a = nullptr;
+        const size_t bytes = spec_area_units(V) * sizeof(uint64_t);
+        if (sg.set(device) != hipSuccess || hipMalloc(&a, bytes) != hipSuccess || hipMemset(a, 0, bytes) != hipSuccess ||
+            hipDeviceSynchronize() != hipSuccess) {
+            if (a) (void)hipFree(a);
+            m->spec = ygg::Kernel();
+        } else {
+            m->spec_area = (uint64_t *)a;
+        }
+        // helper workgroups of 4 wavefronts, with the stream workgroup's 3 others one per candidate token
+        // (ceil((V - 3) / 4) of them, at most 64); YGG_SPEC_HELPERS: fewer
+        m->spec_helpers = std::min(64, V / 4);
+        if (const char *eh = getenv("YGG_SPEC_HELPERS")) m->spec_helpers = std::max(0, std::min(m->spec_helpers, atoi(eh)));
+        // YGG_SPEC_EPOCH: the first call's first epoch (tests of the wrap; 0 is taken as 1)
+        if (const char *ep = getenv("YGG_SPEC_EPOCH")) m->spec_next = (uint32_t)strtoul(ep, nullptr, 0);
+        if (m->spec_next == 0) m->spec_next = 1;
+    }
     m->run = launch;
     // the uncapped per-stream build while every stream of the call is resident with it
     if (family) {
@@ -806,7 +836,7 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
     I.deep_max_streams = m->deep_max_streams;
     I.flow_max_streams = m->flow_max_streams[kModeRun];
     I.router_rounds = L > 1 ? rplan.n : 0;
-    I.solo_max_streams = m->solo_max_streams;
+    I.spec_max_streams = m->spec ? 1 : 0;
     I.grouped = m->grouped_ok ? 1 : 0;
     I.file_array_bytes = fa.bytes;
     I.device_bytes = (int64_t)total;
@@ -820,8 +850,7 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
 constexpr int kFlowMinTokens = 32;
 
 // The kernel of a call of B streams and T tokens in mode (kModeRun, kModeGenerate: ygg_generate, kModeScore: a
-// digest or NLL). YGG_KERNEL=solo: the solo kernel (all wavefronts of a workgroup on one stream) for every call but
-// score calls. Run calls of one token with all their streams resident on the one-token build (one stream per
+// digest or NLL). Run calls of one token with all their streams resident on the one-token build (one stream per
 // workgroup): that build (the deep descent, its second round from global memory). Generation: the deep kernel for
 // >= 8 tokens and B <= deep_max_streams, then the generate build with the one-token build's descent while its
 // workgroups are all resident, else the per-stream kernel (every token needs all layers of the one before
@@ -831,9 +860,8 @@ constexpr int kFlowMinTokens = 32;
 // one while all B streams are resident with it. A kernel forced by YGG_KERNEL takes every call it can run.
 const ygg::Kernel &pick(const ygg_model *m, int B, int T, int mode) {
     const bool gen = mode == kModeGenerate;
-    if (m->solo && mode != kModeScore && (m->solo_all || (B <= m->solo_max_streams && (gen || T == 1))))
-        return m->solo;
     if (m->deep_all) return m->deep;
+    if (gen && m->spec && B == 1 && T >= 8) return m->spec;
     if (m->one && mode == kModeRun && T == 1 && B <= m->one_max_streams) return m->one;
     if (gen && m->deep && B <= m->deep_max_streams && T >= 8) return m->deep;
     if (gen && m->gen_one && B <= m->gen_one_max_streams && T >= 8) return m->gen_one;
@@ -843,18 +871,6 @@ const ygg::Kernel &pick(const ygg_model *m, int B, int T, int mode) {
     return (m->run_few && B <= m->run_few_max_streams[mode]) ? m->run_few : m->run;
 }
 
-struct DeviceGuard {
-    int prev = -1;
-    hipError_t set(int dev) {
-        hipError_t e = hipGetDevice(&prev);
-        if (e != hipSuccess) return e;
-        return prev == dev ? hipSuccess : hipSetDevice(dev);
-    }
-    ~DeviceGuard() {
-        int cur = -1;
-        if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
-    }
-};
 
 }  // namespace
 
@@ -865,7 +881,7 @@ int set_error(int code, const char *msg) { return fail(code, "%s", msg); }
 
 extern "C" {
 
-int ygg_version(void) { return 10; }
+int ygg_version(void) { return 11; }
 
 const char *ygg_last_error(void) { return g_err.c_str(); }
 
@@ -917,6 +933,7 @@ void ygg_free(ygg_model *m) {
     if (g.set(m->device) == hipSuccess) {
         (void)hipFree(m->arena);
         if (m->grp_ws) (void)hipFree(m->grp_ws);
+        if (m->spec_area) (void)hipFree(m->spec_area);
     }
     delete m;
 }
@@ -1041,7 +1058,34 @@ int ygg_generate(const ygg_model *m, const int32_t *d_first, int B, int n, int8_
     io.temperature = temperature;
     io.top_k = top_k;
     io.seed = (unsigned long long)seed;
+    if (&k == &m->spec) {
+        // the call's epochs E0 .. E0 + n (a tag of every unit its stream and helpers store); before they would wrap,
+        // the area is cleared on the stream and the epochs start again at 1
+        std::lock_guard<std::mutex> lk(m->spec_mu);
+        if ((uint64_t)m->spec_next + (uint64_t)n + 1 > 0xFFFFFFFFull) {
+            const size_t units = spec_area_units(m->dev.V);
+            hipLaunchKernelGGL(spec_clear_kernel, dim3((unsigned)((units + 255) / 256)), dim3(256), 0,
+                               (hipStream_t)stream, m->spec_area, units);
+            HIP_TRY(hipGetLastError());
+            m->spec_next = 1;
+        }
+        io.spec = m->spec_area;
+        io.spec_epoch = m->spec_next;
+        io.spec_helpers = m->spec_helpers;
+        m->spec_next += (uint32_t)n + 1;
+    }
     HIP_TRY(k.fn(m->dev, d_first, B, n, d_state, io, (hipStream_t)stream));
+    return YGG_OK;
+}
+
+int ygg_spec_stats(const ygg_model *m, uint64_t *out, int reset) {
+    if (!m || !out) return fail(YGG_ERR_ARG, "NULL argument");
+    memset(out, 0, kSpecNStats * sizeof(uint64_t));
+    if (!m->spec_area) return YGG_OK;
+    DeviceGuard g;
+    HIP_TRY(g.set(m->device));
+    HIP_TRY(hipMemcpy(out, m->spec_area + kSpecStats, kSpecNStats * sizeof(uint64_t), hipMemcpyDeviceToHost));
+    if (reset) HIP_TRY(hipMemset(m->spec_area + kSpecStats, 0, kSpecNStats * sizeof(uint64_t)));
     return YGG_OK;
 }
 

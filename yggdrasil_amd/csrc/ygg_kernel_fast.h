@@ -799,13 +799,18 @@ __device__ __forceinline__ void store_logits(float *o, const float (&lg)[4], int
     }
 }
 
+}  // namespace ygg
+#include "ygg_kernel_spec.h"
+namespace ygg {
+
 // ----------------------------------------------------------------------------------------------- fast_kernel
 
 // MODE: kModeRun (logits, leaves, states), kModeScore (also the digest and the NLL: their constants and lane terms
 // take registers the other modes keep for streams) or kModeGenerate (sample the next input from the logits of every
 // token, io.gen, instead of reading it from tokens); kModeOne: kModeRun with the deep descent for calls of one token
 // (one stream per workgroup, the second round's rows from global memory: nothing staged beyond the usual tables);
-// kModeGenOne: kModeGenerate with kModeOne's descent, for models with no DEEP build. DEEP: one
+// kModeGenOne: kModeGenerate with kModeOne's descent, for models with no DEEP build; kModeGenSpec: kModeGenOne for one
+// stream with speculating helper workgroups (ygg_kernel_spec.h; workgroup 0 runs the stream). DEEP: one
 // stream per workgroup with the deep descent (generation for few streams), else 4 streams per workgroup with
 // descend. CAP (not DEEP): at most 128 VGPRs, 4 wavefronts per SIMD (the most streams resident, some registers
 // spilled), else up to 256 (no spills; for calls whose streams all fit at the lower occupancy).
@@ -824,19 +829,40 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
     using F = SH;
     // one stream per workgroup for the builds of few streams (DEEP, kModeOne, kModeGenOne): a stream's loads then
     // have a CU's memory path to themselves
-    constexpr int W = (DEEP || MODE == kModeOne || MODE == kModeGenOne) ? 1 : kFastWaves, LR = L > 1 ? L - 1 : 1;
-    constexpr bool GEN = MODE == kModeGenerate || MODE == kModeGenOne, SCORE = MODE == kModeScore;
-    constexpr bool DD = DEEP || MODE == kModeOne || MODE == kModeGenOne;   // the deep descent (DEEP: second round in LDS)
+    constexpr bool SPEC = MODE == kModeGenSpec;
+    constexpr int W = (DEEP || MODE == kModeOne || MODE == kModeGenOne || SPEC) ? 1 : kFastWaves, LR = L > 1 ? L - 1 : 1;
+    constexpr bool GEN = MODE == kModeGenerate || MODE == kModeGenOne || SPEC, SCORE = MODE == kModeScore;
+    // the deep descent (DEEP: second round in LDS)
+    constexpr bool DD = DEEP || MODE == kModeOne || MODE == kModeGenOne || SPEC;
+    // SPEC: the routed layers whose descent the helpers take over; every wavefront's state rows (a helper's: the new and
+    // the published states of those layers) and slot tail (ygg_kernel_spec.h)
+    constexpr int SPS = SPEC ? kSpecDepth<L> : 1;
+    using SLY = SpecLayout<SH, SPS>;
+    constexpr int QB = (SPEC && 2 * SPS > L ? 2 * SPS : L) * N;
     __shared__ __attribute__((aligned(16))) SharedTables<SH, L> S;
     __shared__ __attribute__((aligned(16))) GroupTablesOf<SH, L, GROUP> GT;
     __shared__ __attribute__((aligned(16))) int8_t W1s[DEEP ? LR : 1][DEEP ? kR2Slots<N> * N : 16];
-    __shared__ __attribute__((aligned(16))) int8_t qsw[W][L * N];
+    __shared__ __attribute__((aligned(16))) int8_t qsw[SPEC ? kFastWaves : W][QB];
     __shared__ __attribute__((aligned(16))) int8_t zlw[W][SH::ZL];
     __shared__ __attribute__((aligned(16))) int8_t zqw[W][SH::ZQ];
+    __shared__ __attribute__((aligned(16))) int8_t spw[SPEC ? kFastWaves : 1][SPEC ? SLY::TB : 16];
 
     // the wavefront index, stream, tokens and leaves are uniform over a wavefront: kept in scalar registers. With one
     // stream per workgroup (W = 1) wavefronts 1-3 stage the LDS tables and then leave.
     const int tid = threadIdx.x, wv = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    if constexpr (SPEC) {
+        // workgroups 1 .. io.spec_helpers are helper workgroups (ygg_kernel_spec.h); any others leave at once
+        if (blockIdx.x > 0) {
+            if ((int)blockIdx.x > io.spec_helpers) return;
+            load_tables<SH, L, 64 * kFastWaves>(S, m, tid);
+            if constexpr (GROUP) load_group_tables<SH, L, 64 * kFastWaves>(GT, m, tid);
+            if constexpr (DEEP) load_round2<N, L, 64 * kFastWaves>(W1s, m, tid);
+            __syncthreads();
+            spec_helper<SH, L, GROUP, DEEP>(m, io, T, (blockIdx.x - 1) * kFastWaves + wv,
+                                            spec_helper_waves(io.spec_helpers), S, GT, &W1s[0][0], qsw[wv], spw[wv], lane);
+            return;
+        }
+    }
     const int s = blockIdx.x * W + wv;
     const int V = m.V, VP = m.VP;
     const int K4 = FACT ? m.K / 4 : 0;         // factored input rank / 4
@@ -845,7 +871,7 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
     // (a launch of one token would otherwise wait for them one after the other).
     const int32_t *tok = tokens + (size_t)s * (GEN ? 1 : T);
     // (measured: the generation kernels run slower with it, 15% with DEEP; one-token launches faster)
-    if constexpr (!DEEP && MODE != kModeGenOne) touch_args<L>(m);
+    if constexpr (!DEEP && MODE != kModeGenOne && !SPEC) touch_args<L>(m);
     int x_next = (live && T > 0) ? __builtin_amdgcn_readfirstlane(tok[0]) : 0;
     int8_t *st = state + (size_t)s * L * N;
     constexpr int SB = (L * N + 63) / 64;     // state bytes per lane
@@ -862,6 +888,11 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
             if constexpr (GROUP) load_group_tables<SH, L, 64 * (kFastWaves - 1)>(GT, m, tid - 64);
             if constexpr (DEEP) load_round2<N, L, 64 * (kFastWaves - 1)>(W1s, m, tid - 64);
             __syncthreads();
+            // SPEC: then helpers on the stream's own CU
+            if constexpr (SPEC)
+                spec_helper<SH, L, GROUP, DEEP>(m, io, T, io.spec_helpers * kFastWaves + wv - 1,
+                                                spec_helper_waves(io.spec_helpers), S, GT, &W1s[0][0], qsw[wv],
+                                                spw[wv], lane);
             return;
         }
     } else {
@@ -888,6 +919,10 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
     unsigned long long dg = (SCORE && digest) ? digest[s] : 0ull;
     double nacc = 0.0;
     bool staged = W > 1;      // W = 1: the stream's wavefront has met the barrier that waits for the LDS tables
+    // SPEC: steps taken from the helpers' slots and computed here, whether the last one was taken
+    int spec_hits = 0, spec_misses = 0;
+    bool spec_prev = true;
+    int8_t *const sps = spw[0];
 
     for (int t = 0; t < T; t++) {
         const int x = x_next;
@@ -896,18 +931,30 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
             if (lane == 0) atomicOr(m.err, 1u);
             break;
         }
-        // thresholds of the first router round of every routed layer
+        // SPEC: x's slot, which holds this step's layers 0 .. SPS - 1 and layer SPS's leaf and layer input (a short
+        // wait after a step that had its slot, a single look after one that did not)
+        bool hit = false;
+        if constexpr (SPEC) {
+            if (t > 0) {
+                hit = spec_take<SH, SPS>(io, x, t, T, qs, sps, lane, spec_prev ? 400 : 30);
+                spec_prev = hit;
+                spec_hits += hit ? 1 : 0;
+                spec_misses += hit ? 0 : 1;
+            }
+        }
+        // thresholds of the first router round of every routed layer (SPEC with the slot: of the layers after SPS)
         float th1[LR];
 #pragma unroll
         for (int l = 1; l < L; l++)
-            th1[l - 1] = qj < nn1 ? m.layers[l].thr[(size_t)x * m.layers[l].thr_stride + qj] : 0.0f;
+            th1[l - 1] = (qj < nn1 && (!hit || l > SPS)) ? m.layers[l].thr[(size_t)x * m.layers[l].thr_stride + qj]
+                                                         : 0.0f;
         // DEEP: and those of the second round, four per lane (components in separate arrays, which the selects
         // below keep in registers)
         float th2x[LR], th2y[LR], th2z[LR], th2w[LR];
 #pragma unroll
         for (int l = 1; l < L; l++) {
             float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            if (DD && 4 * lane < n2)
+            if (DD && 4 * lane < n2 && (!hit || l > SPS))
                 v = *(const float4 *)(m.layers[l].thr + (size_t)x * m.layers[l].thr_stride + (1 << m.round_h[0]) +
                                       4 * lane);
             th2x[l - 1] = v.x; th2y[l - 1] = v.y; th2z[l - 1] = v.z; th2w[l - 1] = v.w;
@@ -915,6 +962,20 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
         float lg[4];
 #pragma unroll
         for (int u = 0; u < 4; u++) lg[u] = 4 * lane + u < VP ? m.output_bias[4 * lane + u] : 0.0f;
+        // SPEC with the slot: the unembedding terms of layers 0 .. SPS - 1 from its readouts, in layer order
+        if constexpr (SPEC) {
+            if (hit && 4 * lane < VP) {
+#pragma unroll
+                for (int l = 0; l < SPS; l++) {
+                    float term[4];
+                    const float *sq = nullptr;
+                    if constexpr (GROUP) sq = GT.sq[l];
+                    unembed_terms<R, GROUP>(term, sps + l * R, S.Q[l], m.layers[l].unembed_scale, lane, sq);
+#pragma unroll
+                    for (int u = 0; u < 4; u++) lg[u] = lg[u] + term[u];
+                }
+            }
+        }
 
         // The readout of layer l (P_r q -> zq -> Q zq into the logits) is not on the path to layer l + 1, which needs
         // only the new state: it runs while the loads of layer l + 1's first global router round are in flight
@@ -942,12 +1003,17 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
 
         // not unrolled: an unrolled loop keeps every layer's pointers in scalar registers at once and spills them
 #pragma unroll 1
-        for (int l = 0; l < L; l++) {
+        for (int l = (SPEC && hit) ? SPS : 0; l < L; l++) {
             const YggDevLayer &y = m.layers[l];
             int r = x;
             float rho = 0.0f;
             uint32_t qbw[F::QW];
-            if (l > 0) {
+            // SPEC, the slot's layer: leaf and layer input as the helper left them
+            const bool given = SPEC && hit && l == SPS;
+            // (a slot is taken only with every unit of this step: its leaf is one a helper found; the mask keeps
+            // the record address in the layer whatever the word holds)
+            if (given) r = __builtin_amdgcn_readfirstlane(*(const int32_t *)(sps + SPS * R)) & (m.E - 1);
+            if (l > 0 && !given) {
                 float th = th1[0];
 #pragma unroll
                 for (int i = 1; i < LR; i++) th = l - 1 == i ? th1[i] : th;
@@ -982,7 +1048,7 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
                     __syncthreads();
                     staged = true;
                 }
-            if (l > 0) layer_input<SH>(zls, S.V[l - 1], S.mv[l - 1], qbw, rho, lane);
+            if (l > 0 && !given) layer_input<SH>(zls, S.V[l - 1], S.mv[l - 1], qbw, rho, lane);
             wave_sync();
             int qn[F::C];
             const float *mul = nullptr;
@@ -990,13 +1056,17 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
             const uint32_t *vx = nullptr;
             if constexpr (FACT) vx = (const uint32_t *)(y.vt + (size_t)x * m.K);
             if (lane < F::NL)
-                update<SH, GROUP, false, FACT>(qn, G, qs + l * N, zls, y, l > 0, m.shift, lane, mul, nullptr, vx, K4);
+                update<SH, GROUP, false, FACT>(qn, G, qs + l * N, given ? sps + SPS * R + 4 : zls, y, l > 0, m.shift,
+                                               lane, mul, nullptr, vx, K4);
             wave_sync();
             if (lane < F::NL) {
 #pragma unroll
                 for (int c = 0; c < F::C; c++) qs[l * N + F::C * lane + c] = (int8_t)qn[c];
             }
             wave_sync();
+            // SPEC, step computed here: its states of layers 0 .. SPS - 1 for the next step's helpers
+            if constexpr (SPEC)
+                if (!hit && l == SPS - 1 && t + 1 < T) spec_publish<SH, SPS>(io, t, qs, lane);
             if (leaves && lane == 0) leaves[((size_t)s * T + t) * L + l] = r;
             if (SCORE && digest) dg = dg * kDigestMul + digest_term<N>(qn, r, l, lane);
 #pragma unroll
@@ -1026,6 +1096,11 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
         if (!staged) __syncthreads();
     wave_sync();
     for (int i = lane; i < L * N; i += 64) st[i] = qs[i];
+    if constexpr (SPEC)
+        if (lane == 0) {
+            spec_count(io.spec, 0, (unsigned long long)spec_hits);
+            spec_count(io.spec, 1, (unsigned long long)spec_misses);
+        }
     if (SCORE && digest && lane == 0) digest[s] = dg;
     if (SCORE && nll && lane == 0) nll[s] += nacc;
 }

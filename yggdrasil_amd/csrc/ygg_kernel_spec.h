@@ -1,0 +1,272 @@
+// Speculative generation for one stream (kModeGenSpec; included by ygg_kernel_fast.h before fast_body, whose
+// per-layer pieces it uses).
+//
+// Generation is a chain: the token sampled after step t is the input of step t + 1, so every layer of step t + 1
+// waits for all layers of step t. Only two things tie step t + 1 to step t, though: the sampled token x(t + 1), which
+// is one of V values, and the states of the layers. So while the stream finishes step t, helper wavefronts compute
+// step t + 1's first layers for every candidate token at once: given the states of layers 0 .. S - 1 after step t,
+// the helper of candidate x updates the token layer with expert x, descends the router of layer 1 with x's
+// thresholds, updates layer 1, ... up to layer S's router descent and layer input, and leaves the new states, the
+// readouts zq, layer S's leaf and its layer input in x's slot. The stream then samples x(t + 1), reads x's slot and
+// starts step t + 1 at layer S's update: the token layer and S router descents leave its chain.
+//
+// Exchange. Every exchanged word travels in an 8-byte unit with a 32-bit tag, the epoch of the step it belongs to
+// (the call's first epoch, from a host counter, plus the step index), stored with one 64-bit store (single-copy
+// atomic). A reader takes a block only when every unit carries the epoch it expects, so a unit that is stale, torn
+// by a concurrent writer or left by another call is never used; the stream computes the step itself instead, with
+// the same code as without helpers, and every result is the same bit for bit either way.
+//   - publication: after step t's layer S - 1 the stream stores the states of layers 0 .. S - 1 (tag E0 + t);
+//   - slot of x: the helper of x stores step t + 1's results for x (tag E0 + t + 1).
+// Stores and loads are at device scope (written through past the XCD's L2, read past it), coherent between XCDs:
+// each XCD has its own L2, and 255 helpers on the stream's XCD alone move about 9 MB per step through that XCD's
+// share of the fabric, which measured twice as slow a chain for every helper and for the stream itself (10.4 us a
+// step); spread over the 8 XCDs they move about 1 MB each.
+//
+// Waiting. The stream never waits on a helper beyond a short bounded poll of its slot (then it computes). Every
+// helper wait is bounded by the wall clock and a helper that times out leaves, so every wavefront ends.
+//
+// Placement. Workgroup 0 runs the stream, workgroups 1 .. H help (the dispatcher hands workgroups to the XCDs in
+// turn: about H / 8 on each), 4 wavefronts each, and the stream workgroup's 3 staging wavefronts help too: 4 H + 3
+// helper wavefronts, one candidate each; with more candidates than helpers the uncovered ones change with every step
+// (candidate (j + step) mod V for helper j of nh). Every workgroup holds the build's LDS: with the deep descent's
+// second-round rows (the stream's and the helpers' descents both read them from LDS), one workgroup per CU.
+#pragma once
+
+namespace ygg {
+
+constexpr int kSpecMaxHelpers = 64;   // helper workgroups at most (workgroups 1 .. kSpecMaxHelpers)
+// helper wavefronts of h helper workgroups: theirs and the stream workgroup's staging wavefronts
+__host__ __device__ constexpr int spec_helper_waves(int h) { return h * kFastWaves + kFastWaves - 1; }
+
+// routed layers whose descent the helpers take over: 2, or 1 for a 2-layer model
+template <int L> constexpr int kSpecDepth = L > 2 ? 2 : 1;
+
+template <class SH, int S> struct SpecLayout {
+    static constexpr int PW = S * SH::N / 4;                                   // published words
+    static constexpr int KP = (PW + 63) / 64;                                  // their units per lane
+    static constexpr int SW = S * SH::N / 4 + S * SH::R / 4 + 1 + SH::R2P / 4;  // slot words
+    static constexpr int KS = (SW + 63) / 64;
+    static constexpr int TB = S * SH::R + 4 + SH::ZL;    // LDS bytes of a slot after the states: zq .., leaf, zl
+    static_assert(KP <= 4 && KS <= 4 && KS * 64 <= kSpecSlotUnits, "units per lane");
+};
+
+__device__ __forceinline__ uint64_t spec_unit(uint32_t tag, uint32_t word) { return (uint64_t)word << 32 | tag; }
+__device__ __forceinline__ uint64_t spec_load(const uint64_t *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void spec_store(uint64_t *p, uint64_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void spec_count(uint64_t *area, int which, unsigned long long v) {
+    atomicAdd((unsigned long long *)(area + kSpecStats + which), v);
+}
+
+// wall-clock bound (100 MHz ticks)
+constexpr uint64_t kSpecPubWait = 20000;       // 200 us between two publications
+
+// The helper wavefront j of nh: serves every publication of this call from the first (relative epoch 0) to T - 2.
+// qh: this wavefront's LDS states, new states of layers 0 .. S - 1 at qh (the slot's order), the published (old)
+// ones at qh + S N; sp: the slot's tail (zq of layers 0 .. S - 1, layer S's leaf, its layer input). DEEP: the
+// routed layers' second-round rows are in LDS from W1 on (load_round2's layout: kR2Slots N bytes a layer, fast_kernel's
+// deep descent), else read from global memory.
+template <class SH, int L, bool GROUP, bool DEEP>
+__device__ __forceinline__ void spec_helper(const YggDevModel &m, const YggIO &io, int T, int j, int nh,
+                                            const SharedTables<SH, L> &St, const GroupTablesOf<SH, L, GROUP> &GT,
+                                            const int8_t *W1, int8_t *qh, int8_t *sp, int lane) {
+    constexpr int N = SH::N, R = SH::R, S = kSpecDepth<L>;
+    using LY = SpecLayout<SH, S>;
+    using F = SH;
+    uint64_t *const area = io.spec;
+    const uint32_t E0 = io.spec_epoch;
+    // (no publication to serve, or no candidate: helpers past the vocabulary when every candidate has one)
+    if (T < 2 || j >= nh || (nh >= m.V && j >= m.V)) return;
+    const uint32_t span = (uint32_t)T - 2;        // relative epochs of the publications worth serving
+    if (lane == 0) spec_count(area, 3, 1);
+    const int V = m.V;
+    const int n2 = m.n_rounds > 1 ? 1 << (m.round_h[0] + m.round_h[1]) : 0;
+    const int qj = lane >> 2, nn1 = (1 << m.round_h[0]) - 1;
+    const Tail tl = make_tail(m, lane, (!DEEP && tail_fold(m)) ? 1 : 2);
+    int8_t *const qnew = qh, *const qold = qh + S * N;
+    int8_t *const zl = sp + S * R + 4;
+    uint32_t next = 0;
+    int served = 0;
+    bool timed_out = false;
+    while (next <= span) {
+        // the next publication: lane 0's first unit announces it, then every unit must carry its epoch
+        uint64_t u[LY::KP];
+        uint32_t e = 0;
+        bool got = false;
+        const uint64_t t0 = wall_clock64();
+        for (;;) {
+            const uint32_t e0 = __builtin_amdgcn_readfirstlane((uint32_t)spec_load(area + kSpecPub)) - E0;
+            if (e0 >= next && e0 <= span) {
+                bool bad = false;
+#pragma unroll
+                for (int k = 0; k < LY::KP; k++) {
+                    const int w = 64 * k + lane;
+                    u[k] = w < LY::PW ? spec_load(area + kSpecPub + w) : spec_unit(E0 + e0, 0u);
+                    bad = bad || (uint32_t)u[k] != E0 + e0;
+                }
+                if (lane_mask(bad) == 0ull) {
+                    e = e0;
+                    got = true;
+                    break;
+                }
+            }
+            if (wall_clock64() - t0 > kSpecPubWait) break;
+            __builtin_amdgcn_s_sleep(4);
+        }
+        if (!got) {
+            timed_out = true;
+            break;
+        }
+        next = e + 1;
+        const int x = nh >= V ? j : (int)((uint32_t)(j + e) % (uint32_t)V);
+        if (x >= V) continue;
+#pragma unroll
+        for (int k = 0; k < LY::KP; k++) {
+            const int w = 64 * k + lane;
+            if (w < LY::PW) ((uint32_t *)qold)[w] = (uint32_t)(u[k] >> 32);
+        }
+        // x's thresholds of the first two rounds of layers 1 .. S
+        float th1[S];
+        float4 th2[S];
+#pragma unroll
+        for (int l = 1; l <= S; l++) {
+            const YggDevLayer &y = m.layers[l];
+            th1[l - 1] = qj < nn1 ? y.thr[(size_t)x * y.thr_stride + qj] : 0.0f;
+            th2[l - 1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (4 * lane < n2)
+                th2[l - 1] = *(const float4 *)(y.thr + (size_t)x * y.thr_stride + (1 << m.round_h[0]) + 4 * lane);
+        }
+        wave_sync();
+        // the token layer with expert x
+        Gather<SH, false> G;
+        int qn[F::C];
+        {
+            const YggDevLayer &y = m.layers[0];
+            gather<SH, GROUP, true, false>(G, y, x, x, false, lane);
+            const float *mul = nullptr;
+            if constexpr (GROUP) mul = GT.mul[0];
+            if (lane < F::NL) update<SH, GROUP, false, false>(qn, G, qold, zl, y, false, m.shift, lane, mul);
+            wave_sync();
+            if (lane < F::NL) {
+#pragma unroll
+                for (int c = 0; c < F::C; c++) qnew[F::C * lane + c] = (int8_t)qn[c];
+            }
+            wave_sync();
+            readout<SH>(sp, G.pw, qnew, GROUP ? G.mzr : y.readout_scale, lane);
+        }
+        // layers 1 .. S - 1 whole, layer S's descent and layer input
+#pragma unroll
+        for (int l = 1; l <= S; l++) {
+            const YggDevLayer &y = m.layers[l];
+            uint32_t qbw[F::QW];
+            float rho = below_and_rho<N>(qbw, qnew + (l - 1) * N, y.rms_eps, lane);
+            if constexpr (GROUP)
+                if (y.r2b) rho = group_rho<N>(qbw, GT.r2[l - 1], y.rms_eps);
+            int r;
+            if constexpr (DEEP)
+                r = descend_deep<N>(m, y, St.W[l - 1], th1[l - 1], W1 + (l - 1) * kR2Slots<N> * N, th2[l - 1], qbw,
+                                    qnew + (l - 1) * N, rho, x, lane, tl);
+            else
+                r = descend_deep<N, NoHook, true>(m, y, St.W[l - 1], th1[l - 1], y.w + ((size_t)1 << m.round_h[0]) * N,
+                                                  th2[l - 1], qbw, qnew + (l - 1) * N, rho, x, lane, tl);
+            if (l < S) gather<SH, GROUP, true, false>(G, y, r, x, true, lane);
+            layer_input<SH>(zl, St.V[l - 1], St.mv[l - 1], qbw, rho, lane);
+            wave_sync();
+            if (l == S) {
+                if (lane == 0) *(int32_t *)(sp + S * R) = r;
+                break;
+            }
+            const float *mul = nullptr;
+            if constexpr (GROUP) mul = GT.mul[l - 1];
+            if (lane < F::NL) update<SH, GROUP, false, false>(qn, G, qold + l * N, zl, y, true, m.shift, lane, mul);
+            wave_sync();
+            if (lane < F::NL) {
+#pragma unroll
+                for (int c = 0; c < F::C; c++) qnew[l * N + F::C * lane + c] = (int8_t)qn[c];
+            }
+            wave_sync();
+            readout<SH>(sp + l * R, G.pw, qnew + l * N, GROUP ? G.mzr : y.readout_scale, lane);
+        }
+        wave_sync();
+        // x's slot: step e + 1's results
+        uint64_t *slot = area + kSpecSlots + (size_t)x * kSpecSlotUnits;
+#pragma unroll
+        for (int k = 0; k < LY::KS; k++) {
+            const int w = 64 * k + lane;
+            if (w < LY::SW) {
+                const uint32_t word = w < S * N / 4 ? ((const uint32_t *)qnew)[w]
+                                                    : ((const uint32_t *)sp)[w - S * N / 4];
+                spec_store(slot + w, spec_unit(E0 + e + 1, word));
+            }
+        }
+        served++;
+    }
+    if (lane == 0) {
+        if (served) spec_count(area, 2, 1);
+        if (timed_out) spec_count(area, 4, 1);
+    }
+}
+
+// The stream's side. spec_take: x's slot for step t (tag E0 + t), polled for at most `wait` ticks; when every unit
+// carries the tag, the states of layers 0 .. S - 1 go to qs (the stream's state rows), the rest to sp, and (unless
+// t is the last step) the states are published for step t + 1's helpers. Returns whether the slot was taken.
+template <class SH, int S>
+__device__ __forceinline__ bool spec_take(const YggIO &io, int x, int t, int T, int8_t *qs, int8_t *sp, int lane,
+                                          uint64_t wait) {
+    using LY = SpecLayout<SH, S>;
+    constexpr int N = SH::N;
+    const uint32_t tag = io.spec_epoch + (uint32_t)t;
+    const uint64_t *slot = io.spec + kSpecSlots + (size_t)x * kSpecSlotUnits;
+    uint64_t u[LY::KS];
+    const uint64_t t0 = wall_clock64();
+    bool ok = false;
+    for (;;) {
+        bool bad = false;
+#pragma unroll
+        for (int k = 0; k < LY::KS; k++) {
+            const int w = 64 * k + lane;
+            u[k] = w < LY::SW ? spec_load(slot + w) : spec_unit(tag, 0u);
+            bad = bad || (uint32_t)u[k] != tag;
+        }
+        if (lane_mask(bad) == 0ull) {
+            ok = true;
+            break;
+        }
+        if (wall_clock64() - t0 > wait) break;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    if (!ok) return false;
+#pragma unroll
+    for (int k = 0; k < LY::KS; k++) {
+        const int w = 64 * k + lane;
+        const uint32_t word = (uint32_t)(u[k] >> 32);
+        if (w < S * N / 4) ((uint32_t *)qs)[w] = word;
+        else if (w < LY::SW) ((uint32_t *)sp)[w - S * N / 4] = word;
+    }
+    if (t + 1 < T) {
+#pragma unroll
+        for (int k = 0; k < LY::KP; k++) {
+            const int w = 64 * k + lane;
+            if (w < LY::PW) spec_store(io.spec + kSpecPub + w, spec_unit(tag, (uint32_t)(u[k] >> 32)));
+        }
+    }
+    wave_sync();
+    return true;
+}
+
+// the states of layers 0 .. S - 1 after step t (LDS qs), published for step t + 1's helpers
+template <class SH, int S>
+__device__ __forceinline__ void spec_publish(const YggIO &io, int t, const int8_t *qs, int lane) {
+    using LY = SpecLayout<SH, S>;
+    const uint32_t tag = io.spec_epoch + (uint32_t)t;
+#pragma unroll
+    for (int k = 0; k < LY::KP; k++) {
+        const int w = 64 * k + lane;
+        if (w < LY::PW) spec_store(io.spec + kSpecPub + w, spec_unit(tag, ((const uint32_t *)qs)[w]));
+    }
+}
+
+}  // namespace ygg

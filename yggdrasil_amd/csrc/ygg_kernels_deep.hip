@@ -128,6 +128,46 @@ template <int N, int R, int R2, int L, bool GROUP> Kernel gen_one_k() {
         return Kernel();
 }
 
+// generation of one stream with speculating helper workgroups (kModeGenSpec, ygg_kernel_spec.h): workgroup 0 runs the
+// stream, workgroups 1 .. io.spec_helpers help. With the deep descent where its LDS fits, else with the one-token
+// build's. Not for the largest shape (its stream's registers spill at the build's bound)
+template <int N, int R, int R2, int L, bool GROUP, bool DEEP>
+hipError_t launch_spec(const YggDevModel &m, const int32_t *tokens, int B, int T, int8_t *state, const YggIO &io,
+                       hipStream_t stream) {
+    if (io_mode(io) != kModeGenerate || B != 1 || !io.spec || io.spec_helpers < 0 ||
+        io.spec_helpers > kSpecMaxHelpers)
+        return hipErrorInvalidValue;   // (the dispatch's rule)
+    const dim3 grid(1 + io.spec_helpers), block(64 * kFastWaves);
+    hipLaunchKernelGGL((fast_kernel<N, R, R2, L, kModeGenSpec, DEEP, false, GROUP>), grid, block, 0, stream, m,
+                       tokens, B, T, state, io);
+    return hipGetLastError();
+}
+
+// the speculating build's LDS with the deep descent: the deep kernel's, with every wavefront's states and slot tail
+template <int N, int R, int R2, int L, bool GROUP>
+constexpr bool kSpecDeepFits = kTablesBytes<Shape<N, R, R2>, L> + sizeof(GroupTablesOf<Shape<N, R, R2>, L, GROUP>) +
+                                   (L - 1) * kR2Slots<N> * N + kFastWaves * ((L > 4 ? L : 4) * N + 2 * R + 4 + 64) +
+                                   256 <=
+                               160 * 1024;
+
+template <int N, int R, int R2, int L, bool GROUP> Kernel spec_k() {
+    if constexpr (L >= 2 && N <= 128 && (!GROUP || kGroupOk<N>)) {
+        constexpr bool D = kSpecDeepFits<N, R, R2, L, GROUP>;
+        return make_kernel(launch_spec<N, R, R2, L, GROUP, D>, "ygg::fast_kernel<%d, %d, %d, %d, 5, %s, false, %s>",
+                           N, R, R2, L, D ? "true" : "false", GROUP ? "true" : "false");
+    } else {
+        return Kernel();
+    }
+}
+
+template <int N, int R, int R2, bool GROUP> Kernel spec_for(int L) {
+    if (L == 2) return spec_k<N, R, R2, 2, GROUP>();
+    if (L == 3) return spec_k<N, R, R2, 3, GROUP>();
+    if (L == 4) return spec_k<N, R, R2, 4, GROUP>();
+    if (L == 5) return spec_k<N, R, R2, 5, GROUP>();
+    return Kernel();
+}
+
 template <int N, int R, int R2, bool GROUP> Kernel gen_one_for(int L) {
     if (L == 2) return gen_one_k<N, R, R2, 2, GROUP>();
     if (L == 3) return gen_one_k<N, R, R2, 3, GROUP>();
@@ -246,6 +286,15 @@ Kernel find_gen_one_launcher(int n, int R, int R2, int L, bool group) {
 #define YGG_D(N_, R_, R2_) \
     if (n == N_ && R == R_ && R2 == R2_) \
         return group ? gen_one_for<N_, R_, R2_, true>(L) : gen_one_for<N_, R_, R2_, false>(L);
+    YGG_SHAPES(YGG_D)
+#undef YGG_D
+    return Kernel();
+}
+
+// fast_kernel's generation build for one stream with speculating helpers (2 <= L <= 5, d_state <= 128)
+Kernel find_spec_launcher(int n, int R, int R2, int L, bool group) {
+#define YGG_D(N_, R_, R2_) \
+    if (n == N_ && R == R_ && R2 == R2_) return group ? spec_for<N_, R_, R2_, true>(L) : spec_for<N_, R_, R2_, false>(L);
     YGG_SHAPES(YGG_D)
 #undef YGG_D
     return Kernel();

@@ -75,6 +75,8 @@ Kernel find_one_launcher(int n, int R, int R2, int L, bool group);
 // resident workgroups per CU of the one-token build, or (gen) of the generation build with its descent
 int one_blocks_per_cu(int n, int R, int R2, int L, bool group, bool gen);
 Kernel find_gen_one_launcher(int n, int R, int R2, int L, bool group);
+// generation of one stream with speculating helper workgroups (2 <= L <= 5, d_state <= 128): io.spec, io.spec_epoch
+Kernel find_spec_launcher(int n, int R, int R2, int L, bool group);
 Kernel find_pipe_launcher(int n, int R, int R2, int L, bool cap, bool group);
 int pipe_blocks_per_cu(int n, int R, int R2, int L, bool cap, bool group, int mode);
 // flow_kernel, one workgroup per stream, for scoring with the tokens known, router plans of P = 3 or 4 rounds
@@ -82,9 +84,6 @@ int pipe_blocks_per_cu(int n, int R, int R2, int L, bool cap, bool group, int mo
 Kernel find_flow_launcher(int n, int R, int R2, int L, int P, bool group);
 int flow_blocks_per_cu(int n, int R, int R2, int L, int P, bool group, int mode);
 bool flow_split_build(int n, int R, int R2, int L, int mode);
-// solo_kernel, one stream per workgroup with all four wavefronts on it (ygg_kernels_solo.hip): router plans of at
-// most 4 rounds whose first two take at most 8 levels and the others at most 6
-Kernel find_solo_launcher(int n, int R, int R2, int L, bool group);
 // the leaf-grouped step (ygg_kernels_group.hip; n 128, readout rank 8, layer-input rank 16, table storage, tensor
 // scales, at most 16384 experts a layer): every (token, layer) of the call as route, plan and update launches on
 // the stream, in a workspace of grouped_ws_bytes(B, L) bytes at ws

@@ -91,6 +91,9 @@ struct YggIO {
     float temperature;              // generate: 0 = greedy (first maximal class)
     int32_t top_k;                  // generate: keep classes at least the k-th largest logit (0: all)
     unsigned long long seed;        // generate
+    uint64_t *spec;                 // generate, kModeGenSpec: the model's speculation area (tagged 8-byte units)
+    uint32_t spec_epoch;            // generate, kModeGenSpec: the call's first epoch; token t's tag is spec_epoch + t
+    int32_t spec_helpers;           // generate, kModeGenSpec: helper workgroups (workgroups 8 .. 8 spec_helpers)
 };
 
 // What a launch computes, from its outputs: the specialised per-stream kernel has a build per mode (the digest and
@@ -105,6 +108,20 @@ constexpr int kModeOne = 3;
 // per workgroup, for more streams than the deep build takes, or for models with no deep build (their second-round rows
 // do not fit LDS beside the tables)
 constexpr int kModeGenOne = 4;
+// a build of the per-stream kernel, not a mode argument: kModeGenerate for one stream, with helper workgroups on the
+// stream's XCD that compute the next token's first layers for every candidate token while the stream finishes the
+// current one (ygg_kernel_spec.h)
+constexpr int kModeGenSpec = 5;
+
+// The speculation area of a model (kModeGenSpec), in 8-byte units (a 32-bit tag in the low half, a 32-bit word in the
+// high half): the stream's hello (its epoch and XCD) at unit 0, counters at kSpecStats, the published states at
+// kSpecPub, then one slot of kSpecSlotUnits units per candidate token.
+constexpr int kSpecStats = 8;           // 5 counters (uint64): hits, misses, helper waves served, off-XCD, timed out
+constexpr int kSpecNStats = 5;
+constexpr int kSpecPub = 64;
+constexpr int kSpecSlots = 320;
+constexpr int kSpecSlotUnits = 256;
+inline size_t spec_area_units(int V) { return (size_t)kSpecSlots + (size_t)V * kSpecSlotUnits; }
 inline int io_mode(const YggIO &io) {
     return io.gen ? kModeGenerate : ((io.digest || io.nll) ? kModeScore : kModeRun);
 }

@@ -135,6 +135,16 @@ class Yggdrasil:
         check(_lib.lib().ygg_kernel_name(self._h, B, T, 1 if generate else (2 if score else 0), buf, len(buf)))
         return buf.value.decode()
 
+    def spec_stats(self, reset: bool = False) -> dict:
+        """Counters of generation with speculating helpers (one stream): steps taken from a helper's slot, steps the
+        stream computed itself, helper wavefronts that served a step, that started, that stopped waiting. Waits for
+        the device."""
+        import torch
+        torch.cuda.synchronize(self.device)
+        out = (ctypes.c_uint64 * 5)()
+        _lib.check(_lib.lib().ygg_spec_stats(self._h, out, int(reset)))
+        return dict(zip(("hits", "misses", "helpers_served", "helpers_started", "helpers_timed_out"), list(out)))
+
     def close(self):
         if getattr(self, "_h", None):
             self._graphs.clear()
