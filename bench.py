@@ -271,6 +271,7 @@ def main():
     ap.add_argument("--cpu-procs", type=int, default=CPU_SHARE)
     ap.add_argument("--cpu-streams", type=int, default=256, help="streams per CPU baseline process")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-float", action="store_true", help="skip the float step's batch-1 leg")
     ap.add_argument("--entry", default="run", choices=["run", "grouped"],
                     help="the timed C-ABI call: ygg_run (per-stream kernels) or ygg_run_grouped (leaf-grouped "
                          "phases, MFMA tiles from YGG_GROUP_MFMA_MIN streams)")
@@ -412,6 +413,11 @@ def main():
 
     del logits
     torch.cuda.empty_cache()
+    float_b1 = None
+    if not a.no_float and a.entry == "run":
+        float_b1 = run_float_batch1()
+        log(f"float batch-1: {float_b1}")
+        torch.cuda.empty_cache()
     cpu = None
     if not a.no_cpu:
         t0 = time.time()
@@ -441,6 +447,7 @@ def main():
         "softmax": sm,
         "grouped_graph": grouped_graph,
         "batch1": batch1,
+        "float_batch1": float_b1,
     }
     print(json.dumps(out), flush=True)
     model.close()
@@ -547,6 +554,75 @@ def run_batch1(model, w, n_tok: int, L, _lib) -> dict:
             "generate_spec": spec,
             "kernels": {"persistent_launch": model.kernel_name(1, n_tok), "graph_step": model.kernel_name(1, 1),
                         "generate": model.kernel_name(1, n_tok, generate=True)}}
+
+
+# The reference's float GPU figure: its Triton step (yggdrasil/inference_triton.py:196-212, replayed from a CUDA
+# graph) at batch 1 on the large trained model, README.md:43
+REF_FLOAT_GPU_US = 80.1
+
+
+def run_float_batch1(n_tok: int = 1024, graph_steps: int = 256) -> dict:
+    """The float step (the f32 float kernel of a .npz checkpoint, FloatYggdrasil) at batch 1, on a random checkpoint of
+    the reference's large trained shape (configs/enwik8/large.yaml: 5 layers, d_state 256, block 16, router depth
+    10, router token dim 16, input rank 64, readout rank 32, layer-input rank 64; seed 5): (a) one launch of n_tok
+    known tokens, state carried; (b) a per-token step loop (one ygg_float_run of one token, state in place) captured
+    in a hipGraph of graph_steps steps and replayed, as the reference's Triton backend replays its step."""
+    import torch
+    from yggdrasil_amd import _lib
+    from yggdrasil_amd.float_model import FloatSpec, FloatYggdrasil, float_layers, from_params, random_params
+    spec = FloatSpec(d_state=256, block_size=16, router_depth=10, vocab=256, n_layers=5, router_token_dim=16,
+                     input_rank=64, readout_rank=32, layer_input_rank=64)
+    # the checkpoint's arrays in memory (random_checkpoint's, without the 0.8 GB file), tables by matrix products
+    t0 = time.time()
+    raw, ob = from_params(random_params(spec, 5))
+    fm = FloatYggdrasil(float_layers(raw, blas=True), ob, precision=32)
+    del raw
+    log(f"float model (large shape) built in {time.time() - t0:.1f}s")
+    from yggdrasil_amd import synth
+    L = _lib.lib()
+    dev = fm.device
+    x = torch.as_tensor(synth.zipf_bytes(1, n_tok, 11)[0], dtype=torch.int32, device=dev).contiguous()
+    st = fm.init_state(1)
+    lg = torch.empty(n_tok, fm.classes, dtype=torch.float32, device=dev)
+    stream = torch.cuda.current_stream()
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    ptr = lambda t, off=0: ctypes.c_void_p(t.data_ptr() + off)  # noqa: E731
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    _lib.check(L.ygg_float_run(fm._h, ptr(x), 1, n_tok, ptr(st), ptr(lg), None, None, sp))
+    st.zero_()
+    torch.cuda.synchronize()
+    e0.record(stream)
+    _lib.check(L.ygg_float_run(fm._h, ptr(x), 1, n_tok, ptr(st), ptr(lg), None, None, sp))
+    e1.record(stream)
+    torch.cuda.synchronize()
+    run_us = e0.elapsed_time(e1) * 1e3 / n_tok
+    ref = lg[:graph_steps].clone()
+    g = torch.cuda.CUDAGraph()
+    st.zero_()
+    with torch.cuda.graph(g):
+        cs = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        for t in range(graph_steps):
+            _lib.check(L.ygg_float_run(fm._h, ptr(x, 4 * t), 1, 1, ptr(st), ptr(lg, 4 * t * fm.classes), None, None,
+                                       cs))
+    st.zero_()
+    g.replay()
+    torch.cuda.synchronize()
+    st.zero_()
+    torch.cuda.synchronize()
+    e0.record(stream)
+    g.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    step_us = e0.elapsed_time(e1) * 1e3 / graph_steps
+    same = bool(torch.equal(lg[:graph_steps], ref))
+    del g
+    fm.close()
+    return {"model": "random f32 checkpoint of configs/enwik8/large.yaml's shape (5 layers, d_state 256, D 10, R 32, "
+                     "R2 64, input rank 64; seed 5)",
+            "tokens": n_tok, "us_per_token_run": round(run_us, 3), "us_per_token_graph_step": round(step_us, 3),
+            "graph_steps_per_graph": graph_steps, "graph_logits_equal_run": same,
+            "reference_triton_us_per_token": REF_FLOAT_GPU_US, "reference_source": "README.md:43 (GPU µs/tok)",
+            "kernel": "ygg::float_kernel<float>"}
 
 
 if __name__ == "__main__":

@@ -240,4 +240,28 @@ def test_generate_errors(gmodel, monkeypatch):
     assert model.take_errors() == 1
     o = outb.cpu().numpy()
     assert (o[1] == -7).all() and (o[0] >= 0).all()
+    # 10 tokens: the speculating build (one stream), the deep build (B at most the CUs) and the generate build past
+    # it (more streams): a first token out of range stops that stream only (bit 0, its outputs untouched), the
+    # others generate the oracle's argmax loop
+    orc = O.Oracle(gmodel)
+    cus = model.info.deep_max_streams
+    assert cus > 0
+    for B in (1, 5, cus + 3):
+        kname = model.kernel_name(B, 10, generate=True)
+        _say(f"bad first token, B {B}: {kname}")
+        rng = np.random.default_rng(B)
+        good = rng.integers(0, 256, B).astype(np.int32)
+        bad = B // 2
+        first = torch.as_tensor(good, device=model.device).clone()
+        first[bad] = 999
+        st = model.init_state(B)
+        outb = torch.full((B, 10), -7, dtype=torch.int32, device=model.device)
+        _lib.check(L.ygg_generate(model._h, p(first), B, 10, p(st), ctypes.c_float(0.0), 0, 0, p(outb), None, s))
+        assert model.take_errors() == 1, B
+        o = outb.cpu().numpy()
+        assert (o[bad] == -7).all(), B
+        keep = np.array([b for b in range(B) if b != bad], dtype=np.int64)
+        if keep.size:
+            want, _ = _oracle_greedy(orc, good[keep][:, None], 10)
+            np.testing.assert_array_equal(o[keep], want, err_msg=f"B {B}")
     model.close()

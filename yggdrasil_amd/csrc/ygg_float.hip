@@ -1,13 +1,17 @@
 // The float step of Yggdrasil (yggdrasil/inference.py:42-74): the inference model of a float checkpoint, in f32 for
 // serving (the role of the Triton backend, yggdrasil/inference_triton.py) or f64 (the precision cpu/export.py
-// calibrates in, cpu/export.py:101-153). One 64-lane wavefront runs one stream through every layer of every token of
-// a launch; the states of all layers stay in LDS.
+// calibrates in, cpu/export.py:101-153). One workgroup of 256 threads runs one stream through every layer of every
+// token of a launch; the states of all layers stay in LDS.
 //
 // Per token x and layer l (expert r = x in the token layer, else the router's leaf):
 //   route:   node = 1 .. 2^D - 1 (heap), right iff [router_embed[x]; rms(h_below)] . W[node] + b[node] > 0
 //   update:  h = T_r[x];  h += U'_r (V' rms(h_below));  h += A_r h_old   (A_r block-diagonal)
 //   readout: z = P_r h;   logits += Q z
-// and rms(h) = h / sqrt(mean(h^2) + 1e-6) feeds the next layer. Lane i owns coordinates i, i + 64, ...
+// and rms(h) = h / sqrt(mean(h^2) + 1e-6) feeds the next layer.
+// Work split: the router descends in rounds of up to 4 levels, 16 groups of 16 threads each forming one node's dot of
+// the round's subtree (every load of a round issued at once, the input row held in registers for the layer); the
+// layer input takes 4 threads per row of V'; thread i owns coordinate i of the update (its table entry, U' row and A
+// row loaded together); the readout takes 256 / R threads per row of P; thread c owns class c of the logits.
 #include <hip/hip_runtime.h>
 
 #include <cstdarg>
@@ -27,19 +31,21 @@ int set_error(int code, const char *msg);
 
 namespace {
 
-constexpr int kMaxN = 256, kMaxR = 64, kMaxR2 = 64, kMaxClasses = 256, kMaxF = 256;
+constexpr int kMaxN = 256, kMaxR = 64, kMaxR2 = 64, kMaxClasses = 256, kMaxF = 256, kMaxB = 16;
 constexpr double kRmsEps = 1e-6;   // yggdrasil/config.py:8
 
+// Device layouts: the arrays a thread reads a row of at each step of a dot are stored transposed from the checkpoint's,
+// so that the lanes of a wavefront read consecutive addresses at every step.
 template <typename T> struct FloatLayerDev {
     const T *table;          // token layer [V][n] (T_x[x]); routed [E][V][n]
-    const T *A;              // [E][n/b][b][b] or null
+    const T *A;              // [E][n/b][b (column j)][b (row i)] (each block transposed) or null
     const T *P;              // [E][R][n]
-    const T *Q;              // [classes][R]
+    const T *Q;              // [R][classes] (transposed)
     const T *emb;            // routed: [V][F]
     const T *W;              // routed: [nodes][F + n] (router_state) or [nodes][F]
     const T *bias;           // routed: [nodes]
-    const T *Vd;             // [R2][n] or null
-    const T *Up;             // [E][n][R2] or null
+    const T *Vd;             // [n][R2] (transposed) or null
+    const T *Up;             // [E][R2][n] (each expert's matrix transposed) or null
 };
 
 template <typename T> struct FloatDevModel {
@@ -48,6 +54,8 @@ template <typename T> struct FloatDevModel {
     uint32_t *err;
     FloatLayerDev<T> layers[YGG_MAX_LAYERS];
 };
+
+constexpr int kFThreads = 256;
 
 template <typename T> __device__ __forceinline__ T wave_sum(T v) {
     for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
@@ -59,33 +67,81 @@ template <typename T> __device__ __forceinline__ T wave_max(T v) {
     return v;
 }
 
+// the sum over aligned groups of G lanes (G a power of 2, at most 64), in every lane of the group
+template <int G, typename T> __device__ __forceinline__ T group_sum(T v) {
+    for (int o = G / 2; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+template <typename T> __device__ __forceinline__ T group_sum_n(T v, int g) {
+    for (int o = g / 2; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+template <typename T> __device__ __forceinline__ T group_max_n(T v, int g) {
+    for (int o = g / 2; o >= 1; o >>= 1) v = fmax(v, __shfl_xor(v, o));
+    return v;
+}
+
 // atomic max of a non-negative double (its bit pattern orders as an unsigned integer)
 __device__ __forceinline__ void atomic_max_nonneg(double *p, double v) {
     atomicMax((unsigned long long *)p, (unsigned long long)__double_as_longlong(v));
 }
 
+// the sum of v over the workgroup (red: 4 slots of LDS; two barriers)
+template <typename T> __device__ __forceinline__ T block_sum(T v, T *red, int tid) {
+    v = wave_sum(v);
+    if ((tid & 63) == 0) red[tid >> 6] = v;
+    __syncthreads();
+    const T s = (red[0] + red[1]) + (red[2] + red[3]);
+    __syncthreads();
+    return s;
+}
+
+constexpr int kRouteGroup = 16;                           // threads per node of a router round
+constexpr int kRouteElems = (kMaxF + kMaxN) / kRouteGroup; // router inputs per thread at most
+
 // stats (calibration maxima, cpu/export.py:127-153), per layer: [|h|, |V' rms(h_below)|, |P_r h|, |h| per 16
 // coordinates (n/16), |P_r h| per row (R)]
-template <typename T>
-__global__ __launch_bounds__(64) void float_kernel(const FloatDevModel<T> m, const int32_t *__restrict__ tokens,
-                                                   int Tn, T *__restrict__ state, T *__restrict__ logits,
-                                                   int32_t *__restrict__ leaves, double *__restrict__ stats) {
+// NS, RS, R2S, BS: the state width, readout rank, layer-input rank and block size at compile time (the reference's
+// trained shapes: every row length a constant), or 0 for the model's (any shape the loader takes)
+// (one wavefront per SIMD: the unrolled row loads of a thread are its registers)
+template <typename T, int NS = 0, int RS = 0, int R2S = 0, int BS = 0>
+__global__ __launch_bounds__(kFThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void float_kernel(
+    const FloatDevModel<T> m, const int32_t *__restrict__ tokens, int Tn, T *__restrict__ state,
+    T *__restrict__ logits, int32_t *__restrict__ leaves, double *__restrict__ stats) {
+    constexpr int MN = NS ? NS : kMaxN, MR = RS ? RS : kMaxR, MR2 = R2S ? R2S : kMaxR2, MB = BS ? BS : kMaxB;
     __shared__ T hs[YGG_MAX_LAYERS][kMaxN];   // states
     __shared__ T bl[kMaxN];                   // rms(h) of the layer below
     __shared__ T hn[kMaxN];                   // the new state of the current layer
     __shared__ T zl[kMaxR2];
     __shared__ T zs[kMaxR];
+    __shared__ T zp[4][kMaxR2];               // the layer input's partial sums, per quarter of the coordinates
+    __shared__ T red[4];
+    __shared__ int dec[16];                   // a router round's decisions, by breadth-first node of its subtree
     __shared__ double gmax[YGG_MAX_LAYERS][kMaxN / 16];
 
-    const int s = blockIdx.x, lane = threadIdx.x;
-    const int L = m.L, n = m.n, b = m.b, V = m.V, C = m.classes, R = m.R, R2 = m.R2, F = m.F;
+    const int s = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
+    const int L = m.L, n = NS ? NS : m.n, b = BS ? BS : m.b, V = m.V, C = m.classes, R = RS ? RS : m.R,
+              R2 = R2S ? R2S : m.R2, F = m.F;
+    const int width = F + (m.router_state ? n : 0);
+    // readout: TPR threads per row of P (a power of 2 of at most 64 lanes), its coordinates u, u + TPR, ...
+    int Rp = 1;
+    while (Rp < R) Rp <<= 1;
+    const int TPR = kFThreads / Rp > 64 ? 64 : kFThreads / Rp;
+    const int prow = tid / TPR, pu = tid % TPR;
+    // layer input: wave q takes the quarter q of the coordinates, lane k row k of V'
+    const int vrow = lane, vq = tid >> 6, vlen = n / 4;
+    // router rounds: group g of kRouteGroup threads forms node g of the round's subtree
+    const int rg = tid / kRouteGroup, rl = tid % kRouteGroup;
+
     T *st = state + (size_t)s * L * n;
     for (int l = 0; l < L; l++)
-        for (int i = lane; i < n; i += 64) hs[l][i] = st[(size_t)l * n + i];
+        for (int i = tid; i < n; i += kFThreads) hs[l][i] = st[(size_t)l * n + i];
     for (int l = 0; l < L; l++)
-        for (int g = lane; g < n / 16; g += 64) gmax[l][g] = 0.0;
+        for (int g = tid; g < n / 16; g += kFThreads) gmax[l][g] = 0.0;
+    // per-thread maxima (calibration runs only): |h| (thread i's coordinate), |zl| (row vrow's reducer), |z| (row
+    // prow's reducer)
     double smax[YGG_MAX_LAYERS], vmax[YGG_MAX_LAYERS], zmax[YGG_MAX_LAYERS];
-    for (int l = 0; l < L; l++) smax[l] = vmax[l] = zmax[l] = 0.0;
+    for (int l = 0; l < YGG_MAX_LAYERS; l++) smax[l] = vmax[l] = zmax[l] = 0.0;
     const int sstride = 3 + n / 16 + R;
     __syncthreads();
 
@@ -93,111 +149,161 @@ __global__ __launch_bounds__(64) void float_kernel(const FloatDevModel<T> m, con
     for (int t = 0; t < Tn; t++) {
         const int x = __builtin_amdgcn_readfirstlane(tok[t]);
         if (x < 0 || x >= V) {
-            if (lane == 0) atomicOr(m.err, 1u);
+            if (tid == 0) atomicOr(m.err, 1u);
             break;
         }
-        T lg[kMaxClasses / 64];
-#pragma unroll
-        for (int u = 0; u < kMaxClasses / 64; u++) {
-            const int c = lane + 64 * u;
-            lg[u] = c < C ? m.output_bias[c] : T(0);
-        }
+        T lg = tid < C ? m.output_bias[tid] : T(0);
         for (int l = 0; l < L; l++) {
             const FloatLayerDev<T> &y = m.layers[l];
             int r = x;
             if (l > 0) {
-                // router descent over f = [router_embed[x]; rms(h_below)]
+                // router descent over f = [router_embed[x]; rms(h_below)], in rounds of up to 4 levels
+                T f[kRouteElems];
                 const T *e = y.emb + (size_t)x * F;
-                const int width = F + (m.router_state ? n : 0);
-                int node = 0;
-                for (int d = 0; d < m.D; d++) {
-                    const T *w = y.W + (size_t)node * width;
+#pragma unroll
+                for (int k = 0; k < kRouteElems; k++) {
+                    const int i = rl + kRouteGroup * k;
+                    f[k] = i < F ? e[i] : (i < width ? bl[i - F] : T(0));
+                }
+                int root = 0;
+                for (int d0 = 0; d0 < m.D; d0 += 4) {
+                    const int h = m.D - d0 < 4 ? m.D - d0 : 4;
+                    const int nn = (1 << h) - 1;
+                    // node rg of the subtree: depth k = floor(log2(rg + 1)), path p = rg + 1 - 2^k
+                    const int kdep = 31 - __builtin_clz(rg + 1), path = rg + 1 - (1 << kdep);
+                    const int node = ((root + 1) << kdep) - 1 + path;
                     T p = T(0);
-                    for (int i = lane; i < width; i += 64) p += (i < F ? e[i] : bl[i - F]) * w[i];
-                    p = wave_sum(p) + y.bias[node];
-                    node = 2 * node + 1 + (p > T(0) ? 1 : 0);
+                    if (rg < nn) {
+                        const T *w = y.W + (size_t)node * width;
+                        T wl[kRouteElems];
+#pragma unroll
+                        for (int k = 0; k < kRouteElems; k++) {
+                            const int i = rl + kRouteGroup * k;
+                            wl[k] = i < width ? w[i] : T(0);
+                        }
+#pragma unroll
+                        for (int k = 0; k < kRouteElems; k++) p += f[k] * wl[k];
+                    }
+                    p = group_sum<kRouteGroup>(p);
+                    if (rg < nn && rl == 0) dec[rg] = (p + y.bias[node]) > T(0) ? 1 : 0;
+                    __syncthreads();
+                    int q = 0;
+                    for (int k = 0; k < h; k++) q = 2 * q + dec[(1 << k) - 1 + q];
+                    root = ((root + 1) << h) - 1 + q;
+                    __syncthreads();
                 }
-                r = node - ((1 << m.D) - 1);
-            }
-            // h = T_r[x] + U'_r (V' rms(h_below)) + A_r h_old
-            const T *trow = l == 0 ? y.table + (size_t)x * n : y.table + ((size_t)r * V + x) * n;
-            if (l > 0 && y.Vd) {
-                if (lane < R2) {
+                r = root - ((1 << m.D) - 1);
+                // the layer input zl = V' rms(h_below): wave q sums its quarter of the coordinates for row k = lane
+                // (every load issued at once), the four partials then add in quarter order
+                if (y.Vd) {
+                    const bool vlive = vrow < R2;
+                    T vv[MN / 4];
+                    if (vlive) {
+                        const T *vc = y.Vd + (size_t)(vq * vlen) * R2 + vrow;
+#pragma unroll
+                        for (int i = 0; i < MN / 4; i++) vv[i] = i < vlen ? vc[(size_t)i * R2] : T(0);
+                    }
                     T a = T(0);
-                    const T *vr = y.Vd + (size_t)lane * n;
-                    for (int i = 0; i < n; i++) a += vr[i] * bl[i];
-                    zl[lane] = a;
-                    vmax[l] = fmax(vmax[l], (double)fabs(a));
+                    if (vlive) {
+#pragma unroll
+                        for (int i = 0; i < MN / 4; i++)
+                            if (i < vlen) a += vv[i] * bl[vq * vlen + i];
+                        zp[vq][vrow] = a;
+                    }
+                    __syncthreads();
+                    if (tid < R2) {
+                        const T z = ((zp[0][tid] + zp[1][tid]) + zp[2][tid]) + zp[3][tid];
+                        zl[tid] = z;
+                        if (stats) vmax[l] = fmax(vmax[l], (double)fabs(z));
+                    }
+                    __syncthreads();
                 }
-                __syncthreads();
             }
-            for (int i = lane; i < n; i += 64) {
+            // h = T_r[x] + U'_r zl + A_r h_old, thread i for coordinate i
+            T hv = T(0);
+            if (tid < n) {
+                // (the table entry, U' row and A row of coordinate i loaded together; sums in index order)
+                const int i = tid;
+                const T *trow = l == 0 ? y.table + (size_t)x * n : y.table + ((size_t)r * V + x) * n;
+                const bool up = l > 0 && y.Up != nullptr, ta = y.A != nullptr;
+                const int g = i / b, ii = i % b;
+                const T *u = up ? y.Up + (size_t)r * R2 * n + i : nullptr;                    // column i
+                const T *acol = ta ? y.A + ((size_t)r * (n / b) + g) * b * b + ii : nullptr;  // row ii of block g
+                T uw[MR2], aw[MB];
+#pragma unroll
+                for (int k = 0; k < MR2; k++) uw[k] = (up && k < R2) ? u[(size_t)k * n] : T(0);
+#pragma unroll
+                for (int j = 0; j < MB; j++) aw[j] = (ta && j < b) ? acol[j * b] : T(0);
                 T h = trow[i];
-                if (l > 0 && y.Up) {
-                    const T *u = y.Up + ((size_t)r * n + i) * R2;
+                if (up) {
                     T a = T(0);
-                    for (int k = 0; k < R2; k++) a += u[k] * zl[k];
+#pragma unroll
+                    for (int k = 0; k < MR2; k++)
+                        if (k < R2) a += uw[k] * zl[k];
                     h = h + a;
                 }
-                if (y.A) {
-                    const int g = i / b, ii = i % b;
-                    const T *arow = y.A + (((size_t)r * (n / b) + g) * b + ii) * b;
+                if (ta) {
                     T a = T(0);
-                    for (int j = 0; j < b; j++) a += arow[j] * hs[l][g * b + j];
+#pragma unroll
+                    for (int j = 0; j < MB; j++)
+                        if (j < b) a += aw[j] * hs[l][g * b + j];
                     h = h + a;
                 }
-                hn[i] = h;
+                hv = h;
+                if (stats) smax[l] = fmax(smax[l], (double)fabs(h));
             }
+            // (every thread has read hs[l] before it is overwritten below)
+            const T ss = block_sum(tid < n ? hv * hv : T(0), red, tid);
+            if (tid < n) {
+                hn[tid] = hv;
+                hs[l][tid] = hv;
+            }
+            if (stats && tid < n) {
+                // |h| per 16 coordinates: 16 consecutive threads
+                const double a = group_max_n((double)fabs(hv), 16);
+                if ((tid & 15) == 0) gmax[l][tid >> 4] = fmax(gmax[l][tid >> 4], a);
+            }
+            const T rinv = T(1) / sqrt(ss / T(n) + T(kRmsEps));
+            if (tid < n) bl[tid] = hv * rinv;
             __syncthreads();
-            T ss = T(0);
-            double hm = 0.0;
-            for (int i = lane; i < n; i += 64) {
-                const T h = hn[i];
-                hs[l][i] = h;
-                ss += h * h;
-                hm = fmax(hm, (double)fabs(h));
-            }
-            smax[l] = fmax(smax[l], hm);
-            if (stats)
-                for (int g = lane; g < n / 16; g += 64) {
-                    double a = 0.0;
-                    for (int i = 0; i < 16; i++) a = fmax(a, (double)fabs(hn[16 * g + i]));
-                    gmax[l][g] = fmax(gmax[l][g], a);
-                }
-            // z = P_r h (lane j < R), logits += Q z
-            if (lane < R) {
-                const T *pr = y.P + ((size_t)r * R + lane) * n;
+            // z = P_r h: TPR threads per row, coordinates pu, pu + TPR, ... (every load issued at once)
+            if (prow < R) {
+                const T *pr = y.P + ((size_t)r * R + prow) * n;
+                constexpr int PE = RS ? (NS * RS + kFThreads - 1) / kFThreads : MN / 4;   // coordinates per thread
+                T pw[PE];
+#pragma unroll
+                for (int e = 0; e < PE; e++) pw[e] = pu + TPR * e < n ? pr[pu + TPR * e] : T(0);
                 T a = T(0);
-                for (int i = 0; i < n; i++) a += pr[i] * hn[i];
-                zs[lane] = a;
-                zmax[l] = fmax(zmax[l], (double)fabs(a));   // lane j holds row j's maximum
-            }
-            const T rinv = T(1) / sqrt(wave_sum(ss) / T(n) + T(kRmsEps));
-            __syncthreads();
-            for (int i = lane; i < n; i += 64) bl[i] = hn[i] * rinv;
 #pragma unroll
-            for (int u = 0; u < kMaxClasses / 64; u++) {
-                const int c = lane + 64 * u;
-                if (c < C) {
-                    const T *q = y.Q + (size_t)c * R;
-                    T a = T(0);
-                    for (int j = 0; j < R; j++) a += q[j] * zs[j];
-                    lg[u] = lg[u] + a;
+                for (int e = 0; e < PE; e++)
+                    if (pu + TPR * e < n) a += pw[e] * hn[pu + TPR * e];
+                a = group_sum_n(a, TPR);
+                if (pu == 0) {
+                    zs[prow] = a;
+                    if (stats) zmax[l] = fmax(zmax[l], (double)fabs(a));   // row prow's reducer holds its maximum
                 }
             }
-            if (leaves && lane == 0) leaves[((size_t)s * Tn + t) * L + l] = r;
+            __syncthreads();
+            // logits += Q z, thread c for class c
+            if (tid < C) {
+                const T *q = y.Q + tid;                                    // column c of Q^T
+                T qw[MR];
+#pragma unroll
+                for (int j = 0; j < MR; j++) qw[j] = j < R ? q[(size_t)j * C] : T(0);
+                T a = T(0);
+#pragma unroll
+                for (int j = 0; j < MR; j++)
+                    if (j < R) a += qw[j] * zs[j];
+                lg = lg + a;
+            }
+            if (leaves && tid == 0) leaves[((size_t)s * Tn + t) * L + l] = r;
             __syncthreads();
         }
-        if (logits) {
-            T *o = logits + ((size_t)s * Tn + t) * C;
-#pragma unroll
-            for (int u = 0; u < kMaxClasses / 64; u++)
-                if (lane + 64 * u < C) o[lane + 64 * u] = lg[u];
-        }
+        if (logits && tid < C) logits[((size_t)s * Tn + t) * C + tid] = lg;
     }
     __syncthreads();
     for (int l = 0; l < L; l++)
-        for (int i = lane; i < n; i += 64) st[(size_t)l * n + i] = hs[l][i];
+        for (int i = tid; i < n; i += kFThreads) st[(size_t)l * n + i] = hs[l][i];
     if (stats) {
         for (int l = 0; l < L; l++) {
             const double a = wave_max(smax[l]), v = wave_max(vmax[l]), z = wave_max(zmax[l]);
@@ -206,8 +312,9 @@ __global__ __launch_bounds__(64) void float_kernel(const FloatDevModel<T> m, con
                 atomic_max_nonneg(&stats[(size_t)l * sstride + 1], v);
                 atomic_max_nonneg(&stats[(size_t)l * sstride + 2], z);
             }
-            for (int g = lane; g < n / 16; g += 64) atomic_max_nonneg(&stats[(size_t)l * sstride + 3 + g], gmax[l][g]);
-            if (lane < R) atomic_max_nonneg(&stats[(size_t)l * sstride + 3 + n / 16 + lane], zmax[l]);
+            for (int g = tid; g < n / 16; g += kFThreads)
+                atomic_max_nonneg(&stats[(size_t)l * sstride + 3 + g], gmax[l][g]);
+            if (prow < R && pu == 0) atomic_max_nonneg(&stats[(size_t)l * sstride + 3 + n / 16 + prow], zmax[l]);
         }
     }
 }
@@ -256,12 +363,13 @@ template <typename T> int upload(const ygg_float_desc *d, int device, ygg_fmodel
     const int L = d->n_layers, n = d->d_state, b = d->block_size, V = d->vocab, C = d->classes, D = d->router_depth,
               R = d->readout_rank, R2 = d->layer_input_rank, F = d->router_token_dim;
     const int64_t E = (int64_t)1 << D, nodes = E - 1, width = F + (d->router_state ? n : 0);
-    struct Part { const double *src; int64_t count; size_t off; };
+    // a part is `outer` matrices of rows x cols, stored as given (rows = 0) or each transposed
+    struct Part { const double *src; int64_t count; size_t off; int64_t outer, rows, cols; };
     std::vector<Part> parts;
     size_t total = 256;   // the error word first
-    auto add = [&](const double *src, int64_t count) -> int {
+    auto add = [&](const double *src, int64_t count, int64_t rows = 0, int64_t cols = 0) -> int {
         if (!src || count <= 0) return -1;
-        parts.push_back({src, count, total});
+        parts.push_back({src, count, total, rows ? count / (rows * cols) : 0, rows, cols});
         total += ((size_t)count * sizeof(T) + 255) / 256 * 256;
         return (int)parts.size() - 1;
     };
@@ -274,14 +382,14 @@ template <typename T> int upload(const ygg_float_desc *d, int device, ygg_fmodel
         const int64_t El = l == 0 ? V : E;
         Idx &k = idx[l];
         k.table = add(y.table, l == 0 ? (int64_t)V * n : El * V * n);
-        k.A = add(y.transition, El * n * b);
+        k.A = add(y.transition, El * n * b, b, b);
         k.P = add(y.readout, El * R * n);
-        k.Q = add(y.unembed, (int64_t)C * R);
+        k.Q = add(y.unembed, (int64_t)C * R, C, R);
         k.emb = l ? add(y.router_embed, (int64_t)V * F) : -1;
         k.W = l ? add(y.router_weight, nodes * width) : -1;
         k.bias = l ? add(y.router_bias, nodes) : -1;
-        k.Vd = (l && R2) ? add(y.layer_input_down, (int64_t)R2 * n) : -1;
-        k.Up = (l && R2) ? add(y.layer_input_proj, El * n * R2) : -1;
+        k.Vd = (l && R2) ? add(y.layer_input_down, (int64_t)R2 * n, R2, n) : -1;
+        k.Up = (l && R2) ? add(y.layer_input_proj, El * n * R2, n, R2) : -1;
         if (k.table < 0 || k.P < 0 || k.Q < 0 || (l && (k.emb < 0 || k.W < 0 || k.bias < 0)) ||
             (l && R2 && (k.Vd < 0 || k.Up < 0)))
             return fail(YGG_ERR_ARG, "float model: layer %d lacks an array", l);
@@ -298,7 +406,14 @@ template <typename T> int upload(const ygg_float_desc *d, int device, ygg_fmodel
     }
     for (const Part &p : parts) {
         T *dst = (T *)(host.data() + p.off);
-        for (int64_t i = 0; i < p.count; i++) dst[i] = (T)p.src[i];
+        if (!p.rows) {
+            for (int64_t i = 0; i < p.count; i++) dst[i] = (T)p.src[i];
+            continue;
+        }
+        const int64_t mat = p.rows * p.cols;
+        for (int64_t o = 0; o < p.outer; o++)
+            for (int64_t r = 0; r < p.rows; r++)
+                for (int64_t c = 0; c < p.cols; c++) dst[o * mat + c * p.rows + r] = (T)p.src[o * mat + r * p.cols + c];
     }
     DeviceGuard g;
     HIP_TRY(g.set(device));
@@ -335,7 +450,7 @@ int ygg_float_load(const ygg_float_desc *d, int precision, int device, ygg_fmode
     if (!d) return fail(YGG_ERR_ARG, "desc is NULL");
     if (precision != 32 && precision != 64) return fail(YGG_ERR_ARG, "precision %d: 32 or 64", precision);
     const int L = d->n_layers, n = d->d_state, b = d->block_size;
-    if (L < 1 || L > YGG_MAX_LAYERS || n < 16 || n > kMaxN || n % 16 || b < 1 || n % b || d->vocab < 1 ||
+    if (L < 1 || L > YGG_MAX_LAYERS || n < 16 || n > kMaxN || n % 16 || b < 1 || b > kMaxB || n % b || d->vocab < 1 ||
         d->classes < 1 || d->classes > kMaxClasses || d->readout_rank < 1 || d->readout_rank > kMaxR ||
         d->layer_input_rank < 0 || d->layer_input_rank > kMaxR2 || (L > 1 && (d->router_depth < 1 ||
         d->router_depth > 20 || d->router_token_dim < 0 || d->router_token_dim > kMaxF)))
@@ -361,11 +476,19 @@ int ygg_float_run(const ygg_fmodel *m, const int32_t *d_tokens, int B, int T, vo
     if (!d_state || (T > 0 && !d_tokens)) return fail(YGG_ERR_ARG, "tokens or state is NULL");
     DeviceGuard g;
     HIP_TRY(g.set(m->device));
-    if (m->precision == 32)
-        hipLaunchKernelGGL(float_kernel<float>, dim3(B), dim3(64), 0, (hipStream_t)stream, m->m32, d_tokens, T,
-                           (float *)d_state, (float *)d_logits, d_leaves, d_stats);
-    else
-        hipLaunchKernelGGL(float_kernel<double>, dim3(B), dim3(64), 0, (hipStream_t)stream, m->m64, d_tokens, T,
+    if (m->precision == 32) {
+        // the reference's trained shapes (configs/*/{small,medium,large}.yaml: block 16) have builds of their own
+        const FloatDevModel<float> &fm = m->m32;
+        auto go = [&](auto kernel) {
+            hipLaunchKernelGGL(kernel, dim3(B), dim3(kFThreads), 0, (hipStream_t)stream, fm, d_tokens, T,
+                               (float *)d_state, (float *)d_logits, d_leaves, d_stats);
+        };
+        if (fm.b == 16 && fm.n == 64 && fm.R == 8 && fm.R2 == 16) go(float_kernel<float, 64, 8, 16, 16>);
+        else if (fm.b == 16 && fm.n == 128 && fm.R == 16 && fm.R2 == 32) go(float_kernel<float, 128, 16, 32, 16>);
+        else if (fm.b == 16 && fm.n == 256 && fm.R == 32 && fm.R2 == 64) go(float_kernel<float, 256, 32, 64, 16>);
+        else go(float_kernel<float>);
+    } else
+        hipLaunchKernelGGL(float_kernel<double>, dim3(B), dim3(kFThreads), 0, (hipStream_t)stream, m->m64, d_tokens, T,
                            (double *)d_state, (double *)d_logits, d_leaves, d_stats);
     HIP_TRY(hipGetLastError());
     return YGG_OK;

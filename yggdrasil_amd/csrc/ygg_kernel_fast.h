@@ -846,6 +846,7 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
     __shared__ __attribute__((aligned(16))) int8_t zlw[W][SH::ZL];
     __shared__ __attribute__((aligned(16))) int8_t zqw[W][SH::ZQ];
     __shared__ __attribute__((aligned(16))) int8_t spw[SPEC ? kFastWaves : 1][SPEC ? SLY::TB : 16];
+    __shared__ uint32_t pubw[SPEC ? SLY::PW + 2 : 1];     // SPEC, a helper workgroup: the publication it serves
 
     // the wavefront index, stream, tokens and leaves are uniform over a wavefront: kept in scalar registers. With one
     // stream per workgroup (W = 1) wavefronts 1-3 stage the LDS tables and then leave.
@@ -859,7 +860,8 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
             if constexpr (DEEP) load_round2<N, L, 64 * kFastWaves>(W1s, m, tid);
             __syncthreads();
             spec_helper<SH, L, GROUP, DEEP>(m, io, T, (blockIdx.x - 1) * kFastWaves + wv,
-                                            spec_helper_waves(io.spec_helpers), S, GT, &W1s[0][0], qsw[wv], spw[wv], lane);
+                                            spec_helper_waves(io.spec_helpers), S, GT, &W1s[0][0], qsw[wv], spw[wv], lane,
+                                            pubw, blockIdx.x % kSpecPubCopies, true, wv);
             return;
         }
     }
@@ -892,7 +894,7 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
             if constexpr (SPEC)
                 spec_helper<SH, L, GROUP, DEEP>(m, io, T, io.spec_helpers * kFastWaves + wv - 1,
                                                 spec_helper_waves(io.spec_helpers), S, GT, &W1s[0][0], qsw[wv],
-                                                spw[wv], lane);
+                                                spw[wv], lane, pubw, 0, false, wv);
             return;
         }
     } else {
@@ -934,12 +936,18 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
         // SPEC: x's slot, which holds this step's layers 0 .. SPS - 1 and layer SPS's leaf and layer input (a short
         // wait after a step that had its slot, a single look after one that did not)
         bool hit = false;
+        Gather<SH, FACT> Gs;       // SPEC with the slot: layer SPS's record, gathered as soon as its leaf is known
+        int rs = 0;
         if constexpr (SPEC) {
             if (t > 0) {
-                hit = spec_take<SH, SPS>(io, x, t, T, qs, sps, lane, spec_prev ? 400 : 30);
+                hit = spec_take<SH, SPS>(io, x, t, qs, sps, lane, spec_prev ? 400 : 30, rs);
                 spec_prev = hit;
                 spec_hits += hit ? 1 : 0;
                 spec_misses += hit ? 0 : 1;
+                // (a slot is taken only with every unit of this step: its leaf is one a helper found; the mask keeps
+                // the record address in the layer whatever the word holds)
+                rs &= m.E - 1;
+                if (hit) gather<SH, GROUP, true, FACT>(Gs, m.layers[SPS], rs, x, true, lane, K4);
             }
         }
         // thresholds of the first router round of every routed layer (SPEC with the slot: of the layers after SPS)
@@ -962,8 +970,11 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
         float lg[4];
 #pragma unroll
         for (int u = 0; u < 4; u++) lg[u] = 4 * lane + u < VP ? m.output_bias[4 * lane + u] : 0.0f;
-        // SPEC with the slot: the unembedding terms of layers 0 .. SPS - 1 from its readouts, in layer order
+        // SPEC with the slot: publish its states for the next step's helpers (after this step's loads: the waits
+        // for them then leave the stores outstanding), and the unembedding terms of layers 0 .. SPS - 1 from its
+        // readouts, in layer order
         if constexpr (SPEC) {
+            if (hit && t + 1 < T) spec_publish<SH, SPS>(io, t, qs, lane);
             if (hit && 4 * lane < VP) {
 #pragma unroll
                 for (int l = 0; l < SPS; l++) {
@@ -1008,11 +1019,9 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
             int r = x;
             float rho = 0.0f;
             uint32_t qbw[F::QW];
-            // SPEC, the slot's layer: leaf and layer input as the helper left them
+            // SPEC, the slot's layer: leaf, layer input and record as taken above
             const bool given = SPEC && hit && l == SPS;
-            // (a slot is taken only with every unit of this step: its leaf is one a helper found; the mask keeps
-            // the record address in the layer whatever the word holds)
-            if (given) r = __builtin_amdgcn_readfirstlane(*(const int32_t *)(sps + SPS * R)) & (m.E - 1);
+            if (given) r = rs;
             if (l > 0 && !given) {
                 float th = th1[0];
 #pragma unroll
@@ -1042,7 +1051,8 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
                 }
             }
             Gather<SH, FACT> G;
-            gather<SH, GROUP, true, FACT>(G, y, r, x, l > 0, lane, K4);
+            if (given) G = Gs;
+            else gather<SH, GROUP, true, FACT>(G, y, r, x, l > 0, lane, K4);
             if constexpr (W == 1)
                 if (!staged) {      // the LDS tables staged (see above)
                     __syncthreads();

@@ -44,6 +44,7 @@ template <int L> constexpr int kSpecDepth = L > 2 ? 2 : 1;
 template <class SH, int S> struct SpecLayout {
     static constexpr int PW = S * SH::N / 4;                                   // published words
     static constexpr int KP = (PW + 63) / 64;                                  // their units per lane
+    static_assert(KP * 64 <= kSpecPubUnits, "publication units");
     static constexpr int SW = S * SH::N / 4 + S * SH::R / 4 + 1 + SH::R2P / 4;  // slot words
     static constexpr int KS = (SW + 63) / 64;
     static constexpr int TB = S * SH::R + 4 + SH::ZL;    // LDS bytes of a slot after the states: zq .., leaf, zl
@@ -69,19 +70,26 @@ constexpr uint64_t kSpecPubWait = 20000;       // 200 us between two publication
 // ones at qh + S N; sp: the slot's tail (zq of layers 0 .. S - 1, layer S's leaf, its layer input). DEEP: the
 // routed layers' second-round rows are in LDS from W1 on (load_round2's layout: kR2Slots N bytes a layer, fast_kernel's
 // deep descent), else read from global memory.
+// Polling: a helper workgroup's wavefront 0 polls publication copy `copy` for the workgroup and hands each
+// publication to the others in LDS (pubw: the words, then the epoch and whether one came) behind a workgroup barrier
+// (coop); the stream workgroup's helpers, whose workgroup has a wavefront that meets no barrier, poll on their own.
 template <class SH, int L, bool GROUP, bool DEEP>
 __device__ __forceinline__ void spec_helper(const YggDevModel &m, const YggIO &io, int T, int j, int nh,
                                             const SharedTables<SH, L> &St, const GroupTablesOf<SH, L, GROUP> &GT,
-                                            const int8_t *W1, int8_t *qh, int8_t *sp, int lane) {
+                                            const int8_t *W1, int8_t *qh, int8_t *sp, int lane, uint32_t *pubw,
+                                            int copy, bool coop, int wv) {
     constexpr int N = SH::N, R = SH::R, S = kSpecDepth<L>;
     using LY = SpecLayout<SH, S>;
     using F = SH;
     uint64_t *const area = io.spec;
     const uint32_t E0 = io.spec_epoch;
-    // (no publication to serve, or no candidate: helpers past the vocabulary when every candidate has one)
-    if (T < 2 || j >= nh || (nh >= m.V && j >= m.V)) return;
+    // (no publication to serve; with a cooperative workgroup every wavefront stays to meet the barriers, one with no
+    // candidate (past the vocabulary while every candidate has one) idle)
+    if (T < 2 || (!coop && (j >= nh || (nh >= m.V && j >= m.V)))) return;
+    const bool idle = j >= nh || (nh >= m.V && j >= m.V);
     const uint32_t span = (uint32_t)T - 2;        // relative epochs of the publications worth serving
-    if (lane == 0) spec_count(area, 3, 1);
+    const uint64_t *pub = area + kSpecPub + (size_t)copy * kSpecPubUnits;
+    if (lane == 0 && !idle) spec_count(area, 3, 1);
     const int V = m.V;
     const int n2 = m.n_rounds > 1 ? 1 << (m.round_h[0] + m.round_h[1]) : 0;
     const int qj = lane >> 2, nn1 = (1 << m.round_h[0]) - 1;
@@ -92,29 +100,52 @@ __device__ __forceinline__ void spec_helper(const YggDevModel &m, const YggIO &i
     int served = 0;
     bool timed_out = false;
     while (next <= span) {
-        // the next publication: lane 0's first unit announces it, then every unit must carry its epoch
+        // the next publication: every unit in one round trip, lane 0's first naming the epoch the others must carry
+        // (coop: wavefront 0 for the workgroup)
         uint64_t u[LY::KP];
         uint32_t e = 0;
         bool got = false;
-        const uint64_t t0 = wall_clock64();
-        for (;;) {
-            const uint32_t e0 = __builtin_amdgcn_readfirstlane((uint32_t)spec_load(area + kSpecPub)) - E0;
-            if (e0 >= next && e0 <= span) {
-                bool bad = false;
+        if (!coop || wv == 0) {
+            const uint64_t t0 = wall_clock64();
+            for (;;) {
 #pragma unroll
                 for (int k = 0; k < LY::KP; k++) {
                     const int w = 64 * k + lane;
-                    u[k] = w < LY::PW ? spec_load(area + kSpecPub + w) : spec_unit(E0 + e0, 0u);
-                    bad = bad || (uint32_t)u[k] != E0 + e0;
+                    u[k] = w < LY::PW ? spec_load(pub + w) : 0ull;
                 }
-                if (lane_mask(bad) == 0ull) {
-                    e = e0;
-                    got = true;
-                    break;
+                const uint32_t tag = __builtin_amdgcn_readfirstlane((uint32_t)u[0]), e0 = tag - E0;
+                if (e0 >= next && e0 <= span) {
+                    bool bad = false;
+#pragma unroll
+                    for (int k = 0; k < LY::KP; k++) bad = bad || (64 * k + lane < LY::PW && (uint32_t)u[k] != tag);
+                    if (lane_mask(bad) == 0ull) {
+                        e = e0;
+                        got = true;
+                        break;
+                    }
+                }
+                if (wall_clock64() - t0 > kSpecPubWait) break;
+                __builtin_amdgcn_s_sleep(2);
+            }
+        }
+        if (coop) {
+            if (wv == 0) {
+#pragma unroll
+                for (int k = 0; k < LY::KP; k++)
+                    if (64 * k + lane < LY::PW) pubw[64 * k + lane] = (uint32_t)(u[k] >> 32);
+                if (lane == 0) {
+                    pubw[LY::PW] = e;
+                    pubw[LY::PW + 1] = got;
                 }
             }
-            if (wall_clock64() - t0 > kSpecPubWait) break;
-            __builtin_amdgcn_s_sleep(4);
+            __syncthreads();
+            e = __builtin_amdgcn_readfirstlane(pubw[LY::PW]);
+            got = __builtin_amdgcn_readfirstlane(pubw[LY::PW + 1]) != 0;
+#pragma unroll
+            for (int k = 0; k < LY::KP; k++)
+                u[k] = 64 * k + lane < LY::PW ? (uint64_t)pubw[64 * k + lane] << 32 : 0ull;
+            // (every wavefront has its copy before wavefront 0 may overwrite the buffer)
+            __syncthreads();
         }
         if (!got) {
             timed_out = true;
@@ -122,13 +153,20 @@ __device__ __forceinline__ void spec_helper(const YggDevModel &m, const YggIO &i
         }
         next = e + 1;
         const int x = nh >= V ? j : (int)((uint32_t)(j + e) % (uint32_t)V);
-        if (x >= V) continue;
+        if (idle || x >= V) continue;
 #pragma unroll
         for (int k = 0; k < LY::KP; k++) {
             const int w = 64 * k + lane;
             if (w < LY::PW) ((uint32_t *)qold)[w] = (uint32_t)(u[k] >> 32);
         }
-        // x's thresholds of the first two rounds of layers 1 .. S
+        wave_sync();
+        // the token layer with expert x (its record first, then x's thresholds of the first two rounds of layers
+        // 1 .. S, which the update's wait then leaves in flight)
+        Gather<SH, false> G;
+        int qn[F::C];
+        uint32_t ppw[F::SPW];      // the P granules and readout scale of the layer whose readout is pending
+        float pmz;
+        gather<SH, GROUP, true, false>(G, m.layers[0], x, x, false, lane);
         float th1[S];
         float4 th2[S];
 #pragma unroll
@@ -139,13 +177,8 @@ __device__ __forceinline__ void spec_helper(const YggDevModel &m, const YggIO &i
             if (4 * lane < n2)
                 th2[l - 1] = *(const float4 *)(y.thr + (size_t)x * y.thr_stride + (1 << m.round_h[0]) + 4 * lane);
         }
-        wave_sync();
-        // the token layer with expert x
-        Gather<SH, false> G;
-        int qn[F::C];
         {
             const YggDevLayer &y = m.layers[0];
-            gather<SH, GROUP, true, false>(G, y, x, x, false, lane);
             const float *mul = nullptr;
             if constexpr (GROUP) mul = GT.mul[0];
             if (lane < F::NL) update<SH, GROUP, false, false>(qn, G, qold, zl, y, false, m.shift, lane, mul);
@@ -155,9 +188,12 @@ __device__ __forceinline__ void spec_helper(const YggDevModel &m, const YggIO &i
                 for (int c = 0; c < F::C; c++) qnew[F::C * lane + c] = (int8_t)qn[c];
             }
             wave_sync();
-            readout<SH>(sp, G.pw, qnew, GROUP ? G.mzr : y.readout_scale, lane);
+#pragma unroll
+            for (int i = 0; i < F::SPW; i++) ppw[i] = G.pw[i];
+            pmz = GROUP ? G.mzr : y.readout_scale;
         }
-        // layers 1 .. S - 1 whole, layer S's descent and layer input
+        // layers 1 .. S - 1 whole, layer S's descent and layer input; the readout of layer l - 1 runs while layer
+        // l's last router round is loading
 #pragma unroll
         for (int l = 1; l <= S; l++) {
             const YggDevLayer &y = m.layers[l];
@@ -165,13 +201,15 @@ __device__ __forceinline__ void spec_helper(const YggDevModel &m, const YggIO &i
             float rho = below_and_rho<N>(qbw, qnew + (l - 1) * N, y.rms_eps, lane);
             if constexpr (GROUP)
                 if (y.r2b) rho = group_rho<N>(qbw, GT.r2[l - 1], y.rms_eps);
+            auto hook = [&]() { readout<SH>(sp + (l - 1) * R, ppw, qnew + (l - 1) * N, pmz, lane); };
             int r;
             if constexpr (DEEP)
-                r = descend_deep<N>(m, y, St.W[l - 1], th1[l - 1], W1 + (l - 1) * kR2Slots<N> * N, th2[l - 1], qbw,
-                                    qnew + (l - 1) * N, rho, x, lane, tl);
+                r = descend_deep<N, decltype(hook)>(m, y, St.W[l - 1], th1[l - 1], W1 + (l - 1) * kR2Slots<N> * N,
+                                                    th2[l - 1], qbw, qnew + (l - 1) * N, rho, x, lane, tl, hook);
             else
-                r = descend_deep<N, NoHook, true>(m, y, St.W[l - 1], th1[l - 1], y.w + ((size_t)1 << m.round_h[0]) * N,
-                                                  th2[l - 1], qbw, qnew + (l - 1) * N, rho, x, lane, tl);
+                r = descend_deep<N, decltype(hook), true>(m, y, St.W[l - 1], th1[l - 1],
+                                                          y.w + ((size_t)1 << m.round_h[0]) * N, th2[l - 1], qbw,
+                                                          qnew + (l - 1) * N, rho, x, lane, tl, hook);
             if (l < S) gather<SH, GROUP, true, false>(G, y, r, x, true, lane);
             layer_input<SH>(zl, St.V[l - 1], St.mv[l - 1], qbw, rho, lane);
             wave_sync();
@@ -188,7 +226,9 @@ __device__ __forceinline__ void spec_helper(const YggDevModel &m, const YggIO &i
                 for (int c = 0; c < F::C; c++) qnew[l * N + F::C * lane + c] = (int8_t)qn[c];
             }
             wave_sync();
-            readout<SH>(sp + l * R, G.pw, qnew + l * N, GROUP ? G.mzr : y.readout_scale, lane);
+#pragma unroll
+            for (int i = 0; i < F::SPW; i++) ppw[i] = G.pw[i];
+            pmz = GROUP ? G.mzr : y.readout_scale;
         }
         wave_sync();
         // x's slot: step e + 1's results
@@ -204,20 +244,20 @@ __device__ __forceinline__ void spec_helper(const YggDevModel &m, const YggIO &i
         }
         served++;
     }
-    if (lane == 0) {
+    if (lane == 0 && !idle) {
         if (served) spec_count(area, 2, 1);
         if (timed_out) spec_count(area, 4, 1);
     }
 }
 
 // The stream's side. spec_take: x's slot for step t (tag E0 + t), polled for at most `wait` ticks; when every unit
-// carries the tag, the states of layers 0 .. S - 1 go to qs (the stream's state rows), the rest to sp, and (unless
-// t is the last step) the states are published for step t + 1's helpers. Returns whether the slot was taken.
+// carries the tag, the states of layers 0 .. S - 1 go to qs (the stream's state rows), the rest to sp, layer S's
+// leaf to `leaf`, and it returns true.
 template <class SH, int S>
-__device__ __forceinline__ bool spec_take(const YggIO &io, int x, int t, int T, int8_t *qs, int8_t *sp, int lane,
-                                          uint64_t wait) {
+__device__ __forceinline__ bool spec_take(const YggIO &io, int x, int t, int8_t *qs, int8_t *sp, int lane,
+                                          uint64_t wait, int &leaf) {
     using LY = SpecLayout<SH, S>;
-    constexpr int N = SH::N;
+    constexpr int N = SH::N, LW = S * SH::N / 4 + S * SH::R / 4;     // the leaf's word
     const uint32_t tag = io.spec_epoch + (uint32_t)t;
     const uint64_t *slot = io.spec + kSpecSlots + (size_t)x * kSpecSlotUnits;
     uint64_t u[LY::KS];
@@ -239,6 +279,7 @@ __device__ __forceinline__ bool spec_take(const YggIO &io, int x, int t, int T, 
         __builtin_amdgcn_s_sleep(1);
     }
     if (!ok) return false;
+    leaf = __builtin_amdgcn_readlane((int)(uint32_t)(u[LW / 64] >> 32), LW % 64);
 #pragma unroll
     for (int k = 0; k < LY::KS; k++) {
         const int w = 64 * k + lane;
@@ -246,18 +287,11 @@ __device__ __forceinline__ bool spec_take(const YggIO &io, int x, int t, int T, 
         if (w < S * N / 4) ((uint32_t *)qs)[w] = word;
         else if (w < LY::SW) ((uint32_t *)sp)[w - S * N / 4] = word;
     }
-    if (t + 1 < T) {
-#pragma unroll
-        for (int k = 0; k < LY::KP; k++) {
-            const int w = 64 * k + lane;
-            if (w < LY::PW) spec_store(io.spec + kSpecPub + w, spec_unit(tag, (uint32_t)(u[k] >> 32)));
-        }
-    }
     wave_sync();
     return true;
 }
 
-// the states of layers 0 .. S - 1 after step t (LDS qs), published for step t + 1's helpers
+// the states of layers 0 .. S - 1 after step t (LDS qs), published for step t + 1's helpers (in every copy)
 template <class SH, int S>
 __device__ __forceinline__ void spec_publish(const YggIO &io, int t, const int8_t *qs, int lane) {
     using LY = SpecLayout<SH, S>;
@@ -265,7 +299,11 @@ __device__ __forceinline__ void spec_publish(const YggIO &io, int t, const int8_
 #pragma unroll
     for (int k = 0; k < LY::KP; k++) {
         const int w = 64 * k + lane;
-        if (w < LY::PW) spec_store(io.spec + kSpecPub + w, spec_unit(tag, ((const uint32_t *)qs)[w]));
+        if (w < LY::PW) {
+            const uint64_t v = spec_unit(tag, ((const uint32_t *)qs)[w]);
+#pragma unroll
+            for (int c = 0; c < kSpecPubCopies; c++) spec_store(io.spec + kSpecPub + c * kSpecPubUnits + w, v);
+        }
     }
 }
 

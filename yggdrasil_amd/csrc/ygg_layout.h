@@ -114,12 +114,14 @@ constexpr int kModeGenOne = 4;
 constexpr int kModeGenSpec = 5;
 
 // The speculation area of a model (kModeGenSpec), in 8-byte units (a 32-bit tag in the low half, a 32-bit word in the
-// high half): the stream's hello (its epoch and XCD) at unit 0, counters at kSpecStats, the published states at
-// kSpecPub, then one slot of kSpecSlotUnits units per candidate token.
-constexpr int kSpecStats = 8;           // 5 counters (uint64): hits, misses, helper waves served, off-XCD, timed out
+// high half): counters at kSpecStats, the published states at
+// kSpecPub (kSpecPubCopies copies kSpecPubUnits apart: their readers spread over as many memory channels), then one
+// slot of kSpecSlotUnits units per candidate token.
+constexpr int kSpecStats = 8;           // 5 counters (uint64): hits, misses, helper waves served, started, timed out
 constexpr int kSpecNStats = 5;
 constexpr int kSpecPub = 64;
-constexpr int kSpecSlots = 320;
+constexpr int kSpecPubUnits = 256, kSpecPubCopies = 8;
+constexpr int kSpecSlots = kSpecPub + kSpecPubUnits * kSpecPubCopies;
 constexpr int kSpecSlotUnits = 256;
 inline size_t spec_area_units(int V) { return (size_t)kSpecSlots + (size_t)V * kSpecSlotUnits; }
 inline int io_mode(const YggIO &io) {

@@ -61,7 +61,12 @@ def _nest(flat: dict) -> dict:
 def read(path):
     """Checkpoint -> ([token layer, routed layers...] as dicts of float64 arrays, output bias (classes,))."""
     with np.load(path, allow_pickle=False) as z:
-        params = _nest({k: z[k] for k in z.files})
+        return from_params({k: z[k] for k in z.files}, str(path))
+
+
+def from_params(flat: dict, path: str = "parameters"):
+    """Flat "a/b/c" parameter arrays (a checkpoint's contents) -> what read returns."""
+    params = _nest(flat)
     for k in ("token_layer", "output_bias"):
         if k not in params:
             raise ValueError(f"{path}: not a Yggdrasil checkpoint (no {k})")
@@ -117,11 +122,16 @@ class FloatLayer:
         return not self.token_layer and self.router_weight.shape[1] > self.router_embed.shape[1]
 
 
-def float_layers(raw_layers) -> list:
-    """Checkpoint layers -> FloatLayers (T_r[x] and A_r precomputed in float64)."""
+def float_layers(raw_layers, blas: bool = False) -> list:
+    """Checkpoint layers -> FloatLayers (T_r[x] and A_r precomputed in float64). blas: the routed layers' tables as
+    one batched matrix product (the same products summed in another order: last-bit differences from the default,
+    whose bits the export's goldens record; for timing runs on large random models)."""
     out = []
     for i, p in enumerate(raw_layers):
-        table = np.einsum("lkr,vr->lvk", p["input_proj"], p["token_embed"]) + p["bias"][:, None]
+        if blas and i > 0:
+            table = np.matmul(p["token_embed"], np.swapaxes(p["input_proj"], 1, 2)) + p["bias"][:, None]
+        else:
+            table = np.einsum("lkr,vr->lvk", p["input_proj"], p["token_embed"]) + p["bias"][:, None]
         if i == 0:
             ar = np.arange(table.shape[1])
             table = table[ar, ar]                     # the token layer reads only T_x[x]
@@ -153,6 +163,11 @@ class FloatSpec:
 def random_checkpoint(spec: FloatSpec, seed: int, path) -> None:
     """Write a synthetic checkpoint (.npz, the key layout of yggdrasil/config.py:65-82): Gaussian parameters with
     scales that keep the recurrence stable (decays in [0.6, 1), small rotation generators)."""
+    np.savez(path, **random_params(spec, seed))
+
+
+def random_params(spec: FloatSpec, seed: int) -> dict:
+    """The arrays random_checkpoint writes, by flat key."""
     rng = np.random.default_rng(seed)
     n, b, D, V, F, K, R, R2 = (spec.d_state, spec.block_size, spec.router_depth, spec.vocab, spec.router_token_dim,
                                spec.input_rank, spec.readout_rank, spec.layer_input_rank)
@@ -175,7 +190,7 @@ def random_checkpoint(spec: FloatSpec, seed: int, path) -> None:
         for k, v in p.items():
             arrs[f"{pre}/{k}"] = v.astype(np.float32)
     arrs["output_bias"] = rng.normal(0, 0.1, V).astype(np.float32)
-    np.savez(path, **arrs)
+    return arrs
 
 
 # ------------------------------------------------------------------------------------------------ the GPU model
@@ -341,4 +356,5 @@ class FloatYggdrasil:
         return res[0] if prompt.ndim == 1 else res
 
 
-__all__ = ["FloatYggdrasil", "FloatLayer", "FloatSpec", "float_layers", "random_checkpoint", "read", "transitions"]
+__all__ = ["FloatYggdrasil", "FloatLayer", "FloatSpec", "float_layers", "from_params", "random_checkpoint",
+           "random_params", "read", "transitions"]

@@ -211,7 +211,13 @@ class Yggdrasil:
             states: bool = False, digest=False, _entry: str = "ygg_run") -> dict:
         """T tokens per stream in one launch: tokens (B, T) from state (default zero; not modified) ->
         dict(state=(B, layers, n) after the last token, logits=(B, T, classes), leaves=(B, T, layers) int32,
-        states=(B, T, layers, n) int8, digest=(B,) int64 bit pattern of the uint64 digest)."""
+        states=(B, T, layers, n) int8, digest=(B,) int64 bit pattern of the uint64 digest).
+
+        Tokens given on the host are range-checked before the launch (ValueError). Tokens already on the GPU are not
+        read back: a stream whose token t lies outside [0, vocab) stops there, its state stays the one before token
+        t, and its rows of logits, leaves and states from token t on are left unwritten (the uninitialised memory of
+        this call's outputs); take_errors() returns bit 0 for it. So with GPU tokens that may be out of range, call
+        take_errors() (or pass them through device_tokens(..., check_device=True)) before trusting the outputs."""
         x = self._tokens(tokens)
         if x.dim() != 2:
             raise ValueError("tokens must be (B, T)")
