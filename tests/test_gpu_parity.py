@@ -586,7 +586,11 @@ def test_default_dispatch(hip, model_dir, monkeypatch):
     assert model.kernel_name(info.pipe_max_streams + 1, 16) == fast.format(0, "false")
     assert model.kernel_name(16384, 64) == fast.format(0, "true")
     assert model.kernel_name(16384, 64, score=True) == fast.format(2, "true")
-    assert model.kernel_name(1, 100, generate=True) == "ygg::fast_kernel<128, 8, 16, 4, 1, true, false, false>"
+    # one stream of at least 8 tokens: the speculating build; two streams: the generate build with the deep descent;
+    # under 8 tokens the per-stream generate build
+    assert model.kernel_name(1, 100, generate=True) == "ygg::fast_kernel<128, 8, 16, 4, 5, true, false, false>"
+    assert model.kernel_name(2, 100, generate=True) == "ygg::fast_kernel<128, 8, 16, 4, 1, true, false, false>"
+    assert model.kernel_name(1, 7, generate=True) == fast.format(1, "false")
     assert model.kernel_name(1, 4, generate=True) == fast.format(1, "false")
     # more streams than the deep kernel takes: the generation build with the one-token build's descent while its
     # one-stream workgroups are all resident, then the per-stream generate build
@@ -601,7 +605,8 @@ def test_default_dispatch(hip, model_dir, monkeypatch):
     # the NLL's registers it may keep as many); score calls from the smallest batch the uncapped score build cannot
     assert model.kernel_name(info.pipe_max_streams, 16) in ("ygg::pipe_kernel<128, 8, 16, 4, 0, true, false>",
                                                             "ygg::pipe_kernel<128, 8, 16, 4, 0, false, false>")
-    _check_capped_pipe_score(model, path, "ygg::pipe_kernel<128, 8, 16, 4, 2, {}, false>", info.pipe_max_streams, 9)
+    _check_capped_pipe_score(hip, monkeypatch, model, path, "ygg::pipe_kernel<128, 8, 16, 4, 2, {}, false>",
+                             info.pipe_max_streams, 9)
     model.close()
 
 
@@ -619,18 +624,32 @@ def _smallest_batch(model, T, name, hi, score=False, generate=False):
     return lo
 
 
-def _check_capped_pipe_score(model, path, name, hi, seed):
-    """Score calls of 11 tokens on the capped pipe build (name: '{}' for the cap), from the smallest batch that takes
-    it: the fused NLL against the reference formula on the oracle's logits, and the digest of leaves and states."""
+def _check_capped_pipe_score(hip, monkeypatch, model, path, name, hi, seed):
+    """Score calls of 11 tokens on the capped pipe build (name: '{}' for the cap): the fused NLL against the reference
+    formula on the oracle's logits, and the digest of leaves and states. The library takes the capped score build from
+    the smallest batch the uncapped one cannot keep resident when that lies within the pipe limit (hi); when the
+    uncapped score build keeps as many streams resident, it takes the uncapped one up to hi, and YGG_KERNEL=pipe
+    (every multi-token call on the pipe kernel) reaches the capped build from the uncapped build's limit on."""
     from oracle import oracle as O
-    lo = _smallest_batch(model, 11, name.format("true"), hi, score=True)
-    assert lo > 1 and model.kernel_name(lo - 1, 11, score=True) == name.format("false")
+    m = model
+    if model.kernel_name(hi, 11, score=True) == name.format("true"):
+        lo = _smallest_batch(model, 11, name.format("true"), hi, score=True)
+        assert lo > 1 and model.kernel_name(lo - 1, 11, score=True) == name.format("false")
+    else:
+        assert model.kernel_name(hi, 11, score=True) == name.format("false")
+        monkeypatch.setenv("YGG_KERNEL", "pipe")
+        m = hip.load(path)
+        monkeypatch.delenv("YGG_KERNEL")
+        lo = _smallest_batch(m, 11, name.format("true"), 64 * hi, score=True)
+        assert lo > hi and m.kernel_name(lo - 1, 11, score=True) == name.format("false")
     _say(f"capped pipe score build from {lo} streams (pipe_max {hi})")
     x = synth.zipf_bytes(lo, 12, seed)
     ref = Oracle(path).run(x[:, :-1], digest=True)
-    np.testing.assert_allclose(model.score(x), O.nll_bits(ref["logits"], x[:, 1:]), rtol=1e-12, atol=1e-9)
-    dg = model.run(x[:, :-1], logits=False, digest=True)["digest"].cpu().numpy().view(np.uint64)
+    np.testing.assert_allclose(m.score(x, batch=lo), O.nll_bits(ref["logits"], x[:, 1:]), rtol=1e-12, atol=1e-9)
+    dg = m.run(x[:, :-1], logits=False, digest=True)["digest"].cpu().numpy().view(np.uint64)
     np.testing.assert_array_equal(dg, ref["digest"])
+    if m is not model:
+        m.close()
 
 
 def test_group_scales_capped_builds(hip, model_dir, monkeypatch):
@@ -652,7 +671,8 @@ def test_group_scales_capped_builds(hip, model_dir, monkeypatch):
     _say(f"capped per-stream group build from {lo} streams")
     x = synth.zipf_bytes(lo, 4, 5)
     _compare(_gpu_run(model, x), Oracle(path).run(x, states=True))
-    _check_capped_pipe_score(model, path, "ygg::pipe_kernel<128, 8, 16, 4, 2, {}, true>", info.pipe_max_streams, 6)
+    _check_capped_pipe_score(hip, monkeypatch, model, path, "ygg::pipe_kernel<128, 8, 16, 4, 2, {}, true>",
+                             info.pipe_max_streams, 6)
     model.close()
 
 

@@ -963,7 +963,7 @@ int ygg_run_grouped(ygg_model *m, const int32_t *d_tokens, int B, int T, int8_t 
     if (B < 0 || T < 0) return fail(YGG_ERR_ARG, "negative B (%d) or T (%d)", B, T);
     if (!m->grouped_ok)
         return fail(YGG_ERR_LIMITS, "the grouped step takes d_state 128, readout rank 8, layer-input rank 16, block 16, "
-                                    "table storage and tensor scales");
+                                    "table storage, tensor scales and router depth at most 14");
     if (B == 0 || T == 0) return YGG_OK;
     if (!d_state || !d_tokens) return fail(YGG_ERR_ARG, "tokens or state is NULL");
     DeviceGuard g;

@@ -78,26 +78,80 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
     return v;
 }
 
-// -log softmax(lg)[y] in double, the reference's score mode (cpu/ygg.cpp:514-516): mx = max_c lg[c],
-// se = sum_c exp(lg[c] - mx), log(se) + mx - lg[y]. lg: classes [4 lane, 4 lane + 4) of this lane, V classes; y is
-// uniform and in range. The sum over classes runs as a tree over lanes instead of in class order, so se can differ
-// from the reference's in its last bits.
-__device__ __forceinline__ double token_nll(const float (&lg)[4], int V, int y, int lane) {
+// The NLL of a stream's scored tokens in double, the reference's score mode (cpu/ygg.cpp:514-516): per token
+// mx = max_c lg[c], se = sum_c exp(lg[c] - mx) and the term log(se) + mx - lg[y]. The sum over a stream is kept as
+// lin = sum of (mx - lg[y]) and the product of the se (each in [1, V]) as a mantissa pm in [0.5, 1) times 2^pe,
+// renormalised exactly (frexp) after every token, so that one log per stream, value(), replaces one per token (whose
+// polynomial constants would otherwise stay live through the token loop). The product's rounding adds about one ulp
+// of relative error per token to it, a few 1e-14 of absolute error in the log over 1024 tokens.
+// a value every lane of the wavefront holds alike, moved to scalar registers (where a per-stream accumulator then stays)
+__device__ __forceinline__ unsigned long long uniform_u64(unsigned long long u) {
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)u), hi = __builtin_amdgcn_readfirstlane((uint32_t)(u >> 32));
+    return ((unsigned long long)hi << 32) | lo;
+}
+__device__ __forceinline__ double uniform_f64(double v) {
+    return __builtin_bit_cast(double, uniform_u64(__builtin_bit_cast(unsigned long long, v)));
+}
+// (lin, pm and pe are uniform over the wavefront, every lane forming the same sums: kept in scalar registers)
+struct NllSum {
+    double lin = 0.0, pm = 1.0;
+    int pe = 0;
+    __device__ __forceinline__ void add(double se, double lin_t) {
+        lin = uniform_f64(lin + lin_t);
+        int e;
+        pm = uniform_f64(frexp(pm * se, &e));
+        pe = __builtin_amdgcn_readfirstlane(pe + e);
+    }
+    __device__ __forceinline__ double value() const { return log(pm) + (double)pe * 0.69314718055994530942 + lin; }
+};
+
+// e^d for d <= 0 in double: d = k ln 2 + r with k = rint(d / ln 2), |r| <= ln 2 / 2 (Cody and Waite's reduction: ln 2
+// in two parts, the first with 20 significant bits, so that k times it is exact), e^r by its Taylor series to degree
+// 13 (the remainder r^14 / 14! stays below 2^-57 of e^r), scaled by 2^k; below -745.5 the result is 0 (e^d is then
+// below half the smallest subnormal double). Within one ulp of the C library's exp (checked on the host over 2e7
+// arguments in [-800, 0]). The coefficients come from kExpNeg through c, a pointer the caller launders once per call
+// (an empty asm), so that they are scalar loads at each call instead of 12 double constants the compiler would keep
+// in vector registers through the token loop.
+static __constant__ double kExpNeg[14] = {
+    1.4426950408889634,                    // 1 / ln 2
+    0x1.62e42p-1, 0x1.fdf473de6af28p-22,   // ln 2 = high part + low part
+    1.0 / 6227020800.0, 1.0 / 479001600.0, 1.0 / 39916800.0, 1.0 / 3628800.0, 1.0 / 362880.0, 1.0 / 40320.0,
+    1.0 / 5040.0, 1.0 / 720.0, 1.0 / 120.0, 1.0 / 24.0, 1.0 / 6.0};   // 1 / j! for j = 13 .. 3
+typedef const __attribute__((address_space(4))) double *ConstF64;
+__device__ __forceinline__ double exp_neg(double d, ConstF64 c) {
+    const double k = rint(d * c[0]);
+    double r = fma(-k, c[1], d);
+    r = fma(-k, c[2], r);
+    double p = c[3];
+#pragma unroll
+    for (int j = 4; j < 14; j++) p = fma(p, r, c[j]);
+    p = fma(p, r, 0.5);
+    p = fma(p, r, 1.0);
+    p = fma(p, r, 1.0);
+    return d < -745.5 ? 0.0 : ldexp(p, (int)k);
+}
+
+// Token t's term into acc: lg classes [4 lane, 4 lane + 4) of this lane, V classes; y is uniform and in range. The
+// sum over classes runs as a tree over lanes instead of in class order, so se can differ from the reference's in its
+// last bits.
+__device__ __forceinline__ void token_nll(NllSum &acc, const float (&lg)[4], int V, int y, int lane) {
     float mx = -__builtin_huge_valf();
 #pragma unroll
     for (int u = 0; u < 4; u++)
         if (4 * lane + u < V) mx = fmaxf(mx, lg[u]);
     mx = wave_max_f32(mx);
+    ConstF64 c = (ConstF64)kExpNeg;
+    asm volatile("" : "+s"(c));
     double se = 0.0;
 #pragma unroll
     for (int u = 0; u < 4; u++)
-        if (4 * lane + u < V) se += exp((double)lg[u] - (double)mx);
+        if (4 * lane + u < V) se += exp_neg((double)lg[u] - (double)mx, c);
     se = wave_sum_f64(se);
     float ly = lg[0];
 #pragma unroll
     for (int u = 1; u < 4; u++) ly = (y & 3) == u ? lg[u] : ly;
     ly = __shfl(ly, y >> 2);
-    return log(se) + (double)mx - (double)ly;
+    acc.add(se, (double)mx - (double)ly);
 }
 
 __device__ __forceinline__ float wave_sum_f32(float v) {
@@ -356,7 +410,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void ru
     for (int i = lane; i < YGG_MAX_RANK; i += 64) zls[i] = 0;
     __syncthreads();
     unsigned long long dg = digest ? digest[s] : 0ull;
-    double nacc = 0.0;
+    NllSum nacc;
     const int32_t *tok = tokens + (size_t)s * (GEN ? 1 : T);
     int x_next = T > 0 ? __builtin_amdgcn_readfirstlane(tok[0]) : 0;
 
@@ -601,7 +655,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void ru
         }
         if (nll) {
             const int yv = targets[(size_t)s * T + t];
-            if (yv >= 0 && yv < V) nacc += token_nll(lg, V, yv, lane);
+            if (yv >= 0 && yv < V) token_nll(nacc, lg, V, yv, lane);
             else if (lane == 0) atomicOr(m.err, 2u);
         }
         if (GEN) {
@@ -616,7 +670,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void ru
     __syncthreads();
     for (int i = lane; i < L * N; i += 64) st[i] = qs[i];
     if (digest && lane == 0) digest[s] = dg;
-    if (nll && lane == 0) nll[s] += nacc;
+    if (nll && lane == 0) nll[s] += nacc.value();
 }
 
 }  // namespace ygg

@@ -919,7 +919,7 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
     if (lane < SH::ZL) zls[lane] = 0;
     wave_sync();
     unsigned long long dg = (SCORE && digest) ? digest[s] : 0ull;
-    double nacc = 0.0;
+    NllSum nacc;
     bool staged = W > 1;      // W = 1: the stream's wavefront has met the barrier that waits for the LDS tables
     // SPEC: steps taken from the helpers' slots and computed here, whether the last one was taken
     int spec_hits = 0, spec_misses = 0;
@@ -1089,7 +1089,7 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
         if (logits) store_logits(logits + ((size_t)s * T + t) * V, lg, V, lane);
         if (SCORE && nll) {
             const int yv = targets[(size_t)s * T + t];
-            if (yv >= 0 && yv < V) nacc += token_nll(lg, V, yv, lane);
+            if (yv >= 0 && yv < V) token_nll(nacc, lg, V, yv, lane);
             else if (lane == 0) atomicOr(m.err, 2u);
         }
         if (GEN) {
@@ -1112,7 +1112,7 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
             spec_count(io.spec, 1, (unsigned long long)spec_misses);
         }
     if (SCORE && digest && lane == 0) digest[s] = dg;
-    if (SCORE && nll && lane == 0) nll[s] += nacc;
+    if (SCORE && nll && lane == 0) nll[s] += nacc.value();
 }
 
 
@@ -1199,7 +1199,7 @@ void pipe_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
     const int qj = lane >> 2;
     const int nn1 = (1 << m.round_h[0]) - 1;
     unsigned long long dg = (digest && l == L - 1) ? digest[s] : 0ull;
-    double nacc = 0.0;
+    NllSum nacc;
     // loaded a tick ahead: the first-round thresholds (routed layers) or the gather record (token layer; not for the
     // largest shape, whose two records in flight would spill: the token layer's chain is the shortest anyway)
     constexpr bool kAhead = N * R2 < 256 * 64;
@@ -1287,12 +1287,13 @@ void pipe_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
                     if (logits) store_logits(logits + ((size_t)s * T + t) * V, lg, V, lane);
                     if (nll) {
                         const int yv = targets[(size_t)s * T + t];
-                        if (yv >= 0 && yv < V) nacc += token_nll(lg, V, yv, lane);
+                        if (yv >= 0 && yv < V) token_nll(nacc, lg, V, yv, lane);
                         else if (lane == 0) atomicOr(m.err, 2u);
                     }
                     if (digest) {
 #pragma unroll
                         for (int j = 0; j < L; j++) dg = dg * kDigestMul + dterm[t % L][j];
+                        dg = uniform_u64(dg);
                     }
                 }
             }
@@ -1302,7 +1303,7 @@ void pipe_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
     const int te = T < stop_t ? T : stop_t;                          // tokens processed
     for (int i = lane; i < N; i += 64) st[i] = qbuf[l][(te + 1) & 1][i];
     if (digest && l == L - 1 && lane == 0) digest[s] = dg;
-    if (nll && l == L - 1 && lane == 0) nll[s] += nacc;
+    if (nll && l == L - 1 && lane == 0) nll[s] += nacc.value();
 }
 
 
@@ -1449,7 +1450,7 @@ __device__ __forceinline__ void flow_outputs(FlowShared<SH, L, P, GROUP, SCORE> 
 template <class SH, int L, int P, bool SCORE, bool GROUP>
 __device__ __forceinline__ void flow_finish(FlowShared<SH, L, P, GROUP, SCORE> &sh, const YggDevModel &m,
                                             const float (&lg)[4], int t, int s, int T, const YggIO &io,
-                                            unsigned long long &dg, double &nacc, int lane) {
+                                            unsigned long long &dg, NllSum &nacc, int lane) {
     using FS = FlowShared<SH, L, P, GROUP, SCORE>;
     constexpr int LG = FS::LG;
     const int V = m.V;
@@ -1460,7 +1461,7 @@ __device__ __forceinline__ void flow_finish(FlowShared<SH, L, P, GROUP, SCORE> &
     if (io.logits) store_logits(io.logits + ((size_t)s * T + t) * V, lg, V, lane);
     if (SCORE && !ROW && io.nll) {
         const int yv = scalar_load(io.targets + (size_t)s * T + t);
-        if (yv >= 0 && yv < V) nacc += token_nll(lg, V, yv, lane);
+        if (yv >= 0 && yv < V) token_nll(nacc, lg, V, yv, lane);
         else if (lane == 0) atomicOr(m.err, 2u);
     }
     if (SCORE && io.digest) {
@@ -1478,7 +1479,7 @@ template <class SH, int L, int P, bool SCORE, bool GROUP, class Mid = NoHook>
 __device__ __forceinline__ void flow_update(FlowShared<SH, L, P, GROUP, SCORE> &sh, const YggDevModel &m,
                                             const YggDevLayer &y, const Gather<SH> &G, const float (&bias)[4],
                                             int l, int t, bool ok, int r, int s, int T, const YggIO &io,
-                                            unsigned long long &dg, double &nacc, int lane, Mid mid = Mid()) {
+                                            unsigned long long &dg, NllSum &nacc, int lane, Mid mid = Mid()) {
     using F = SH;
     using FS = FlowShared<SH, L, P, GROUP, SCORE>;
     constexpr int QM = FS::QR - 1, LG = FS::LG;
@@ -1555,14 +1556,14 @@ __device__ __forceinline__ void flow_update(FlowShared<SH, L, P, GROUP, SCORE> &
 // the NLL of token t, whose logits the last layer left in lgs[t & 1] last tick (the NLL wave)
 template <class SH, int L, int P, bool GROUP>
 __device__ __forceinline__ void flow_nll(FlowShared<SH, L, P, GROUP, true> &sh, const YggDevModel &m, int t, int s,
-                                         int T, const YggIO &io, double &nacc, int lane) {
+                                         int T, const YggIO &io, NllSum &nacc, int lane) {
     const int V = m.V, VP = m.VP;
     const float *lr = sh.lgs[t & 1];
     float lg[4];
 #pragma unroll
     for (int u = 0; u < 4; u++) lg[u] = 4 * lane + u < VP ? lr[4 * lane + u] : 0.0f;
     const int yv = scalar_load(io.targets + (size_t)s * T + t);
-    if (yv >= 0 && yv < V) nacc += token_nll(lg, V, yv, lane);
+    if (yv >= 0 && yv < V) token_nll(nacc, lg, V, yv, lane);
     else if (lane == 0) atomicOr(m.err, 2u);
 }
 
@@ -1571,7 +1572,7 @@ __device__ __forceinline__ void flow_nll(FlowShared<SH, L, P, GROUP, true> &sh, 
 template <class SH, int L, int P, bool SCORE, bool GROUP>
 __device__ __forceinline__ void flow_logits(FlowShared<SH, L, P, GROUP, SCORE> &sh, const YggDevModel &m,
                                             const float (&bias)[4], int t, int s, int T, const YggIO &io,
-                                            unsigned long long &dg, double &nacc, int lane) {
+                                            unsigned long long &dg, NllSum &nacc, int lane) {
     using FS = FlowShared<SH, L, P, GROUP, SCORE>;
     float lg[4];
 #pragma unroll
@@ -1681,7 +1682,7 @@ void flow_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
     // the wave that finishes the tokens: the logits wave, else the last layer's update wave
     const bool fin = LOGW ? logw : (l == L - 1 && !descent);
     unsigned long long dg = (SCORE && io.digest && fin) ? io.digest[s] : 0ull;
-    double nacc = 0.0;
+    NllSum nacc;
     // everything loaded so far has arrived: no value from before the ticks is waited for inside them
     __builtin_amdgcn_s_waitcnt(0);
 
@@ -1974,7 +1975,7 @@ void flow_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B,
         for (int i = lane; i < N; i += 64) st[i] = sh.qring[l][te & QM][i];
     }
     if (SCORE && io.digest && fin && lane == 0) io.digest[s] = dg;
-    if (SCORE && io.nll && (NLLW ? nllw : fin) && lane == 0) io.nll[s] += nacc;
+    if (SCORE && io.nll && (NLLW ? nllw : fin) && lane == 0) io.nll[s] += nacc.value();
 }
 
 }  // namespace ygg
