@@ -406,6 +406,30 @@ def main():
         log(f"softmax of {B * T} rows: {sm}")
         del pr
 
+    # the score mode on the same streams (ygg_score: the step and the float64 NLL of each token's next token, the
+    # last token of a stream scored against its first; no logits written), timed like the step
+    score = None
+    if a.entry == "run":
+        yt = torch.roll(x, -1, dims=1).contiguous()
+        nll = torch.zeros(B, dtype=torch.float64, device=dev)
+
+        def score_launch():
+            st.zero_()
+            _lib.check(L.ygg_score(model._h, p(x), p(yt), B, T, p(st), p(nll), sp))
+        score_launch()
+        torch.cuda.synchronize()
+        c0, c1 = ev(), ev()
+        c0.record(stream)
+        for _ in range(a.steps):
+            score_launch()
+        c1.record(stream)
+        torch.cuda.synchronize()
+        sc_ms = c0.elapsed_time(c1) / a.steps
+        score = {"ms": round(sc_ms, 4), "tokens_per_s": round(B * T / (sc_ms / 1e3), 1),
+                 "over_run_step": round(sc_ms / ms, 4), "kernel": model.kernel_name(B, T, score=True)}
+        log(f"score: {score}")
+        del yt, nll
+
     batch1 = None
     if a.batch1_tokens > 0 and a.entry == "run":
         batch1 = run_batch1(model, w, a.batch1_tokens, L, _lib)
@@ -445,6 +469,7 @@ def main():
                      "kernel": kernel, "kernel_ms": round(kernel_ms, 4)},
         "cpu_baseline": cpu,
         "softmax": sm,
+        "score": score,
         "grouped_graph": grouped_graph,
         "batch1": batch1,
         "float_batch1": float_b1,

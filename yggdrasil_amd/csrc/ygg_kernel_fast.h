@@ -933,6 +933,23 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
             if (lane == 0) atomicOr(m.err, 1u);
             break;
         }
+        // thresholds of the first router round of every routed layer (SPEC: loaded before the slot is polled for, so
+        // that they are in by the time the layers after SPS need them; every layer's, the slot not being known yet)
+        float th1[LR];
+#pragma unroll
+        for (int l = 1; l < L; l++)
+            th1[l - 1] = qj < nn1 ? m.layers[l].thr[(size_t)x * m.layers[l].thr_stride + qj] : 0.0f;
+        // DEEP: and those of the second round, four per lane (components in separate arrays, which the selects
+        // below keep in registers)
+        float th2x[LR], th2y[LR], th2z[LR], th2w[LR];
+#pragma unroll
+        for (int l = 1; l < L; l++) {
+            float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (DD && 4 * lane < n2)
+                v = *(const float4 *)(m.layers[l].thr + (size_t)x * m.layers[l].thr_stride + (1 << m.round_h[0]) +
+                                      4 * lane);
+            th2x[l - 1] = v.x; th2y[l - 1] = v.y; th2z[l - 1] = v.z; th2w[l - 1] = v.w;
+        }
         // SPEC: x's slot, which holds this step's layers 0 .. SPS - 1 and layer SPS's leaf and layer input (a short
         // wait after a step that had its slot, a single look after one that did not)
         bool hit = false;
@@ -949,23 +966,6 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
                 rs &= m.E - 1;
                 if (hit) gather<SH, GROUP, true, FACT>(Gs, m.layers[SPS], rs, x, true, lane, K4);
             }
-        }
-        // thresholds of the first router round of every routed layer (SPEC with the slot: of the layers after SPS)
-        float th1[LR];
-#pragma unroll
-        for (int l = 1; l < L; l++)
-            th1[l - 1] = (qj < nn1 && (!hit || l > SPS)) ? m.layers[l].thr[(size_t)x * m.layers[l].thr_stride + qj]
-                                                         : 0.0f;
-        // DEEP: and those of the second round, four per lane (components in separate arrays, which the selects
-        // below keep in registers)
-        float th2x[LR], th2y[LR], th2z[LR], th2w[LR];
-#pragma unroll
-        for (int l = 1; l < L; l++) {
-            float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            if (DD && 4 * lane < n2 && (!hit || l > SPS))
-                v = *(const float4 *)(m.layers[l].thr + (size_t)x * m.layers[l].thr_stride + (1 << m.round_h[0]) +
-                                      4 * lane);
-            th2x[l - 1] = v.x; th2y[l - 1] = v.y; th2z[l - 1] = v.z; th2w[l - 1] = v.w;
         }
         float lg[4];
 #pragma unroll

@@ -99,33 +99,71 @@ __device__ __forceinline__ void spec_helper(const YggDevModel &m, const YggIO &i
     uint32_t next = 0;
     int served = 0;
     bool timed_out = false;
+    // every candidate has a wavefront of its own (x = j at every epoch): its token-layer record and thresholds load
+    // while the publication is awaited
+    const bool fixed = nh >= m.V && !idle;
     while (next <= span) {
+        Gather<SH, false> G;
+        float th1[S];
+        float4 th2[S];
+        // the token layer with expert x's record, then x's thresholds of the first two rounds of layers 1 .. S
+        auto prefetch = [&](int xx) {
+            gather<SH, GROUP, true, false>(G, m.layers[0], xx, xx, false, lane);
+#pragma unroll
+            for (int l = 1; l <= S; l++) {
+                const YggDevLayer &y = m.layers[l];
+                th1[l - 1] = qj < nn1 ? y.thr[(size_t)xx * y.thr_stride + qj] : 0.0f;
+                th2[l - 1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                if (4 * lane < n2)
+                    th2[l - 1] = *(const float4 *)(y.thr + (size_t)xx * y.thr_stride + (1 << m.round_h[0]) + 4 * lane);
+            }
+        };
+        if (fixed) prefetch(j);
         // the next publication: every unit in one round trip, lane 0's first naming the epoch the others must carry
         // (coop: wavefront 0 for the workgroup)
         uint64_t u[LY::KP];
         uint32_t e = 0;
         bool got = false;
         if (!coop || wv == 0) {
-            const uint64_t t0 = wall_clock64();
-            for (;;) {
+            // two looks in flight (as in spec_take); a look is whole when every unit carries the tag of an epoch not
+            // served yet
+            uint64_t v[LY::KP];
+            auto look = [&](uint64_t (&d)[LY::KP]) {
 #pragma unroll
                 for (int k = 0; k < LY::KP; k++) {
                     const int w = 64 * k + lane;
-                    u[k] = w < LY::PW ? spec_load(pub + w) : 0ull;
+                    d[k] = w < LY::PW ? spec_load(pub + w) : 0ull;
                 }
-                const uint32_t tag = __builtin_amdgcn_readfirstlane((uint32_t)u[0]), e0 = tag - E0;
-                if (e0 >= next && e0 <= span) {
-                    bool bad = false;
+            };
+            auto whole = [&](const uint64_t (&d)[LY::KP]) {
+                const uint32_t tag = __builtin_amdgcn_readfirstlane((uint32_t)d[0]), e0 = tag - E0;
+                if (e0 < next || e0 > span) return false;
+                bool bad = false;
 #pragma unroll
-                    for (int k = 0; k < LY::KP; k++) bad = bad || (64 * k + lane < LY::PW && (uint32_t)u[k] != tag);
-                    if (lane_mask(bad) == 0ull) {
-                        e = e0;
-                        got = true;
-                        break;
-                    }
+                for (int k = 0; k < LY::KP; k++) bad = bad || (64 * k + lane < LY::PW && (uint32_t)d[k] != tag);
+                if (lane_mask(bad) != 0ull) return false;
+                e = e0;
+                return true;
+            };
+            const uint64_t t0 = wall_clock64();
+            look(u);
+            for (;;) {
+                __builtin_amdgcn_s_sleep(1);
+                look(v);
+                if (whole(u)) {
+                    got = true;
+                    break;
                 }
                 if (wall_clock64() - t0 > kSpecPubWait) break;
-                __builtin_amdgcn_s_sleep(2);
+                __builtin_amdgcn_s_sleep(1);
+                look(u);
+                if (whole(v)) {
+#pragma unroll
+                    for (int k = 0; k < LY::KP; k++) u[k] = v[k];
+                    got = true;
+                    break;
+                }
+                if (wall_clock64() - t0 > kSpecPubWait) break;
             }
         }
         if (coop) {
@@ -160,23 +198,12 @@ __device__ __forceinline__ void spec_helper(const YggDevModel &m, const YggIO &i
             if (w < LY::PW) ((uint32_t *)qold)[w] = (uint32_t)(u[k] >> 32);
         }
         wave_sync();
-        // the token layer with expert x (its record first, then x's thresholds of the first two rounds of layers
-        // 1 .. S, which the update's wait then leaves in flight)
-        Gather<SH, false> G;
+        // the token layer with expert x (loaded above for a fixed candidate; else now, the thresholds after the
+        // record, which the update's wait then leaves in flight)
         int qn[F::C];
         uint32_t ppw[F::SPW];      // the P granules and readout scale of the layer whose readout is pending
         float pmz;
-        gather<SH, GROUP, true, false>(G, m.layers[0], x, x, false, lane);
-        float th1[S];
-        float4 th2[S];
-#pragma unroll
-        for (int l = 1; l <= S; l++) {
-            const YggDevLayer &y = m.layers[l];
-            th1[l - 1] = qj < nn1 ? y.thr[(size_t)x * y.thr_stride + qj] : 0.0f;
-            th2[l - 1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            if (4 * lane < n2)
-                th2[l - 1] = *(const float4 *)(y.thr + (size_t)x * y.thr_stride + (1 << m.round_h[0]) + 4 * lane);
-        }
+        if (!fixed) prefetch(x);
         {
             const YggDevLayer &y = m.layers[0];
             const float *mul = nullptr;
@@ -260,23 +287,42 @@ __device__ __forceinline__ bool spec_take(const YggIO &io, int x, int t, int8_t 
     constexpr int N = SH::N, LW = S * SH::N / 4 + S * SH::R / 4;     // the leaf's word
     const uint32_t tag = io.spec_epoch + (uint32_t)t;
     const uint64_t *slot = io.spec + kSpecSlots + (size_t)x * kSpecSlotUnits;
-    uint64_t u[LY::KS];
-    const uint64_t t0 = wall_clock64();
-    bool ok = false;
-    for (;;) {
-        bool bad = false;
+    // two looks in flight: the next is issued before the last one is examined, so that the slot is seen about one
+    // load latency after it lands (a look-wait-look loop sees it up to two later)
+    uint64_t u[LY::KS], v[LY::KS];
+    auto look = [&](uint64_t (&d)[LY::KS]) {
 #pragma unroll
         for (int k = 0; k < LY::KS; k++) {
             const int w = 64 * k + lane;
-            u[k] = w < LY::SW ? spec_load(slot + w) : spec_unit(tag, 0u);
-            bad = bad || (uint32_t)u[k] != tag;
+            d[k] = w < LY::SW ? spec_load(slot + w) : spec_unit(tag, 0u);
         }
-        if (lane_mask(bad) == 0ull) {
+    };
+    auto whole = [&](const uint64_t (&d)[LY::KS]) {
+        bool bad = false;
+#pragma unroll
+        for (int k = 0; k < LY::KS; k++) bad = bad || (uint32_t)d[k] != tag;
+        return lane_mask(bad) == 0ull;
+    };
+    const uint64_t t0 = wall_clock64();
+    bool ok = false;
+    look(u);
+    for (;;) {
+        __builtin_amdgcn_s_sleep(1);
+        look(v);
+        if (whole(u)) {
             ok = true;
             break;
         }
         if (wall_clock64() - t0 > wait) break;
         __builtin_amdgcn_s_sleep(1);
+        look(u);
+        if (whole(v)) {
+#pragma unroll
+            for (int k = 0; k < LY::KS; k++) u[k] = v[k];
+            ok = true;
+            break;
+        }
+        if (wall_clock64() - t0 > wait) break;
     }
     if (!ok) return false;
     leaf = __builtin_amdgcn_readlane((int)(uint32_t)(u[LW / 64] >> 32), LW % 64);
