@@ -457,7 +457,7 @@ struct ygg_model {
     uint64_t *spec_area = nullptr;    // its speculation area (spec_area_units(V) tagged units)
     mutable uint32_t spec_next = 1;   // the next call's first epoch (epoch 0 never occurs: a cleared unit is stale)
     mutable std::mutex spec_mu;
-    int spec_helpers = 0;             // helper workgroups of a call: enough for every candidate token, at most 63
+    int spec_helpers = 0;             // helper workgroups of a call: enough for every candidate token
     bool grouped_ok = false;          // the leaf-grouped step takes the model (ygg_run_grouped)
     void *grp_ws = nullptr;           // its workspace, grown to the largest call
     size_t grp_ws_bytes = 0;
@@ -769,9 +769,10 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
         } else {
             m->spec_area = (uint64_t *)a;
         }
-        // helper workgroups of 4 wavefronts, with the stream workgroup's 3 others one per candidate token
-        // (ceil((V - 3) / 4) of them, at most 64); YGG_SPEC_HELPERS: fewer
-        m->spec_helpers = std::min(64, V / 4);
+        // helper workgroups of kSpecWPW helper wavefronts, with the stream workgroup's 3 others one per candidate
+        // token (at most kSpecMaxHelpers of them); YGG_SPEC_HELPERS: fewer
+        // (each workgroup holds a CU: the stream's and the helpers' all resident at once)
+        m->spec_helpers = std::min(std::min(kSpecMaxHelpers, cus - 1), V / kSpecWPW);
         if (const char *eh = getenv("YGG_SPEC_HELPERS")) m->spec_helpers = std::max(0, std::min(m->spec_helpers, atoi(eh)));
         // YGG_SPEC_EPOCH: the first call's first epoch (tests of the wrap; 0 is taken as 1)
         if (const char *ep = getenv("YGG_SPEC_EPOCH")) m->spec_next = (uint32_t)strtoul(ep, nullptr, 0);

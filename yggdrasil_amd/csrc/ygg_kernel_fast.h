@@ -859,9 +859,10 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
             if constexpr (GROUP) load_group_tables<SH, L, 64 * kFastWaves>(GT, m, tid);
             if constexpr (DEEP) load_round2<N, L, 64 * kFastWaves>(W1s, m, tid);
             __syncthreads();
-            spec_helper<SH, L, GROUP, DEEP>(m, io, T, (blockIdx.x - 1) * kFastWaves + wv,
+            if (wv >= kSpecWPW) return;
+            spec_helper<SH, L, GROUP, DEEP>(m, io, T, (blockIdx.x - 1) * kSpecWPW + wv,
                                             spec_helper_waves(io.spec_helpers), S, GT, &W1s[0][0], qsw[wv], spw[wv], lane,
-                                            pubw, blockIdx.x % kSpecPubCopies, true, wv);
+                                            pubw, blockIdx.x % kSpecPubCopies, kSpecWPW == kFastWaves, wv);
             return;
         }
     }
@@ -892,7 +893,7 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
             __syncthreads();
             // SPEC: then helpers on the stream's own CU
             if constexpr (SPEC)
-                spec_helper<SH, L, GROUP, DEEP>(m, io, T, io.spec_helpers * kFastWaves + wv - 1,
+                spec_helper<SH, L, GROUP, DEEP>(m, io, T, io.spec_helpers * kSpecWPW + wv - 1,
                                                 spec_helper_waves(io.spec_helpers), S, GT, &W1s[0][0], qsw[wv],
                                                 spw[wv], lane, pubw, 0, false, wv);
             return;

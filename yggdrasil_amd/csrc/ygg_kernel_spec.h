@@ -26,17 +26,19 @@
 // helper wait is bounded by the wall clock and a helper that times out leaves, so every wavefront ends.
 //
 // Placement. Workgroup 0 runs the stream, workgroups 1 .. H help (the dispatcher hands workgroups to the XCDs in
-// turn: about H / 8 on each), 4 wavefronts each, and the stream workgroup's 3 staging wavefronts help too: 4 H + 3
-// helper wavefronts, one candidate each; with more candidates than helpers the uncovered ones change with every step
-// (candidate (j + step) mod V for helper j of nh). Every workgroup holds the build's LDS: with the deep descent's
-// second-round rows (the stream's and the helpers' descents both read them from LDS), one workgroup per CU.
+// turn: about H / 8 on each), kSpecWPW wavefronts each (all 4 stage the LDS tables; the others then leave: two helper
+// wavefronts on a CU instead of four took the descents of configuration 4 from 1.9 to 1.3 us), and the stream
+// workgroup's 3 staging wavefronts help too: kSpecWPW H + 3 helper wavefronts, one candidate each (with H = V /
+// kSpecWPW those of the stream's CU have none and leave); with more candidates than helpers the uncovered ones change
+// with every step (candidate (j + step) mod V for helper j of nh). Every workgroup holds the build's LDS: with the
+// deep descent's second-round rows (the stream's and the helpers' descents both read them from LDS), one workgroup
+// per CU.
 #pragma once
 
 namespace ygg {
 
-constexpr int kSpecMaxHelpers = 64;   // helper workgroups at most (workgroups 1 .. kSpecMaxHelpers)
 // helper wavefronts of h helper workgroups: theirs and the stream workgroup's staging wavefronts
-__host__ __device__ constexpr int spec_helper_waves(int h) { return h * kFastWaves + kFastWaves - 1; }
+__host__ __device__ constexpr int spec_helper_waves(int h) { return h * kSpecWPW + kFastWaves - 1; }
 
 // routed layers whose descent the helpers take over: 2, or 1 for a 2-layer model
 template <int L> constexpr int kSpecDepth = L > 2 ? 2 : 1;
@@ -70,9 +72,10 @@ constexpr uint64_t kSpecPubWait = 20000;       // 200 us between two publication
 // ones at qh + S N; sp: the slot's tail (zq of layers 0 .. S - 1, layer S's leaf, its layer input). DEEP: the
 // routed layers' second-round rows are in LDS from W1 on (load_round2's layout: kR2Slots N bytes a layer, fast_kernel's
 // deep descent), else read from global memory.
-// Polling: a helper workgroup's wavefront 0 polls publication copy `copy` for the workgroup and hands each
-// publication to the others in LDS (pubw: the words, then the epoch and whether one came) behind a workgroup barrier
-// (coop); the stream workgroup's helpers, whose workgroup has a wavefront that meets no barrier, poll on their own.
+// Polling: with coop (a helper workgroup whose 4 wavefronts all help), wavefront 0 polls publication copy `copy` for
+// the workgroup and hands each publication to the others in LDS (pubw: the words, then the epoch and whether one
+// came) behind a workgroup barrier; otherwise (fewer helper wavefronts in a workgroup, and the stream workgroup's,
+// which has a wavefront that meets no barrier) every helper wavefront polls on its own.
 template <class SH, int L, bool GROUP, bool DEEP>
 __device__ __forceinline__ void spec_helper(const YggDevModel &m, const YggIO &io, int T, int j, int nh,
                                             const SharedTables<SH, L> &St, const GroupTablesOf<SH, L, GROUP> &GT,

@@ -123,6 +123,9 @@ constexpr int kSpecPub = 64;
 constexpr int kSpecPubUnits = 256, kSpecPubCopies = 8;
 constexpr int kSpecSlots = kSpecPub + kSpecPubUnits * kSpecPubCopies;
 constexpr int kSpecSlotUnits = 256;
+// helper workgroups: kSpecWPW helper wavefronts each (the others stage the LDS tables with them and leave), at most
+// kSpecMaxHelpers of them
+constexpr int kSpecWPW = 2, kSpecMaxHelpers = 128;
 inline size_t spec_area_units(int V) { return (size_t)kSpecSlots + (size_t)V * kSpecSlotUnits; }
 inline int io_mode(const YggIO &io) {
     return io.gen ? kModeGenerate : ((io.digest || io.nll) ? kModeScore : kModeRun);
