@@ -9,9 +9,12 @@
 //   readout: z = P_r h;   logits += Q z
 // and rms(h) = h / sqrt(mean(h^2) + 1e-6) feeds the next layer.
 // Work split: the router descends in rounds of up to 4 levels, 16 groups of 16 threads each forming one node's dot of
-// the round's subtree (every load of a round issued at once, the input row held in registers for the layer); the
-// layer input takes 4 threads per row of V'; thread i owns coordinate i of the update (its table entry, U' row and A
-// row loaded together); the readout takes 256 / R threads per row of P; thread c owns class c of the logits.
+// the round's subtree (every load of a round issued at once, the input row held in registers for the layer); for the
+// layer input wavefront q sums its quarter of the coordinates for row k = lane of V'; thread i owns coordinate i of
+// the update (its table entry, U' column and A row loaded together); the readout takes 256 / R threads per row of P;
+// thread c owns class c of the logits. The builds specialised on a shape issue a layer's constant loads (Q's column
+// of each class, V''s share of each thread) at the layer's start, before its route, and the readout's P row with the
+// update's record, so that a layer waits for the route's rounds and one record load only.
 #include <hip/hip_runtime.h>
 
 #include <cstdarg>
@@ -119,6 +122,9 @@ __global__ __launch_bounds__(kFThreads) __attribute__((amdgpu_waves_per_eu(1, 1)
     __shared__ int dec[16];                   // a router round's decisions, by breadth-first node of its subtree
     __shared__ double gmax[YGG_MAX_LAYERS][kMaxN / 16];
 
+    // PF (the specialised builds): a layer's loads issued early (see above); the general builds load at each use
+    constexpr bool PF = NS != 0;
+    constexpr int PE = RS ? (NS * RS + kFThreads - 1) / kFThreads : MN / 4;   // readout coordinates per thread
     const int s = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
     const int L = m.L, n = NS ? NS : m.n, b = BS ? BS : m.b, V = m.V, C = m.classes, R = RS ? RS : m.R,
               R2 = R2S ? R2S : m.R2, F = m.F;
@@ -156,6 +162,28 @@ __global__ __launch_bounds__(kFThreads) __attribute__((amdgpu_waves_per_eu(1, 1)
         for (int l = 0; l < L; l++) {
             const FloatLayerDev<T> &y = m.layers[l];
             int r = x;
+            // the layer's constants: class c's column of Q^T (thread c) and this thread's share of V' (wave q's quarter
+            // of the coordinates of row k = lane)
+            T qw[MR], vv[MN / 4];
+            auto load_q = [&]() {
+                if (tid < C) {
+                    const T *q = y.Q + tid;
+#pragma unroll
+                    for (int j = 0; j < MR; j++) qw[j] = j < R ? q[(size_t)j * C] : T(0);
+                }
+            };
+            const bool vlive = l > 0 && y.Vd != nullptr && vrow < R2;
+            auto load_v = [&]() {
+                if (vlive) {
+                    const T *vc = y.Vd + (size_t)(vq * vlen) * R2 + vrow;
+#pragma unroll
+                    for (int i = 0; i < MN / 4; i++) vv[i] = i < vlen ? vc[(size_t)i * R2] : T(0);
+                }
+            };
+            if constexpr (PF) {
+                load_q();
+                load_v();
+            }
             if (l > 0) {
                 // router descent over f = [router_embed[x]; rms(h_below)], in rounds of up to 4 levels
                 T f[kRouteElems];
@@ -193,18 +221,12 @@ __global__ __launch_bounds__(kFThreads) __attribute__((amdgpu_waves_per_eu(1, 1)
                     __syncthreads();
                 }
                 r = root - ((1 << m.D) - 1);
-                // the layer input zl = V' rms(h_below): wave q sums its quarter of the coordinates for row k = lane
-                // (every load issued at once), the four partials then add in quarter order
+                // the layer input zl = V' rms(h_below): each wave's partial sum for row k = lane over its quarter of
+                // the coordinates, the four partials then added in quarter order
                 if (y.Vd) {
-                    const bool vlive = vrow < R2;
-                    T vv[MN / 4];
+                    if constexpr (!PF) load_v();
                     if (vlive) {
-                        const T *vc = y.Vd + (size_t)(vq * vlen) * R2 + vrow;
-#pragma unroll
-                        for (int i = 0; i < MN / 4; i++) vv[i] = i < vlen ? vc[(size_t)i * R2] : T(0);
-                    }
-                    T a = T(0);
-                    if (vlive) {
+                        T a = T(0);
 #pragma unroll
                         for (int i = 0; i < MN / 4; i++)
                             if (i < vlen) a += vv[i] * bl[vq * vlen + i];
@@ -219,10 +241,19 @@ __global__ __launch_bounds__(kFThreads) __attribute__((amdgpu_waves_per_eu(1, 1)
                     __syncthreads();
                 }
             }
+            // expert r's P row share for the readout: TPR threads per row, coordinates pu, pu + TPR, ...
+            T pw[PE];
+            auto load_p = [&]() {
+                if (prow < R) {
+                    const T *pr = y.P + ((size_t)r * R + prow) * n;
+#pragma unroll
+                    for (int e = 0; e < PE; e++) pw[e] = pu + TPR * e < n ? pr[pu + TPR * e] : T(0);
+                }
+            };
             // h = T_r[x] + U'_r zl + A_r h_old, thread i for coordinate i
             T hv = T(0);
             if (tid < n) {
-                // (the table entry, U' row and A row of coordinate i loaded together; sums in index order)
+                // (the table entry, U' column and A row of coordinate i loaded together; sums in index order)
                 const int i = tid;
                 const T *trow = l == 0 ? y.table + (size_t)x * n : y.table + ((size_t)r * V + x) * n;
                 const bool up = l > 0 && y.Up != nullptr, ta = y.A != nullptr;
@@ -235,6 +266,7 @@ __global__ __launch_bounds__(kFThreads) __attribute__((amdgpu_waves_per_eu(1, 1)
 #pragma unroll
                 for (int j = 0; j < MB; j++) aw[j] = (ta && j < b) ? acol[j * b] : T(0);
                 T h = trow[i];
+                if constexpr (PF) load_p();
                 if (up) {
                     T a = T(0);
 #pragma unroll
@@ -251,6 +283,8 @@ __global__ __launch_bounds__(kFThreads) __attribute__((amdgpu_waves_per_eu(1, 1)
                 }
                 hv = h;
                 if (stats) smax[l] = fmax(smax[l], (double)fabs(h));
+            } else if constexpr (PF) {
+                load_p();
             }
             // (every thread has read hs[l] before it is overwritten below)
             const T ss = block_sum(tid < n ? hv * hv : T(0), red, tid);
@@ -266,13 +300,9 @@ __global__ __launch_bounds__(kFThreads) __attribute__((amdgpu_waves_per_eu(1, 1)
             const T rinv = T(1) / sqrt(ss / T(n) + T(kRmsEps));
             if (tid < n) bl[tid] = hv * rinv;
             __syncthreads();
-            // z = P_r h: TPR threads per row, coordinates pu, pu + TPR, ... (every load issued at once)
+            // z = P_r h (every load issued at once)
+            if constexpr (!PF) load_p();
             if (prow < R) {
-                const T *pr = y.P + ((size_t)r * R + prow) * n;
-                constexpr int PE = RS ? (NS * RS + kFThreads - 1) / kFThreads : MN / 4;   // coordinates per thread
-                T pw[PE];
-#pragma unroll
-                for (int e = 0; e < PE; e++) pw[e] = pu + TPR * e < n ? pr[pu + TPR * e] : T(0);
                 T a = T(0);
 #pragma unroll
                 for (int e = 0; e < PE; e++)
@@ -285,11 +315,8 @@ __global__ __launch_bounds__(kFThreads) __attribute__((amdgpu_waves_per_eu(1, 1)
             }
             __syncthreads();
             // logits += Q z, thread c for class c
+            if constexpr (!PF) load_q();
             if (tid < C) {
-                const T *q = y.Q + tid;                                    // column c of Q^T
-                T qw[MR];
-#pragma unroll
-                for (int j = 0; j < MR; j++) qw[j] = j < R ? q[(size_t)j * C] : T(0);
                 T a = T(0);
 #pragma unroll
                 for (int j = 0; j < MR; j++)
