@@ -647,7 +647,7 @@ def run_float_batch1(n_tok: int = 1024, graph_steps: int = 256) -> dict:
             "tokens": n_tok, "us_per_token_run": round(run_us, 3), "us_per_token_graph_step": round(step_us, 3),
             "graph_steps_per_graph": graph_steps, "graph_logits_equal_run": same,
             "reference_triton_us_per_token": REF_FLOAT_GPU_US, "reference_source": "README.md:43 (GPU µs/tok)",
-            "kernel": "ygg::float_kernel<float>"}
+            "kernel": fm.kernel_name}
 
 
 if __name__ == "__main__":

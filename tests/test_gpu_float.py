@@ -73,6 +73,37 @@ def test_float32_kernel_close_to_restatement(ckpt):
     m.close()
 
 
+@pytest.mark.parametrize("shape", [(128, 16, 32), (256, 32, 64)], ids=["medium", "large"])
+def test_float32_trained_shape_builds(shape):
+    """The f32 builds specialised on the reference's medium and large trained shapes (5 layers, block 16, router depth
+    10: rounds of 4, 4 and 2 levels, the first from LDS; configs/enwik8/{medium,large}.yaml), against the float64
+    restatement as in test_float32_kernel_close_to_restatement. A vocabulary of 32 keeps the precomputed tables small
+    (the build is picked by the shape alone)."""
+    import torch
+    n, R, R2 = shape
+    spec = FM.FloatSpec(d_state=n, block_size=16, router_depth=10, vocab=32, n_layers=5, router_token_dim=16,
+                        input_rank=64 if n == 256 else 32, readout_rank=R, layer_input_rank=R2)
+    raw, ob = FM.from_params(FM.random_params(spec, 7))
+    layers = FM.float_layers(raw, blas=True)
+    x = np.random.default_rng(3).integers(0, spec.vocab, (8, 24))
+    ref = FO.run(layers, ob, x)
+    m = FM.FloatYggdrasil(layers, ob, precision=32)
+    assert m.kernel_name == "ygg::float_kernel<float, %d, %d, %d, 16>" % shape, m.kernel_name
+    _say(f"trained shape {shape}: {m.kernel_name}")
+    r = m.run(x, leaves=True)
+    torch.cuda.synchronize()
+    lv, lg = r["leaves"].cpu().numpy(), r["logits"].cpu().numpy().astype(np.float64)
+    differs = (lv != ref["leaves"]).any(-1)
+    split = 0
+    for s in range(x.shape[0]):
+        t1 = int(np.argmax(differs[s])) if differs[s].any() else x.shape[1]
+        split += t1 < x.shape[1]
+        np.testing.assert_allclose(lg[s, :t1], ref["logits"][s, :t1], rtol=2e-4, atol=2e-4)
+    _say(f"  {split} of {x.shape[0]} streams leave the f64 route somewhere in {x.shape[1]} tokens")
+    assert split <= 2
+    m.close()
+
+
 def test_float32_step_reference_protocol(ckpt):
     """The reference's check of its float32 GPU step (cpu/tests/test_triton.py:28-67): 64 streams x 256 steps, every
     step started from the float64 state of the restatement, log-probabilities within ATOL = 1e-4, and at most

@@ -255,6 +255,13 @@ class FloatYggdrasil:
         check(L.ygg_float_load(ctypes.byref(d), precision, self.device.index, ctypes.byref(h)))
         self._h = h
         self.output_bias = np.asarray(output_bias, np.float64)
+        # the build ygg_float_run launches (csrc/ygg_float.hip: f32 builds of their own for the reference's trained
+        # shapes (n, R, R2) at block 16, else the general one), as profilers name it
+        shape = (self.n, R, R2)
+        if precision == 32 and d.block_size == 16 and shape in ((64, 8, 16), (128, 16, 32), (256, 32, 64)):
+            self.kernel_name = "ygg::float_kernel<float, %d, %d, %d, 16>" % shape
+        else:
+            self.kernel_name = "ygg::float_kernel<%s>" % ("float" if precision == 32 else "double")
 
     @classmethod
     def load(cls, path, backend: str = "hip", precision: int = 32, **kw):
