@@ -49,12 +49,12 @@ def _model(model_dir, n, D, V, L, R=8, R2=16, group=False, router="gauss", seed=
 
 CASES = [
     # (d_state, depth, vocab, layers, R, R2, group): configuration 4's shape, configuration 1's, configuration 3's,
-    # the reference's medium shape, other plans (8: two rounds; 10, 13: folded tails; 12: 4, 4, 4; 14: 4, 4, 3, 3),
-    # group scales, a 2-layer model (one routed layer: the slot holds the token layer and layer 1's route)
+    # the reference's small shape (5 layers), other plans (8: two rounds; 10, 13: folded tails; 12: 4, 4, 4; 14: 4, 4,
+    # 3, 3), group scales, a 2-layer model (one routed layer: the slot holds the token layer and layer 1's route)
     (128, 14, 256, 4, 8, 16, False),
     (64, 10, 256, 2, 8, 16, False),
     (96, 13, 5, 3, 8, 16, False),
-    (128, 10, 256, 5, 16, 32, False),
+    (64, 10, 256, 5, 8, 16, False),
     (128, 8, 27, 4, 8, 16, False),
     (128, 12, 256, 3, 8, 16, True),
     (64, 14, 256, 5, 8, 16, True),
@@ -155,4 +155,24 @@ def test_spec_epoch_wrap_and_off(model_dir, monkeypatch):
     assert model.info.spec_max_streams == 0
     assert not _is_spec(model.kernel_name(1, steps, generate=True))
     np.testing.assert_array_equal(model.generate(prompt, steps, temperature=0)[4:], want[0])
+    model.close()
+
+
+def test_spec_only_with_deep_descent(model_dir, monkeypatch):
+    """A shape whose deep descent does not fit LDS (the reference's medium shape at 5 layers) has no speculating build:
+    one stream's generation takes the generate build with the one-token build's descent, and equals the oracle."""
+    import torch
+    from yggdrasil_amd.inference import Yggdrasil
+    monkeypatch.delenv("YGG_KERNEL", raising=False)
+    monkeypatch.delenv("YGG_SPEC", raising=False)
+    path = _model(model_dir, 128, 10, 256, 5, 16, 32)
+    model = Yggdrasil.load(path)
+    assert model.info.spec_max_streams == 0
+    name = model.kernel_name(1, 64, generate=True)
+    assert name == "ygg::fast_kernel<128, 16, 32, 5, 4, false, false, false>", name
+    prompt = synth.zipf_bytes(1, 4, 9)[0]
+    out = model.generate(prompt, 48, temperature=0)
+    torch.cuda.synchronize()
+    want, _ = _greedy(O.Oracle(path), prompt[None, :], 48)
+    np.testing.assert_array_equal(out[4:], want[0])
     model.close()
