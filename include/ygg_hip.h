@@ -71,7 +71,8 @@ typedef struct {
     int32_t router_rounds;     /* rounds of the router plan (levels read per dependent step of the descent) */
     int32_t spec_max_streams;  /* 1: ygg_generate calls of one stream (B = 1) and at least 8 tokens run with helper
                                   workgroups that compute the next token's first layers for every candidate token
-                                  (d_state <= 128, the deep descent's plans; YGG_SPEC=0 at load time: off); 0: never */
+                                  (d_state <= 128, 2 to 5 layers, where the deep descent's plans and LDS tables fit;
+                                  YGG_SPEC=0 at load time: off); 0: never */
     int32_t grouped;           /* 1: ygg_run_grouped takes the model (d_state 128, readout rank 8, layer-input rank 16,
                                   block 16, table storage, tensor scales, router depth <= 14); 0: it reports
                                   YGG_ERR_LIMITS */
@@ -155,8 +156,8 @@ int ygg_score(const ygg_model *m, const int32_t *d_tokens, const int32_t *d_targ
    d_out (B, n) int32; d_logits (B, n, vocab) f32 or NULL. A first token outside [0, vocab) sets bit 0 of the error
    word and leaves that stream's d_out unwritten.
    One stream (B = 1) and n >= 8 on a model with info.spec_max_streams = 1: the launch also runs helper workgroups
-   that compute step t + 1's first layers for every candidate token while step t finishes, in the model's
-   speculation area; results are the same bit for bit. Calls of this kind that overlap on one model (other
+   (up to 128, one CU each) that compute step t + 1's first layers for every candidate token while step t
+   finishes, in the model's speculation area; results are the same bit for bit. Calls of this kind that overlap on one model (other
    streams, other threads) share that area: each one's results stay correct, but they take each other's slots and
    run slower. */
 int ygg_generate(const ygg_model *m, const int32_t *d_first, int B, int n, int8_t *d_state, float temperature,
@@ -165,8 +166,9 @@ int ygg_generate(const ygg_model *m, const int32_t *d_first, int B, int n, int8_
 /* Counters of the speculating generation since the last reset (no counterpart in the reference; for tests and
    benchmarks): out[0] steps whose first layers came from a helper, out[1] steps the stream computed itself (after
    the first of each call), out[2] helper wavefronts that served a step, out[3] helper wavefronts that started (one
-   per candidate token they cover), out[4] helper wavefronts that stopped waiting (no publication for 200 us). Synchronous: call after the generating stream has finished. reset != 0
-   sets them to zero. All zero for a model without the speculating build. */
+   per candidate token they cover), out[4] helper wavefronts that stopped waiting (no publication for 200 us).
+   Synchronous: call after the generating stream has finished. reset != 0 sets them to zero. All zero for a model
+   without the speculating build. */
 int ygg_spec_stats(const ygg_model *m, uint64_t out[5], int reset);
 
 /* Wait for `stream`, then return and clear the model's error word: bit 0 set when a kernel met a token outside
