@@ -926,6 +926,17 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
     int spec_hits = 0, spec_misses = 0;
     bool spec_prev = true;
     int8_t *const sps = spw[0];
+    // SPEC: the output bias, loaded once (a load issued after the publication's stores would wait for them too); the
+    // sampled tokens, written 64 at a time (lane t % 64 holds step t's), so that no store waits ahead of a slot's look
+    float bias[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        bias[u] = (SPEC && 4 * lane + u < VP) ? m.output_bias[4 * lane + u] : 0.0f;
+        // (waited for here: a load still in flight at the loop's entry would be waited for, with every later one, in
+        // the loop)
+        if constexpr (SPEC) asm volatile("" : "+v"(bias[u]));
+    }
+    int gen_held = 0, sampled = 0;
 
     for (int t = 0; t < T; t++) {
         const int x = x_next;
@@ -934,23 +945,27 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
             if (lane == 0) atomicOr(m.err, 1u);
             break;
         }
-        // thresholds of the first router round of every routed layer (SPEC: loaded before the slot is polled for, so
-        // that they are in by the time the layers after SPS need them; every layer's, the slot not being known yet)
+        // thresholds of the first router round of every routed layer (SPEC: issued after the slot's poll, behind the
+        // slot's record: loads issued before the poll's loop are waited for, at their use, with every later one,
+        // the publication's stores included)
         float th1[LR];
-#pragma unroll
-        for (int l = 1; l < L; l++)
-            th1[l - 1] = qj < nn1 ? m.layers[l].thr[(size_t)x * m.layers[l].thr_stride + qj] : 0.0f;
         // DEEP: and those of the second round, four per lane (components in separate arrays, which the selects
         // below keep in registers)
         float th2x[LR], th2y[LR], th2z[LR], th2w[LR];
+        auto load_thresholds = [&]() {
 #pragma unroll
-        for (int l = 1; l < L; l++) {
-            float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            if (DD && 4 * lane < n2)
-                v = *(const float4 *)(m.layers[l].thr + (size_t)x * m.layers[l].thr_stride + (1 << m.round_h[0]) +
-                                      4 * lane);
-            th2x[l - 1] = v.x; th2y[l - 1] = v.y; th2z[l - 1] = v.z; th2w[l - 1] = v.w;
-        }
+            for (int l = 1; l < L; l++)
+                th1[l - 1] = qj < nn1 ? m.layers[l].thr[(size_t)x * m.layers[l].thr_stride + qj] : 0.0f;
+#pragma unroll
+            for (int l = 1; l < L; l++) {
+                float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                if (DD && 4 * lane < n2)
+                    v = *(const float4 *)(m.layers[l].thr + (size_t)x * m.layers[l].thr_stride +
+                                          (1 << m.round_h[0]) + 4 * lane);
+                th2x[l - 1] = v.x; th2y[l - 1] = v.y; th2z[l - 1] = v.z; th2w[l - 1] = v.w;
+            }
+        };
+        if constexpr (!SPEC) load_thresholds();
         // SPEC: x's slot, which holds this step's layers 0 .. SPS - 1 and layer SPS's leaf and layer input (a short
         // wait after a step that had its slot, a single look after one that did not)
         bool hit = false;
@@ -958,7 +973,8 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
         int rs = 0;
         if constexpr (SPEC) {
             if (t > 0) {
-                hit = spec_take<SH, SPS>(io, x, t, qs, sps, lane, spec_prev ? 400 : 30, rs);
+                hit = __builtin_amdgcn_readfirstlane(
+                          (int)spec_take<SH, SPS>(io, x, t, qs, sps, lane, spec_prev ? 400 : 30, rs)) != 0;
                 spec_prev = hit;
                 spec_hits += hit ? 1 : 0;
                 spec_misses += hit ? 0 : 1;
@@ -967,10 +983,11 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
                 rs &= m.E - 1;
                 if (hit) gather<SH, GROUP, true, FACT>(Gs, m.layers[SPS], rs, x, true, lane, K4);
             }
+            load_thresholds();
         }
         float lg[4];
 #pragma unroll
-        for (int u = 0; u < 4; u++) lg[u] = 4 * lane + u < VP ? m.output_bias[4 * lane + u] : 0.0f;
+        for (int u = 0; u < 4; u++) lg[u] = SPEC ? bias[u] : (4 * lane + u < VP ? m.output_bias[4 * lane + u] : 0.0f);
         // SPEC with the slot: publish its states for the next step's helpers (after this step's loads: the waits
         // for them then leave the stores outstanding), and the unembedding terms of layers 0 .. SPS - 1 from its
         // readouts, in layer order
@@ -1014,8 +1031,11 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
         };
 
         // not unrolled: an unrolled loop keeps every layer's pointers in scalar registers at once and spills them
+        // (the first layer taken through readfirstlane: a per-lane index would read every layer's fields with vector
+        // loads)
+        const int l0 = __builtin_amdgcn_readfirstlane((SPEC && hit) ? SPS : 0);
 #pragma unroll 1
-        for (int l = (SPEC && hit) ? SPS : 0; l < L; l++) {
+        for (int l = l0; l < L; l++) {
             const YggDevLayer &y = m.layers[l];
             int r = x;
             float rho = 0.0f;
@@ -1095,7 +1115,13 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
         }
         if (GEN) {
             x_next = __builtin_amdgcn_readfirstlane(sample_token(lg, V, io.temperature, io.top_k, io.seed, s, t, lane));
-            if (lane == 0) io.gen[(size_t)s * T + t] = x_next;
+            if constexpr (SPEC) {
+                if (lane == (t & 63)) gen_held = x_next;
+                if ((t & 63) == 63) io.gen[(size_t)s * T + t - 63 + lane] = gen_held;
+                sampled = t + 1;
+            } else if (lane == 0) {
+                io.gen[(size_t)s * T + t] = x_next;
+            }
         }
         if (states) {
             int8_t *so = states + ((size_t)s * T + t) * L * N;
@@ -1107,6 +1133,11 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
         if (!staged) __syncthreads();
     wave_sync();
     for (int i = lane; i < L * N; i += 64) st[i] = qs[i];
+    if constexpr (SPEC) {
+        // the sampled tokens after the last whole 64
+        const int rest = sampled & 63;
+        if (lane < rest) io.gen[(size_t)s * T + sampled - rest + lane] = gen_held;
+    }
     if constexpr (SPEC)
         if (lane == 0) {
             spec_count(io.spec, 0, (unsigned long long)spec_hits);
