@@ -166,7 +166,7 @@ int ygg_generate(const ygg_model *m, const int32_t *d_first, int B, int n, int8_
 /* Counters of the speculating generation since the last reset (no counterpart in the reference; for tests and
    benchmarks): out[0] steps whose first layers came from a helper, out[1] steps the stream computed itself (after
    the first of each call), out[2] helper wavefronts that served a step, out[3] helper wavefronts that started (one
-   per candidate token they cover), out[4] helper wavefronts that stopped waiting (no publication for 200 us).
+   per candidate token they cover), out[4] helper wavefronts that stopped waiting (no step's states for 200 us).
    Synchronous: call after the generating stream has finished. reset != 0 sets them to zero. All zero for a model
    without the speculating build. */
 int ygg_spec_stats(const ygg_model *m, uint64_t out[5], int reset);

@@ -835,7 +835,7 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
     // the deep descent (DEEP: second round in LDS)
     constexpr bool DD = DEEP || MODE == kModeOne || MODE == kModeGenOne || SPEC;
     // SPEC: the routed layers whose descent the helpers take over; every wavefront's state rows (a helper's: the new and
-    // the published states of those layers) and slot tail (ygg_kernel_spec.h)
+    // the old states of those layers) and slot tail (ygg_kernel_spec.h)
     constexpr int SPS = SPEC ? kSpecDepth<L> : 1;
     using SLY = SpecLayout<SH, SPS>;
     constexpr int QB = (SPEC && 2 * SPS > L ? 2 * SPS : L) * N;
@@ -846,7 +846,6 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
     __shared__ __attribute__((aligned(16))) int8_t zlw[W][SH::ZL];
     __shared__ __attribute__((aligned(16))) int8_t zqw[W][SH::ZQ];
     __shared__ __attribute__((aligned(16))) int8_t spw[SPEC ? kFastWaves : 1][SPEC ? SLY::TB : 16];
-    __shared__ uint32_t pubw[SPEC ? SLY::PW + 2 : 1];     // SPEC, a helper workgroup: the publication it serves
 
     // the wavefront index, stream, tokens and leaves are uniform over a wavefront: kept in scalar registers. With one
     // stream per workgroup (W = 1) wavefronts 1-3 stage the LDS tables and then leave.
@@ -862,7 +861,7 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
             if (wv >= kSpecWPW) return;
             spec_helper<SH, L, GROUP, DEEP>(m, io, T, (blockIdx.x - 1) * kSpecWPW + wv,
                                             spec_helper_waves(io.spec_helpers), S, GT, &W1s[0][0], qsw[wv], spw[wv], lane,
-                                            pubw, blockIdx.x % kSpecPubCopies, kSpecWPW == kFastWaves, wv);
+                                            blockIdx.x % kSpecCopies);
             return;
         }
     }
@@ -895,7 +894,7 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
             if constexpr (SPEC)
                 spec_helper<SH, L, GROUP, DEEP>(m, io, T, io.spec_helpers * kSpecWPW + wv - 1,
                                                 spec_helper_waves(io.spec_helpers), S, GT, &W1s[0][0], qsw[wv],
-                                                spw[wv], lane, pubw, 0, false, wv);
+                                                spw[wv], lane, 0);
             return;
         }
     } else {
@@ -926,8 +925,9 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
     int spec_hits = 0, spec_misses = 0;
     bool spec_prev = true;
     int8_t *const sps = spw[0];
-    // SPEC: the output bias, loaded once (a load issued after the publication's stores would wait for them too); the
-    // sampled tokens, written 64 at a time (lane t % 64 holds step t's), so that no store waits ahead of a slot's look
+    // SPEC: the output bias, loaded once (the wait for a load issued after a store waits for the store too); the
+    // sampled tokens, written 64 at a time (lane t % 64 holds step t's), so that no such store waits ahead of a slot's
+    // look
     float bias[4];
 #pragma unroll
     for (int u = 0; u < 4; u++) {
@@ -937,6 +937,9 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
         if constexpr (SPEC) asm volatile("" : "+v"(bias[u]));
     }
     int gen_held = 0, sampled = 0;
+    // SPEC: the first step's input for its helpers
+    if constexpr (SPEC)
+        if (T >= 2 && x_next >= 0 && x_next < V) spec_token(io, 0, x_next, lane);
 
     for (int t = 0; t < T; t++) {
         const int x = x_next;
@@ -946,8 +949,8 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
             break;
         }
         // thresholds of the first router round of every routed layer (SPEC: issued after the slot's poll, behind the
-        // slot's record: loads issued before the poll's loop are waited for, at their use, with every later one,
-        // the publication's stores included)
+        // slot's record: loads issued before the poll's loop are waited for, at their use, with every later load and
+        // store)
         float th1[LR];
         // DEEP: and those of the second round, four per lane (components in separate arrays, which the selects
         // below keep in registers)
@@ -988,11 +991,8 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
         float lg[4];
 #pragma unroll
         for (int u = 0; u < 4; u++) lg[u] = SPEC ? bias[u] : (4 * lane + u < VP ? m.output_bias[4 * lane + u] : 0.0f);
-        // SPEC with the slot: publish its states for the next step's helpers (after this step's loads: the waits
-        // for them then leave the stores outstanding), and the unembedding terms of layers 0 .. SPS - 1 from its
-        // readouts, in layer order
+        // SPEC with the slot: the unembedding terms of layers 0 .. SPS - 1 from its readouts, in layer order
         if constexpr (SPEC) {
-            if (hit && t + 1 < T) spec_publish<SH, SPS>(io, t, qs, lane);
             if (hit && 4 * lane < VP) {
 #pragma unroll
                 for (int l = 0; l < SPS; l++) {
@@ -1097,7 +1097,7 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
             wave_sync();
             // SPEC, step computed here: its states of layers 0 .. SPS - 1 for the next step's helpers
             if constexpr (SPEC)
-                if (!hit && l == SPS - 1 && t + 1 < T) spec_publish<SH, SPS>(io, t, qs, lane);
+                if (!hit && l == SPS - 1 && t + 1 < T) spec_publish<SH, SPS>(io, t, x, qs, lane);
             if (leaves && lane == 0) leaves[((size_t)s * T + t) * L + l] = r;
             if (SCORE && digest) dg = dg * kDigestMul + digest_term<N>(qn, r, l, lane);
 #pragma unroll
@@ -1116,6 +1116,8 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
         if (GEN) {
             x_next = __builtin_amdgcn_readfirstlane(sample_token(lg, V, io.temperature, io.top_k, io.seed, s, t, lane));
             if constexpr (SPEC) {
+                // the next step's input for its helpers (steps up to T - 2 have them)
+                if (t + 2 < T) spec_token(io, t + 1, x_next, lane);
                 if (lane == (t & 63)) gen_held = x_next;
                 if ((t & 63) == 63) io.gen[(size_t)s * T + t - 63 + lane] = gen_held;
                 sampled = t + 1;

@@ -15,8 +15,12 @@
 // atomic). A reader takes a block only when every unit carries the epoch it expects, so a unit that is stale, torn
 // by a concurrent writer or left by another call is never used; the stream computes the step itself instead, with
 // the same code as without helpers, and every result is the same bit for bit either way.
-//   - publication: after step t's layer S - 1 the stream stores the states of layers 0 .. S - 1 (tag E0 + t);
-//   - slot of x: the helper of x stores step t + 1's results for x (tag E0 + t + 1).
+//   - token unit: the stream stores its input x(t) of step t as soon as it has sampled it (tag E0 + t);
+//   - slot of x: the helper of x stores step t + 1's results for x (tag E0 + t + 1), the states of layers
+//     0 .. S - 1 in every copy. A step the stream computes itself (the first, or one whose slot did not come in
+//     time) it stores the same states into the slot of its input (tag E0 + t), as a helper would have.
+// The helpers of step t + 1 thus read the states after step t from the slot of x(t) as soon as its helper has stored
+// them, not after the stream has taken them: the stream's own poll is off their chain.
 // Stores and loads are at device scope (written through past the XCD's L2, read past it), coherent between XCDs:
 // each XCD has its own L2, and 255 helpers on the stream's XCD alone move about 9 MB per step through that XCD's
 // share of the fabric, which measured twice as slow a chain for every helper and for the stream itself (10.4 us a
@@ -44,13 +48,12 @@ __host__ __device__ constexpr int spec_helper_waves(int h) { return h * kSpecWPW
 template <int L> constexpr int kSpecDepth = L > 2 ? 2 : 1;
 
 template <class SH, int S> struct SpecLayout {
-    static constexpr int PW = S * SH::N / 4;                                   // published words
+    static constexpr int PW = S * SH::N / 4;                                   // state words (in every copy)
     static constexpr int KP = (PW + 63) / 64;                                  // their units per lane
-    static_assert(KP * 64 <= kSpecPubUnits, "publication units");
     static constexpr int SW = S * SH::N / 4 + S * SH::R / 4 + 1 + SH::R2P / 4;  // slot words
     static constexpr int KS = (SW + 63) / 64;
     static constexpr int TB = S * SH::R + 4 + SH::ZL;    // LDS bytes of a slot after the states: zq .., leaf, zl
-    static_assert(KP <= 4 && KS <= 4 && KS * 64 <= kSpecSlotUnits, "units per lane");
+    static_assert(KP <= 4 && KS <= 4 && KS * 64 <= kSpecCopyUnits, "units per lane");
 };
 
 __device__ __forceinline__ uint64_t spec_unit(uint32_t tag, uint32_t word) { return (uint64_t)word << 32 | tag; }
@@ -65,34 +68,28 @@ __device__ __forceinline__ void spec_count(uint64_t *area, int which, unsigned l
 }
 
 // wall-clock bound (100 MHz ticks)
-constexpr uint64_t kSpecPubWait = 20000;       // 200 us between two publications
+constexpr uint64_t kSpecPubWait = 20000;       // 200 us between two steps' states
 
-// The helper wavefront j of nh: serves every publication of this call from the first (relative epoch 0) to T - 2.
-// qh: this wavefront's LDS states, new states of layers 0 .. S - 1 at qh (the slot's order), the published (old)
-// ones at qh + S N; sp: the slot's tail (zq of layers 0 .. S - 1, layer S's leaf, its layer input). DEEP: the
-// routed layers' second-round rows are in LDS from W1 on (load_round2's layout: kR2Slots N bytes a layer, fast_kernel's
-// deep descent), else read from global memory.
-// Polling: with coop (a helper workgroup whose 4 wavefronts all help), wavefront 0 polls publication copy `copy` for
-// the workgroup and hands each publication to the others in LDS (pubw: the words, then the epoch and whether one
-// came) behind a workgroup barrier; otherwise (fewer helper wavefronts in a workgroup, and the stream workgroup's,
-// which has a wavefront that meets no barrier) every helper wavefront polls on its own.
+// The helper wavefront j of nh: serves every step of this call from the first (relative epoch 0) to T - 2: for the
+// stream's input xe of step e (its token unit), it reads the states after step e from xe's slot (copy `copy`) and
+// computes step e + 1 for its candidate. qh: this wavefront's LDS states, new states of layers 0 .. S - 1 at qh (the
+// slot's order), the old ones at qh + S N; sp: the slot's tail (zq of layers 0 .. S - 1, layer S's leaf, its layer
+// input). DEEP: the routed layers' second-round rows are in LDS from W1 on (load_round2's layout: kR2Slots N bytes a
+// layer, fast_kernel's deep descent), else read from global memory. Every helper wavefront polls on its own.
 template <class SH, int L, bool GROUP, bool DEEP>
 __device__ __forceinline__ void spec_helper(const YggDevModel &m, const YggIO &io, int T, int j, int nh,
                                             const SharedTables<SH, L> &St, const GroupTablesOf<SH, L, GROUP> &GT,
-                                            const int8_t *W1, int8_t *qh, int8_t *sp, int lane, uint32_t *pubw,
-                                            int copy, bool coop, int wv) {
+                                            const int8_t *W1, int8_t *qh, int8_t *sp, int lane, int copy) {
     constexpr int N = SH::N, R = SH::R, S = kSpecDepth<L>;
     using LY = SpecLayout<SH, S>;
     using F = SH;
     uint64_t *const area = io.spec;
     const uint32_t E0 = io.spec_epoch;
-    // (no publication to serve; with a cooperative workgroup every wavefront stays to meet the barriers, one with no
-    // candidate (past the vocabulary while every candidate has one) idle)
-    if (T < 2 || (!coop && (j >= nh || (nh >= m.V && j >= m.V)))) return;
-    const bool idle = j >= nh || (nh >= m.V && j >= m.V);
-    const uint32_t span = (uint32_t)T - 2;        // relative epochs of the publications worth serving
-    const uint64_t *pub = area + kSpecPub + (size_t)copy * kSpecPubUnits;
-    if (lane == 0 && !idle) spec_count(area, 3, 1);
+    // (no step to serve, or no candidate: past the vocabulary while every candidate has a wavefront)
+    if (T < 2 || j >= nh || (nh >= m.V && j >= m.V)) return;
+    const uint32_t span = (uint32_t)T - 2;        // relative epochs worth serving
+    const uint64_t *tokp = area + kSpecTok + (size_t)copy * kSpecCopyUnits;
+    if (lane == 0) spec_count(area, 3, 1);
     const int V = m.V;
     const int n2 = m.n_rounds > 1 ? 1 << (m.round_h[0] + m.round_h[1]) : 0;
     const int qj = lane >> 2, nn1 = (1 << m.round_h[0]) - 1;
@@ -103,8 +100,8 @@ __device__ __forceinline__ void spec_helper(const YggDevModel &m, const YggIO &i
     int served = 0;
     bool timed_out = false;
     // every candidate has a wavefront of its own (x = j at every epoch): its token-layer record and thresholds load
-    // while the publication is awaited
-    const bool fixed = nh >= m.V && !idle;
+    // while the states are awaited
+    const bool fixed = nh >= m.V;
     while (next <= span) {
         Gather<SH, false> G;
         float th1[S];
@@ -122,79 +119,101 @@ __device__ __forceinline__ void spec_helper(const YggDevModel &m, const YggIO &i
             }
         };
         if (fixed) prefetch(j);
-        // the next publication: every unit in one round trip, lane 0's first naming the epoch the others must carry
-        // (coop: wavefront 0 for the workgroup)
-        uint64_t u[LY::KP];
+        // the newest token not served yet (epoch e, the stream's input xe of step e), then copy `copy` of xe's states
+        // after step e in xe's slot: two looks in flight each (as in spec_take); the slot is whole when every unit
+        // carries tag E0 + e, and a unit with a later tag means that the slot has been rewritten for a later step (this
+        // wavefront is behind: it goes on to the next token)
+        const uint64_t t0 = wall_clock64();
         uint32_t e = 0;
+        int xe = 0;
         bool got = false;
-        if (!coop || wv == 0) {
-            // two looks in flight (as in spec_take); a look is whole when every unit carries the tag of an epoch not
-            // served yet
-            uint64_t v[LY::KP];
-            auto look = [&](uint64_t (&d)[LY::KP]) {
-#pragma unroll
-                for (int k = 0; k < LY::KP; k++) {
-                    const int w = 64 * k + lane;
-                    d[k] = w < LY::PW ? spec_load(pub + w) : 0ull;
-                }
+        {
+            auto fresh = [&](uint64_t d) {
+                const uint32_t e0 = (uint32_t)d - E0;
+                return e0 >= next && e0 <= span;
             };
-            auto whole = [&](const uint64_t (&d)[LY::KP]) {
-                const uint32_t tag = __builtin_amdgcn_readfirstlane((uint32_t)d[0]), e0 = tag - E0;
-                if (e0 < next || e0 > span) return false;
-                bool bad = false;
-#pragma unroll
-                for (int k = 0; k < LY::KP; k++) bad = bad || (64 * k + lane < LY::PW && (uint32_t)d[k] != tag);
-                if (lane_mask(bad) != 0ull) return false;
-                e = e0;
-                return true;
-            };
-            const uint64_t t0 = wall_clock64();
-            look(u);
+            uint64_t a = spec_load(tokp), b;
             for (;;) {
                 __builtin_amdgcn_s_sleep(1);
-                look(v);
-                if (whole(u)) {
+                b = spec_load(tokp);
+                a = uniform_u64(a);
+                if (fresh(a)) {
                     got = true;
                     break;
                 }
                 if (wall_clock64() - t0 > kSpecPubWait) break;
                 __builtin_amdgcn_s_sleep(1);
-                look(u);
-                if (whole(v)) {
-#pragma unroll
-                    for (int k = 0; k < LY::KP; k++) u[k] = v[k];
+                a = spec_load(tokp);
+                b = uniform_u64(b);
+                if (fresh(b)) {
+                    a = b;
                     got = true;
                     break;
                 }
                 if (wall_clock64() - t0 > kSpecPubWait) break;
             }
-        }
-        if (coop) {
-            if (wv == 0) {
-#pragma unroll
-                for (int k = 0; k < LY::KP; k++)
-                    if (64 * k + lane < LY::PW) pubw[64 * k + lane] = (uint32_t)(u[k] >> 32);
-                if (lane == 0) {
-                    pubw[LY::PW] = e;
-                    pubw[LY::PW + 1] = got;
-                }
-            }
-            __syncthreads();
-            e = __builtin_amdgcn_readfirstlane(pubw[LY::PW]);
-            got = __builtin_amdgcn_readfirstlane(pubw[LY::PW + 1]) != 0;
-#pragma unroll
-            for (int k = 0; k < LY::KP; k++)
-                u[k] = 64 * k + lane < LY::PW ? (uint64_t)pubw[64 * k + lane] << 32 : 0ull;
-            // (every wavefront has its copy before wavefront 0 may overwrite the buffer)
-            __syncthreads();
+            e = (uint32_t)a - E0;
+            xe = (int)(uint32_t)(a >> 32);
         }
         if (!got) {
             timed_out = true;
             break;
         }
+        // (the stream writes only tokens it sampled; the bound keeps every address in the area whatever a unit holds)
+        if ((uint32_t)xe >= (uint32_t)V) xe = 0;
+        uint64_t u[LY::KP];
+        {
+            const uint32_t tag = E0 + e;
+            const uint64_t *src = area + kSpecSlots + (size_t)xe * kSpecSlotUnits + (size_t)copy * kSpecCopyUnits;
+            uint64_t v[LY::KP];
+            auto look = [&](uint64_t (&d)[LY::KP]) {
+#pragma unroll
+                for (int k = 0; k < LY::KP; k++) {
+                    const int w = 64 * k + lane;
+                    d[k] = w < LY::PW ? spec_load(src + w) : spec_unit(tag, 0u);
+                }
+            };
+            // 1: whole, -1: rewritten for a later step, 0: not yet
+            auto state = [&](const uint64_t (&d)[LY::KP]) {
+                bool bad = false, late = false;
+#pragma unroll
+                for (int k = 0; k < LY::KP; k++) {
+                    const int32_t dt = (int32_t)((uint32_t)d[k] - tag);
+                    bad = bad || dt != 0;
+                    late = late || dt > 0;
+                }
+                return lane_mask(late) != 0ull ? -1 : (lane_mask(bad) == 0ull ? 1 : 0);
+            };
+            int st = 0;
+            look(u);
+            for (;;) {
+                __builtin_amdgcn_s_sleep(1);
+                look(v);
+                st = state(u);
+                if (st != 0) break;
+                if (wall_clock64() - t0 > kSpecPubWait) break;
+                __builtin_amdgcn_s_sleep(1);
+                look(u);
+                st = state(v);
+                if (st != 0) {
+#pragma unroll
+                    for (int k = 0; k < LY::KP; k++) u[k] = v[k];
+                    break;
+                }
+                if (wall_clock64() - t0 > kSpecPubWait) break;
+            }
+            if (st == 0) {
+                timed_out = true;
+                break;
+            }
+            if (st < 0) {
+                next = e + 1;
+                continue;
+            }
+        }
         next = e + 1;
         const int x = nh >= V ? j : (int)((uint32_t)(j + e) % (uint32_t)V);
-        if (idle || x >= V) continue;
+        if (x >= V) continue;
 #pragma unroll
         for (int k = 0; k < LY::KP; k++) {
             const int w = 64 * k + lane;
@@ -269,12 +288,17 @@ __device__ __forceinline__ void spec_helper(const YggDevModel &m, const YggIO &i
             if (w < LY::SW) {
                 const uint32_t word = w < S * N / 4 ? ((const uint32_t *)qnew)[w]
                                                     : ((const uint32_t *)sp)[w - S * N / 4];
-                spec_store(slot + w, spec_unit(E0 + e + 1, word));
+                const uint64_t v = spec_unit(E0 + e + 1, word);
+                spec_store(slot + w, v);
+                if (w < LY::PW) {
+#pragma unroll
+                    for (int c = 1; c < kSpecCopies; c++) spec_store(slot + c * kSpecCopyUnits + w, v);
+                }
             }
         }
         served++;
     }
-    if (lane == 0 && !idle) {
+    if (lane == 0) {
         if (served) spec_count(area, 2, 1);
         if (timed_out) spec_count(area, 4, 1);
     }
@@ -340,20 +364,28 @@ __device__ __forceinline__ bool spec_take(const YggIO &io, int x, int t, int8_t 
     return true;
 }
 
-// the states of layers 0 .. S - 1 after step t (LDS qs), published for step t + 1's helpers (in every copy)
+// A step the stream computed itself: the states of layers 0 .. S - 1 after step t (LDS qs) into every copy of the
+// slot of its input x (tag E0 + t), for step t + 1's helpers
 template <class SH, int S>
-__device__ __forceinline__ void spec_publish(const YggIO &io, int t, const int8_t *qs, int lane) {
+__device__ __forceinline__ void spec_publish(const YggIO &io, int t, int x, const int8_t *qs, int lane) {
     using LY = SpecLayout<SH, S>;
     const uint32_t tag = io.spec_epoch + (uint32_t)t;
+    uint64_t *const slot = io.spec + kSpecSlots + (size_t)x * kSpecSlotUnits;
 #pragma unroll
     for (int k = 0; k < LY::KP; k++) {
         const int w = 64 * k + lane;
         if (w < LY::PW) {
             const uint64_t v = spec_unit(tag, ((const uint32_t *)qs)[w]);
 #pragma unroll
-            for (int c = 0; c < kSpecPubCopies; c++) spec_store(io.spec + kSpecPub + c * kSpecPubUnits + w, v);
+            for (int c = 0; c < kSpecCopies; c++) spec_store(slot + c * kSpecCopyUnits + w, v);
         }
     }
+}
+
+// the stream's input x of step t, for step t's helpers (lane c stores copy c)
+__device__ __forceinline__ void spec_token(const YggIO &io, int t, int x, int lane) {
+    if (lane < kSpecCopies)
+        spec_store(io.spec + kSpecTok + (size_t)lane * kSpecCopyUnits, spec_unit(io.spec_epoch + (uint32_t)t, (uint32_t)x));
 }
 
 }  // namespace ygg

@@ -114,15 +114,15 @@ constexpr int kModeGenOne = 4;
 constexpr int kModeGenSpec = 5;
 
 // The speculation area of a model (kModeGenSpec), in 8-byte units (a 32-bit tag in the low half, a 32-bit word in the
-// high half): counters at kSpecStats, the published states at
-// kSpecPub (kSpecPubCopies copies kSpecPubUnits apart: their readers spread over as many memory channels), then one
-// slot of kSpecSlotUnits units per candidate token.
+// high half): counters at kSpecStats, the token units at kSpecTok (kSpecCopies copies kSpecCopyUnits apart: their
+// readers spread over as many memory channels), then one slot of kSpecSlotUnits units per candidate token: copy 0 of
+// its states and the rest of its words at its start, copies 1 .. kSpecCopies - 1 of its states kSpecCopyUnits apart.
 constexpr int kSpecStats = 8;           // 5 counters (uint64): hits, misses, helper waves served, started, timed out
 constexpr int kSpecNStats = 5;
-constexpr int kSpecPub = 64;
-constexpr int kSpecPubUnits = 256, kSpecPubCopies = 8;
-constexpr int kSpecSlots = kSpecPub + kSpecPubUnits * kSpecPubCopies;
-constexpr int kSpecSlotUnits = 256;
+constexpr int kSpecTok = 64;
+constexpr int kSpecCopyUnits = 256, kSpecCopies = 8;
+constexpr int kSpecSlots = kSpecTok + kSpecCopyUnits * kSpecCopies;
+constexpr int kSpecSlotUnits = kSpecCopyUnits * kSpecCopies;
 // helper workgroups: kSpecWPW helper wavefronts each (the others stage the LDS tables with them and leave), at most
 // kSpecMaxHelpers of them
 constexpr int kSpecWPW = 2, kSpecMaxHelpers = 128;
