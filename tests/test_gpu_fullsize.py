@@ -173,6 +173,45 @@ def test_few_streams_full_model(cfg, monkeypatch):
 
 
 @pytest.mark.timeout(600)
+@pytest.mark.parametrize("cfg", [3, 4])
+def test_spec_generation_full_model(cfg, monkeypatch):
+    """Greedy generation of one stream on the full configuration 3 and 4 models through the speculating build (the
+    one bench.py's batch-1 leg times): 256 tokens after a 4-token prompt. Every token and every logit equals the
+    oracle's argmax loop, and the helpers served the steps (nearly every step taken from a slot)."""
+    import torch
+    from yggdrasil_amd.inference import Yggdrasil
+    for k in ("YGG_KERNEL", "YGG_SPEC", "YGG_SPEC_EPOCH", "YGG_SPEC_HELPERS"):
+        monkeypatch.delenv(k, raising=False)
+    w = synth.CONFIGS[cfg]
+    path = _model(cfg)
+    steps = 256
+    model = Yggdrasil.load(path)
+    name = model.kernel_name(1, steps, generate=True)
+    _say(f"config {cfg}: speculating generation, {name}")
+    assert name.startswith("ygg::fast_kernel<") and name[len("ygg::fast_kernel<"):-1].split(", ")[4] == "5", name
+    prompt = w.make_tokens(1, 4)[0]
+    model.spec_stats(reset=True)
+    out, lg = model.generate(prompt, steps, temperature=0, return_logits=True)
+    torch.cuda.synchronize()
+    st = model.spec_stats()
+    _say(f"  stats {st}")
+    orc = O.Oracle(path)
+    r = orc.run(prompt[None, :])
+    olg, ost = r["logits"][:, -1], r["state"]
+    for i in range(steps):
+        tok = olg.argmax(-1).astype(np.int32)
+        assert out[4 + i] == tok[0], (cfg, i, int(out[4 + i]), int(tok[0]))
+        np.testing.assert_array_equal(lg[0, i].cpu().numpy(), olg[0], err_msg=f"config {cfg} step {i}")
+        if i + 1 < steps:
+            r = orc.run(tok[:, None], state=ost)
+            olg, ost = r["logits"][:, 0], r["state"]
+    assert st["hits"] + st["misses"] == steps - 1, st
+    assert st["hits"] >= steps - 8 and st["helpers_timed_out"] == 0, st
+    model.close()
+    torch.cuda.empty_cache()
+
+
+@pytest.mark.timeout(600)
 def test_reference_large_shape_full_model():
     """The reference's largest trained shape (configs/enwik8/large.yaml: 5 layers, d = 256, D = 10, R = 32, R2 = 64;
     a random 0.68 GB model of the 681 MB published file's size) over 512 streams x 256 Zipf tokens in one launch, on
