@@ -30,7 +30,7 @@
 // helper wait is bounded by the wall clock and a helper that times out leaves, so every wavefront ends.
 //
 // Placement. Workgroup 0 runs the stream, workgroups 1 .. H help (the dispatcher hands workgroups to the XCDs in
-// turn: about H / 8 on each), kSpecWPW wavefronts each (all 4 stage the LDS tables; the others then leave: two helper
+// turn: workgroup i runs on XCD i mod 8, each on a CU of its own, as read from the hardware XCC and CU ids), kSpecWPW wavefronts each (all 4 stage the LDS tables; the others then leave: two helper
 // wavefronts on a CU instead of four took the descents of configuration 4 from 1.9 to 1.3 us), and the stream
 // workgroup's 3 staging wavefronts help too: kSpecWPW H + 3 helper wavefronts, one candidate each (with H = V /
 // kSpecWPW those of the stream's CU have none and leave); with more candidates than helpers the uncovered ones change
