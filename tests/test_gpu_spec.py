@@ -158,6 +158,39 @@ def test_spec_epoch_wrap_and_off(model_dir, monkeypatch):
     model.close()
 
 
+@pytest.mark.parametrize("case", [(256, 0), (256, 2), (27, 4)], ids=lambda c: f"V{c[0]}_h{c[1]}")
+def test_spec_fewer_helpers_than_candidates(model_dir, monkeypatch, case):
+    """YGG_SPEC_HELPERS=h: h helper workgroups (2 h + 3 helper wavefronts) for more candidates than that, each helper
+    taking candidate (j + step) mod V: most steps find no slot, and the stream computes them and stores their states
+    into its input's slot for the next step's helpers. Greedy tokens and logits equal the oracle's, and both kinds of
+    step occur."""
+    import torch
+    from yggdrasil_amd.inference import Yggdrasil
+    monkeypatch.delenv("YGG_KERNEL", raising=False)
+    monkeypatch.delenv("YGG_SPEC", raising=False)
+    monkeypatch.delenv("YGG_SPEC_EPOCH", raising=False)
+    V, h = case
+    monkeypatch.setenv("YGG_SPEC_HELPERS", str(h))
+    path = _model(model_dir, 128, 14 if V == 256 else 8, V, 4)
+    model = Yggdrasil.load(path)
+    steps = 160
+    assert _is_spec(model.kernel_name(1, steps, generate=True)), model.kernel_name(1, steps, generate=True)
+    orc = O.Oracle(path)
+    prompt = synth.zipf_bytes(1, 6, 11)[0] if V == 256 else synth.uniform_tokens(V, 1, 6, 7)[0]
+    model.spec_stats(reset=True)
+    out, lg = model.generate(prompt, steps, temperature=0, return_logits=True)
+    torch.cuda.synchronize()
+    st = model.spec_stats()
+    _say(f"spec with {h} helper workgroups, V {V}: stats {st}")
+    want, want_lg = _greedy(orc, prompt[None, :], steps)
+    np.testing.assert_array_equal(out[6:], want[0])
+    np.testing.assert_array_equal(lg.cpu().numpy()[0], want_lg[0])
+    assert st["hits"] + st["misses"] == steps - 1, st
+    assert st["misses"] > 0 and st["helpers_started"] == 2 * h + 3, st
+    assert st["helpers_timed_out"] == 0, st
+    model.close()
+
+
 def test_spec_only_with_deep_descent(model_dir, monkeypatch):
     """A shape whose deep descent does not fit LDS (the reference's medium shape at 5 layers) has no speculating build:
     one stream's generation takes the generate build with the one-token build's descent, and equals the oracle."""
