@@ -27,16 +27,17 @@
 // step); spread over the 8 XCDs they move about 1 MB each.
 //
 // Waiting. The stream never waits on a helper beyond a short bounded poll of its slot (then it computes). Every
-// helper wait is bounded by the wall clock and a helper that times out leaves, so every wavefront ends.
+// helper wait is bounded by the wall clock and a helper that times out leaves, so every wavefront ends; a helper that
+// finds the slot it waits for already rewritten for a later step skips to the next token.
 //
 // Placement. Workgroup 0 runs the stream, workgroups 1 .. H help (the dispatcher hands workgroups to the XCDs in
-// turn: workgroup i runs on XCD i mod 8, each on a CU of its own, as read from the hardware XCC and CU ids), kSpecWPW wavefronts each (all 4 stage the LDS tables; the others then leave: two helper
-// wavefronts on a CU instead of four took the descents of configuration 4 from 1.9 to 1.3 us), and the stream
-// workgroup's 3 staging wavefronts help too: kSpecWPW H + 3 helper wavefronts, one candidate each (with H = V /
-// kSpecWPW those of the stream's CU have none and leave); with more candidates than helpers the uncovered ones change
-// with every step (candidate (j + step) mod V for helper j of nh). Every workgroup holds the build's LDS: with the
-// deep descent's second-round rows (the stream's and the helpers' descents both read them from LDS), one workgroup
-// per CU.
+// turn: workgroup i runs on XCD i mod 8, each on a CU of its own, as read from the hardware XCC and CU ids),
+// kSpecWPW wavefronts each (all 4 stage the LDS tables; the others then leave: two helper wavefronts on a CU instead
+// of four took the descents of configuration 4 from 1.9 to 1.3 us), and the stream workgroup's 3 staging wavefronts
+// help too: kSpecWPW H + 3 helper wavefronts, one candidate each (with H = V / kSpecWPW those of the stream's CU have
+// none and leave); with more candidates than helpers the uncovered ones change with every step (candidate
+// (j + step) mod V for helper j of nh). Every workgroup holds the build's LDS: with the deep descent's second-round
+// rows (the stream's and the helpers' descents both read them from LDS), one workgroup per CU.
 #pragma once
 
 namespace ygg {
@@ -385,7 +386,8 @@ __device__ __forceinline__ void spec_publish(const YggIO &io, int t, int x, cons
 // the stream's input x of step t, for step t's helpers (lane c stores copy c)
 __device__ __forceinline__ void spec_token(const YggIO &io, int t, int x, int lane) {
     if (lane < kSpecCopies)
-        spec_store(io.spec + kSpecTok + (size_t)lane * kSpecCopyUnits, spec_unit(io.spec_epoch + (uint32_t)t, (uint32_t)x));
+        spec_store(io.spec + kSpecTok + (size_t)lane * kSpecCopyUnits,
+                   spec_unit(io.spec_epoch + (uint32_t)t, (uint32_t)x));
 }
 
 }  // namespace ygg
