@@ -1150,9 +1150,11 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
 }
 
 
+// (one wave per SIMD for the deep builds and the speculating build, which hold a CU per workgroup: their registers
+// spill to AGPRs instead of scratch)
 template <int N, int R, int R2, int L, int MODE, bool DEEP, bool CAP, bool GROUP>
 __global__ __launch_bounds__(64 * kFastWaves)
-__attribute__((amdgpu_waves_per_eu(DEEP ? 1 : (CAP ? 4 : 2))))
+__attribute__((amdgpu_waves_per_eu((DEEP || MODE == kModeGenSpec) ? 1 : (CAP ? 4 : 2))))
 void fast_kernel(const YggDevModel m, const int32_t *__restrict__ tokens, int B, int T, int8_t *__restrict__ state,
                  const YggIO io) {
     fast_body<N, R, R2, L, MODE, DEEP, CAP, GROUP, false>(m, tokens, B, T, state, io);

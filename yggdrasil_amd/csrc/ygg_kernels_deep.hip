@@ -129,8 +129,7 @@ template <int N, int R, int R2, int L, bool GROUP> Kernel gen_one_k() {
 }
 
 // generation of one stream with speculating helper workgroups (kModeGenSpec, ygg_kernel_spec.h): workgroup 0 runs the
-// stream, workgroups 1 .. io.spec_helpers help; built with the deep descent (spec_k below). Not for the largest shape
-// (its stream's registers spill at the build's bound)
+// stream, workgroups 1 .. io.spec_helpers help (spec_k below)
 template <int N, int R, int R2, int L, bool GROUP, bool DEEP>
 hipError_t launch_spec(const YggDevModel &m, const int32_t *tokens, int B, int T, int8_t *state, const YggIO &io,
                        hipStream_t stream) {
@@ -146,16 +145,19 @@ hipError_t launch_spec(const YggDevModel &m, const int32_t *tokens, int B, int T
 // the speculating build's LDS with the deep descent: the deep kernel's, with every wavefront's states and slot tail
 template <int N, int R, int R2, int L, bool GROUP>
 constexpr bool kSpecDeepFits = kTablesBytes<Shape<N, R, R2>, L> + sizeof(GroupTablesOf<Shape<N, R, R2>, L, GROUP>) +
-                                   (L - 1) * kR2Slots<N> * N + kFastWaves * ((L > 4 ? L : 4) * N + 2 * R + 4 + 64) +
+                                   (L - 1) * kR2Slots<N> * N +
+                                   kFastWaves * ((2 * kSpecDepth<L> > L ? 2 * kSpecDepth<L> : L) * N +
+                                                 kSpecDepth<L> * R + 4 + 64) +
                                    256 <=
                                160 * 1024;
 
-// (only where the deep descent's LDS fits: with the one-token build's descent the stream's registers spill, and the
-// reference's medium shape at 5 layers generated at 11.4 us/token on it against 7.8 on the generate build without it)
+// (with the deep descent where its LDS fits, else with the one-token build's descent; not for n = 256, whose
+// stream's registers spill to scratch even at one wave per SIMD)
 template <int N, int R, int R2, int L, bool GROUP> Kernel spec_k() {
-    if constexpr (L >= 2 && N <= 128 && (!GROUP || kGroupOk<N>) && kSpecDeepFits<N, R, R2, L, GROUP>) {
-        return make_kernel(launch_spec<N, R, R2, L, GROUP, true>, "ygg::fast_kernel<%d, %d, %d, %d, 5, true, false, %s>",
-                           N, R, R2, L, GROUP ? "true" : "false");
+    if constexpr (L >= 2 && N <= 128 && (!GROUP || kGroupOk<N>)) {
+        constexpr bool D = kSpecDeepFits<N, R, R2, L, GROUP>;
+        return make_kernel(launch_spec<N, R, R2, L, GROUP, D>, "ygg::fast_kernel<%d, %d, %d, %d, 5, %s, false, %s>",
+                           N, R, R2, L, D ? "true" : "false", GROUP ? "true" : "false");
     } else {
         return Kernel();
     }
