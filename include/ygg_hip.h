@@ -71,8 +71,8 @@ typedef struct {
     int32_t router_rounds;     /* rounds of the router plan (levels read per dependent step of the descent) */
     int32_t spec_max_streams;  /* 1: ygg_generate calls of one stream (B = 1) and at least 8 tokens run with helper
                                   workgroups that compute the next token's first layers for every candidate token
-                                  (d_state <= 128, 2 to 5 layers, a router plan the deep descent takes; YGG_SPEC=0
-                                  at load time: off); 0: never */
+                                  (2 to 5 layers, a router plan the deep descent takes; YGG_SPEC=0 at load time:
+                                  off); 0: never */
     int32_t grouped;           /* 1: ygg_run_grouped takes the model (d_state 128, readout rank 8, layer-input rank 16,
                                   block 16, table storage, tensor scales, router depth <= 14); 0: it reports
                                   YGG_ERR_LIMITS */

@@ -1071,9 +1071,11 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
                                                                    qs + (l - 1) * N, rho, x, lane, tl, flush);
                 }
             }
-            Gather<SH, FACT> G;
-            if (given) G = Gs;
-            else gather<SH, GROUP, true, FACT>(G, y, r, x, l > 0, lane, K4);
+            // (SPEC: the slot layer's record and every later one in the same registers: a separate copy would stay
+            // live through the loop)
+            Gather<SH, FACT> Gl;
+            Gather<SH, FACT> &G = SPEC ? Gs : Gl;
+            if (!given) gather<SH, GROUP, true, FACT>(G, y, r, x, l > 0, lane, K4);
             if constexpr (W == 1)
                 if (!staged) {      // the LDS tables staged (see above)
                     __syncthreads();

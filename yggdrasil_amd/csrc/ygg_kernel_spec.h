@@ -47,7 +47,7 @@ __host__ __device__ constexpr int spec_helper_waves(int h) { return h * kSpecWPW
 
 // routed layers whose descent the helpers take over: 1 for a 2-layer model, 2 for 3 or 4 layers, 3 for 5 (the
 // stream then keeps two layers, as with 4: with 2 the stream's side of 5 layers set the period, 6.8 us/token on the
-// reference's small shape and 7.1 on its medium one against 4.9 and 5.4 with 3)
+// reference's small shape, 7.1 on its medium one and 12.8 on its large one against 4.9, 5.3 and 10.6 with 3)
 template <int L> constexpr int kSpecDepth = L > 4 ? 3 : (L > 2 ? 2 : 1);
 
 template <class SH, int S> struct SpecLayout {

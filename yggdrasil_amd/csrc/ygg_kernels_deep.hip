@@ -151,10 +151,9 @@ constexpr bool kSpecDeepFits = kTablesBytes<Shape<N, R, R2>, L> + sizeof(GroupTa
                                    256 <=
                                160 * 1024;
 
-// (with the deep descent where its LDS fits, else with the one-token build's descent; not for n = 256, whose
-// stream's registers spill to scratch even at one wave per SIMD)
+// (with the deep descent where its LDS fits, else with the one-token build's descent)
 template <int N, int R, int R2, int L, bool GROUP> Kernel spec_k() {
-    if constexpr (L >= 2 && N <= 128 && (!GROUP || kGroupOk<N>)) {
+    if constexpr (L >= 2 && (!GROUP || kGroupOk<N>)) {
         constexpr bool D = kSpecDeepFits<N, R, R2, L, GROUP>;
         return make_kernel(launch_spec<N, R, R2, L, GROUP, D>, "ygg::fast_kernel<%d, %d, %d, %d, 5, %s, false, %s>",
                            N, R, R2, L, D ? "true" : "false", GROUP ? "true" : "false");
