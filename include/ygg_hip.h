@@ -172,7 +172,9 @@ int ygg_generate(const ygg_model *m, const int32_t *d_first, int B, int n, int8_
 int ygg_spec_stats(const ygg_model *m, uint64_t out[5], int reset);
 
 /* Wait for `stream`, then return and clear the model's error word: bit 0 set when a kernel met a token outside
-   [0, vocab), bit 1 when ygg_score met a target outside it, since the last call. */
+   [0, vocab), bit 1 when ygg_score met a target outside it, bit 2 when a one-token launch's wait for its LDS tables
+   passed 1 ms (a safety bound that a working device never reaches; that launch's results are then undefined), since
+   the last call. */
 int ygg_take_errors(const ygg_model *m, void *stream, uint32_t *errors);
 
 /* ---- The float step (yggdrasil/inference.py:42-74): the inference model of a float checkpoint (.npz), in f32 (the

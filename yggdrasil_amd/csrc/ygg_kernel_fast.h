@@ -239,6 +239,95 @@ __device__ __forceinline__ void load_tables(SharedTables<SH, L, WITHV> &S, const
         if (tid + k * NT < MVN) S.mv[(tid + k * NT) / R2D][(tid + k * NT) % R2D] = mvv[k];
 }
 
+// load_tables for the one-token build, in layer order. Unit j is layer j's unembedding Q and, for a routed layer
+// (j >= 1), its first-round rows and V' rows (unit 0 also carries every m_v). Every load is issued first, in unit
+// order, then each unit's stores, after which the wavefront adds 1 to *done (LDS, workgroup scope): unit j is in LDS
+// once *done reaches NW (j + 1), NW the staging wavefronts. The stream's wavefront waits for a routed layer's unit
+// before that layer's descent instead of for every table at once (the widest shape stages 129 KB).
+template <class SH, int L, int NT>
+__device__ __forceinline__ void load_tables_units(SharedTables<SH, L, true> &S, const YggDevModel &m, int tid,
+                                                  uint32_t *done) {
+    constexpr int N = SH::N, R2 = SH::R2P, QC = SH::QC;
+    constexpr int RC = N / 16, SC = kLdsRow<N> / 16, LR = L > 1 ? L - 1 : 1;
+    constexpr int QK = (16 * SH::R + NT - 1) / NT;
+    constexpr int VR = 15 + R2;
+    constexpr int RK = (VR * RC + NT - 1) / NT;
+    constexpr int R2D = R2 > 0 ? R2 : 1, MVN = L > 1 ? R2 * (L - 1) : 0;
+    constexpr int MVK = MVN > 0 ? (MVN + NT - 1) / NT : 1;
+    const int qch = m.VP * SH::R / 16, rows = (1 << m.round_h[0]) - 1;
+    uint4 qv[L][QK], rv[LR][RK];
+    float mvv[MVK];
+#pragma unroll
+    for (int k = 0; k < MVK; k++) {
+        const int c = tid + k * NT;
+        mvv[k] = 0.0f;
+#pragma unroll
+        for (int l = 1; l < L; l++)
+            if (c < MVN && c / R2D == l - 1) mvv[k] = m.layers[l].mv[c % R2D];
+    }
+#pragma unroll
+    for (int j = 0; j < L; j++) {
+#pragma unroll
+        for (int k = 0; k < QK; k++) {
+            const int c = tid + k * NT;
+            qv[j][k] = make_uint4(0u, 0u, 0u, 0u);
+            if (c < qch) qv[j][k] = ((const uint4 *)m.layers[j].Q)[c];
+        }
+        if (j >= 1) {
+            const YggDevLayer &y = m.layers[j];
+#pragma unroll
+            for (int k = 0; k < RK; k++) {
+                const int c = tid + k * NT;
+                rv[j - 1][k] = make_uint4(0u, 0u, 0u, 0u);
+                if (c < rows * RC)
+                    rv[j - 1][k] = ((const uint4 *)y.w)[c];
+                else if (c >= 15 * RC && c < VR * RC)
+                    rv[j - 1][k] = ((const uint4 *)y.vl)[c - 15 * RC];
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < L; j++) {
+        if (j == 0) {
+#pragma unroll
+            for (int k = 0; k < MVK; k++)
+                if (tid + k * NT < MVN) S.mv[(tid + k * NT) / R2D][(tid + k * NT) % R2D] = mvv[k];
+        }
+#pragma unroll
+        for (int k = 0; k < QK; k++) {
+            const int c = tid + k * NT;
+            if (c < qch) ((uint4 *)S.Q[j])[(c % QC) * 64 + c / QC] = qv[j][k];
+        }
+        if (j >= 1) {
+#pragma unroll
+            for (int k = 0; k < RK; k++) {
+                const int c = tid + k * NT;
+                if (c < 15 * RC)
+                    ((uint4 *)S.W[j - 1])[(c / RC) * SC + c % RC] = rv[j - 1][k];
+                else if (c < VR * RC)
+                    ((uint4 *)S.V[j - 1])[((c - 15 * RC) / RC) * SC + (c - 15 * RC) % RC] = rv[j - 1][k];
+            }
+        }
+        // (the wavefront's LDS stores done, then its count; the wavefront runs in lockstep)
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+        if ((tid & 63) == 0) __hip_atomic_fetch_add(done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+}
+
+// the stream's wait for *done >= need (load_tables_units); the staging wavefronts wait on nothing, so the count
+// arrives; the wall-clock bound (1 ms, then error bit 4) only keeps a fault elsewhere from becoming a hang
+__device__ __forceinline__ void stage_wait(const uint32_t *done, uint32_t need, uint32_t *err, int lane) {
+    const uint64_t t0 = wall_clock64();
+    while (__hip_atomic_load(done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < need) {
+        __builtin_amdgcn_s_sleep(1);
+        if (wall_clock64() - t0 > 100000) {
+            if (lane == 0) atomicOr(err, 4u);
+            break;
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Touch every 64-byte line of the kernel argument (the model description, read by scalar loads) at entry: the
 // scalar cache starts each launch cold, and a layer's fields would otherwise first be read when that layer starts
 // (worth 1 us in a launch of one token; launches of many tokens do without).
@@ -846,6 +935,10 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
     __shared__ __attribute__((aligned(16))) int8_t zlw[W][SH::ZL];
     __shared__ __attribute__((aligned(16))) int8_t zqw[W][SH::ZQ];
     __shared__ __attribute__((aligned(16))) int8_t spw[SPEC ? kFastWaves : 1][SPEC ? SLY::TB : 16];
+    // the one-token build without group scales stages its tables layer by layer (load_tables_units): the count of
+    // staged units, set to 0 before the one barrier every wavefront meets, at entry
+    constexpr bool UNITS = MODE == kModeOne && !GROUP;
+    __shared__ uint32_t stage_done;
 
     // the wavefront index, stream, tokens and leaves are uniform over a wavefront: kept in scalar registers. With one
     // stream per workgroup (W = 1) wavefronts 1-3 stage the LDS tables and then leave.
@@ -874,6 +967,13 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
     const int32_t *tok = tokens + (size_t)s * (GEN ? 1 : T);
     // (measured: the generation kernels run slower with it, 15% with DEEP; one-token launches faster)
     if constexpr (!DEEP && MODE != kModeGenOne && !SPEC) touch_args<L>(m);
+    if constexpr (UNITS) {
+        // (an LDS-only barrier: global loads issued before it stay in flight)
+        if (tid == 0) stage_done = 0u;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    }
     int x_next = (live && T > 0) ? __builtin_amdgcn_readfirstlane(tok[0]) : 0;
     int8_t *st = state + (size_t)s * L * N;
     constexpr int SB = (L * N + 63) / 64;     // state bytes per lane
@@ -886,6 +986,10 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
         // before it first reads them, ahead of the first token's first update. Every wavefront meets exactly one
         // barrier, whatever the number of tokens
         if (wv > 0) {
+            if constexpr (UNITS) {
+                load_tables_units<SH, L, 64 * (kFastWaves - 1)>(S, m, tid - 64, &stage_done);
+                return;
+            }
             load_tables<SH, L, 64 * (kFastWaves - 1)>(S, m, tid - 64);
             if constexpr (GROUP) load_group_tables<SH, L, 64 * (kFastWaves - 1)>(GT, m, tid - 64);
             if constexpr (DEEP) load_round2<N, L, 64 * (kFastWaves - 1)>(W1s, m, tid - 64);
@@ -920,7 +1024,9 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
     wave_sync();
     unsigned long long dg = (SCORE && digest) ? digest[s] : 0ull;
     NllSum nacc;
-    bool staged = W > 1;      // W = 1: the stream's wavefront has met the barrier that waits for the LDS tables
+    // W = 1: the stream's wavefront has met the barrier that waits for the LDS tables (UNITS: met at entry; it waits
+    // for each routed layer's tables before that layer's descent)
+    bool staged = W > 1 || UNITS;
     // SPEC: steps taken from the helpers' slots and computed here, whether the last one was taken
     int spec_hits = 0, spec_misses = 0;
     bool spec_prev = true;
@@ -1044,6 +1150,7 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
             const bool given = SPEC && hit && l == SPS;
             if (given) r = rs;
             if (l > 0 && !given) {
+                if constexpr (UNITS) stage_wait(&stage_done, (uint32_t)((kFastWaves - 1) * (l + 1)), m.err, lane);
                 float th = th1[0];
 #pragma unroll
                 for (int i = 1; i < LR; i++) th = l - 1 == i ? th1[i] : th;
