@@ -156,7 +156,7 @@ int ygg_score(const ygg_model *m, const int32_t *d_tokens, const int32_t *d_targ
    d_out (B, n) int32; d_logits (B, n, vocab) f32 or NULL. A first token outside [0, vocab) sets bit 0 of the error
    word and leaves that stream's d_out unwritten.
    One stream (B = 1) and n >= 8 on a model with info.spec_max_streams = 1: the launch also runs helper workgroups
-   (up to 128, one CU each) that compute step t + 1's first layers for every candidate token while step t
+   (up to one per CU but the stream's) that compute step t + 1's first layers for every candidate token while step t
    finishes, in the model's speculation area; results are the same bit for bit. Calls of this kind that overlap on one model (other
    streams, other threads) share that area: each one's results stay correct, but they take each other's slots and
    run slower. */

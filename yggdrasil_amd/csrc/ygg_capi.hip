@@ -769,10 +769,11 @@ int load_impl(const uint8_t *data, size_t size, int device, ygg_model **out) {
         } else {
             m->spec_area = (uint64_t *)a;
         }
-        // helper workgroups of kSpecWPW helper wavefronts, with the stream workgroup's 3 others one per candidate
-        // token (at most kSpecMaxHelpers of them); YGG_SPEC_HELPERS: fewer
-        // (each workgroup holds a CU: the stream's and the helpers' all resident at once)
-        m->spec_helpers = std::min(std::min(kSpecMaxHelpers, cus - 1), V / kSpecWPW);
+        // helper workgroups, one CU each (the stream's and the helpers' all resident at once), one helper wavefront
+        // per candidate token: one per workgroup where the CUs allow, two on as many as needed (spec_pairs); at
+        // d_state 256 two on every one (one wavefront per CU: configuration 4 4.63 -> 4.55 us per token, the
+        // reference's medium shape 5.26 -> 5.03, its large shape 10.5 -> 10.8); YGG_SPEC_HELPERS: fewer
+        m->spec_helpers = std::min(std::min(kSpecMaxHelpers, cus - 1), n > 128 ? (V + 1) / 2 : V);
         if (const char *eh = getenv("YGG_SPEC_HELPERS")) m->spec_helpers = std::max(0, std::min(m->spec_helpers, atoi(eh)));
         // YGG_SPEC_EPOCH: the first call's first epoch (tests of the wrap; 0 is taken as 1)
         if (const char *ep = getenv("YGG_SPEC_EPOCH")) m->spec_next = (uint32_t)strtoul(ep, nullptr, 0);

@@ -951,9 +951,10 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
             if constexpr (GROUP) load_group_tables<SH, L, 64 * kFastWaves>(GT, m, tid);
             if constexpr (DEEP) load_round2<N, L, 64 * kFastWaves>(W1s, m, tid);
             __syncthreads();
-            if (wv >= kSpecWPW) return;
-            spec_helper<SH, L, GROUP, DEEP>(m, io, T, (blockIdx.x - 1) * kSpecWPW + wv,
-                                            spec_helper_waves(io.spec_helpers), S, GT, &W1s[0][0], qsw[wv], spw[wv], lane,
+            const int j = spec_helper_index(blockIdx.x, wv, io.spec_helpers, m.V);
+            if (j < 0) return;
+            spec_helper<SH, L, GROUP, DEEP>(m, io, T, j, spec_helper_waves(io.spec_helpers, m.V), S, GT, &W1s[0][0],
+                                            qsw[wv], spw[wv], lane,
                                             blockIdx.x % kSpecCopies);
             return;
         }
@@ -996,8 +997,8 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
             __syncthreads();
             // SPEC: then helpers on the stream's own CU
             if constexpr (SPEC)
-                spec_helper<SH, L, GROUP, DEEP>(m, io, T, io.spec_helpers * kSpecWPW + wv - 1,
-                                                spec_helper_waves(io.spec_helpers), S, GT, &W1s[0][0], qsw[wv],
+                spec_helper<SH, L, GROUP, DEEP>(m, io, T, io.spec_helpers + spec_pairs(io.spec_helpers, m.V) + wv - 1,
+                                                spec_helper_waves(io.spec_helpers, m.V), S, GT, &W1s[0][0], qsw[wv],
                                                 spw[wv], lane, 0);
             return;
         }

@@ -31,19 +31,29 @@
 // finds the slot it waits for already rewritten for a later step skips to the next token.
 //
 // Placement. Workgroup 0 runs the stream, workgroups 1 .. H help (the dispatcher hands workgroups to the XCDs in
-// turn: workgroup i runs on XCD i mod 8, each on a CU of its own, as read from the hardware XCC and CU ids),
-// kSpecWPW wavefronts each (all 4 stage the LDS tables; the others then leave: two helper wavefronts on a CU instead
-// of four took the descents of configuration 4 from 1.9 to 1.3 us), and the stream workgroup's 3 staging wavefronts
-// help too: kSpecWPW H + 3 helper wavefronts, one candidate each (with H = V / kSpecWPW those of the stream's CU have
-// none and leave); with more candidates than helpers the uncovered ones change with every step (candidate
-// (j + step) mod V for helper j of nh). Every workgroup holds the build's LDS: with the deep descent's second-round
-// rows (the stream's and the helpers' descents both read them from LDS), one workgroup per CU.
+// turn: workgroup i runs on XCD i mod 8, each on a CU of its own, as read from the hardware XCC and CU ids). All 4
+// wavefronts of a helper workgroup stage the LDS tables; then one of them helps, or two in the first spec_pairs(H, V)
+// workgroups, so that H workgroups cover up to 2 H candidates, and the others leave (one helper wavefront per CU made
+// the descents faster: configuration 4's 1.9 us with four, 1.3 with two, 1.16 with one). The stream workgroup's 3
+// staging wavefronts help too, one candidate each (those past the last candidate leave); with more candidates than
+// helpers the uncovered ones change with every step (candidate (j + step) mod V for helper j of nh). Every workgroup
+// holds the build's LDS: with the deep descent's second-round rows (the stream's and the helpers' descents both read
+// them from LDS), one workgroup per CU.
 #pragma once
 
 namespace ygg {
 
+// of h helper workgroups for V candidates, the first spec_pairs(h, V) run two helper wavefronts, the others one (one
+// candidate per wavefront, as many as fit)
+__host__ __device__ constexpr int spec_pairs(int h, int V) { return V <= h ? 0 : (V - h > h ? h : V - h); }
 // helper wavefronts of h helper workgroups: theirs and the stream workgroup's staging wavefronts
-__host__ __device__ constexpr int spec_helper_waves(int h) { return h * kSpecWPW + kFastWaves - 1; }
+__host__ __device__ constexpr int spec_helper_waves(int h, int V) { return h + spec_pairs(h, V) + kFastWaves - 1; }
+// the helper index of wavefront wv of helper workgroup b (1 .. h), or -1 for a wavefront that does not help
+__device__ __forceinline__ int spec_helper_index(int b, int wv, int h, int V) {
+    const int p = spec_pairs(h, V);
+    if (b <= p) return wv < 2 ? 2 * (b - 1) + wv : -1;
+    return wv < 1 ? p + b - 1 : -1;
+}
 
 // routed layers whose descent the helpers take over: 1 for a 2-layer model, 2 for 3 or 4 layers, 3 for 5 (the
 // stream then keeps two layers, as with 4: with 2 the stream's side of 5 layers set the period, 6.8 us/token on the

@@ -123,9 +123,8 @@ constexpr int kSpecTok = 64;
 constexpr int kSpecCopyUnits = 256, kSpecCopies = 8;
 constexpr int kSpecSlots = kSpecTok + kSpecCopyUnits * kSpecCopies;
 constexpr int kSpecSlotUnits = kSpecCopyUnits * kSpecCopies;
-// helper workgroups: kSpecWPW helper wavefronts each (the others stage the LDS tables with them and leave), at most
-// kSpecMaxHelpers of them
-constexpr int kSpecWPW = 2, kSpecMaxHelpers = 128;
+// helper workgroups (workgroups 1 .. h of the launch, one CU each): at most kSpecMaxHelpers of them
+constexpr int kSpecMaxHelpers = 255;
 inline size_t spec_area_units(int V) { return (size_t)kSpecSlots + (size_t)V * kSpecSlotUnits; }
 inline int io_mode(const YggIO &io) {
     return io.gen ? kModeGenerate : ((io.digest || io.nll) ? kModeScore : kModeRun);
