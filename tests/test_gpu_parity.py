@@ -477,12 +477,13 @@ def test_deep_descent_plans(hip, model_dir, c12, monkeypatch, which, plan):
 @pytest.mark.parametrize("which,plan", [
     ("c4small", None), ("c4small", "4,4,2"), ("c4small", "2,4,2,2"), ("c4small", "4,2,3,1"), ("c4small", "4,4,1,1"),
     ("c4small", "1,3,3,3"), ("c12", None), ("c12", "2,2,3,3"), ("group", None), ("ref_small", None),
-    ("ref_medium", None), ("ref_large", None), ("c3", None)])
+    ("ref_medium", None), ("ref_large", None), ("ref_medium5", None), ("ref_large5", None), ("c3", None)])
 def test_one_token_build(hip, model_dir, c12, c3, monkeypatch, which, plan):
     """Calls of one token (ygg_step, and ygg_run with T = 1) whose streams are all resident take the one-token build
     (the deep descent with its second round read from global memory, or folded into the tail for three-round plans;
     one stream per workgroup) wherever the deep descent takes the plan: 12 streams stepped 6 tokens with the state
-    carried, leaves, states and logits equal the oracle's."""
+    carried, leaves, states and logits equal the oracle's. At 5 layers the build stages its LDS tables layer by layer
+    (the stream waits for each routed layer's before its descent)."""
     import torch
     if which in ("c4small", "group"):
         path = model_dir / ("c4small_gauss.bin" if which == "c4small" else "c4small_group.bin")
@@ -490,10 +491,12 @@ def test_one_token_build(hip, model_dir, c12, c3, monkeypatch, which, plan):
             synth.write_model(synth.ModelSpec(128, 16, 10, 256, 4, router="gauss", group=which == "group"), 11, path)
     elif which.startswith("ref_"):
         # (the reference's trained shapes: n, readout rank, layer-input rank)
-        n, R, R2 = {"ref_small": (64, 8, 16), "ref_medium": (128, 16, 32), "ref_large": (256, 32, 64)}[which]
+        n, R, R2 = {"ref_small": (64, 8, 16), "ref_medium": (128, 16, 32), "ref_large": (256, 32, 64),
+                    "ref_medium5": (128, 16, 32), "ref_large5": (256, 32, 64)}[which]
+        L = 5 if which.endswith("5") else 3
         path = model_dir / f"one_{which}.bin"
         if not path.exists():
-            synth.write_model(synth.ModelSpec(n, 16, 10, 256, 3, readout_rank=R, layer_input_rank=R2, router="gauss"),
+            synth.write_model(synth.ModelSpec(n, 16, 10, 256, L, readout_rank=R, layer_input_rank=R2, router="gauss"),
                               12, path)
     else:
         path = c12 if which == "c12" else c3
