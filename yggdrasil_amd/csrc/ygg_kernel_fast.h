@@ -1048,7 +1048,15 @@ __device__ __forceinline__ void fast_body(const YggDevModel &m, const int32_t *_
     if constexpr (SPEC)
         if (T >= 2 && x_next >= 0 && x_next < V) spec_token(io, 0, x_next, lane);
 
+    const int lane_out = lane;
     for (int t = 0; t < T; t++) {
+        // SPEC at d_state 256: the lane index made opaque at each step, so that every layer's per-lane addresses are
+        // formed in the step instead of hoisted out of the loop and kept live (that shape's stream spilled them to
+        // scratch: 536 -> 368 bytes, 10.5 -> 9.8 us per generated token; the narrower shapes, which do not spill
+        // them, lost 1-8% with it)
+        int lane_in = lane_out;
+        if constexpr (SPEC && N > 128) asm volatile("" : "+v"(lane_in));
+        const int lane = lane_in;
         const int x = x_next;
         if (!GEN && t + 1 < T) x_next = __builtin_amdgcn_readfirstlane(tok[t + 1]);
         if (x < 0 || x >= V) {
